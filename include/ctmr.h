@@ -1,0 +1,170 @@
+/*
+ * ctmr.h — C ABI of libctmr_hip.so, the MI355X (gfx950) implementation of
+ * mlx-generate-ctmr's fast FP32 convolution / group-norm hot path.
+ *
+ * Every activation is NDHWC (channels innermost), fp32 unless a descriptor
+ * says bf16.  All pointers are device pointers owned by the caller; the
+ * library never allocates or frees device memory.  Every call is enqueued on
+ * the caller's HIP stream (`stream`, a hipStream_t passed as void*; NULL is
+ * the default stream) and returns immediately.  Return value: CTMR_OK (0) or
+ * one of the negative CTMR_E* codes; ctmr_last_error() gives a message for
+ * the calling thread.  Nothing in the library calls exit/abort.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   ctmr_conv3d               <- _nax_conv.nax_conv3d (src/mlx_generate_ctmr/_nax_conv.py:475-684),
+ *                                i.e. its pack (:144-198), conv (:200-318) and
+ *                                reduce (:320-332) metal_kernel launches (:586-665)
+ *   ctmr_conv3d_workspace_bytes <- the packed-copy / split-plane sizing in
+ *                                nax_conv3d (:571-581, :667-672)
+ *   ctmr_pack_weight          <- _nax_conv.pack_weight (:391-404)
+ *   ctmr_pack_upsample_weight <- _nax_conv.pack_upsample_weight (:407-445)
+ *   ctmr_gn_affine            <- medmlx_core.group_norm.group_norm_affine, called at
+ *                                fast_fp32.py:185-189 (per-(b,c) scale/offset pairs,
+ *                                layout described at _nax_conv.py:502-504)
+ *   ctmr_gn_apply             <- fast_fp32.group_norm_ncdhw (fast_fp32.py:102-118)
+ *   ctmr_conv3d (ksize 1)     <- fast_fp32.pointwise_conv_ncdhw (fast_fp32.py:121-130)
+ *   ctmr_resample             <- medmlx_core.ops.avg_pool3d_ncdhw / upsample_nearest_ncdhw
+ *                                (fast_fp32.py:48-59) and source_vae.upsample_trilinear_ncdhw
+ *                                (fast_fp32.py:66-68; formula at _nax_conv.py:115-142)
+ */
+#ifndef CTMR_H
+#define CTMR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CTMR_ABI_VERSION 1
+
+enum ctmr_status {
+  CTMR_OK = 0,
+  CTMR_E_INVALID = -1,     /* bad descriptor / shape / null pointer */
+  CTMR_E_UNSUPPORTED = -2, /* valid request this build does not implement */
+  CTMR_E_WORKSPACE = -3,   /* workspace smaller than ctmr_conv3d_workspace_bytes */
+  CTMR_E_LAUNCH = -4       /* HIP reported an error at launch */
+};
+
+/* Input resampling applied while staging the convolution input. */
+enum ctmr_conv_mode {
+  CTMR_MODE_PLAIN = 0,       /* conv of x itself (stride 1 or 2) */
+  CTMR_MODE_NEAREST2X = 1,   /* conv of nearest-2x upsampled x; weights from
+                                ctmr_pack_upsample_weight (parity fold) */
+  CTMR_MODE_TRILINEAR2X = 2  /* conv of half-pixel trilinear-2x upsampled x */
+};
+
+enum ctmr_conv_flags {
+  CTMR_F_AFFINE = 1,     /* y = x*affine[b,c,0] + affine[b,c,1] before the conv */
+  CTMR_F_SILU = 2,       /* SiLU after the affine (or on x) before the conv */
+  CTMR_F_BATCH_BIAS = 4, /* bias is (N, Cout) instead of (Cout) */
+  CTMR_F_RESIDUAL = 8    /* residual (output-shaped, NDHWC) added before the store */
+};
+
+enum ctmr_dtype {
+  CTMR_F32 = 0,  /* fp32 operands, FP32 MFMA (v_mfma_f32_16x16x4_f32) */
+  CTMR_BF16 = 1  /* bf16 operands, fp32 accumulate (v_mfma_f32_16x16x32_bf16);
+                    activations and outputs stay fp32 in memory */
+};
+
+typedef struct ctmr_conv_desc {
+  int32_t n, d, h, w;   /* input (source-grid) batch and spatial size */
+  int32_t cin, cout;    /* channels */
+  int32_t ksize;        /* 3 (padding 1) or 1 (padding 0) */
+  int32_t stride;       /* 1 or 2 (2 only for ksize 3, CTMR_MODE_PLAIN) */
+  int32_t mode;         /* enum ctmr_conv_mode */
+  int32_t flags;        /* enum ctmr_conv_flags, OR-ed */
+  int32_t dtype;        /* enum ctmr_dtype */
+  int32_t split;        /* tap split for small grids: 0 = library policy, else 1, 3, 9, 27 */
+} ctmr_conv_desc;
+
+/* Library identity; returns CTMR_ABI_VERSION. */
+int ctmr_abi_version(void);
+/* Message for the last non-zero status returned on this thread. */
+const char* ctmr_last_error(void);
+
+/* Output spatial extent of a conv described by `desc` (out[0..2] = D', H', W'). */
+int ctmr_conv3d_output_dims(const ctmr_conv_desc* desc, int32_t out[3]);
+
+/* Packed-weight element count (fp32 for CTMR_F32, bf16 for CTMR_BF16). */
+int64_t ctmr_packed_weight_elems(const ctmr_conv_desc* desc);
+
+/* Scratch bytes ctmr_conv3d needs for `desc` (padded input copy + split planes). */
+int64_t ctmr_conv3d_workspace_bytes(const ctmr_conv_desc* desc);
+
+/* The split ctmr_conv3d will use for `desc` (resolves desc->split == 0). */
+int ctmr_conv3d_split(const ctmr_conv_desc* desc);
+
+/*
+ * Reorder a Torch-layout weight (Cout, Cin, k, k, k) fp32 into the layout the
+ * conv kernel reads.  desc->mode NEAREST2X is rejected here (use
+ * ctmr_pack_upsample_weight); desc->dtype selects fp32 or bf16 output.
+ */
+int ctmr_pack_weight(const ctmr_conv_desc* desc, const float* weight, void* packed,
+                     void* stream);
+
+/* Fold a 3x3x3 weight into the eight 2x2x2 nearest-2x parity filters, summed
+ * in fp32 (mirrors pack_upsample_weight's fold, _nax_conv.py:407-445). */
+int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, void* packed,
+                              void* stream);
+
+/*
+ * y = conv(resample(silu?(affine?(x)))) + bias (+ residual), NDHWC fp32.
+ *   x        (n, d, h, w, cin)
+ *   packed   from ctmr_pack_weight / ctmr_pack_upsample_weight with the same desc
+ *   bias     (cout) or (n, cout) with CTMR_F_BATCH_BIAS; may be NULL (zero bias)
+ *   affine   (n, cin, 2) fp32 (scale, offset) pairs with CTMR_F_AFFINE, else NULL
+ *   residual output-shaped NDHWC with CTMR_F_RESIDUAL, else NULL
+ *   y        (n, D', H', W', cout); must not alias x or residual
+ * Accumulation order is fixed: taps kd*9+kh*3+kw ascending (outer), input
+ * channels in ascending 16-wide blocks (inner); split partial planes are
+ * added in ascending order.  Results are bit-identical run to run.
+ */
+int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed,
+                const float* bias, const float* affine, const float* residual, float* y,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The two stages of ctmr_conv3d, callable separately with the same arguments
+ * (ctmr_conv3d == ctmr_conv3d_pack then ctmr_conv3d_gemm on one stream).
+ * _pack writes the zero-padded, transformed input copy (the reference's pack
+ * kernel, _nax_conv.py:144-198) at the start of `workspace`; _gemm runs the
+ * implicit GEMM (and split reduce) reading it (_nax_conv.py:200-332).  A
+ * packed input may be reused by several _gemm calls with the same desc.
+ * For a 1x1x1 fp32 conv with cin % 16 == 0 and no affine/SiLU nothing is
+ * packed and _gemm reads x directly.
+ */
+int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* affine,
+                     void* workspace, size_t workspace_bytes, void* stream);
+int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* packed,
+                     const float* bias, const float* residual, float* y, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* Group-norm statistics: affine (n, c, 2) = (gamma*rstd, beta - mean*gamma*rstd)
+ * over (c/groups channels) x s voxels, biased variance, fp64 accumulation in a
+ * fixed-order tree.  Needs ctmr_gn_workspace_bytes(n, s, c) of scratch. */
+int64_t ctmr_gn_workspace_bytes(int32_t n, int64_t s, int32_t c);
+int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, const float* x,
+                   const float* gamma, const float* beta, float* affine, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* y = silu?(x*scale + offset) with affine from ctmr_gn_affine; y may equal x. */
+int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,
+                  int32_t silu, float* y, void* stream);
+
+/* Elementwise SiLU, y may equal x. */
+int ctmr_silu(int64_t count, const float* x, float* y, void* stream);
+
+enum ctmr_resample_op {
+  CTMR_AVGPOOL2 = 0,     /* (d,h,w) -> (d/2,h/2,w/2), mean of 2x2x2 */
+  CTMR_NEAREST2X = 1,    /* (d,h,w) -> (2d,2h,2w) */
+  CTMR_TRILINEAR2X = 2   /* (d,h,w) -> (2d,2h,2w), half-pixel, clamped */
+};
+int ctmr_resample(int32_t op, int32_t n, int32_t d, int32_t h, int32_t w, int32_t c,
+                  const float* x, float* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CTMR_H */

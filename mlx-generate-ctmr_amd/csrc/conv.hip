@@ -1,0 +1,692 @@
+// Implicit-GEMM 3x3x3 / 1x1x1 convolution for MI355X (gfx950) on NDHWC fp32
+// activations, with FP32 MFMA (v_mfma_f32_16x16x4_f32) or bf16-in /
+// fp32-accumulate MFMA (v_mfma_f32_16x16x32_bf16).
+//
+// Dataflow (reference: src/mlx_generate_ctmr/_nax_conv.py:1-35, 475-684):
+//   1. pack_input: x (NDHWC) -> zero-padded NDHWC copy with channels rounded up
+//      to the MFMA K block, applying group-norm affine + SiLU (fast_fp32.py:
+//      162-211) or the trilinear-2x sample (_nax_conv.py:115-142) on the way,
+//      in fp32 or rounded once to bf16.  Padding voxels are zero after the
+//      transform, as in the reference pack (_nax_conv.py:185-197).
+//   2. conv_kernel: GEMM rows are output voxels, columns output channels, K is
+//      taps x input channels.  Tap (kd,kh,kw) of the window starting at padded
+//      row r reads row r + kd*P + kh*Q + kw (P, Q = padded plane / row pitch),
+//      so no im2col buffer exists.  K order per output is fixed: taps
+//      kd*9+kh*3+kw ascending, then 64-byte channel blocks ascending.  Bias,
+//      per-batch bias and residual join the fp32 sum before the single store
+//      (_nax_conv.py:282-317).
+//   3. split_reduce: when the grid is small the taps are split into equal
+//      ranges whose fp32 partial planes are added in ascending order with bias
+//      and residual (_nax_conv.py:320-332).
+//
+// Wave tile: 64 output voxels (4 MFMA row blocks of 16) x NSUB*16 channels;
+// a 256-thread workgroup holds WM x WN waves.  Each lane loads 16 bytes per
+// fragment: for fp32, channels 4g..4g+3 of a 16-channel block (g = lane/16),
+// consumed by four 16x16x4 MFMAs; for bf16, channels 8g..8g+7 of a 32-channel
+// block, consumed by one 16x16x32 MFMA.  The packed weight stores each
+// (block, output channel) pair as 64 contiguous bytes in the same order, so A
+// and B lanes always pair the same input channel.
+#include "ctmr_common.hpp"
+
+#include <algorithm>
+#include <cstdarg>
+
+namespace ctmr {
+
+static thread_local char g_error[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// 1. Input packing
+// ---------------------------------------------------------------------------
+struct PackArgs {
+  const float* x;
+  void* out;
+  const float* affine;
+  int64_t total4;       // 4-channel groups to write
+  int gd, gh, gw;       // interior grid of the packed copy
+  int halo;             // 1 for 3x3x3, 0 for 1x1x1
+  int c, cp;            // source / packed channels
+  int id, ih, iw;       // source grid (trilinear)
+  int affine_on, silu_on, trilinear, bf16;
+};
+
+__global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total4;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+  const int c4n = a.cp >> 2;
+  const int c4 = (int)(idx % c4n);
+  int64_t pos = idx / c4n;
+  const int PW = a.gw + 2 * a.halo, PH = a.gh + 2 * a.halo, PD = a.gd + 2 * a.halo;
+  const int px = (int)(pos % PW);
+  pos /= PW;
+  const int py = (int)(pos % PH);
+  pos /= PH;
+  const int pz = (int)(pos % PD);
+  const int b = (int)(pos / PD);
+  const int z = pz - a.halo, y = py - a.halo, x = px - a.halo;
+  const int ch = c4 * 4;
+  f4 v = {0.f, 0.f, 0.f, 0.f};
+  if (z >= 0 && z < a.gd && y >= 0 && y < a.gh && x >= 0 && x < a.gw && ch < a.c) {
+    if ((a.c & 3) == 0) {
+      if (a.trilinear) {
+        const float* src = a.x + (int64_t)b * a.id * a.ih * a.iw * a.c;
+        v = trilinear_sample4(src, a.id, a.ih, a.iw, a.c, ch, z, y, x);
+      } else {
+        v = *reinterpret_cast<const f4*>(
+            a.x + ((((int64_t)b * a.gd + z) * a.gh + y) * a.gw + x) * a.c + ch);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (ch + k < a.c) {
+          if (a.trilinear) {
+            const float* src = a.x + (int64_t)b * a.id * a.ih * a.iw * a.c;
+            v[k] = trilinear_sample1(src, a.id, a.ih, a.iw, a.c, ch + k, z, y, x);
+          } else {
+            v[k] = a.x[((((int64_t)b * a.gd + z) * a.gh + y) * a.gw + x) * a.c + ch + k];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (ch + k < a.c) {
+        float t = v[k];
+        if (a.affine_on) {
+          const float* p = a.affine + ((int64_t)b * a.c + ch + k) * 2;
+          t = fmaf(t, p[0], p[1]);
+        }
+        if (a.silu_on) t = silu_f(t);
+        v[k] = t;
+      }
+    }
+  }
+  if (a.bf16) {
+    unsigned short h0 = f32_to_bf16_bits(v[0]), h1 = f32_to_bf16_bits(v[1]);
+    unsigned short h2 = f32_to_bf16_bits(v[2]), h3 = f32_to_bf16_bits(v[3]);
+    uint2 packed;
+    packed.x = (unsigned)h0 | ((unsigned)h1 << 16);
+    packed.y = (unsigned)h2 | ((unsigned)h3 << 16);
+    reinterpret_cast<uint2*>(a.out)[idx] = packed;
+  } else {
+    reinterpret_cast<f4*>(a.out)[idx] = v;
+  }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Weight packing (reference: _nax_conv.py:372-445)
+// ---------------------------------------------------------------------------
+// Packed layout: [phase][tap][kblock][np][KSTEP] where KSTEP is 16 fp32 or 32
+// bf16 values (64 bytes), tap = kd*KT*KT + kh*KT + kw, channel = kblock*KSTEP + e,
+// zero for channels >= cin or columns >= cout.
+struct WPackArgs {
+  const float* w;  // Torch (cout, cin, ks, ks, ks)
+  void* out;
+  int64_t total;
+  int cout, cin, ks, np, kblocks, kstep, taps, up, bf16;
+};
+
+// Nearest-2x parity fold: tap t of parity p on one axis merges the 3x3x3
+// taps k in [lo, hi]: p=0 -> t0:{0}, t1:{1,2}; p=1 -> t0:{0,1}, t1:{2}
+// (derivation at _nax_conv.py:407-414).
+__device__ __forceinline__ void fold_range(int p, int t, int& lo, int& hi) {
+  lo = (p == 0) ? (t == 0 ? 0 : 1) : (t == 0 ? 0 : 2);
+  hi = (p == 0) ? (t == 0 ? 0 : 2) : (t == 0 ? 1 : 2);
+}
+
+__global__ __launch_bounds__(256) void pack_weight_kernel(WPackArgs a) {
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+  int64_t t = idx;
+  const int e = (int)(t % a.kstep);
+  t /= a.kstep;
+  const int col = (int)(t % a.np);
+  t /= a.np;
+  const int kb = (int)(t % a.kblocks);
+  t /= a.kblocks;
+  const int tap = (int)(t % a.taps);
+  const int phase = (int)(t / a.taps);
+  const int c = kb * a.kstep + e;
+  float val = 0.f;
+  if (col < a.cout && c < a.cin) {
+    const float* wc = a.w + ((int64_t)col * a.cin + c) * a.ks * a.ks * a.ks;
+    if (!a.up) {
+      const int kd = tap / (a.ks * a.ks), kh = (tap / a.ks) % a.ks, kw = tap % a.ks;
+      val = wc[(kd * a.ks + kh) * a.ks + kw];
+    } else {
+      const int td = tap >> 2, th = (tap >> 1) & 1, tw = tap & 1;
+      const int pd = phase >> 2, ph = (phase >> 1) & 1, pw = phase & 1;
+      int d0, d1, h0, h1, w0, w1;
+      fold_range(pd, td, d0, d1);
+      fold_range(ph, th, h0, h1);
+      fold_range(pw, tw, w0, w1);
+      float s = 0.f;
+      for (int kd = d0; kd <= d1; ++kd)
+        for (int kh = h0; kh <= h1; ++kh)
+          for (int kw = w0; kw <= w1; ++kw) s += wc[(kd * 3 + kh) * 3 + kw];
+      val = s;
+    }
+  }
+  if (a.bf16)
+    reinterpret_cast<unsigned short*>(a.out)[idx] = f32_to_bf16_bits(val);
+  else
+    reinterpret_cast<float*>(a.out)[idx] = val;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. Implicit-GEMM convolution
+// ---------------------------------------------------------------------------
+struct ConvArgs {
+  const char* xp;          // packed input (or x itself for unpacked 1x1)
+  const char* wp;          // packed weight
+  const float* bias;       // (cout) or (n, cout) or null
+  const float* res;        // output-shaped residual or null
+  float* y;                // output, or split partial planes
+  int64_t rows_per_batch;  // rows of the packed input per batch item
+  int64_t row_bytes;       // bytes per packed row (cp * element size)
+  int64_t plane;           // elements per split plane (n * s_out * cout)
+  int kb, np, cout;        // 64-byte K blocks per tap, packed / real columns
+  int gd, gh, gw;          // iteration grid (output grid; source grid for UP)
+  int P, Q;                // padded plane / row pitch in rows
+  int oh, ow, s_out;       // output H, W and voxel count (UP remap)
+  int taps, split, m_tiles, n_tiles;
+  int batch_bias, has_res, has_bias;
+};
+
+template <int DT>
+__device__ __forceinline__ void mfma_step(f4& acc, const u4& a, const u4& b);
+
+template <>
+__device__ __forceinline__ void mfma_step<CTMR_F32>(f4& acc, const u4& a, const u4& b) {
+  const f4 fa = __builtin_bit_cast(f4, a), fb = __builtin_bit_cast(f4, b);
+  // Four K=4 products; component j of lane group g is input channel 4g + j.
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[0], fb[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[1], fb[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[2], fb[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[3], fb[3], acc, 0, 0, 0);
+}
+
+template <>
+__device__ __forceinline__ void mfma_step<CTMR_BF16>(f4& acc, const u4& a, const u4& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a),
+                                                 __builtin_bit_cast(bf8, b), acc, 0, 0, 0);
+}
+
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
+__global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
+  static_assert(WM * WN == 4, "four waves per workgroup");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_m = wave % WM, wave_n = wave / WM;
+
+  // XCD-aware tile order: hardware deals consecutive workgroups round-robin
+  // to the 8 XCDs; give each XCD a contiguous range of tiles so neighbouring
+  // windows (shared halo rows) and column tiles of one voxel tile share an L2.
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int xcd = bid & 7, slot = bid >> 3, per = nb >> 3, rem = nb & 7;
+  const int tile = (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int n_tile = tile % p.n_tiles;
+  const int rest = tile / p.n_tiles;
+  const int m_tile = rest % p.m_tiles;
+  const int z = rest / p.m_tiles;
+  const int split_id = z % p.split, zb = z / p.split;
+  const int b = UP ? (zb >> 3) : zb;
+  const int phase = UP ? (zb & 7) : 0;
+  const int pd = phase >> 2, ph = (phase >> 1) & 1, pw = phase & 1;
+
+  const int ghw = p.gh * p.gw;
+  const int S = p.gd * ghw;
+  const int m0 = m_tile * (WM * 64) + wave_m * 64;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+
+  // A: one window-start row per 16-voxel block; rows past the grid reuse the
+  // last voxel and are not stored.
+  const char* xb = p.xp + (int64_t)b * p.rows_per_batch * p.row_bytes + lgrp * 16;
+  const char* arow[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+    const int v = min(m0 + ms * 16 + lrow, S - 1);
+    const int d = v / ghw, r = v - d * ghw;
+    const int h = r / p.gw, w = r - h * p.gw;
+    const int64_t row =
+        (int64_t)(STRIDE * d + pd) * p.P + (int64_t)(STRIDE * h + ph) * p.Q + STRIDE * w + pw;
+    arow[ms] = xb + row * p.row_bytes;
+  }
+  // B: one output column per lane per 16-column block.
+  const int n0 = n_tile * (WN * NSUB * 16) + wave_n * (NSUB * 16);
+  const char* bcol[NSUB];
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) {
+    const int col = min(n0 + ns * 16 + lrow, p.np - 1);
+    bcol[ns] = p.wp + ((int64_t)phase * p.taps * p.kb * p.np + col) * 64 + lgrp * 16;
+  }
+
+  f4 acc[4][NSUB];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int taps_per = p.taps / p.split;
+  const int s_begin = split_id * taps_per * p.kb;
+  const int s_end = s_begin + taps_per * p.kb;
+  const int64_t bstep = (int64_t)p.np * 64;
+
+  auto a_offset = [&](int s) -> int64_t {
+    const int tap = s / p.kb, kb = s - tap * p.kb;
+    const int td = tap / (KT * KT), th = (tap / KT) % KT, tw = tap % KT;
+    return ((int64_t)td * p.P + (int64_t)th * p.Q + tw) * p.row_bytes + kb * 64;
+  };
+  auto load = [&](int s, u4 (&A)[4], u4 (&B)[NSUB]) {
+    const int64_t ao = a_offset(s);
+    const int64_t bo = (int64_t)s * bstep;
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) A[ms] = *reinterpret_cast<const u4*>(arow[ms] + ao);
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) B[ns] = *reinterpret_cast<const u4*>(bcol[ns] + bo);
+  };
+  auto compute = [&](const u4 (&A)[4], const u4 (&B)[NSUB]) {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) mfma_step<DT>(acc[ms][ns], A[ms], B[ns]);
+  };
+
+  // Register double buffer: the next K block is in flight while this one
+  // multiplies.
+  u4 A0[4], B0[NSUB], A1[4], B1[NSUB];
+  load(s_begin, A0, B0);
+  for (int s = s_begin; s < s_end; s += 2) {
+    if (s + 1 < s_end) load(s + 1, A1, B1);
+    compute(A0, B0);
+    if (s + 1 >= s_end) break;
+    if (s + 2 < s_end) load(s + 2, A0, B0);
+    compute(A1, B1);
+  }
+
+  // Epilogue: D row 4*(lane/16)+r, column lane%16 of each 16x16 block.
+  const bool partial = p.split > 1;
+  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
+  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int v = m0 + ms * 16 + lgrp * 4 + r;
+      if (v >= S) continue;
+      int o = v;
+      if (UP) {
+        const int d = v / ghw, rr = v - d * ghw;
+        const int h = rr / p.gw, w = rr - h * p.gw;
+        o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
+      }
+      const int64_t base = ((int64_t)b * p.s_out + o) * p.cout;
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) {
+        const int col = n0 + ns * 16 + lrow;
+        if (col >= p.cout) continue;
+        float sum = acc[ms][ns][r];
+        if (!partial) {
+          if (p.has_bias) sum += bias_b[col];
+          if (p.has_res) sum += p.res[base + col];
+        }
+        out[base + col] = sum;
+      }
+    }
+  }
+}
+
+// Sum of split partial planes in ascending order, then residual; bias first
+// as in the reference reduce (_nax_conv.py:320-332).
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
+                                                           int64_t plane, int split,
+                                                           const float* __restrict__ bias,
+                                                           int has_bias, int batch_bias,
+                                                           const float* __restrict__ res,
+                                                           float* __restrict__ y, int cout,
+                                                           int64_t s_out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < plane;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % cout);
+    const int64_t b = i / (s_out * cout);
+    float v = has_bias ? bias[(batch_bias ? b * cout : 0) + c] : 0.f;
+    for (int k = 0; k < split; ++k) v += part[(int64_t)k * plane + i];
+    if (res) v += res[i];
+    y[i] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: geometry, policy and dispatch
+// ---------------------------------------------------------------------------
+struct Geometry {
+  int ks, halo, KT, taps, phases;
+  int gd, gh, gw;        // iteration grid
+  int td, th, tw;        // packed interior grid
+  int od, oh, ow;        // output grid
+  bool pack;             // build a packed copy of the input
+  int kstep, esize, cp, np, kblocks;
+  int P, Q;
+  int64_t rows_per_batch;
+  int split;
+  int nsub, wm, wn, m_tiles, n_tiles;
+  int64_t pack_bytes, part_bytes;
+};
+
+static int geometry(const ctmr_conv_desc* d, Geometry& g) {
+  if (!d) return fail(CTMR_E_INVALID, "null descriptor");
+  if (d->n <= 0 || d->d <= 0 || d->h <= 0 || d->w <= 0 || d->cin <= 0 || d->cout <= 0)
+    return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (d->dtype != CTMR_F32 && d->dtype != CTMR_BF16) return fail(CTMR_E_INVALID, "bad dtype");
+  if (d->ksize != 1 && d->ksize != 3) return fail(CTMR_E_UNSUPPORTED, "ksize must be 1 or 3");
+  if (d->stride != 1 && d->stride != 2) return fail(CTMR_E_UNSUPPORTED, "stride must be 1 or 2");
+  if (d->mode < CTMR_MODE_PLAIN || d->mode > CTMR_MODE_TRILINEAR2X)
+    return fail(CTMR_E_INVALID, "bad mode");
+  if (d->mode != CTMR_MODE_PLAIN && d->stride != 1)
+    return fail(CTMR_E_UNSUPPORTED, "upsampling modes need stride 1");
+  if (d->mode == CTMR_MODE_TRILINEAR2X && (d->flags & (CTMR_F_AFFINE | CTMR_F_SILU)))
+    return fail(CTMR_E_UNSUPPORTED, "trilinear packing supports only a plain convolution");
+  if (d->ksize == 1 && (d->mode != CTMR_MODE_PLAIN || d->stride != 1))
+    return fail(CTMR_E_UNSUPPORTED, "1x1x1 conv supports only stride 1, no resampling");
+  g.ks = d->ksize;
+  g.kstep = d->dtype == CTMR_F32 ? 16 : 32;
+  g.esize = d->dtype == CTMR_F32 ? 4 : 2;
+  g.np = (int)round_up(d->cout, 16);
+  g.phases = 1;
+  if (d->ksize == 3) {
+    g.halo = 1;
+    g.KT = 3;
+    g.taps = 27;
+    g.td = d->d; g.th = d->h; g.tw = d->w;
+    if (d->mode == CTMR_MODE_TRILINEAR2X) { g.td *= 2; g.th *= 2; g.tw *= 2; }
+    if (d->stride == 2) {
+      g.gd = (d->d - 1) / 2 + 1; g.gh = (d->h - 1) / 2 + 1; g.gw = (d->w - 1) / 2 + 1;
+    } else {
+      g.gd = g.td; g.gh = g.th; g.gw = g.tw;
+    }
+    g.od = g.gd; g.oh = g.gh; g.ow = g.gw;
+    if (d->mode == CTMR_MODE_NEAREST2X) {
+      g.KT = 2;
+      g.taps = 8;
+      g.phases = 8;
+      g.od = 2 * g.gd; g.oh = 2 * g.gh; g.ow = 2 * g.gw;
+    }
+    g.pack = true;
+  } else {
+    g.halo = 0;
+    g.KT = 1;
+    g.taps = 1;
+    g.td = g.gd = g.od = d->d;
+    g.th = g.gh = g.oh = d->h;
+    g.tw = g.gw = g.ow = d->w;
+    g.pack = (d->flags & (CTMR_F_AFFINE | CTMR_F_SILU)) || d->dtype != CTMR_F32 ||
+             (d->cin % g.kstep) != 0;
+  }
+  g.cp = g.pack ? (int)round_up(d->cin, g.kstep) : d->cin;
+  g.kblocks = g.cp / g.kstep;
+  if (g.pack) {
+    g.Q = g.tw + 2 * g.halo;
+    g.P = (g.th + 2 * g.halo) * g.Q;
+    g.rows_per_batch = (int64_t)(g.td + 2 * g.halo) * g.P;
+  } else {
+    g.Q = g.tw;
+    g.P = g.th * g.tw;
+    g.rows_per_batch = (int64_t)g.td * g.P;
+  }
+  const int64_t S = (int64_t)g.gd * g.gh * g.gw;
+  const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
+  if (S > (1ll << 30) || s_out * d->cout > (1ll << 40))
+    return fail(CTMR_E_UNSUPPORTED, "volume too large for 32-bit voxel indexing");
+  // Tile shape by output width.
+  if (d->cout <= 16) { g.nsub = 1; g.wm = 4; g.wn = 1; }
+  else if (d->cout <= 32) { g.nsub = 2; g.wm = 4; g.wn = 1; }
+  else if (d->cout <= 64) { g.nsub = 4; g.wm = 4; g.wn = 1; }
+  else { g.nsub = 4; g.wm = 2; g.wn = 2; }
+  g.m_tiles = (int)ceil_div(S, g.wm * 64);
+  g.n_tiles = (int)ceil_div(g.np, g.wn * g.nsub * 16);
+  // Tap split: chosen from the shape only (never from the device), so each
+  // output's summation order is fixed for a given problem.
+  if (d->split > 0) {
+    if (g.taps % d->split != 0) return fail(CTMR_E_INVALID, "split must divide the tap count");
+    g.split = d->split;
+  } else {
+    const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases;
+    g.split = 1;
+    const int64_t target = 512;  // two workgroups per CU on 256 CUs
+    if (g.taps > 1 && base < target && d->cin >= 64) {
+      static const int cands27[3] = {3, 9, 27}, cands8[3] = {2, 4, 8};
+      const int* cands = g.taps == 27 ? cands27 : cands8;
+      for (int i = 0; i < 3; ++i) {
+        g.split = cands[i];
+        if (base * g.split >= target) break;
+      }
+    }
+  }
+  const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases * g.split;
+  if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
+  g.pack_bytes = g.pack ? round_up((int64_t)d->n * g.rows_per_batch * g.cp * g.esize, 256) : 0;
+  g.part_bytes = g.split > 1 ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
+  return CTMR_OK;
+}
+
+typedef void (*ConvFn)(dim3, dim3, hipStream_t, const ConvArgs&);
+
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
+static void launch_conv(dim3 grid, dim3 block, hipStream_t st, const ConvArgs& a) {
+  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP>), grid, block, 0, st, a);
+}
+
+template <int DT, int NSUB, int WM, int WN>
+static ConvFn pick_kind(int KT, int stride, bool up) {
+  if (up) return launch_conv<DT, NSUB, WM, WN, 2, 1, true>;
+  if (KT == 1) return launch_conv<DT, NSUB, WM, WN, 1, 1, false>;
+  if (stride == 2) return launch_conv<DT, NSUB, WM, WN, 3, 2, false>;
+  return launch_conv<DT, NSUB, WM, WN, 3, 1, false>;
+}
+
+static ConvFn pick(const ctmr_conv_desc* d, const Geometry& g) {
+  const bool up = d->mode == CTMR_MODE_NEAREST2X;
+  const int st = d->stride;
+#define CTMR_PICK(DT)                                                            \
+  if (g.nsub == 1) return pick_kind<DT, 1, 4, 1>(g.KT, st, up);                  \
+  if (g.nsub == 2) return pick_kind<DT, 2, 4, 1>(g.KT, st, up);                  \
+  if (g.wn == 1) return pick_kind<DT, 4, 4, 1>(g.KT, st, up);                    \
+  return pick_kind<DT, 4, 2, 2>(g.KT, st, up);
+  if (d->dtype == CTMR_F32) {
+    CTMR_PICK(CTMR_F32)
+  } else {
+    CTMR_PICK(CTMR_BF16)
+  }
+#undef CTMR_PICK
+}
+
+}  // namespace ctmr
+
+using namespace ctmr;
+
+extern "C" {
+
+int ctmr_abi_version(void) { return CTMR_ABI_VERSION; }
+
+const char* ctmr_last_error(void) { return g_error; }
+
+int ctmr_conv3d_output_dims(const ctmr_conv_desc* desc, int32_t out[3]) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  if (!out) return fail(CTMR_E_INVALID, "null output");
+  out[0] = g.od; out[1] = g.oh; out[2] = g.ow;
+  return CTMR_OK;
+}
+
+int64_t ctmr_packed_weight_elems(const ctmr_conv_desc* desc) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  const int kblocks = (int)ceil_div(desc->cin, g.kstep);
+  return (int64_t)g.phases * g.taps * kblocks * g.np * g.kstep;
+}
+
+int64_t ctmr_conv3d_workspace_bytes(const ctmr_conv_desc* desc) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  return g.pack_bytes + g.part_bytes;
+}
+
+int ctmr_conv3d_split(const ctmr_conv_desc* desc) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  return g.split;
+}
+
+static int pack_weight_impl(const ctmr_conv_desc* desc, const float* weight, void* packed,
+                            void* stream, bool up) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  if (!weight || !packed) return fail(CTMR_E_INVALID, "null pointer");
+  if (up != (desc->mode == CTMR_MODE_NEAREST2X))
+    return fail(CTMR_E_INVALID, up ? "ctmr_pack_upsample_weight needs CTMR_MODE_NEAREST2X"
+                                   : "use ctmr_pack_upsample_weight for CTMR_MODE_NEAREST2X");
+  WPackArgs a;
+  a.w = weight;
+  a.out = packed;
+  a.cout = desc->cout;
+  a.cin = desc->cin;
+  a.ks = desc->ksize;
+  a.np = g.np;
+  a.kstep = g.kstep;
+  a.kblocks = (int)ceil_div(desc->cin, g.kstep);
+  a.taps = g.taps;
+  a.up = up ? 1 : 0;
+  a.bf16 = desc->dtype == CTMR_BF16;
+  a.total = (int64_t)g.phases * g.taps * a.kblocks * g.np * g.kstep;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3(elementwise_blocks(a.total)), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return check_launch("pack_weight");
+}
+
+int ctmr_pack_weight(const ctmr_conv_desc* desc, const float* weight, void* packed, void* stream) {
+  return pack_weight_impl(desc, weight, packed, stream, false);
+}
+
+int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, void* packed,
+                              void* stream) {
+  return pack_weight_impl(desc, weight, packed, stream, true);
+}
+
+static int check_workspace(const Geometry& g, const void* workspace, size_t workspace_bytes) {
+  const int64_t need = g.pack_bytes + g.part_bytes;
+  if ((int64_t)workspace_bytes < need || (need > 0 && !workspace)) {
+    set_error("workspace %zu bytes < required %lld", workspace_bytes, (long long)need);
+    return CTMR_E_WORKSPACE;
+  }
+  return CTMR_OK;
+}
+
+int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* affine,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  if (!x) return fail(CTMR_E_INVALID, "null input");
+  if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
+  if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
+  if (!g.pack) return CTMR_OK;
+  if ((desc->cin & 3) == 0 && ((uintptr_t)x & 15) != 0)
+    return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
+  PackArgs pa;
+  pa.x = x;
+  pa.out = workspace;
+  pa.affine = affine;
+  pa.gd = g.td; pa.gh = g.th; pa.gw = g.tw;
+  pa.halo = g.halo;
+  pa.c = desc->cin;
+  pa.cp = g.cp;
+  pa.id = desc->d; pa.ih = desc->h; pa.iw = desc->w;
+  pa.affine_on = (desc->flags & CTMR_F_AFFINE) != 0;
+  pa.silu_on = (desc->flags & CTMR_F_SILU) != 0;
+  pa.trilinear = desc->mode == CTMR_MODE_TRILINEAR2X;
+  pa.bf16 = desc->dtype == CTMR_BF16;
+  pa.total4 = (int64_t)desc->n * g.rows_per_batch * (g.cp / 4);
+  hipLaunchKernelGGL(pack_input_kernel, dim3(elementwise_blocks(pa.total4)), dim3(256), 0,
+                     (hipStream_t)stream, pa);
+  return check_launch("pack_input");
+}
+
+int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* packed,
+                     const float* bias, const float* residual, float* y, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  if (!packed || !y || (!g.pack && !x)) return fail(CTMR_E_INVALID, "null input, weight or output");
+  if ((desc->flags & CTMR_F_RESIDUAL) && !residual)
+    return fail(CTMR_E_INVALID, "residual flag without residual");
+  if ((desc->flags & CTMR_F_BATCH_BIAS) && !bias) return fail(CTMR_E_INVALID, "batch bias flag without bias");
+  if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
+  const char* xp = g.pack ? (const char*)workspace : (const char*)x;
+  if (!g.pack && ((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
+  ConvArgs a;
+  a.xp = xp;
+  a.wp = (const char*)packed;
+  a.bias = bias;
+  a.res = residual;
+  a.has_bias = bias != nullptr;
+  a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
+  a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
+  a.rows_per_batch = g.rows_per_batch;
+  a.row_bytes = (int64_t)g.cp * g.esize;
+  a.plane = (int64_t)desc->n * s_out * desc->cout;
+  a.kb = g.kblocks;
+  a.np = g.np;
+  a.cout = desc->cout;
+  a.gd = g.gd; a.gh = g.gh; a.gw = g.gw;
+  a.P = g.P; a.Q = g.Q;
+  a.oh = g.oh; a.ow = g.ow; a.s_out = (int)s_out;
+  a.taps = g.taps;
+  a.split = g.split;
+  a.m_tiles = g.m_tiles;
+  a.n_tiles = g.n_tiles;
+  float* part = (float*)((char*)workspace + g.pack_bytes);
+  a.y = g.split > 1 ? part : y;
+  if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
+  const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
+  ConvFn fn = pick(desc, g);
+  fn(dim3((unsigned)blocks), dim3(256), st, a);
+  if ((rc = check_launch("conv"))) return rc;
+  if (g.split > 1) {
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(elementwise_blocks(a.plane)), dim3(256), 0, st,
+                       part, a.plane, g.split, bias, bias != nullptr ? 1 : 0, a.batch_bias,
+                       (desc->flags & CTMR_F_RESIDUAL) ? residual : nullptr, y, desc->cout, s_out);
+    if ((rc = check_launch("split_reduce"))) return rc;
+  }
+  return CTMR_OK;
+}
+
+int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                const float* affine, const float* residual, float* y, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  if (!x || !packed || !y) return fail(CTMR_E_INVALID, "null input, weight or output");
+  if ((rc = ctmr_conv3d_pack(desc, x, affine, workspace, workspace_bytes, stream))) return rc;
+  return ctmr_conv3d_gemm(desc, x, packed, bias, residual, y, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,278 @@
+// Group-norm statistics, group-norm apply (+SiLU), SiLU and the 2x resampling
+// kernels for NDHWC fp32 activations on MI355X.
+//
+// Group norm (semantics of medmlx_core.group_norm_affine as used at
+// src/mlx_generate_ctmr/fast_fp32.py:102-118,185-189 and restated in
+// tests/test_fast_fp32.py:41-48): per (batch item, group) the mean and the
+// biased variance over (C/G channels) x (all voxels); the output is per
+// (batch item, channel) scale = gamma*rstd and offset = beta - mean*scale so a
+// consumer computes x*scale + offset (fused into the conv input pack).
+//
+// Statistics are HBM-bound (4 bytes read per element).  Pass 1 splits the
+// voxels of each batch item into fixed-size chunks (the chunk size depends on
+// C only); each 256-thread workgroup streams one chunk with coalesced 16-byte
+// loads, every thread owning 4 channels, and accumulates sum and sum of
+// squares in fp64.  The per-thread partials are combined in a fixed order, so
+// the result is bit-identical run to run and independent of the device.
+// Pass 2 combines the chunk partials of one group, again in fixed order.
+#include "ctmr_common.hpp"
+
+#include <algorithm>
+
+namespace ctmr {
+
+// Voxels per statistics chunk: 512 KiB of fp32 input per chunk.
+static inline int64_t gn_chunk_voxels(int c) { return std::max<int64_t>(1, 131072 / c); }
+
+__global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict__ x, int64_t s,
+                                                         int c, int64_t chunk_vox, int chunks,
+                                                         double* __restrict__ part) {
+  const int chunk = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int c4n = c >> 2;
+  const int vl_count = 256 / c4n;
+  const int c4 = t % c4n, vl = t / c4n;
+  double sm[4] = {0, 0, 0, 0}, sq[4] = {0, 0, 0, 0};
+  const int64_t v0 = (int64_t)chunk * chunk_vox;
+  const int64_t v1 = min(s, v0 + chunk_vox);
+  if (vl < vl_count) {
+    const float* xb = x + (int64_t)b * s * c + c4 * 4;
+    for (int64_t v = v0 + vl; v < v1; v += vl_count) {
+      const f4 q = *reinterpret_cast<const f4*>(xb + v * c);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const double d = (double)q[k];
+        sm[k] += d;
+        sq[k] = fma(d, d, sq[k]);
+      }
+    }
+  }
+  __shared__ double red[256 * 8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    red[t * 8 + k] = sm[k];
+    red[t * 8 + 4 + k] = sq[k];
+  }
+  __syncthreads();
+  if (t < c4n) {
+    double a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < vl_count; ++j) {
+      const double* r = red + (j * c4n + t) * 8;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a[k] += r[k];
+    }
+    double* out = part + (((int64_t)b * chunks + chunk) * c + t * 4) * 2;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      out[2 * k] = a[k];
+      out[2 * k + 1] = a[4 + k];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void gn_finalize_kernel(const double* __restrict__ part,
+                                                          int chunks, int c, int groups,
+                                                          int64_t count,
+                                                          const float* __restrict__ gamma,
+                                                          const float* __restrict__ beta,
+                                                          float eps, float* __restrict__ affine) {
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int cpg = c / groups;
+  const int64_t items = (int64_t)chunks * cpg;
+  double sm = 0, sq = 0;
+  for (int64_t i = t; i < items; i += 256) {
+    const int chunk = (int)(i / cpg), cc = (int)(i % cpg);
+    const double* p = part + (((int64_t)b * chunks + chunk) * c + g * cpg + cc) * 2;
+    sm += p[0];
+    sq += p[1];
+  }
+  __shared__ double rs[256], rq[256];
+  __shared__ double stat[2];
+  rs[t] = sm;
+  rq[t] = sq;
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride >>= 1) {
+    if (t < stride) {
+      rs[t] += rs[t + stride];
+      rq[t] += rq[t + stride];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    const double n = (double)count;
+    const double mean = rs[0] / n;
+    double var = rq[0] / n - mean * mean;
+    if (var < 0) var = 0;
+    stat[0] = mean;
+    stat[1] = 1.0 / sqrt(var + (double)eps);
+  }
+  __syncthreads();
+  for (int cc = t; cc < cpg; cc += 256) {
+    const int ch = g * cpg + cc;
+    const double scale = (double)gamma[ch] * stat[1];
+    const double offset = (double)beta[ch] - stat[0] * scale;
+    affine[((int64_t)b * c + ch) * 2] = (float)scale;
+    affine[((int64_t)b * c + ch) * 2 + 1] = (float)offset;
+  }
+}
+
+__global__ __launch_bounds__(256) void gn_apply_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ affine,
+                                                       int64_t total4, int64_t s, int c, int silu,
+                                                       float* __restrict__ y) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total4;
+       i += (int64_t)gridDim.x * blockDim.x) {
+  const int c4n = c >> 2;
+  const int ch = (int)(i % c4n) * 4;
+  const int64_t b = i / ((int64_t)c4n * s);
+  f4 q = reinterpret_cast<const f4*>(x)[i];
+  const float* a = affine + (b * c + ch) * 2;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float t = fmaf(q[k], a[2 * k], a[2 * k + 1]);
+    q[k] = silu ? silu_f(t) : t;
+  }
+  reinterpret_cast<f4*>(y)[i] = q;
+  }
+}
+
+__global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ x, int64_t count,
+                                                   float* __restrict__ y) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = silu_f(x[i]);
+}
+
+// One thread per output (voxel, 4 channels) when c % 4 == 0, else per channel.
+__global__ __launch_bounds__(256) void resample_kernel(int op, int n, int d, int h, int w, int c,
+                                                       int vec, const float* __restrict__ x,
+                                                       float* __restrict__ y) {
+#pragma clang fp contract(off)
+  const int od = op == CTMR_AVGPOOL2 ? d / 2 : 2 * d;
+  const int oh = op == CTMR_AVGPOOL2 ? h / 2 : 2 * h;
+  const int ow = op == CTMR_AVGPOOL2 ? w / 2 : 2 * w;
+  const int cg = vec ? c / 4 : c;
+  const int64_t total = (int64_t)n * od * oh * ow * cg;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+  int64_t t = i;
+  const int cc = (int)(t % cg);
+  t /= cg;
+  const int xo = (int)(t % ow);
+  t /= ow;
+  const int yo = (int)(t % oh);
+  t /= oh;
+  const int zo = (int)(t % od);
+  const int b = (int)(t / od);
+  const float* src = x + (int64_t)b * d * h * w * c;
+  auto at4 = [&](int zz, int yy, int xx) -> f4 {
+    return *reinterpret_cast<const f4*>(src + (((int64_t)zz * h + yy) * w + xx) * c + cc * 4);
+  };
+  auto at1 = [&](int zz, int yy, int xx) -> float {
+    return src[(((int64_t)zz * h + yy) * w + xx) * c + cc];
+  };
+  const int64_t obase = ((((int64_t)b * od + zo) * oh + yo) * ow + xo) * c;
+  if (op == CTMR_AVGPOOL2) {
+    if (vec) {
+      f4 s = {0.f, 0.f, 0.f, 0.f};
+      for (int a = 0; a < 2; ++a)
+        for (int bb = 0; bb < 2; ++bb)
+          for (int e = 0; e < 2; ++e) s += at4(2 * zo + a, 2 * yo + bb, 2 * xo + e);
+      *reinterpret_cast<f4*>(y + obase + cc * 4) = s * 0.125f;
+    } else {
+      float s = 0.f;
+      for (int a = 0; a < 2; ++a)
+        for (int bb = 0; bb < 2; ++bb)
+          for (int e = 0; e < 2; ++e) s += at1(2 * zo + a, 2 * yo + bb, 2 * xo + e);
+      y[obase + cc] = s * 0.125f;
+    }
+  } else if (op == CTMR_NEAREST2X) {
+    if (vec)
+      *reinterpret_cast<f4*>(y + obase + cc * 4) = at4(zo >> 1, yo >> 1, xo >> 1);
+    else
+      y[obase + cc] = at1(zo >> 1, yo >> 1, xo >> 1);
+  } else {
+    if (vec)
+      *reinterpret_cast<f4*>(y + obase + cc * 4) = trilinear_sample4(src, d, h, w, c, cc * 4, zo, yo, xo);
+    else
+      y[obase + cc] = trilinear_sample1(src, d, h, w, c, cc, zo, yo, xo);
+  }
+  }
+}
+
+}  // namespace ctmr
+
+using namespace ctmr;
+
+extern "C" {
+
+int64_t ctmr_gn_workspace_bytes(int32_t n, int64_t s, int32_t c) {
+  if (n <= 0 || s <= 0 || c <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
+  const int64_t chunks = ceil_div(s, gn_chunk_voxels(c));
+  return (int64_t)n * chunks * c * 2 * (int64_t)sizeof(double);
+}
+
+int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, const float* x,
+                   const float* gamma, const float* beta, float* affine, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  if (n <= 0 || s <= 0 || c <= 0 || groups <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (c % groups != 0) return fail(CTMR_E_INVALID, "channels must be divisible by groups");
+  if (c % 4 != 0 || c > 1024) return fail(CTMR_E_UNSUPPORTED, "group norm needs c % 4 == 0 and c <= 1024");
+  if (!x || !gamma || !beta || !affine) return fail(CTMR_E_INVALID, "null pointer");
+  if (((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
+  const int64_t chunk_vox = gn_chunk_voxels(c);
+  const int64_t chunks = ceil_div(s, chunk_vox);
+  const int64_t need = (int64_t)n * chunks * c * 2 * (int64_t)sizeof(double);
+  if ((int64_t)workspace_bytes < need || !workspace) {
+    set_error("group-norm workspace %zu bytes < required %lld", workspace_bytes, (long long)need);
+    return CTMR_E_WORKSPACE;
+  }
+  if (chunks >= (1 << 30) || n > 65535) return fail(CTMR_E_UNSUPPORTED, "volume too large");
+  hipStream_t st = (hipStream_t)stream;
+  double* part = (double*)workspace;
+  hipLaunchKernelGGL(gn_partial_kernel, dim3((unsigned)chunks, n), dim3(256), 0, st, x, s, c,
+                     chunk_vox, (int)chunks, part);
+  int rc = check_launch("gn_partial");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups, n), dim3(256), 0, st, part, (int)chunks, c,
+                     groups, s * (c / groups), gamma, beta, eps, affine);
+  return check_launch("gn_finalize");
+}
+
+int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,
+                  int32_t silu, float* y, void* stream) {
+  if (n <= 0 || s <= 0 || c <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (c % 4 != 0) return fail(CTMR_E_UNSUPPORTED, "group norm apply needs c % 4 == 0");
+  if (!x || !affine || !y) return fail(CTMR_E_INVALID, "null pointer");
+  if ((((uintptr_t)x | (uintptr_t)y) & 15) != 0) return fail(CTMR_E_INVALID, "x and y must be 16-byte aligned");
+  const int64_t total4 = (int64_t)n * s * (c / 4);
+  hipLaunchKernelGGL(gn_apply_kernel, dim3(elementwise_blocks(total4)), dim3(256), 0,
+                     (hipStream_t)stream, x, affine, total4, s, c, silu, y);
+  return check_launch("gn_apply");
+}
+
+int ctmr_silu(int64_t count, const float* x, float* y, void* stream) {
+  if (count < 0 || (count > 0 && (!x || !y))) return fail(CTMR_E_INVALID, "bad arguments");
+  if (count == 0) return CTMR_OK;
+  hipLaunchKernelGGL(silu_kernel, dim3(elementwise_blocks(count)), dim3(256), 0,
+                     (hipStream_t)stream, x, count, y);
+  return check_launch("silu");
+}
+
+int ctmr_resample(int32_t op, int32_t n, int32_t d, int32_t h, int32_t w, int32_t c,
+                  const float* x, float* y, void* stream) {
+  if (op < CTMR_AVGPOOL2 || op > CTMR_TRILINEAR2X) return fail(CTMR_E_INVALID, "bad resample op");
+  if (n <= 0 || d <= 0 || h <= 0 || w <= 0 || c <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (op == CTMR_AVGPOOL2 && (d < 2 || h < 2 || w < 2))
+    return fail(CTMR_E_INVALID, "average pooling needs every axis >= 2");
+  if (!x || !y) return fail(CTMR_E_INVALID, "null pointer");
+  const int vec = (c % 4 == 0) && ((((uintptr_t)x | (uintptr_t)y) & 15) == 0);
+  const int64_t od = op == CTMR_AVGPOOL2 ? d / 2 : 2 * (int64_t)d;
+  const int64_t oh = op == CTMR_AVGPOOL2 ? h / 2 : 2 * (int64_t)h;
+  const int64_t ow = op == CTMR_AVGPOOL2 ? w / 2 : 2 * (int64_t)w;
+  const int64_t total = (int64_t)n * od * oh * ow * (vec ? c / 4 : c);
+  hipLaunchKernelGGL(resample_kernel, dim3(elementwise_blocks(total)), dim3(256), 0,
+                     (hipStream_t)stream, op, n, d, h, w, c, vec, x, y);
+  return check_launch("resample");
+}
+
+}  // extern "C"

@@ -1,0 +1,427 @@
+"""Fast FP32 arithmetic for the MAISI UNet, ControlNet and VAE decoder on MI355X.
+
+Drop-in counterpart of the reference's arithmetic plug-in
+``src/mlx_generate_ctmr/fast_fp32.py`` (entry points at :102-349) and of the
+kernel orchestrator ``_nax_conv.nax_conv3d`` (``_nax_conv.py:475-684``), with
+tensors held by PyTorch-ROCm on the GPU and every hot operation running in the
+hand-written HIP kernels of ``libctmr_hip.so``:
+
+* padding-1 3x3x3 convolutions (stride 1/2, nearest-2x folded into parity
+  weights, trilinear-2x computed while packing the input) and 1x1x1
+  convolutions are implicit GEMMs on FP32 MFMA (or bf16 MFMA with fp32
+  accumulation inside ``precision("bf16")``);
+* a preceding group norm + SiLU is applied while packing the convolution
+  input; bias, the residual block's per-batch time-embedding bias and the
+  residual join the fp32 sum before the single store;
+* group-norm statistics are a deterministic fp64 reduction.
+
+The native activation layout is NDHWC (``(N, D, H, W, C)`` contiguous).  The
+reference's NCDHW entry points (``*_ncdhw``, same names and keywords; the
+``mx`` argument is accepted and ignored) permute to NDHWC and back.
+Weights keep the Torch layouts the reference uses: conv ``(O, C, k, k, k)``,
+linear ``(O, I)``.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import threading
+import weakref
+from collections.abc import Iterable, Iterator, Mapping
+from contextvars import ContextVar
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _lib, ops
+
+# ---------------------------------------------------------------------------
+# precision selection (the reference's request-scoped arithmetic switch,
+# arithmetic_mode.py:28-60, reduced to the two MFMA variants of this path)
+# ---------------------------------------------------------------------------
+PRECISIONS = ("fp32", "bf16")
+_precision: ContextVar[str] = ContextVar("ctmr_precision", default="fp32")
+
+
+@contextlib.contextmanager
+def precision(mode: str) -> Iterator[None]:
+    """Select ``"fp32"`` (FP32 MFMA) or ``"bf16"`` (bf16 MFMA, fp32 accumulate) convs."""
+    if mode not in PRECISIONS:
+        raise ValueError(f"precision must be one of {PRECISIONS}; got {mode!r}")
+    token = _precision.set(mode)
+    try:
+        yield
+    finally:
+        _precision.reset(token)
+
+
+def active_precision() -> str:
+    return _precision.get()
+
+
+def _dtype_code() -> int:
+    return _lib.DT_BF16 if _precision.get() == "bf16" else _lib.DT_F32
+
+
+# ---------------------------------------------------------------------------
+# validation helpers
+# ---------------------------------------------------------------------------
+def _require(x: Tensor, name: str, ndim: int = 5) -> Tensor:
+    if not isinstance(x, Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if x.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D; got shape {tuple(x.shape)}")
+    if x.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32; got {x.dtype}")
+    if x.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU (there is no CPU path); got {x.device}")
+    return x.contiguous()
+
+
+def _vec(t: Optional[Tensor], n: int, name: str, device: torch.device) -> Optional[Tensor]:
+    if t is None:
+        return None
+    t = t.to(device=device, dtype=torch.float32).contiguous()
+    if t.shape[-1] != n:
+        raise ValueError(f"{name} last axis {t.shape[-1]} != {n}")
+    return t
+
+
+# ---------------------------------------------------------------------------
+# packed-weight cache (fast_fp32.py:70-91): keyed by (id(weight), mode,
+# dtype); the weak reference validates the id and evicts on collection.
+# ---------------------------------------------------------------------------
+_packed: dict[tuple[int, int, int], tuple[weakref.ref, Tensor]] = {}
+_packed_lock = threading.Lock()
+
+
+def pack_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tensor:
+    """Packed ``(O, C, k, k, k)`` weight for ``implicit_gemm_conv3d`` (``_nax_conv.pack_weight``)."""
+    code = _lib.DT_BF16 if (dtype or _precision.get()) == "bf16" else _lib.DT_F32
+    w = weight.to(torch.float32).contiguous()
+    o, c, k = int(w.shape[0]), int(w.shape[1]), int(w.shape[2])
+    return ops.pack_weight(w, c, o, k, _lib.MODE_PLAIN, code)
+
+
+def pack_upsample_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tensor:
+    """Eight 2x2x2 nearest-2x parity filters folded in fp32 (``_nax_conv.pack_upsample_weight``)."""
+    code = _lib.DT_BF16 if (dtype or _precision.get()) == "bf16" else _lib.DT_F32
+    w = weight.to(torch.float32).contiguous()
+    if tuple(w.shape[2:]) != (3, 3, 3):
+        raise ValueError("upsample packing needs a 3x3x3 weight")
+    return ops.pack_weight(w, int(w.shape[1]), int(w.shape[0]), 3, _lib.MODE_NEAREST2X, code)
+
+
+def _pack(weight: Tensor, mode: int) -> Tensor:
+    code = _dtype_code()
+    key = (id(weight), mode, code)
+    with _packed_lock:
+        hit = _packed.get(key)
+        if hit is not None and hit[0]() is weight:
+            return hit[1]
+    dtype = "bf16" if code == _lib.DT_BF16 else "fp32"
+    packed = (pack_upsample_weight if mode == _lib.MODE_NEAREST2X else pack_weight)(weight, dtype=dtype)
+
+    def _evict(_ref, key=key):
+        with _packed_lock:
+            _packed.pop(key, None)
+
+    with _packed_lock:
+        _packed[key] = (weakref.ref(weight, _evict), packed)
+    return packed
+
+
+def drop_packed_weights(weights: Iterable[Tensor]) -> None:
+    """Forget the packed copies of ``weights``; a later use packs them again."""
+    ids = {id(w) for w in weights}
+    with _packed_lock:
+        for key in [k for k in _packed if k[0] in ids]:
+            del _packed[key]
+
+
+# ---------------------------------------------------------------------------
+# NDHWC-native operators
+# ---------------------------------------------------------------------------
+def implicit_gemm_conv3d(
+    x: Tensor,
+    packed: Tensor,
+    bias: Optional[Tensor],
+    *,
+    cout: int,
+    ksize: int = 3,
+    affine: Optional[Tensor] = None,
+    silu: bool = False,
+    stride: int = 1,
+    upsample: bool = False,
+    trilinear: bool = False,
+    residual: Optional[Tensor] = None,
+    split: int = 0,
+) -> Tensor:
+    """Padding-1 3x3x3 (or 1x1x1) convolution of NDHWC ``x`` (``_nax_conv.nax_conv3d``).
+
+    Args mirror the reference (``_nax_conv.py:488-525``): ``bias`` is ``(O,)``
+    or per batch item ``(N, O)``; ``affine`` is ``(N, C, 2)`` (scale, offset)
+    pairs applied before SiLU; ``upsample`` convolves the nearest-2x upsampling
+    with weights from ``pack_upsample_weight``; ``trilinear`` convolves the
+    half-pixel trilinear-2x upsampling (plain stride-1 only); ``residual`` has
+    the output's shape.  ``split`` forces a tap split (0: library policy).
+
+    Raises:
+        ValueError: on a packed weight that does not fit, unsupported option
+            combinations, or a residual of the wrong shape.
+    """
+    x = _require(x, "x")
+    n, d, h, w, cin = (int(v) for v in x.shape)
+    if trilinear and (upsample or stride != 1 or affine is not None or silu):
+        raise ValueError("trilinear packing supports only a plain stride-1 convolution")
+    if upsample and stride != 1:
+        raise ValueError("nearest upsampling supports only stride 1")
+    if ksize == 1 and (upsample or trilinear or stride != 1):
+        raise ValueError("1x1x1 convolution supports only stride 1 without resampling")
+    mode = _lib.MODE_NEAREST2X if upsample else (_lib.MODE_TRILINEAR2X if trilinear else _lib.MODE_PLAIN)
+    code = _lib.DT_BF16 if packed.dtype == torch.bfloat16 else _lib.DT_F32
+    desc = ops.make_desc(tuple(x.shape), cout, ksize, stride, mode, 0, code, split)
+    if packed.numel() != _lib.packed_weight_elems(desc):
+        raise ValueError(
+            f"packed weight of {packed.numel()} elements does not fit {cin} input / {cout} output "
+            f"channels ({'nearest-2x' if upsample else 'plain'}, {'bf16' if code else 'fp32'})"
+        )
+    bias = _vec(bias, cout, "bias", x.device)
+    if bias is not None and bias.dim() == 2 and bias.shape[0] != n:
+        raise ValueError(f"per-batch bias has {bias.shape[0]} rows for batch {n}")
+    if affine is not None:
+        affine = affine.to(torch.float32).contiguous()
+        if tuple(affine.shape) != (n, cin, 2):
+            raise ValueError(f"affine shape {tuple(affine.shape)} != {(n, cin, 2)}")
+    out_shape = (n, *_lib.output_dims(desc), cout)
+    if residual is not None:
+        residual = _require(residual, "residual")
+        if tuple(residual.shape) != out_shape:
+            raise ValueError(f"residual shape {tuple(residual.shape)} != output {out_shape}")
+    return ops.conv3d(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split)
+
+
+def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, stride: int = 1) -> Tensor:
+    """NDHWC convolution with a Torch ``(O, C, k, k, k)`` weight (``fast_fp32.conv3d_ncdhw``, :133-154)."""
+    k = int(weight.shape[2])
+    if tuple(weight.shape[2:]) != (k, k, k) or (k, padding) not in ((3, 1), (1, 0)):
+        raise ValueError(f"supported kernels: 3x3x3 padding 1 and 1x1x1 padding 0; got k={k}, padding={padding}")
+    if k == 1 and stride != 1:
+        raise ValueError("1x1x1 convolution supports only stride 1")
+    if int(weight.shape[1]) != int(x.shape[-1]):
+        raise ValueError(f"weight expects {int(weight.shape[1])} input channels; x has {int(x.shape[-1])}")
+    return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_PLAIN), bias, cout=int(weight.shape[0]),
+                                ksize=k, stride=stride)
+
+
+def pointwise_conv(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """1x1x1 convolution on FP32 MFMA (``fast_fp32.pointwise_conv_ncdhw``, :121-130)."""
+    o = int(weight.shape[0])
+    w = weight.reshape(o, -1, 1, 1, 1) if weight.dim() != 5 else weight
+    return conv3d(x, w, bias, padding=0)
+
+
+def group_norm_affine(x: Tensor, weight: Tensor, bias: Tensor, *, groups: int, eps: float) -> Tensor:
+    """``(N, C, 2)`` scale/offset pairs of a group norm of NDHWC ``x`` (``medmlx_core.group_norm_affine``)."""
+    x = _require(x, "x")
+    c = int(x.shape[-1])
+    if c % groups != 0:
+        raise ValueError(f"{c} channels are not divisible by {groups} groups")
+    gamma = _vec(weight, c, "norm weight", x.device)
+    beta = _vec(bias, c, "norm bias", x.device)
+    return ops.gn_affine(x, gamma, beta, int(groups), float(eps))
+
+
+def group_norm(x: Tensor, weight: Tensor, bias: Tensor, *, num_groups: int, eps: float,
+               apply_silu: bool = False) -> Tensor:
+    """Group norm with fp64-accumulated statistics and optional fused SiLU (:102-118)."""
+    affine = group_norm_affine(x, weight, bias, groups=num_groups, eps=eps)
+    return ops.gn_apply(x.contiguous(), affine, bool(apply_silu))
+
+
+def silu_ndhwc(x: Tensor) -> Tensor:
+    return ops.silu(x.contiguous())
+
+
+def avg_pool3d(x: Tensor) -> Tensor:
+    """2x2x2 average pooling, stride 2."""
+    return ops.resample(_require(x, "x"), _lib.AVGPOOL2)
+
+
+def upsample_nearest(x: Tensor) -> Tensor:
+    """Nearest-neighbour 2x upsampling."""
+    return ops.resample(_require(x, "x"), _lib.NEAREST2X)
+
+
+def upsample_trilinear(x: Tensor) -> Tensor:
+    """Half-pixel (align_corners=False) trilinear 2x upsampling, clamped at the edges."""
+    return ops.resample(_require(x, "x"), _lib.TRILINEAR2X)
+
+
+def norm_conv3d(
+    x: Tensor,
+    weight: Tensor,
+    bias: Tensor,
+    *,
+    norm: Optional[tuple[Tensor, Tensor]],
+    num_groups: int,
+    eps: float,
+    apply_silu: bool,
+    upsample: bool = False,
+    residual: Optional[Tensor] = None,
+) -> Tensor:
+    """``conv(upsample?(silu?(norm?(x)))) + bias (+ residual)`` for 3x3x3 kernels (:162-211)."""
+    x = _require(x, "x")
+    affine = None if norm is None else group_norm_affine(x, norm[0], norm[1], groups=num_groups, eps=eps)
+    mode = _lib.MODE_NEAREST2X if upsample else _lib.MODE_PLAIN
+    return implicit_gemm_conv3d(x, _pack(weight, mode), bias, cout=int(weight.shape[0]), affine=affine,
+                                silu=apply_silu, upsample=upsample, residual=residual)
+
+
+def trilinear_conv3d(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+    """Padding-1 3x3x3 conv of the trilinear 2x upsampling, sampled while packing (:339-349)."""
+    return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_PLAIN), bias, cout=int(weight.shape[0]),
+                                trilinear=True)
+
+
+def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """FP32 ``x @ weight.T + bias`` (embedding MLPs; not on the conv hot path)."""
+    return F.linear(x, weight, bias)
+
+
+def residual_block(
+    x: Tensor,
+    emb: Tensor,
+    weights: Mapping[str, Tensor],
+    *,
+    num_groups: int,
+    eps: float,
+    up: bool = False,
+    down: bool = False,
+) -> Tensor:
+    """Fused ``DiffusionUNetResnetBlock`` on NDHWC ``x`` (``fast_fp32.residual_block_ncdhw``, :214-291).
+
+    The time-embedding projection joins conv1's bias per batch item, the skip
+    path (after its optional 1x1x1 projection) joins conv2's accumulator.
+    ``down`` normalizes separately before pooling (pooling does not commute
+    with SiLU); ``up`` folds the nearest-2x upsampling into conv1's weights and
+    projects the skip before upsampling it.
+    """
+    temb = linear(F.silu(emb), weights["time_emb_proj.weight"], weights["time_emb_proj.bias"])
+    bias1 = weights["conv1.conv.bias"].reshape(1, -1) + temb
+    norm1 = (weights["norm1.weight"], weights["norm1.bias"])
+    project = int(x.shape[-1]) != int(weights["conv1.conv.weight"].shape[0])
+
+    def project_skip(skip: Tensor) -> Tensor:
+        if not project:
+            return skip
+        return pointwise_conv(skip, weights["skip_connection.conv.weight"], weights["skip_connection.conv.bias"])
+
+    if down:
+        skip = project_skip(avg_pool3d(x))
+        hidden = avg_pool3d(group_norm(x, *norm1, num_groups=num_groups, eps=eps, apply_silu=True))
+        hidden = norm_conv3d(hidden, weights["conv1.conv.weight"], bias1, norm=None, num_groups=num_groups,
+                             eps=eps, apply_silu=False)
+    else:
+        skip = project_skip(x)
+        if up:
+            skip = upsample_nearest(skip)
+        hidden = norm_conv3d(x, weights["conv1.conv.weight"], bias1, norm=norm1, num_groups=num_groups,
+                             eps=eps, apply_silu=True, upsample=up)
+    return norm_conv3d(hidden, weights["conv2.conv.weight"], weights["conv2.conv.bias"],
+                       norm=(weights["norm2.weight"], weights["norm2.bias"]), num_groups=num_groups,
+                       eps=eps, apply_silu=True, residual=skip)
+
+
+def vae_resblock(
+    state: list[Tensor],
+    conv1: tuple[Tensor, Tensor],
+    conv2: tuple[Tensor, Tensor],
+    norm1: tuple[Tensor, Tensor],
+    norm2: tuple[Tensor, Tensor],
+    shortcut: Optional[tuple[Tensor, Tensor]],
+    *,
+    num_groups: int,
+    eps: float,
+) -> Tensor:
+    """Fused ``MaisiResBlock``: GN-SiLU-conv twice, skip in conv2's accumulator (:294-336).
+
+    ``state`` holds the block input and is emptied so the caller's reference
+    does not keep a multi-gigabyte input alive past its last use.
+    """
+    x = state.pop()
+    hidden = norm_conv3d(x, *conv1, norm=norm1, num_groups=num_groups, eps=eps, apply_silu=True)
+    skip = x if shortcut is None else pointwise_conv(x, *shortcut)
+    del x
+    return norm_conv3d(hidden, *conv2, norm=norm2, num_groups=num_groups, eps=eps, apply_silu=True,
+                       residual=skip)
+
+
+# ---------------------------------------------------------------------------
+# NCDHW adapters with the reference's names and keywords
+# ---------------------------------------------------------------------------
+def to_ndhwc(x: Tensor) -> Tensor:
+    return x.permute(0, 2, 3, 4, 1).contiguous()
+
+
+def to_ncdhw(x: Tensor) -> Tensor:
+    return x.permute(0, 4, 1, 2, 3).contiguous()
+
+
+def conv3d_ncdhw(array: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, mx=None,
+                 stride: int = 1) -> Tensor:
+    return to_ncdhw(conv3d(to_ndhwc(array), weight, bias, padding=padding, stride=stride))
+
+
+def pointwise_conv_ncdhw(array: Tensor, weight: Tensor, bias: Optional[Tensor], *, mx=None) -> Tensor:
+    return to_ncdhw(pointwise_conv(to_ndhwc(array), weight, bias))
+
+
+def group_norm_ncdhw(array: Tensor, weight: Tensor, bias: Tensor, *, num_groups: int, eps: float, mx=None,
+                     apply_silu: bool = False) -> Tensor:
+    return to_ncdhw(group_norm(to_ndhwc(array), weight, bias, num_groups=num_groups, eps=eps,
+                               apply_silu=apply_silu))
+
+
+def norm_conv3d_ncdhw(array: Tensor, weight: Tensor, bias: Tensor, *, norm, num_groups: int, eps: float,
+                      apply_silu: bool, mx=None, upsample: bool = False,
+                      residual: Optional[Tensor] = None) -> Tensor:
+    res = None if residual is None else to_ndhwc(residual)
+    return to_ncdhw(norm_conv3d(to_ndhwc(array), weight, bias, norm=norm, num_groups=num_groups, eps=eps,
+                                apply_silu=apply_silu, upsample=upsample, residual=res))
+
+
+def residual_block_ncdhw(x: Tensor, emb: Tensor, weights: Mapping[str, Tensor], *, num_groups: int, eps: float,
+                         mx=None, up: bool = False, down: bool = False) -> Tensor:
+    return to_ncdhw(residual_block(to_ndhwc(x), emb, weights, num_groups=num_groups, eps=eps, up=up, down=down))
+
+
+def vae_resblock_ncdhw(state: list[Tensor], conv1, conv2, norm1, norm2, shortcut, *, num_groups: int,
+                       eps: float, mx=None) -> Tensor:
+    inner = [to_ndhwc(state.pop())]
+    return to_ncdhw(vae_resblock(inner, conv1, conv2, norm1, norm2, shortcut, num_groups=num_groups, eps=eps))
+
+
+def trilinear_conv3d_ncdhw(array: Tensor, weight: Tensor, bias: Tensor, *, mx=None) -> Tensor:
+    return to_ncdhw(trilinear_conv3d(to_ndhwc(array), weight, bias))
+
+
+def avg_pool3d_ncdhw(array: Tensor, *, mx=None) -> Tensor:
+    return to_ncdhw(avg_pool3d(to_ndhwc(array)))
+
+
+def upsample_nearest_ncdhw(array: Tensor, *, mx=None) -> Tensor:
+    return to_ncdhw(upsample_nearest(to_ndhwc(array)))
+
+
+def upsample_trilinear_ncdhw(array: Tensor, *, mx=None, scale: int = 2) -> Tensor:
+    if scale != 2:
+        raise ValueError("only 2x trilinear upsampling is supported")
+    return to_ncdhw(upsample_trilinear(to_ndhwc(array)))
+
+
+def silu(array: Tensor, mx=None) -> Tensor:
+    """SiLU of any-layout fp32 tensor on the GPU (HIP kernel)."""
+    return ops.silu(array.contiguous())

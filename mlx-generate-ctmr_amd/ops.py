@@ -1,0 +1,213 @@
+"""PyTorch-ROCm custom operators (``ctmr::*``) over the C ABI of ``libctmr_hip.so``.
+
+Each operator allocates its outputs and scratch through PyTorch's caching
+allocator, passes raw device pointers and the current HIP stream to the
+library, and raises on a non-zero status.  Shapes are validated by the
+callers in ``fast_fp32``; these functions assume contiguous fp32 NDHWC CUDA
+tensors.  Every operator has a fake (meta) implementation so it traces.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device(*tensors: Optional[Tensor]) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("ctmr operators run only on the GPU (HIP); got a CPU tensor")
+
+
+def _flags(affine: bool, silu: bool, batch_bias: bool, residual: bool) -> int:
+    return (
+        (_lib.F_AFFINE if affine else 0)
+        | (_lib.F_SILU if silu else 0)
+        | (_lib.F_BATCH_BIAS if batch_bias else 0)
+        | (_lib.F_RESIDUAL if residual else 0)
+    )
+
+
+def make_desc(
+    x_shape: tuple[int, ...],
+    cout: int,
+    ksize: int,
+    stride: int,
+    mode: int,
+    flags: int,
+    dtype: int,
+    split: int,
+) -> _lib.ConvDesc:
+    n, d, h, w, cin = (int(v) for v in x_shape)
+    return _lib.conv_desc(n, d, h, w, cin, cout, ksize=ksize, stride=stride, mode=mode,
+                          flags=flags, dtype=dtype, split=split)
+
+
+# ---------------------------------------------------------------------------
+# weight packing
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("ctmr::pack_weight", mutates_args=())
+def pack_weight(weight: Tensor, cin: int, cout: int, ksize: int, mode: int, dtype: int) -> Tensor:
+    """Packed conv weight (``ctmr_pack_weight`` / ``ctmr_pack_upsample_weight``)."""
+    _require_device(weight)
+    desc = _lib.conv_desc(1, 2, 2, 2, cin, cout, ksize=ksize, mode=mode, dtype=dtype)
+    elems = _lib.packed_weight_elems(desc)
+    out = torch.empty(elems, device=weight.device,
+                      dtype=torch.float32 if dtype == _lib.DT_F32 else torch.bfloat16)
+    fn = _lib.lib().ctmr_pack_upsample_weight if mode == _lib.MODE_NEAREST2X else _lib.lib().ctmr_pack_weight
+    _lib.check(fn(ctypes.byref(desc), weight.data_ptr(), out.data_ptr(), _stream(weight.device)),
+               "ctmr_pack_weight")
+    return out
+
+
+@pack_weight.register_fake
+def _(weight, cin, cout, ksize, mode, dtype):
+    desc = _lib.conv_desc(1, 2, 2, 2, cin, cout, ksize=ksize, mode=mode, dtype=dtype)
+    return weight.new_empty(_lib.packed_weight_elems(desc),
+                            dtype=torch.float32 if dtype == _lib.DT_F32 else torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# convolution
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("ctmr::conv3d", mutates_args=())
+def conv3d(
+    x: Tensor,
+    packed: Tensor,
+    bias: Optional[Tensor],
+    affine: Optional[Tensor],
+    residual: Optional[Tensor],
+    cout: int,
+    ksize: int,
+    stride: int,
+    mode: int,
+    silu: bool,
+    dtype: int,
+    split: int,
+) -> Tensor:
+    """``ctmr_conv3d`` on an NDHWC fp32 tensor; returns the NDHWC output."""
+    _require_device(x, packed, bias, affine, residual)
+    batch_bias = bias is not None and bias.dim() == 2
+    flags = _flags(affine is not None, silu, batch_bias, residual is not None)
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split)
+    od, oh, ow = _lib.output_dims(desc)
+    y = torch.empty((x.shape[0], od, oh, ow, cout), device=x.device, dtype=torch.float32)
+    ws_bytes = _lib.workspace_bytes(desc)
+    ws = torch.empty(max(ws_bytes, 1), device=x.device, dtype=torch.uint8)
+    _lib.check(
+        _lib.lib().ctmr_conv3d(
+            ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
+            _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, _stream(x.device),
+        ),
+        "ctmr_conv3d",
+    )
+    return y
+
+
+@conv3d.register_fake
+def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split):
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, 0, dtype, split)
+    od, oh, ow = _lib.output_dims(desc)
+    return x.new_empty((x.shape[0], od, oh, ow, cout))
+
+
+# ---------------------------------------------------------------------------
+# group norm
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("ctmr::gn_affine", mutates_args=())
+def gn_affine(x: Tensor, gamma: Tensor, beta: Tensor, groups: int, eps: float) -> Tensor:
+    """Per-(batch, channel) (scale, offset) pairs, shape ``(N, C, 2)``."""
+    _require_device(x, gamma, beta)
+    n, c = int(x.shape[0]), int(x.shape[-1])
+    s = x.numel() // (n * c)
+    out = torch.empty((n, c, 2), device=x.device, dtype=torch.float32)
+    ws_bytes = _lib.gn_workspace_bytes(n, s, c)
+    ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    _lib.check(
+        _lib.lib().ctmr_gn_affine(n, s, c, groups, float(eps), x.data_ptr(), gamma.data_ptr(),
+                                  beta.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                  _stream(x.device)),
+        "ctmr_gn_affine",
+    )
+    return out
+
+
+@gn_affine.register_fake
+def _(x, gamma, beta, groups, eps):
+    return x.new_empty((x.shape[0], x.shape[-1], 2))
+
+
+@torch.library.custom_op("ctmr::gn_apply", mutates_args=())
+def gn_apply(x: Tensor, affine: Tensor, silu: bool) -> Tensor:
+    """``silu?(x * scale + offset)`` with pairs from ``gn_affine``."""
+    _require_device(x, affine)
+    n, c = int(x.shape[0]), int(x.shape[-1])
+    s = x.numel() // (n * c)
+    y = torch.empty_like(x)
+    _lib.check(
+        _lib.lib().ctmr_gn_apply(n, s, c, x.data_ptr(), affine.data_ptr(), int(silu), y.data_ptr(),
+                                 _stream(x.device)),
+        "ctmr_gn_apply",
+    )
+    return y
+
+
+@gn_apply.register_fake
+def _(x, affine, silu):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("ctmr::silu", mutates_args=())
+def silu(x: Tensor) -> Tensor:
+    """Elementwise ``x / (1 + exp(-x))``."""
+    _require_device(x)
+    y = torch.empty_like(x)
+    _lib.check(_lib.lib().ctmr_silu(x.numel(), x.data_ptr(), y.data_ptr(), _stream(x.device)),
+               "ctmr_silu")
+    return y
+
+
+@silu.register_fake
+def _(x):
+    return torch.empty_like(x)
+
+
+# ---------------------------------------------------------------------------
+# resampling
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("ctmr::resample", mutates_args=())
+def resample(x: Tensor, op: int) -> Tensor:
+    """2x average pool, nearest or trilinear upsampling of an NDHWC tensor."""
+    _require_device(x)
+    n, d, h, w, c = (int(v) for v in x.shape)
+    if op == _lib.AVGPOOL2:
+        shape = (n, d // 2, h // 2, w // 2, c)
+    else:
+        shape = (n, 2 * d, 2 * h, 2 * w, c)
+    y = torch.empty(shape, device=x.device, dtype=torch.float32)
+    _lib.check(
+        _lib.lib().ctmr_resample(op, n, d, h, w, c, x.data_ptr(), y.data_ptr(), _stream(x.device)),
+        "ctmr_resample",
+    )
+    return y
+
+
+@resample.register_fake
+def _(x, op):
+    n, d, h, w, c = x.shape
+    if op == _lib.AVGPOOL2:
+        return x.new_empty((n, d // 2, h // 2, w // 2, c))
+    return x.new_empty((n, 2 * d, 2 * h, 2 * w, c))

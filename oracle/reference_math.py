@@ -1,0 +1,210 @@
+"""Float64 NumPy restatement of the reference's conv / norm math — test infrastructure only.
+
+Layout: activations NDHWC ``(N, D, H, W, C)`` (the reference is NCDHW; the
+math is layout-independent), conv weights Torch ``(O, C, k, k, k)``.
+Every function returns float64.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+F64 = np.float64
+
+
+def conv3d(x: np.ndarray, w: np.ndarray, b: np.ndarray | None = None, *, stride: int = 1,
+           padding: int | None = None) -> np.ndarray:
+    """Cross-correlation of NDHWC ``x`` with ``(O, C, k, k, k)`` weight, float64.
+
+    Follows the reference's float64 test conv (tests/test_fast_fp32.py:21-38):
+    pad by ``padding`` (default k // 2), then for each tap (kd, kh, kw) add the
+    strided window times ``w[:, :, kd, kh, kw]``.  Output extent per axis is
+    ``(n + 2p - k) // stride + 1``.
+    """
+    x = np.asarray(x, F64)
+    w = np.asarray(w, F64)
+    k = w.shape[2]
+    p = k // 2 if padding is None else padding
+    n, d, h, wd, c = x.shape
+    xp = np.pad(x, [(0, 0), (p, p), (p, p), (p, p), (0, 0)])
+    od, oh, ow = ((s + 2 * p - k) // stride + 1 for s in (d, h, wd))
+    out = np.zeros((n, od, oh, ow, w.shape[0]), F64)
+    for kd in range(k):
+        for kh in range(k):
+            for kw in range(k):
+                win = xp[:, kd : kd + stride * od : stride, kh : kh + stride * oh : stride,
+                         kw : kw + stride * ow : stride, :]
+                out += win @ w[:, :, kd, kh, kw].T
+    if b is not None:
+        b = np.asarray(b, F64)
+        out += b.reshape(b.shape[0], 1, 1, 1, -1) if b.ndim == 2 else b
+    return out
+
+
+def conv3d_points(x: np.ndarray, w: np.ndarray, b: np.ndarray | None, points: np.ndarray, *,
+                  stride: int = 1) -> np.ndarray:
+    """The same padding-1 3x3x3 (or 1x1x1) conv evaluated only at output voxels ``points``.
+
+    ``points`` is ``(P, 4)`` integer ``(n, d, h, w)`` output coordinates; the
+    result is ``(P, O)`` float64.  Used to spot-check full-size volumes whose
+    complete float64 convolution would take too long on the CPU.
+    """
+    x = np.asarray(x, F64)
+    w = np.asarray(w, F64)
+    k = w.shape[2]
+    p = k // 2
+    xp = np.pad(x, [(0, 0), (p, p), (p, p), (p, p), (0, 0)])
+    out = np.zeros((len(points), w.shape[0]), F64)
+    for i, (n, d, h, wi) in enumerate(np.asarray(points)):
+        patch = xp[n, stride * d : stride * d + k, stride * h : stride * h + k, stride * wi : stride * wi + k, :]
+        out[i] = np.einsum("dhwc,ocdhw->o", patch, w)
+    if b is not None:
+        b = np.asarray(b, F64)
+        out += b[np.asarray(points)[:, 0]] if b.ndim == 2 else b
+    return out
+
+
+def upsample_nearest(x: np.ndarray) -> np.ndarray:
+    """Nearest 2x upsampling of NDHWC ``x`` (repeat each voxel 2x per axis;
+    the reference test materializes it the same way, test_fast_fp32.py:123-125)."""
+    x = np.asarray(x, F64)
+    return x.repeat(2, 1).repeat(2, 2).repeat(2, 3)
+
+
+def _tri_axis(n_in: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Half-pixel 2x source indices and upper weight per output index:
+    src = max(0, o/2 - 1/4), i0 = floor(src), i1 = min(i0 + 1, n - 1)
+    (_nax_conv.py:122-128)."""
+    o = np.arange(2 * n_in, dtype=F64)
+    src = np.maximum(0.0, 0.5 * o - 0.25)
+    i0 = np.floor(src).astype(np.int64)
+    i1 = np.minimum(i0 + 1, n_in - 1)
+    return i0, i1, src - i0
+
+
+def upsample_trilinear(x: np.ndarray) -> np.ndarray:
+    """Trilinear 2x upsampling, align_corners=False, clamped upper neighbours
+    (source_vae.upsample_trilinear_ncdhw; formula at _nax_conv.py:115-142)."""
+    y = np.asarray(x, F64)
+    for axis in (1, 2, 3):
+        i0, i1, l1 = _tri_axis(y.shape[axis])
+        shape = [1] * y.ndim
+        shape[axis] = -1
+        l1 = l1.reshape(shape)
+        y = np.take(y, i0, axis=axis) * (1.0 - l1) + np.take(y, i1, axis=axis) * l1
+    return y
+
+
+def avg_pool(x: np.ndarray) -> np.ndarray:
+    """2x2x2 mean pooling with stride 2 (medmlx_core avg_pool3d_ncdhw as used at
+    fast_fp32.py:251-255 and residual.py:93-95)."""
+    x = np.asarray(x, F64)
+    n, d, h, w, c = x.shape
+    x = x[:, : d // 2 * 2, : h // 2 * 2, : w // 2 * 2]
+    return x.reshape(n, d // 2, 2, h // 2, 2, w // 2, 2, c).mean(axis=(2, 4, 6))
+
+
+def fold_upsample_weight(w: np.ndarray) -> np.ndarray:
+    """Nearest-2x parity fold of a 3x3x3 weight (_nax_conv.pack_upsample_weight, :407-445).
+
+    Returns ``(8, O, C, 2, 2, 2)``: parity ``pd*4 + ph*2 + pw``, taps ``(td, th, tw)``.
+    Per axis, parity 0 taps are ``(k0, k1 + k2)`` and parity 1 taps ``(k0 + k1, k2)``.
+    """
+    w = np.asarray(w, F64)
+    sets = {(0, 0): [0], (0, 1): [1, 2], (1, 0): [0, 1], (1, 1): [2]}
+    out = np.zeros((8, w.shape[0], w.shape[1], 2, 2, 2), F64)
+    for pd in range(2):
+        for ph in range(2):
+            for pw in range(2):
+                for td in range(2):
+                    for th in range(2):
+                        for tw in range(2):
+                            acc = 0.0
+                            for kd in sets[(pd, td)]:
+                                for kh in sets[(ph, th)]:
+                                    for kw in sets[(pw, tw)]:
+                                        acc = acc + w[:, :, kd, kh, kw]
+                            out[pd * 4 + ph * 2 + pw, :, :, td, th, tw] = acc
+    return out
+
+
+def conv3d_upsample_folded(x: np.ndarray, w: np.ndarray, b: np.ndarray | None = None) -> np.ndarray:
+    """Conv of the nearest-2x upsampling computed with the parity-folded 2x2x2 filters.
+
+    Output voxel ``2m + p`` (per axis) is the 2x2x2 conv of the zero-padded
+    source over padded offsets ``m + p + t``, t in {0, 1} (_nax_conv.py:218-233).
+    """
+    x = np.asarray(x, F64)
+    folded = fold_upsample_weight(w)
+    n, d, h, wd, _ = x.shape
+    xp = np.pad(x, [(0, 0), (1, 1), (1, 1), (1, 1), (0, 0)])
+    out = np.zeros((n, 2 * d, 2 * h, 2 * wd, w.shape[0]), F64)
+    for pd in range(2):
+        for ph in range(2):
+            for pw in range(2):
+                f = folded[pd * 4 + ph * 2 + pw]
+                acc = np.zeros((n, d, h, wd, w.shape[0]), F64)
+                for td in range(2):
+                    for th in range(2):
+                        for tw in range(2):
+                            win = xp[:, pd + td : pd + td + d, ph + th : ph + th + h, pw + tw : pw + tw + wd, :]
+                            acc += win @ f[:, :, td, th, tw].T
+                out[:, pd::2, ph::2, pw::2, :] = acc
+    if b is not None:
+        b = np.asarray(b, F64)
+        out += b.reshape(b.shape[0], 1, 1, 1, -1) if b.ndim == 2 else b
+    return out
+
+
+def group_norm_affine(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, groups: int,
+                      eps: float) -> np.ndarray:
+    """``(N, C, 2)`` per-channel (scale, offset) of a group norm of NDHWC ``x``.
+
+    Mean and biased variance per (n, group) over (C/G channels) x voxels
+    (tests/test_fast_fp32.py:41-48); scale = gamma / sqrt(var + eps),
+    offset = beta - mean * scale (the pair layout of _nax_conv.py:502-504).
+    """
+    x = np.asarray(x, F64)
+    n, c = x.shape[0], x.shape[-1]
+    g = x.reshape(n, -1, groups, c // groups)
+    mean = g.mean(axis=(1, 3))
+    var = g.var(axis=(1, 3))
+    rstd = 1.0 / np.sqrt(var + eps)
+    scale = np.asarray(gamma, F64)[None, :] * np.repeat(rstd, c // groups, axis=1)
+    offset = np.asarray(beta, F64)[None, :] - np.repeat(mean, c // groups, axis=1) * scale
+    return np.stack([scale, offset], axis=-1)
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    """``x / (1 + exp(-x))`` (_nax_conv.py:177)."""
+    x = np.asarray(x, F64)
+    return x / (1.0 + np.exp(-x))
+
+
+def group_norm(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, groups: int, eps: float,
+               apply_silu: bool = False) -> np.ndarray:
+    """Group norm (+ SiLU) of NDHWC ``x`` (tests/test_fast_fp32.py:41-48)."""
+    return apply_affine(x, group_norm_affine(x, gamma, beta, groups, eps), apply_silu)
+
+
+def apply_affine(x: np.ndarray, affine: np.ndarray, apply_silu: bool) -> np.ndarray:
+    """``silu?(x * scale + offset)`` with ``(N, C, 2)`` pairs."""
+    x = np.asarray(x, F64)
+    a = np.asarray(affine, F64)
+    n, c = x.shape[0], x.shape[-1]
+    y = x * a[..., 0].reshape(n, 1, 1, 1, c) + a[..., 1].reshape(n, 1, 1, 1, c)
+    return silu(y) if apply_silu else y
+
+
+def ncdhw_to_ndhwc(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(np.moveaxis(np.asarray(x), 1, -1))
+
+
+def ndhwc_to_ncdhw(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(np.moveaxis(np.asarray(x), -1, 1))
+
+
+def max_rel_error(actual: np.ndarray, expected: np.ndarray) -> float:
+    """``max|actual - expected| / max|expected|`` (the per-layer error measure)."""
+    expected = np.asarray(expected, F64)
+    return float(np.abs(np.asarray(actual, F64) - expected).max() / max(np.abs(expected).max(), 1e-300))

@@ -1,0 +1,113 @@
+"""CPU tests of the C ABI: the library loads, exports every declared symbol, and
+its host-side geometry, policy and error paths behave (no kernel is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+
+import pytest
+
+
+def test_library_exports_every_header_symbol(ctmr, native_loaded):
+    declared = ctmr._lib.header_symbols()
+    assert "ctmr_conv3d" in declared and len(declared) >= 14
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ctmr._lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    for name in declared:
+        getattr(native_loaded, name)
+    assert native_loaded.ctmr_abi_version() == ctmr._lib.ABI_VERSION
+
+
+def test_prototypes_cover_header(ctmr):
+    assert sorted(ctmr._lib._PROTOTYPES) == ctmr._lib.header_symbols()
+
+
+@pytest.mark.parametrize(
+    ("dims", "kw", "expected"),
+    [
+        ((1, 64, 64, 64, 64, 64), {}, (64, 64, 64)),
+        ((1, 7, 6, 5, 32, 64), {"stride": 2}, (4, 3, 3)),
+        ((2, 4, 8, 8, 256, 128), {"mode": 1}, (8, 16, 16)),
+        ((2, 3, 5, 6, 24, 32), {"mode": 2}, (6, 10, 12)),
+        ((1, 9, 6, 8, 128, 256), {"ksize": 1}, (9, 6, 8)),
+    ],
+)
+def test_output_dims(ctmr, dims, kw, expected):
+    L = ctmr._lib
+    assert L.output_dims(L.conv_desc(*dims, **kw)) == expected
+
+
+def test_workspace_and_packed_sizes(ctmr):
+    L = ctmr._lib
+    d = L.conv_desc(1, 64, 64, 64, 64, 64)
+    # padded copy: 66^3 rows x 64 fp32 channels, 256-byte aligned; no split
+    assert L.workspace_bytes(d) == ((66**3 * 64 * 4 + 255) // 256) * 256
+    assert L.packed_weight_elems(d) == 27 * 64 * 64
+    assert L.conv_split(d) == 1
+    # bf16 halves the copy and rounds channels to 32
+    d16 = L.conv_desc(1, 8, 8, 8, 4, 4, dtype=L.DT_BF16)
+    assert L.packed_weight_elems(d16) == 27 * 32 * 16
+    # nearest-2x parity weights: 8 phases x 8 taps
+    du = L.conv_desc(1, 4, 4, 4, 32, 48, mode=L.MODE_NEAREST2X)
+    assert L.packed_weight_elems(du) == 8 * 8 * 32 * 48
+    # 1x1 with 16-aligned channels reads x directly: no workspace
+    assert L.workspace_bytes(L.conv_desc(1, 4, 4, 4, 128, 256, ksize=1)) == 0
+    assert L.workspace_bytes(L.conv_desc(1, 4, 4, 4, 4, 4, ksize=1)) > 0
+
+
+def test_split_policy_is_shape_only(ctmr):
+    L = ctmr._lib
+    # UNet deepest level (512 ch on 8x8x4, batch 2): few tiles -> full tap split
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512)) == 27
+    # large grids never split
+    assert L.conv_split(L.conv_desc(1, 128, 128, 128, 128, 128)) == 1
+    # explicit split must divide the tap count
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=3)) == 3
+    with pytest.raises(L.CtmrError, match="divide"):
+        L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=4))
+
+
+@pytest.mark.parametrize(
+    ("kw", "status", "message"),
+    [
+        ({"ksize": 5}, -2, "ksize"),
+        ({"stride": 3}, -2, "stride"),
+        ({"mode": 2, "flags": 1}, -2, "trilinear"),
+        ({"mode": 1, "stride": 2}, -2, "stride 1"),
+        ({"ksize": 1, "stride": 2}, -2, "1x1x1"),
+        ({"dtype": 7}, -1, "dtype"),
+    ],
+)
+def test_invalid_descriptors(ctmr, native_loaded, kw, status, message):
+    L = ctmr._lib
+    d = L.conv_desc(1, 4, 4, 4, 16, 16, **kw)
+    assert native_loaded.ctmr_conv3d_workspace_bytes(ctypes.byref(d)) == status
+    assert message in L.last_error()
+
+
+def test_conv_rejects_null_and_small_workspace_before_launch(ctmr, native_loaded):
+    L = ctmr._lib
+    d = L.conv_desc(1, 4, 4, 4, 16, 16)
+    rc = native_loaded.ctmr_conv3d(ctypes.byref(d), None, None, None, None, None, None, None, 0, None)
+    assert rc == L.E_INVALID
+    fake = 0x1000  # never dereferenced: the size check fails first
+    rc = native_loaded.ctmr_conv3d(ctypes.byref(d), fake, fake, None, None, None, fake, fake, 16, None)
+    assert rc == L.E_WORKSPACE and "workspace" in L.last_error()
+    d.flags = L.F_RESIDUAL
+    rc = native_loaded.ctmr_conv3d_gemm(ctypes.byref(d), fake, fake, None, None, fake, fake, 1 << 40, None)
+    assert rc == L.E_INVALID and "residual" in L.last_error()
+
+
+def test_group_norm_host_checks(ctmr, native_loaded):
+    L = ctmr._lib
+    assert L.gn_workspace_bytes(1, 128**3, 128) == 1 * 2048 * 128 * 2 * 8
+    rc = native_loaded.ctmr_gn_affine(1, 64, 12, 5, 1e-6, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1 << 30, None)
+    assert rc == L.E_INVALID and "divisible" in L.last_error()
+    rc = native_loaded.ctmr_gn_affine(1, 64, 6, 3, 1e-6, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1 << 30, None)
+    assert rc == L.E_UNSUPPORTED
+    rc = native_loaded.ctmr_resample(0, 1, 1, 4, 4, 4, 0x1000, 0x1000, None)
+    assert rc == L.E_INVALID and "pooling" in L.last_error()

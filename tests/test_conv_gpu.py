@@ -1,0 +1,212 @@
+"""GPU parity of the HIP conv / norm kernels against the float64 CPU oracle.
+
+The first three tests restate the reference's own kernel tests
+(tests/test_fast_fp32.py:59-150) with the same seeds, shapes and draw order,
+so the inputs are identical to the ones the reference checks.  Bars:
+* reference bar: ``max|y - ref| <= 2e-6 * max|ref|`` (test_fast_fp32.py:16-18);
+* per-layer max relative error <= 1e-5 (FP32), <= 2e-2 (bf16);
+* bitwise: repeat runs, fused vs materialized trilinear.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference_math as rm
+
+pytestmark = pytest.mark.gpu
+
+REF_REL = 2e-6  # the reference's kernel-test tolerance, relative to max|ref|
+FP32_REL = 1e-5
+BF16_REL = 2e-2
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _h(t):
+    return t.detach().cpu().numpy().astype(np.float64)
+
+
+def _assert_rel(actual, expected, bound, what=""):
+    expected = np.asarray(expected, np.float64)
+    actual = np.asarray(actual, np.float64)
+    assert actual.shape == expected.shape, (actual.shape, expected.shape)
+    assert np.isfinite(actual).all(), f"{what}: non-finite output"
+    err = rm.max_rel_error(actual, expected)
+    print(f"{what}: max rel error {err:.3e} (bound {bound:g})", flush=True)
+    assert err <= bound, f"{what}: max rel error {err:.3e} > {bound:g}"
+
+
+@pytest.mark.parametrize(
+    ("shape", "out_channels", "stride"),
+    [
+        ((2, 64, 8, 16, 16), 64, 1),
+        ((2, 512, 4, 8, 8), 512, 1),  # deep level: tap split
+        ((2, 256, 8, 16, 16), 128, 1),
+        ((1, 4, 8, 8, 8), 4, 1),  # padded channels, 16-column tile
+        ((1, 32, 8, 12, 16), 64, 2),
+    ],
+)
+def test_conv_matches_float64(ctmr, dev, shape, out_channels, stride):
+    """Reference test_nax_conv_matches_float64 (test_fast_fp32.py:59-88), NCDHW entry point."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(shape).astype(np.float32)
+    w = (rng.standard_normal((out_channels, shape[1], 3, 3, 3)) / np.sqrt(27 * shape[1])).astype(np.float32)
+    b = rng.standard_normal(out_channels).astype(np.float32)
+    y = ctmr.fast_fp32.conv3d_ncdhw(_t(x, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
+    expected = rm.ndhwc_to_ncdhw(rm.conv3d(rm.ncdhw_to_ndhwc(x), w, b, stride=stride))
+    _assert_rel(_h(y), expected, REF_REL, f"conv {shape}->{out_channels} s{stride}")
+
+
+@pytest.mark.parametrize("upsample", [False, True])
+def test_fused_norm_conv_matches_float64(ctmr, dev, upsample):
+    """Reference test_fused_norm_conv_matches_float64 (test_fast_fp32.py:91-127)."""
+    rng = np.random.default_rng(5)
+    batch, channels, out_channels, groups = 2, 64, 32, 8
+    x = (3 * rng.standard_normal((batch, channels, 4, 8, 8)) + 1).astype(np.float32)
+    w = (rng.standard_normal((out_channels, channels, 3, 3, 3)) / np.sqrt(27 * channels)).astype(np.float32)
+    batch_bias = rng.standard_normal((batch, out_channels)).astype(np.float32)
+    norm_w = (1 + 0.1 * rng.standard_normal(channels)).astype(np.float32)
+    norm_b = (0.1 * rng.standard_normal(channels)).astype(np.float32)
+    scale = 2 if upsample else 1
+    residual = rng.standard_normal((batch, out_channels, 4 * scale, 8 * scale, 8 * scale)).astype(np.float32)
+    y = ctmr.fast_fp32.norm_conv3d_ncdhw(
+        _t(x, dev), _t(w, dev), _t(batch_bias, dev), norm=(_t(norm_w, dev), _t(norm_b, dev)),
+        num_groups=groups, eps=1e-6, apply_silu=True, upsample=upsample, residual=_t(residual, dev))
+    prepared = rm.group_norm(rm.ncdhw_to_ndhwc(x), norm_w, norm_b, groups, 1e-6, apply_silu=True)
+    if upsample:
+        prepared = rm.upsample_nearest(prepared)
+    expected = rm.conv3d(prepared, w) + batch_bias[:, None, None, None, :] + rm.ncdhw_to_ndhwc(residual)
+    _assert_rel(_h(y), rm.ndhwc_to_ncdhw(expected), REF_REL, f"fused norm conv up={upsample}")
+
+
+def test_trilinear_conv_matches_materialized_upsampling(ctmr, dev):
+    """Reference test_trilinear_conv_matches_materialized_upsampling (test_fast_fp32.py:130-150): bitwise."""
+    rng = np.random.default_rng(7)
+    x = _t(rng.standard_normal((2, 24, 3, 5, 6)).astype(np.float32), dev)
+    w = _t((rng.standard_normal((32, 24, 3, 3, 3)) / np.sqrt(27 * 24)).astype(np.float32), dev)
+    b = _t(rng.standard_normal(32).astype(np.float32), dev)
+    f = ctmr.fast_fp32
+    fused = f.trilinear_conv3d_ncdhw(x, w, b)
+    materialized = f.conv3d_ncdhw(f.upsample_trilinear_ncdhw(x), w, b, padding=1)
+    assert tuple(fused.shape) == (2, 32, 6, 10, 12)
+    assert torch.equal(fused, materialized)
+    expected = rm.conv3d(rm.upsample_trilinear(rm.ncdhw_to_ndhwc(_h(x))), _h(w), _h(b))
+    _assert_rel(_h(fused), rm.ndhwc_to_ncdhw(expected), REF_REL, "trilinear conv")
+
+
+@pytest.mark.parametrize("split", [1, 3, 9, 27])
+def test_forced_tap_split_matches_float64(ctmr, dev, split):
+    """Every tap split gives the same result to fp32 rounding; each is deterministic."""
+    rng = np.random.default_rng(11)
+    x = (3 * rng.standard_normal((1, 6, 4, 4, 256)) + 1).astype(np.float32)
+    w = (rng.standard_normal((256, 256, 3, 3, 3)) / np.sqrt(27 * 256)).astype(np.float32)
+    b = rng.standard_normal(256).astype(np.float32)
+    res = rng.standard_normal((1, 6, 4, 4, 256)).astype(np.float32)
+    f = ctmr.fast_fp32
+    packed = f.pack_weight(_t(w, dev))
+    run = lambda: f.implicit_gemm_conv3d(_t(x, dev), packed, _t(b, dev), cout=256, split=split,
+                                         residual=_t(res, dev))
+    y1, y2 = run(), run()
+    assert torch.equal(y1, y2)
+    _assert_rel(_h(y1), rm.conv3d(x, w, b) + res, REF_REL, f"split {split}")
+
+
+def test_repeat_runs_are_bitwise_identical(ctmr, dev):
+    rng = np.random.default_rng(13)
+    x = _t(rng.standard_normal((2, 12, 10, 9, 48)).astype(np.float32), dev)
+    w = _t((rng.standard_normal((80, 48, 3, 3, 3)) / np.sqrt(27 * 48)).astype(np.float32), dev)
+    b = _t(rng.standard_normal(80).astype(np.float32), dev)
+    f = ctmr.fast_fp32
+    first = f.conv3d(x, w, b, padding=1)
+    for _ in range(3):
+        assert torch.equal(f.conv3d(x, w, b, padding=1), first)
+
+
+@pytest.mark.parametrize(("cin", "cout"), [(128, 256), (4, 4), (64, 1), (48, 40)])
+def test_pointwise_conv_matches_matmul(ctmr, dev, cin, cout):
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((2, 5, 6, 7, cin)).astype(np.float32)
+    w = (rng.standard_normal((cout, cin, 1, 1, 1)) / np.sqrt(cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    y = ctmr.fast_fp32.pointwise_conv(_t(x, dev), _t(w, dev), _t(b, dev))
+    _assert_rel(_h(y), x.astype(np.float64) @ w[:, :, 0, 0, 0].T.astype(np.float64) + b, REF_REL, f"1x1 {cin}->{cout}")
+
+
+@pytest.mark.parametrize(("shape", "cout", "stride", "mode"), [
+    ((2, 64, 8, 16, 16), 64, 1, "plain"),
+    ((1, 32, 8, 12, 16), 64, 2, "plain"),
+    ((2, 64, 4, 8, 8), 32, 1, "nearest"),
+    ((1, 4, 8, 8, 8), 4, 1, "plain"),
+])
+def test_bf16_variant_within_2e2(ctmr, dev, shape, cout, stride, mode):
+    rng = np.random.default_rng(19)
+    x = rng.standard_normal(shape).astype(np.float32)
+    w = (rng.standard_normal((cout, shape[1], 3, 3, 3)) / np.sqrt(27 * shape[1])).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    f = ctmr.fast_fp32
+    xn = rm.ncdhw_to_ndhwc(x)
+    with f.precision("bf16"):
+        if mode == "nearest":
+            y = f.norm_conv3d(_t(xn, dev), _t(w, dev), _t(b, dev), norm=None, num_groups=1, eps=1e-6,
+                              apply_silu=False, upsample=True)
+            expected = rm.conv3d(rm.upsample_nearest(xn), w, b)
+        else:
+            y = f.conv3d(_t(xn, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
+            expected = rm.conv3d(xn, w, b, stride=stride)
+    _assert_rel(_h(y), expected, BF16_REL, f"bf16 {shape}->{cout} {mode}")
+
+
+def test_group_norm_affine_and_apply(ctmr, dev):
+    rng = np.random.default_rng(23)
+    x = (3 * rng.standard_normal((2, 6, 5, 7, 64)) + 1).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(64)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(64)).astype(np.float32)
+    f = ctmr.fast_fp32
+    aff = f.group_norm_affine(_t(x, dev), _t(gamma, dev), _t(beta, dev), groups=32, eps=1e-6)
+    _assert_rel(_h(aff), rm.group_norm_affine(x, gamma, beta, 32, 1e-6), 1e-6, "gn affine")
+    for silu in (False, True):
+        y = f.group_norm(_t(x, dev), _t(gamma, dev), _t(beta, dev), num_groups=32, eps=1e-6, apply_silu=silu)
+        _assert_rel(_h(y), rm.group_norm(x, gamma, beta, 32, 1e-6, apply_silu=silu), 1e-6, f"gn silu={silu}")
+
+
+def test_group_norm_matches_recorded_golden(ctmr, dev):
+    from golden_util import load_fixture
+
+    g = load_fixture("source_fp32.npz")
+    f = ctmr.fast_fp32
+    y = f.group_norm_ncdhw(_t(g["input.x"], dev), _t(g["input.norm_w"], dev), _t(g["input.norm_b"], dev),
+                           num_groups=2, eps=1e-6)
+    np.testing.assert_allclose(_h(y), g["output.norm"], rtol=1e-5, atol=1e-6)
+    y = f.conv3d_ncdhw(_t(g["input.x"], dev), _t(g["input.kernel_w"], dev), _t(g["input.kernel_b"], dev), padding=1)
+    np.testing.assert_allclose(_h(y), g["output.conv"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(_h(f.silu(_t(g["input.x"], dev))), g["output.silu"], rtol=1e-6, atol=1e-7)
+    y = f.upsample_trilinear_ncdhw(_t(g["input.x"], dev))
+    np.testing.assert_allclose(_h(y), g["output.trilinear"], rtol=1e-6, atol=1e-7)
+
+
+def test_resampling_kernels(ctmr, dev):
+    rng = np.random.default_rng(29)
+    f = ctmr.fast_fp32
+    for c in (8, 3):
+        x = rng.standard_normal((2, 4, 6, 5, c)).astype(np.float32)
+        np.testing.assert_array_equal(_h(f.upsample_nearest(_t(x, dev))), rm.upsample_nearest(x))
+        _assert_rel(_h(f.upsample_trilinear(_t(x, dev))), rm.upsample_trilinear(x), 1e-6, f"trilinear c={c}")
+        _assert_rel(_h(f.avg_pool3d(_t(x, dev))), rm.avg_pool(x), 1e-6, f"avgpool c={c}")
+
+
+def test_validation_errors(ctmr, dev):
+    f = ctmr.fast_fp32
+    x = torch.zeros((1, 4, 4, 4, 16), device=dev)
+    w = torch.zeros((16, 16, 3, 3, 3), device=dev)
+    packed = f.pack_weight(w)
+    with pytest.raises(ValueError, match="trilinear"):
+        f.implicit_gemm_conv3d(x, packed, None, cout=16, trilinear=True, silu=True)
+    with pytest.raises(ValueError, match="residual shape"):
+        f.implicit_gemm_conv3d(x, packed, None, cout=16, residual=torch.zeros((1, 4, 4, 4, 8), device=dev))
+    with pytest.raises(ValueError, match="does not fit"):
+        f.implicit_gemm_conv3d(torch.zeros((1, 4, 4, 4, 32), device=dev), packed, None, cout=16)

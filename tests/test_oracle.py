@@ -1,0 +1,168 @@
+"""Pin the CPU oracle (oracle/reference_math.py) before it is trusted as the checker.
+
+Each oracle function is checked against (a) the reference's recorded goldens
+(tests/golden/source_fp32.npz, Torch 2.14 CPU on darwin-arm64), (b) an
+independent implementation (PyTorch CPU in float64) and (c) closed forms or
+brute force, chosen so that a dropped term, a wrong sign or index, or a
+transposed operand fails.  A planted-mistake test shows the golden check
+rejects a transposed kernel.
+"""
+
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from golden_util import load_fixture
+from oracle import reference_math as rm
+
+GOLD = load_fixture("source_fp32.npz")
+
+
+def _nd(x):
+    return rm.ncdhw_to_ndhwc(x)
+
+
+def _close(actual, expected, rtol=1e-5, atol=1e-6):
+    np.testing.assert_allclose(np.asarray(actual, np.float64), np.asarray(expected, np.float64), rtol=rtol, atol=atol)
+
+
+# --- goldens ---------------------------------------------------------------
+def test_conv_matches_recorded_golden():
+    x, w, b = GOLD["input.x"], GOLD["input.kernel_w"], GOLD["input.kernel_b"]
+    y = rm.conv3d(_nd(x), w, b)
+    _close(rm.ndhwc_to_ncdhw(y), GOLD["output.conv"])
+
+
+def test_planted_transposed_kernel_fails_golden():
+    """A plausible mistake (kernel applied flipped, i.e. convolution instead of
+    cross-correlation) must not pass the golden check."""
+    x, w, b = GOLD["input.x"], GOLD["input.kernel_w"], GOLD["input.kernel_b"]
+    wrong = rm.conv3d(_nd(x), w[:, :, ::-1, ::-1, ::-1], b)
+    with pytest.raises(AssertionError):
+        _close(rm.ndhwc_to_ncdhw(wrong), GOLD["output.conv"])
+
+
+@pytest.mark.parametrize("name", ["norm", "vae_norm"])
+def test_group_norm_matches_recorded_golden(name):
+    x = GOLD["input.x"]
+    y = rm.group_norm(_nd(x), GOLD["input.norm_w"], GOLD["input.norm_b"], groups=2, eps=1e-6)
+    _close(rm.ndhwc_to_ncdhw(y), GOLD[f"output.{name}"])
+
+
+def test_planted_unbiased_variance_fails_golden():
+    x = _nd(GOLD["input.x"]).astype(np.float64)
+    g = x.reshape(1, -1, 2, 2)
+    mean, var = g.mean(axis=(1, 3)), g.var(axis=(1, 3), ddof=1)  # the mistake: ddof=1
+    y = (g - mean[:, None, :, None]) / np.sqrt(var[:, None, :, None] + 1e-6)
+    y = y.reshape(x.shape) * GOLD["input.norm_w"] + GOLD["input.norm_b"]
+    with pytest.raises(AssertionError):
+        _close(rm.ndhwc_to_ncdhw(y), GOLD["output.norm"])
+
+
+def test_silu_matches_recorded_golden():
+    _close(rm.silu(GOLD["input.x"]), GOLD["output.silu"])
+
+
+def test_trilinear_matches_recorded_golden():
+    y = rm.upsample_trilinear(_nd(GOLD["input.x"]))
+    _close(rm.ndhwc_to_ncdhw(y), GOLD["output.trilinear"])
+
+
+# --- independent implementations and closed forms -------------------------
+def _rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape)
+
+
+def test_conv_brute_force_tiny():
+    x = _rand((1, 3, 4, 2, 3), 1)
+    w = _rand((2, 3, 3, 3, 3), 2)
+    b = _rand(2, 3)
+    y = rm.conv3d(x, w, b)
+    xp = np.pad(x, [(0, 0), (1, 1), (1, 1), (1, 1), (0, 0)])
+    ref = np.zeros_like(y)
+    for d, h, wi, o in itertools.product(range(3), range(4), range(2), range(2)):
+        acc = b[o]
+        for kd, kh, kw, c in itertools.product(range(3), range(3), range(3), range(3)):
+            acc += xp[0, d + kd, h + kh, wi + kw, c] * w[o, c, kd, kh, kw]
+        ref[0, d, h, wi, o] = acc
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("stride", [1, 2])
+def test_conv_matches_torch_float64(stride):
+    x = _rand((2, 5, 7, 6, 4), 4)
+    w = _rand((3, 4, 3, 3, 3), 5)
+    b = _rand(3, 6)
+    y = rm.conv3d(x, w, b, stride=stride)
+    ref = F.conv3d(torch.from_numpy(np.moveaxis(x, -1, 1)), torch.from_numpy(w), torch.from_numpy(b),
+                   stride=stride, padding=1).numpy()
+    np.testing.assert_allclose(y, np.moveaxis(ref, 1, -1), rtol=1e-12, atol=1e-12)
+
+
+def test_stride2_is_subsampled_stride1():
+    x = _rand((1, 7, 6, 5, 3), 7)
+    w = _rand((2, 3, 3, 3, 3), 8)
+    np.testing.assert_allclose(rm.conv3d(x, w, stride=2), rm.conv3d(x, w)[:, ::2, ::2, ::2], rtol=1e-12, atol=1e-12)
+
+
+def test_pointwise_is_matmul():
+    x = _rand((2, 3, 4, 5, 6), 9)
+    w = _rand((7, 6, 1, 1, 1), 10)
+    b = _rand(7, 11)
+    np.testing.assert_allclose(rm.conv3d(x, w, b), x @ w[:, :, 0, 0, 0].T + b, rtol=1e-12, atol=1e-12)
+
+
+def test_conv_points_match_full_conv():
+    x = _rand((2, 5, 4, 6, 3), 12)
+    w = _rand((4, 3, 3, 3, 3), 13)
+    b = _rand((2, 4), 14)
+    full = rm.conv3d(x, w, b)
+    pts = np.array([[0, 0, 0, 0], [1, 4, 3, 5], [0, 2, 1, 3], [1, 0, 3, 0]])
+    np.testing.assert_allclose(rm.conv3d_points(x, w, b, pts), full[tuple(pts.T)], rtol=1e-12, atol=1e-12)
+    full2 = rm.conv3d(x, w, b, stride=2)
+    pts2 = np.array([[0, 0, 0, 0], [1, 2, 1, 2]])
+    np.testing.assert_allclose(rm.conv3d_points(x, w, b, pts2, stride=2), full2[tuple(pts2.T)], rtol=1e-12, atol=1e-12)
+
+
+def test_upsample_fold_is_exact_identity():
+    x = _rand((2, 3, 4, 5, 3), 15)
+    w = _rand((2, 3, 3, 3, 3), 16)
+    b = _rand(2, 17)
+    np.testing.assert_allclose(rm.conv3d_upsample_folded(x, w, b), rm.conv3d(rm.upsample_nearest(x), w, b),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_upsampling_matches_torch():
+    x = _rand((2, 3, 5, 4, 2), 18)
+    t = torch.from_numpy(np.moveaxis(x, -1, 1))
+    tri = F.interpolate(t, scale_factor=2, mode="trilinear", align_corners=False).numpy()
+    np.testing.assert_allclose(rm.upsample_trilinear(x), np.moveaxis(tri, 1, -1), rtol=1e-12, atol=1e-12)
+    near = F.interpolate(t, scale_factor=2, mode="nearest").numpy()
+    np.testing.assert_allclose(rm.upsample_nearest(x), np.moveaxis(near, 1, -1), rtol=0, atol=0)
+
+
+def test_avg_pool_matches_torch():
+    x = _rand((2, 4, 6, 8, 3), 19)
+    ref = F.avg_pool3d(torch.from_numpy(np.moveaxis(x, -1, 1)), 2).numpy()
+    np.testing.assert_allclose(rm.avg_pool(x), np.moveaxis(ref, 1, -1), rtol=1e-12, atol=1e-12)
+
+
+def test_group_norm_matches_torch_and_is_shift_invariant():
+    x = 3 * _rand((2, 3, 4, 5, 8), 20) + 1
+    gamma, beta = 1 + 0.1 * _rand(8, 21), 0.1 * _rand(8, 22)
+    y = rm.group_norm(x, gamma, beta, groups=4, eps=1e-6, apply_silu=False)
+    ref = F.group_norm(torch.from_numpy(np.moveaxis(x, -1, 1)), 4, torch.from_numpy(gamma),
+                       torch.from_numpy(beta), eps=1e-6).numpy()
+    np.testing.assert_allclose(y, np.moveaxis(ref, 1, -1), rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(rm.group_norm(x + 5.0, gamma, beta, 4, 1e-6), y, rtol=1e-9, atol=1e-9)
+
+
+def test_silu_closed_form():
+    v = np.array([0.0, 1.0, -1.0, 20.0, -20.0])
+    np.testing.assert_allclose(rm.silu(v), [0.0, 1 / (1 + np.exp(-1)), -1 / (1 + np.e), 20 / (1 + np.exp(-20)), -20 * np.exp(-20) / (1 + np.exp(-20))],
+                               rtol=1e-12, atol=1e-12)
