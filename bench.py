@@ -164,6 +164,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (N=1); multi-GPU runs are not part of it",
@@ -172,6 +174,16 @@ def main() -> int:
 
     import numpy as np
     import torch
+
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, device="cuda:0")  # 1 GiB fp32
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4,
+                          "launches": 3}), flush=True)
+        return 0
 
     pkg = importlib.import_module("mlx-generate-ctmr_amd")
     f = pkg.fast_fp32
@@ -225,6 +237,12 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK, 4), "traffic": None,
                      "kernel": "conv_kernel<f32> (implicit GEMM)", "kernel_ms": round(gemm_ms, 4)},
     }
+    # HBM bytes per GEMM launch from the committed rocprofv3 --pmc passes
+    # (FETCH_SIZE x read scale + WRITE_SIZE x write scale, copy-calibrated).
+    traffic_file = REPO / "profiles" / "conv3d_config0_traffic.json"
+    if traffic_file.exists():
+        result["roofline"]["traffic"] = json.loads(traffic_file.read_text())["traffic_bytes"]
+        result["roofline"]["traffic_source"] = "profiles/conv3d_config0_traffic.json"
     sec = {"config0_bf16_gemm": {"ms": round(bf16_ms, 4), "tflops": round(flops / bf16_ms / 1e9, 2),
                                  "frac_bf16_peak": round(flops / (bf16_ms * 1e-3) / BF16_PEAK, 4)}}
     if not args.no_secondary:

@@ -113,7 +113,10 @@ def test_forced_tap_split_matches_float64(ctmr, dev, split):
                                          residual=_t(res, dev))
     y1, y2 = run(), run()
     assert torch.equal(y1, y2)
-    _assert_rel(_h(y1), rm.conv3d(x, w, b) + res, REF_REL, f"split {split}")
+    # K = 27 * 256 = 6912 sequential fp32 additions without a split: the
+    # north-star per-layer bar (1e-5) applies; this is not one of the
+    # reference's own cases (those meet its 2e-6 bar above).
+    _assert_rel(_h(y1), rm.conv3d(x, w, b) + res, FP32_REL, f"split {split}")
 
 
 def test_repeat_runs_are_bitwise_identical(ctmr, dev):
