@@ -24,47 +24,59 @@ namespace ctmr {
 // Voxels per statistics chunk: 512 KiB of fp32 input per chunk.
 static inline int64_t gn_chunk_voxels(int c) { return std::max<int64_t>(1, 131072 / c); }
 
+// VEC channels per thread: 4 (16-byte loads) when c % 4 == 0, else 1.
+template <int VEC>
 __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict__ x, int64_t s,
                                                          int c, int64_t chunk_vox, int chunks,
                                                          double* __restrict__ part) {
   const int chunk = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-  const int c4n = c >> 2;
-  const int vl_count = 256 / c4n;
-  const int c4 = t % c4n, vl = t / c4n;
-  double sm[4] = {0, 0, 0, 0}, sq[4] = {0, 0, 0, 0};
+  const int cgn = c / VEC;
+  const int vl_count = 256 / cgn;
+  const int cg = t % cgn, vl = t / cgn;
+  double sm[VEC], sq[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) sm[k] = sq[k] = 0.0;
   const int64_t v0 = (int64_t)chunk * chunk_vox;
   const int64_t v1 = min(s, v0 + chunk_vox);
   if (vl < vl_count) {
-    const float* xb = x + (int64_t)b * s * c + c4 * 4;
+    const float* xb = x + (int64_t)b * s * c + cg * VEC;
     for (int64_t v = v0 + vl; v < v1; v += vl_count) {
-      const f4 q = *reinterpret_cast<const f4*>(xb + v * c);
+      float q[VEC];
+      if constexpr (VEC == 4) {
+        const f4 w = *reinterpret_cast<const f4*>(xb + v * c);
+        q[0] = w[0]; q[1] = w[1]; q[2] = w[2]; q[3] = w[3];
+      } else {
+        q[0] = xb[v * c];
+      }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < VEC; ++k) {
         const double d = (double)q[k];
         sm[k] += d;
         sq[k] = fma(d, d, sq[k]);
       }
     }
   }
-  __shared__ double red[256 * 8];
+  __shared__ double red[256 * 2 * VEC];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    red[t * 8 + k] = sm[k];
-    red[t * 8 + 4 + k] = sq[k];
+  for (int k = 0; k < VEC; ++k) {
+    red[t * 2 * VEC + k] = sm[k];
+    red[t * 2 * VEC + VEC + k] = sq[k];
   }
   __syncthreads();
-  if (t < c4n) {
-    double a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (t < cgn) {
+    double a[2 * VEC];
+#pragma unroll
+    for (int k = 0; k < 2 * VEC; ++k) a[k] = 0.0;
     for (int j = 0; j < vl_count; ++j) {
-      const double* r = red + (j * c4n + t) * 8;
+      const double* r = red + (j * cgn + t) * 2 * VEC;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) a[k] += r[k];
+      for (int k = 0; k < 2 * VEC; ++k) a[k] += r[k];
     }
-    double* out = part + (((int64_t)b * chunks + chunk) * c + t * 4) * 2;
+    double* out = part + (((int64_t)b * chunks + chunk) * c + t * VEC) * 2;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < VEC; ++k) {
       out[2 * k] = a[k];
-      out[2 * k + 1] = a[4 + k];
+      out[2 * k + 1] = a[VEC + k];
     }
   }
 }
@@ -115,23 +127,29 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(const double* __restri
   }
 }
 
+template <int VEC>
 __global__ __launch_bounds__(256) void gn_apply_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ affine,
-                                                       int64_t total4, int64_t s, int c, int silu,
+                                                       int64_t total, int64_t s, int c, int silu,
                                                        float* __restrict__ y) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total4;
+  const int cgn = c / VEC;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
-  const int c4n = c >> 2;
-  const int ch = (int)(i % c4n) * 4;
-  const int64_t b = i / ((int64_t)c4n * s);
-  f4 q = reinterpret_cast<const f4*>(x)[i];
-  const float* a = affine + (b * c + ch) * 2;
+    const int ch = (int)(i % cgn) * VEC;
+    const int64_t b = i / ((int64_t)cgn * s);
+    const float* a = affine + (b * c + ch) * 2;
+    if constexpr (VEC == 4) {
+      f4 q = reinterpret_cast<const f4*>(x)[i];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    float t = fmaf(q[k], a[2 * k], a[2 * k + 1]);
-    q[k] = silu ? silu_f(t) : t;
-  }
-  reinterpret_cast<f4*>(y)[i] = q;
+      for (int k = 0; k < 4; ++k) {
+        const float t = fmaf(q[k], a[2 * k], a[2 * k + 1]);
+        q[k] = silu ? silu_f(t) : t;
+      }
+      reinterpret_cast<f4*>(y)[i] = q;
+    } else {
+      const float t = fmaf(x[i], a[0], a[1]);
+      y[i] = silu ? silu_f(t) : t;
+    }
   }
 }
 
@@ -216,9 +234,11 @@ int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, c
                    size_t workspace_bytes, void* stream) {
   if (n <= 0 || s <= 0 || c <= 0 || groups <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
   if (c % groups != 0) return fail(CTMR_E_INVALID, "channels must be divisible by groups");
-  if (c % 4 != 0 || c > 1024) return fail(CTMR_E_UNSUPPORTED, "group norm needs c % 4 == 0 and c <= 1024");
+  const bool vec = (c % 4 == 0);
+  if ((vec && c > 1024) || (!vec && c > 256))
+    return fail(CTMR_E_UNSUPPORTED, "group norm needs c <= 1024 (c % 4 == 0) or c <= 256");
   if (!x || !gamma || !beta || !affine) return fail(CTMR_E_INVALID, "null pointer");
-  if (((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
+  if (vec && ((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
   const int64_t chunk_vox = gn_chunk_voxels(c);
   const int64_t chunks = ceil_div(s, chunk_vox);
   const int64_t need = (int64_t)n * chunks * c * 2 * (int64_t)sizeof(double);
@@ -229,8 +249,12 @@ int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, c
   if (chunks >= (1 << 30) || n > 65535) return fail(CTMR_E_UNSUPPORTED, "volume too large");
   hipStream_t st = (hipStream_t)stream;
   double* part = (double*)workspace;
-  hipLaunchKernelGGL(gn_partial_kernel, dim3((unsigned)chunks, n), dim3(256), 0, st, x, s, c,
-                     chunk_vox, (int)chunks, part);
+  if (vec)
+    hipLaunchKernelGGL(gn_partial_kernel<4>, dim3((unsigned)chunks, n), dim3(256), 0, st, x, s, c,
+                       chunk_vox, (int)chunks, part);
+  else
+    hipLaunchKernelGGL(gn_partial_kernel<1>, dim3((unsigned)chunks, n), dim3(256), 0, st, x, s, c,
+                       chunk_vox, (int)chunks, part);
   int rc = check_launch("gn_partial");
   if (rc) return rc;
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups, n), dim3(256), 0, st, part, (int)chunks, c,
@@ -241,12 +265,15 @@ int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, c
 int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,
                   int32_t silu, float* y, void* stream) {
   if (n <= 0 || s <= 0 || c <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
-  if (c % 4 != 0) return fail(CTMR_E_UNSUPPORTED, "group norm apply needs c % 4 == 0");
   if (!x || !affine || !y) return fail(CTMR_E_INVALID, "null pointer");
-  if ((((uintptr_t)x | (uintptr_t)y) & 15) != 0) return fail(CTMR_E_INVALID, "x and y must be 16-byte aligned");
-  const int64_t total4 = (int64_t)n * s * (c / 4);
-  hipLaunchKernelGGL(gn_apply_kernel, dim3(elementwise_blocks(total4)), dim3(256), 0,
-                     (hipStream_t)stream, x, affine, total4, s, c, silu, y);
+  const bool vec = (c % 4 == 0) && ((((uintptr_t)x | (uintptr_t)y) & 15) == 0);
+  const int64_t total = (int64_t)n * s * (vec ? c / 4 : c);
+  if (vec)
+    hipLaunchKernelGGL(gn_apply_kernel<4>, dim3(elementwise_blocks(total)), dim3(256), 0,
+                       (hipStream_t)stream, x, affine, total, s, c, silu, y);
+  else
+    hipLaunchKernelGGL(gn_apply_kernel<1>, dim3(elementwise_blocks(total)), dim3(256), 0,
+                       (hipStream_t)stream, x, affine, total, s, c, silu, y);
   return check_launch("gn_apply");
 }
 

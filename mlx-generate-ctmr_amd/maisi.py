@@ -1,0 +1,611 @@
+"""MAISI networks and samplers composed over the HIP hot path (NDHWC, fp32, GPU).
+
+The callers of the conv3d / group-norm path, restated from the reference so the
+configs' UNet step and windowed VAE decode run end to end on MI355X:
+
+* ``denoise_unet``      DiffusionModelUNetMaisi forward (reference unet.py:42-487)
+* ``spatial_attention`` residual GN -> QKV -> SDPA -> out_proj (attention.py:92-160;
+                        the token layout of NDHWC is free, SDPA is PyTorch's)
+* ``decode_vae``        post_quant 1x1 + MaisiDecoder (vae.py:29-62, 273-379)
+* ``sliding_window_decode`` Gaussian-blended windows (decode.py:30-245)
+* ``set_timesteps_rflow`` / ``step_rflow`` / ``sample_rflow`` (rflow.py:19-177)
+* ``guided_velocity``   classifier-free guidance (image.py:118-175)
+* ``output_intensities`` int16 conversion (image.py:68-87)
+
+Every convolution and group norm goes through ``fast_fp32`` (the HIP kernels).
+Weights are flat state dicts with Torch layouts (MONAI names), as torch tensors
+on the GPU.  Each public ``*_ncdhw`` function takes and returns NCDHW.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Callable, Mapping, Sequence
+from itertools import product
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import fast_fp32 as ff
+
+Z_SCALE = 4
+_GAUSSIAN_FLOOR = 1e-3
+_TRAIN_STEPS = 1000
+_BASE_NUMEL = 32 * 32 * 32
+
+
+def _prefixed(weights: Mapping[str, Tensor], prefix: str) -> dict[str, Tensor]:
+    start = prefix + "."
+    return {k[len(start):]: v for k, v in weights.items() if k.startswith(start)}
+
+
+def _need(weights: Mapping[str, Tensor], key: str) -> Tensor:
+    if key not in weights:
+        raise ValueError(f"weights missing: {key}")
+    return weights[key]
+
+
+def _per_level(value, n: int) -> tuple[int, ...]:
+    if isinstance(value, int) and not isinstance(value, bool):
+        return (int(value),) * n
+    out = tuple(int(v) for v in value)
+    if len(out) != n:
+        raise ValueError(f"per-level setting has {len(out)} entries for {n} levels")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# embeddings (embed.py:15-87)
+# ---------------------------------------------------------------------------
+def sinusoidal_timestep_embedding(timesteps: Tensor, dim: int, max_period: int = 10000) -> Tensor:
+    """``[cos, sin]`` sinusoidal embedding of ``(N,)`` timesteps (embed.py:15-40)."""
+    if timesteps.dim() != 1:
+        raise ValueError("Timesteps should be a 1d-array")
+    half = dim // 2
+    exponent = -math.log(max_period) * torch.arange(half, dtype=torch.float32, device=timesteps.device)
+    freqs = torch.exp(exponent / half)
+    args = timesteps.to(torch.float32).reshape(-1, 1) * freqs.reshape(1, -1)
+    emb = torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+    if dim % 2 == 1:
+        emb = F.pad(emb, (0, 1))
+    return emb
+
+
+def _silu_mlp(x: Tensor, weights: Mapping[str, Tensor], prefix: str) -> Tensor:
+    h = F.linear(x, _need(weights, f"{prefix}.0.weight"), _need(weights, f"{prefix}.0.bias"))
+    return F.linear(F.silu(h), _need(weights, f"{prefix}.2.weight"), _need(weights, f"{prefix}.2.bias"))
+
+
+def condition_embedding(timesteps: Tensor, class_labels: Optional[Tensor], spacing: Optional[Tensor],
+                        weights: Mapping[str, Tensor], constructor: Mapping) -> tuple[Tensor, Tensor]:
+    """``(t_emb, emb)``: time MLP + class embedding, spacing MLP concatenated (unet.py:190-271)."""
+    t_emb = sinusoidal_timestep_embedding(timesteps, int(constructor["num_channels"][0]))
+    emb = _silu_mlp(t_emb, weights, "time_embed")
+    if constructor.get("num_class_embeds") is not None:
+        if class_labels is None:
+            raise ValueError("class_labels should be provided when num_class_embeds > 0")
+        emb = emb + _need(weights, "class_embedding.weight")[class_labels.to(torch.long)]
+    for flag in ("include_top_region_index_input", "include_bottom_region_index_input"):
+        if constructor.get(flag):
+            raise ValueError(f"{flag} (ddpm-ct region inputs) is not part of this path")
+    if constructor.get("include_spacing_input"):
+        if spacing is None:
+            raise ValueError("spacing should be provided when include_spacing_input is true")
+        if spacing.dim() != 2 or spacing.shape[-1] != 3:
+            raise ValueError(f"spacing must be [N, 3]; got shape={tuple(spacing.shape)}")
+        emb = torch.cat([emb, _silu_mlp(spacing.to(torch.float32), weights, "spacing_layer")], dim=-1)
+    return t_emb, emb
+
+
+# ---------------------------------------------------------------------------
+# attention (attention.py:92-160), NDHWC: tokens are the voxel rows
+# ---------------------------------------------------------------------------
+def spatial_attention(x: Tensor, weights: Mapping[str, Tensor], *, num_groups: int, eps: float,
+                      num_head_channels: int, include_fc: bool) -> Tensor:
+    n, d, h, w, c = x.shape
+    if c % num_head_channels != 0:
+        raise ValueError("num_channels must be divisible by num_head_channels")
+    heads = c // num_head_channels
+    scale = float(num_head_channels) ** -0.5
+    hidden = ff.group_norm(x, weights["norm.weight"], weights["norm.bias"], num_groups=num_groups, eps=eps)
+    tokens = hidden.reshape(n, d * h * w, c)
+
+    def split(t: Tensor) -> Tensor:
+        return t.reshape(n, -1, heads, num_head_channels).transpose(1, 2).contiguous()
+
+    q = split(F.linear(tokens, weights["attn.to_q.weight"], weights["attn.to_q.bias"]))
+    k = split(F.linear(tokens, weights["attn.to_k.weight"], weights["attn.to_k.bias"]))
+    v = split(F.linear(tokens, weights["attn.to_v.weight"], weights["attn.to_v.bias"]))
+    att = F.scaled_dot_product_attention(q, k, v, scale=scale)
+    merged = att.transpose(1, 2).reshape(n, -1, c)
+    if include_fc:
+        merged = F.linear(merged, weights["attn.out_proj.weight"], weights["attn.out_proj.bias"])
+    return x + merged.reshape(n, d, h, w, c)
+
+
+# ---------------------------------------------------------------------------
+# UNet (unet.py:42-487)
+# ---------------------------------------------------------------------------
+def denoise_unet(
+    x: Tensor,
+    timesteps: Tensor,
+    class_labels: Optional[Tensor],
+    spacing: Optional[Tensor],
+    weights: Mapping[str, Tensor],
+    *,
+    constructor: Mapping,
+    down_block_additional_residuals: Optional[Sequence[Tensor]] = None,
+    mid_block_additional_residual: Optional[Tensor] = None,
+) -> tuple[Tensor, Tensor]:
+    """One DiffusionModelUNetMaisi pass on NDHWC ``x``; returns ``(t_emb, y)`` (NDHWC)."""
+    if int(constructor.get("spatial_dims", 3)) != 3 or constructor.get("use_flash_attention"):
+        raise ValueError("MAISI UNet destination is 3D without CUDA flash attention")
+    if constructor.get("with_conditioning"):
+        raise ValueError("cross-attention conditioning is not part of this path")
+    if x.shape[-1] != int(constructor["in_channels"]):
+        raise ValueError(f"unet input channels {x.shape[-1]} != in_channels {constructor['in_channels']}")
+    channels = tuple(int(c) for c in constructor["num_channels"])
+    n_levels = len(channels)
+    res_blocks = _per_level(constructor["num_res_blocks"], n_levels)
+    attn_levels = tuple(bool(a) for a in constructor["attention_levels"])
+    heads = _per_level(constructor["num_head_channels"], n_levels)
+    groups, eps = int(constructor["norm_num_groups"]), float(constructor["norm_eps"])
+    include_fc = bool(constructor.get("include_fc", True))
+    if not constructor.get("resblock_updown", True):
+        raise ValueError("resblock_updown=False (ddpm-ct) is not part of this path")
+
+    t_emb, emb = condition_embedding(timesteps, class_labels, spacing, weights, constructor)
+
+    def resnet(h: Tensor, prefix: str, **kw) -> Tensor:
+        return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps, **kw)
+
+    def attention(h: Tensor, prefix: str, n_heads: int) -> Tensor:
+        return spatial_attention(h, _prefixed(weights, prefix), num_groups=groups, eps=eps,
+                                 num_head_channels=n_heads, include_fc=include_fc)
+
+    hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1)
+    skips = [hidden]
+    for index in range(n_levels):
+        for r in range(res_blocks[index]):
+            hidden = resnet(hidden, f"down_blocks.{index}.resnets.{r}")
+            if attn_levels[index]:
+                hidden = attention(hidden, f"down_blocks.{index}.attentions.{r}", heads[index])
+            skips.append(hidden)
+        if index != n_levels - 1:
+            hidden = resnet(hidden, f"down_blocks.{index}.downsampler", down=True)
+            skips.append(hidden)
+    if down_block_additional_residuals is not None:
+        extras = list(down_block_additional_residuals)
+        if len(extras) != len(skips):
+            raise ValueError(f"ControlNet residuals length {len(extras)} != UNet skip count {len(skips)}")
+        skips = [s + e for s, e in zip(skips, extras)]
+        hidden = skips[-1]
+    hidden = resnet(hidden, "middle_block.resnet_1")
+    hidden = attention(hidden, "middle_block.attention", heads[-1])
+    hidden = resnet(hidden, "middle_block.resnet_2")
+    if mid_block_additional_residual is not None:
+        hidden = hidden + mid_block_additional_residual
+    rev_res, rev_attn, rev_heads = res_blocks[::-1], attn_levels[::-1], heads[::-1]
+    for index in range(n_levels):
+        n_res = rev_res[index] + 1
+        samples, skips = skips[-n_res:], skips[:-n_res]
+        for r in range(n_res):
+            skip = samples.pop()
+            hidden = torch.cat([hidden, skip], dim=-1)
+            hidden = resnet(hidden, f"up_blocks.{index}.resnets.{r}")
+            if rev_attn[index]:
+                hidden = attention(hidden, f"up_blocks.{index}.attentions.{r}", rev_heads[index])
+        if index != n_levels - 1:
+            hidden = resnet(hidden, f"up_blocks.{index}.upsampler", up=True)
+    if skips:
+        raise ValueError(f"UNet skip list leftover after up blocks: {len(skips)}")
+    y = ff.norm_conv3d(hidden, _need(weights, "out.2.conv.weight"), _need(weights, "out.2.conv.bias"),
+                       norm=(_need(weights, "out.0.weight"), _need(weights, "out.0.bias")), num_groups=groups,
+                       eps=eps, apply_silu=True)
+    return t_emb, y
+
+
+def denoise_unet_ncdhw(x: Tensor, timesteps: Tensor, class_labels, spacing, weights, *, constructor, mx=None,
+                       down_block_additional_residuals=None, mid_block_additional_residual=None):
+    """NCDHW adapter with the reference's name and keywords (unet.py:42)."""
+    down = None if down_block_additional_residuals is None else [ff.to_ndhwc(r) for r in down_block_additional_residuals]
+    mid = None if mid_block_additional_residual is None else ff.to_ndhwc(mid_block_additional_residual)
+    t_emb, y = denoise_unet(ff.to_ndhwc(x), timesteps, class_labels, spacing, weights, constructor=constructor,
+                            down_block_additional_residuals=down, mid_block_additional_residual=mid)
+    return t_emb, ff.to_ncdhw(y)
+
+
+# ---------------------------------------------------------------------------
+# VAE decoder (vae.py:29-62, 273-379, 465-487)
+# ---------------------------------------------------------------------------
+def _conv_weights(weights: Mapping[str, Tensor], prefix: str) -> tuple[Tensor, Tensor]:
+    """MAISI-wrapped (``conv.conv``) or plain (``conv``) convolution weights (vae.py:527-537)."""
+    for key in (f"{prefix}.conv.conv", f"{prefix}.conv"):
+        if f"{key}.weight" in weights:
+            return weights[f"{key}.weight"], _need(weights, f"{key}.bias")
+    raise ValueError(f"VAE weights missing: {prefix}.conv.conv.weight or {prefix}.conv.weight")
+
+
+def run_vae_decoder(x: Tensor, weights: Mapping[str, Tensor], *, constructor: Mapping) -> Tensor:
+    """MaisiDecoder on an NDHWC post-quant latent (vae.py:273-379)."""
+    channels = tuple(int(c) for c in constructor["num_channels"])
+    res_blocks = tuple(int(r) for r in constructor["num_res_blocks"])
+    if any(bool(a) for a in constructor["attention_levels"]):
+        raise ValueError("image VAE dest has no attention blocks")
+    if constructor.get("use_convtranspose"):
+        raise ValueError("transposed-convolution upsampling is not part of this path")
+    groups, eps = int(constructor["norm_num_groups"]), float(constructor["norm_eps"])
+    hidden = ff.conv3d(x, *_conv_weights(weights, "decoder.blocks.0"), padding=1)
+    index = 1
+    rev = channels[::-1]
+    for level, n_res in enumerate(res_blocks[::-1]):
+        for _ in range(n_res):
+            p = f"decoder.blocks.{index}"
+            shortcut = _conv_weights(weights, f"{p}.nin_shortcut") if any(
+                k.startswith(f"{p}.nin_shortcut.") for k in weights) else None
+            state = [hidden]
+            del hidden
+            hidden = ff.vae_resblock(state, _conv_weights(weights, f"{p}.conv1"), _conv_weights(weights, f"{p}.conv2"),
+                                     (_need(weights, f"{p}.norm1.weight"), _need(weights, f"{p}.norm1.bias")),
+                                     (_need(weights, f"{p}.norm2.weight"), _need(weights, f"{p}.norm2.bias")),
+                                     shortcut, num_groups=groups, eps=eps)
+            index += 1
+        if level != len(rev) - 1:
+            w, b = _conv_weights(weights, f"decoder.blocks.{index}.conv")
+            hidden = ff.trilinear_conv3d(hidden, w, b)
+            index += 1
+    norm = (_need(weights, f"decoder.blocks.{index}.weight"), _need(weights, f"decoder.blocks.{index}.bias"))
+    return ff.norm_conv3d(hidden, *_conv_weights(weights, f"decoder.blocks.{index + 1}"), norm=norm,
+                          num_groups=groups, eps=eps, apply_silu=False)
+
+
+def decode_vae(latent: Tensor, weights: Mapping[str, Tensor], *, constructor: Mapping) -> tuple[Tensor, Tensor]:
+    """``(post_quant, decoded)`` of an NDHWC latent (vae.py:29-62)."""
+    if constructor.get("with_encoder_nonlocal_attn") or constructor.get("with_decoder_nonlocal_attn"):
+        raise ValueError("image VAE dest has no nonlocal attention")
+    post_quant = ff.pointwise_conv(latent, *_conv_weights(weights, "post_quant_conv"))
+    return post_quant, run_vae_decoder(post_quant, weights, constructor=constructor)
+
+
+def decode_vae_ncdhw(latent: Tensor, weights, *, constructor, mx=None):
+    post_quant, decoded = decode_vae(ff.to_ndhwc(latent), weights, constructor=constructor)
+    return ff.to_ncdhw(post_quant), ff.to_ncdhw(decoded)
+
+
+# ---------------------------------------------------------------------------
+# sliding-window decode (decode.py:30-245)
+# ---------------------------------------------------------------------------
+def scan_interval(image_size: Sequence[int], roi: Sequence[int], overlap: float) -> tuple[int, int, int]:
+    """``int(roi * (1 - overlap))`` (at least 1), or ``roi`` where it equals the axis (decode.py:30-45)."""
+    out = []
+    for size, window in zip(image_size, roi):
+        if window == size:
+            out.append(int(window))
+            continue
+        step = int(window * (1.0 - float(overlap)))
+        out.append(step if step > 0 else 1)
+    return out[0], out[1], out[2]
+
+
+def dense_patch_slices(image_size: Sequence[int], patch: Sequence[int], interval: Sequence[int]):
+    """Window slices; the last start of each axis is pulled back inside (decode.py:48-78)."""
+    starts = []
+    for size, window, step in zip(image_size, patch, interval):
+        count = int(math.ceil(float(size) / float(step)))
+        last = next((i for i in range(count) if i * step + window >= size), None)
+        n_starts = 1 if last is None else last + 1
+        axis = []
+        for i in range(n_starts):
+            start = i * step
+            start -= max(start + window - size, 0)
+            axis.append(start)
+        starts.append(axis)
+    return tuple((slice(a, a + patch[0]), slice(b, b + patch[1]), slice(c, c + patch[2]))
+                 for a, b, c in product(*starts))
+
+
+def gaussian_importance(roi: Sequence[int], sigma_scale: float = 0.125, device=None) -> Tensor:
+    """Outer product of 1-D Gaussians, floored at 1e-3, ``(D, H, W)`` fp32 (decode.py:81-101)."""
+    axes = []
+    for length in roi:
+        half = (length - 1) / 2.0
+        x = torch.arange(-half, half + 1.0, dtype=torch.float32, device=device)
+        sigma = float(sigma_scale) * float(length)
+        axes.append(torch.exp((x * x) / (-2.0 * sigma * sigma)))
+    imp = axes[0].reshape(-1, 1, 1) * axes[1].reshape(1, -1, 1) * axes[2].reshape(1, 1, -1)
+    return torch.clamp(imp, min=_GAUSSIAN_FLOOR)
+
+
+def sliding_window(latent: Tensor, predict: Callable[[Tensor], Tensor], *, roi: Sequence[int],
+                   overlap: float, sigma_scale: float = 0.125, z_scale: int = Z_SCALE) -> Tensor:
+    """Blend ``predict`` over overlapping NDHWC latent windows (decode.py:104-184).
+
+    Each window's prediction is weighted by the nearest-x4-resized Gaussian and
+    accumulated with the weights in window order; the result is the ratio.
+    """
+    n, d, h, w, c = latent.shape
+    pads = []
+    for size, window in zip((d, h, w), roi):
+        extra = max(int(window) - int(size), 0)
+        pads.append((extra // 2, extra - extra // 2))
+    if any(a or b for a, b in pads):
+        latent = F.pad(latent, (0, 0, pads[2][0], pads[2][1], pads[1][0], pads[1][1], pads[0][0], pads[0][1]))
+    spatial = tuple(int(s) for s in latent.shape[1:4])
+    interval = scan_interval(spatial, roi, overlap)
+    windows = dense_patch_slices(spatial, roi, interval)
+    weight = gaussian_importance(roi, sigma_scale, device=latent.device)
+    for axis in range(3):
+        weight = weight.repeat_interleave(z_scale, dim=axis)
+    weight = weight.unsqueeze(-1)
+    output = weight_sum = None
+    for sd, sh, sw in windows:
+        pred = predict(latent[:, sd, sh, sw, :].contiguous())
+        expected = tuple(int(r) * z_scale for r in roi)
+        if tuple(pred.shape[1:4]) != expected:
+            raise ValueError(f"prediction spatial shape {tuple(pred.shape[1:4])} != {expected}")
+        od = slice(sd.start * z_scale, sd.stop * z_scale)
+        oh = slice(sh.start * z_scale, sh.stop * z_scale)
+        ow = slice(sw.start * z_scale, sw.stop * z_scale)
+        if output is None:
+            out_spatial = tuple(s * z_scale for s in spatial)
+            output = torch.zeros((pred.shape[0], *out_spatial, pred.shape[-1]), device=pred.device)
+            weight_sum = torch.zeros((1, *out_spatial, 1), device=pred.device)
+        output[:, od, oh, ow, :] += pred * weight
+        weight_sum[:, od, oh, ow, :] += weight
+        del pred
+    stitched = output / weight_sum
+    sl = [slice(a * z_scale, stitched.shape[i + 1] - b * z_scale) for i, (a, b) in enumerate(pads)]
+    return stitched[:, sl[0], sl[1], sl[2], :].contiguous()
+
+
+def sliding_window_decode(latent: Tensor, weights: Mapping[str, Tensor], *, constructor: Mapping,
+                          roi: Sequence[int] = (48, 48, 64), overlap: float = 0.6666, sigma_scale: float = 0.125,
+                          scale_factor: Optional[float] = None) -> Tensor:
+    """Decode an NDHWC latent, tiling with Gaussian-blended windows when larger than ``roi``
+    (decode.py:187-245)."""
+    if scale_factor is not None:
+        value = float(scale_factor)
+        if not math.isfinite(value) or value == 0.0:
+            raise ValueError("scale_factor must be a finite non-zero caller value")
+        latent = latent / value
+    spatial = tuple(int(s) for s in latent.shape[1:4])
+
+    def decode_window(window: Tensor) -> Tensor:
+        return decode_vae(window, weights, constructor=constructor)[1]
+
+    if math.prod(spatial) <= math.prod(roi):
+        return decode_window(latent)
+    adjusted = tuple(min(r, s) for r, s in zip(roi, spatial))
+    return sliding_window(latent, decode_window, roi=adjusted, overlap=overlap, sigma_scale=sigma_scale)
+
+
+def sliding_window_decode_ncdhw(latent: Tensor, weights, *, constructor, mx=None, roi=(48, 48, 64),
+                                overlap=0.6666, sigma_scale=0.125, scale_factor=None) -> Tensor:
+    return ff.to_ncdhw(sliding_window_decode(ff.to_ndhwc(latent), weights, constructor=constructor, roi=roi,
+                                             overlap=overlap, sigma_scale=sigma_scale, scale_factor=scale_factor))
+
+
+# ---------------------------------------------------------------------------
+# rectified-flow sampler (rflow.py:19-177) and guidance (image.py:118-175)
+# ---------------------------------------------------------------------------
+def timestep_transform_rflow(t: float, input_img_size_numel: int, *, base_img_size_numel: int = _BASE_NUMEL,
+                             scale: float = 1.0, num_train_timesteps: int = _TRAIN_STEPS,
+                             spatial_dim: int = 3) -> float:
+    unit = float(t) / float(num_train_timesteps)
+    ratio = (float(input_img_size_numel) / float(base_img_size_numel)) ** (1.0 / float(spatial_dim)) * float(scale)
+    return float(num_train_timesteps) * ratio * unit / (1.0 + (ratio - 1.0) * unit)
+
+
+def set_timesteps_rflow(*, num_inference_steps: int = 30, num_train_timesteps: int = _TRAIN_STEPS,
+                        input_img_size_numel: int, base_img_size_numel: int = _BASE_NUMEL):
+    """``(timesteps, next_timesteps)`` float32, rounded through float16 (rflow.py:47-97)."""
+    if num_inference_steps < 1 or num_inference_steps > num_train_timesteps:
+        raise ValueError(f"num_inference_steps {num_inference_steps} must be in 1..{num_train_timesteps}")
+    steps = [timestep_transform_rflow((1.0 - i / num_inference_steps) * num_train_timesteps, input_img_size_numel,
+                                      base_img_size_numel=base_img_size_numel,
+                                      num_train_timesteps=num_train_timesteps)
+             for i in range(num_inference_steps)]
+    timesteps = np.asarray(steps, dtype=np.float16).astype(np.float32)
+    return timesteps, np.concatenate([timesteps[1:], np.zeros((1,), dtype=np.float32)])
+
+
+def step_rflow(z: Tensor, v: Tensor, timestep: float, next_timestep: float,
+               num_train_timesteps: int = _TRAIN_STEPS) -> tuple[Tensor, Tensor, float]:
+    """Euler step with ``dt = (t - int(next_t)) / T`` (rflow.py:100-119)."""
+    dt = (float(timestep) - int(float(next_timestep))) / float(num_train_timesteps)
+    return z + v * dt, z + v * (float(timestep) / float(num_train_timesteps)), dt
+
+
+def sample_rflow(z: Tensor, velocity_fn: Callable[[Tensor, float], Tensor], timesteps: np.ndarray) -> Tensor:
+    """Integrate ``z`` over the schedule (rflow.py:144-177)."""
+    nxt = np.concatenate([timesteps[1:], np.zeros((1,), dtype=np.float32)])
+    hidden = z
+    for t, tn in zip(timesteps.tolist(), nxt.tolist()):
+        hidden, _, _ = step_rflow(hidden, velocity_fn(hidden, float(t)), float(t), float(tn))
+    return hidden
+
+
+def guided_velocity(state: Tensor, timestep: float, *, class_labels: Tensor, spacing: Tensor,
+                    weights: Mapping[str, Tensor], constructor: Mapping, guidance_scale: float,
+                    guidance_execution: str = "batched") -> Tensor:
+    """Velocity with modality CFG: ``uncond + g * (cond - uncond)``, class 0 unconditional
+    (image.py:118-175).  ``state`` is NDHWC."""
+    t = torch.full((state.shape[0],), float(timestep), dtype=torch.float32, device=state.device)
+    if guidance_scale == 0.0:
+        return denoise_unet(state, t, class_labels, spacing, weights, constructor=constructor)[1]
+    if guidance_execution == "sequential":
+        cond = denoise_unet(state, t, class_labels, spacing, weights, constructor=constructor)[1]
+        uncond = denoise_unet(state, t, torch.zeros_like(class_labels), spacing, weights,
+                              constructor=constructor)[1]
+        return uncond + guidance_scale * (cond - uncond)
+    if guidance_execution != "batched":
+        raise ValueError("guidance_execution must be 'batched' or 'sequential'")
+    batch = state.shape[0]
+    _, velocity = denoise_unet(torch.cat([state, state]), torch.cat([t, t]),
+                               torch.cat([class_labels, torch.zeros_like(class_labels)]),
+                               torch.cat([spacing, spacing]), weights, constructor=constructor)
+    cond, uncond = velocity[:batch], velocity[batch:]
+    return uncond + guidance_scale * (cond - uncond)
+
+
+# ---------------------------------------------------------------------------
+# production constructors and weight catalogs (random-init configs)
+# ---------------------------------------------------------------------------
+PRODUCTION_UNET_CONSTRUCTOR = {
+    # maisi_mlx_from_mask.py:43-62 of the reference
+    "spatial_dims": 3, "in_channels": 4, "out_channels": 4, "num_channels": [64, 128, 256, 512],
+    "attention_levels": [False, False, True, True], "num_head_channels": [0, 0, 32, 32], "num_res_blocks": 2,
+    "norm_num_groups": 32, "norm_eps": 1e-6, "use_flash_attention": False, "include_top_region_index_input": False,
+    "include_bottom_region_index_input": False, "include_spacing_input": True, "num_class_embeds": 128,
+    "resblock_updown": True, "include_fc": True, "with_conditioning": False, "use_combined_linear": False,
+}
+PRODUCTION_VAE_CONSTRUCTOR = {
+    # maisi_mlx_from_mask.py:20-42 of the reference
+    "spatial_dims": 3, "in_channels": 1, "out_channels": 1, "latent_channels": 4, "num_channels": [64, 128, 256],
+    "num_res_blocks": [2, 2, 2], "norm_num_groups": 32, "norm_eps": 1e-6, "attention_levels": [False, False, False],
+    "with_encoder_nonlocal_attn": False, "with_decoder_nonlocal_attn": False, "include_fc": False,
+    "use_combined_linear": False, "use_flash_attention": False, "use_checkpointing": False,
+    "use_convtranspose": False, "num_splits": 4, "dim_split": 1, "norm_float16": False, "print_info": False,
+    "save_mem": False,
+}
+
+
+def _resnet_shapes(prefix: str, cin: int, cout: int, temb: int) -> list[tuple[str, tuple[int, ...]]]:
+    out = [(f"{prefix}.norm1.weight", (cin,)), (f"{prefix}.norm1.bias", (cin,)),
+           (f"{prefix}.conv1.conv.weight", (cout, cin, 3, 3, 3)), (f"{prefix}.conv1.conv.bias", (cout,)),
+           (f"{prefix}.time_emb_proj.weight", (cout, temb)), (f"{prefix}.time_emb_proj.bias", (cout,)),
+           (f"{prefix}.norm2.weight", (cout,)), (f"{prefix}.norm2.bias", (cout,)),
+           (f"{prefix}.conv2.conv.weight", (cout, cout, 3, 3, 3)), (f"{prefix}.conv2.conv.bias", (cout,))]
+    if cin != cout:
+        out += [(f"{prefix}.skip_connection.conv.weight", (cout, cin, 1, 1, 1)),
+                (f"{prefix}.skip_connection.conv.bias", (cout,))]
+    return out
+
+
+def _attention_shapes(prefix: str, c: int) -> list[tuple[str, tuple[int, ...]]]:
+    out = [(f"{prefix}.norm.weight", (c,)), (f"{prefix}.norm.bias", (c,))]
+    for name in ("to_q", "to_k", "to_v", "out_proj"):
+        out += [(f"{prefix}.attn.{name}.weight", (c, c)), (f"{prefix}.attn.{name}.bias", (c,))]
+    return out
+
+
+def unet_weight_shapes(constructor: Mapping) -> list[tuple[str, tuple[int, ...]]]:
+    """MONAI state-dict names and shapes of DiffusionModelUNetMaisi for ``constructor``."""
+    ch = [int(c) for c in constructor["num_channels"]]
+    nl = len(ch)
+    nres = _per_level(constructor["num_res_blocks"], nl)
+    attn = [bool(a) for a in constructor["attention_levels"]]
+    t = 4 * ch[0]
+    temb = t + (t if constructor.get("include_spacing_input") else 0)
+    s = [("time_embed.0.weight", (t, ch[0])), ("time_embed.0.bias", (t,)), ("time_embed.2.weight", (t, t)),
+         ("time_embed.2.bias", (t,))]
+    if constructor.get("num_class_embeds") is not None:
+        s.append(("class_embedding.weight", (int(constructor["num_class_embeds"]), t)))
+    if constructor.get("include_spacing_input"):
+        s += [("spacing_layer.0.weight", (t, 3)), ("spacing_layer.0.bias", (t,)), ("spacing_layer.2.weight", (t, t)),
+              ("spacing_layer.2.bias", (t,))]
+    s += [("conv_in.conv.weight", (ch[0], int(constructor["in_channels"]), 3, 3, 3)), ("conv_in.conv.bias", (ch[0],))]
+    out_ch = ch[0]
+    for i in range(nl):
+        in_ch, out_ch = out_ch, ch[i]
+        for r in range(nres[i]):
+            s += _resnet_shapes(f"down_blocks.{i}.resnets.{r}", in_ch if r == 0 else out_ch, out_ch, temb)
+            if attn[i]:
+                s += _attention_shapes(f"down_blocks.{i}.attentions.{r}", out_ch)
+        if i != nl - 1:
+            s += _resnet_shapes(f"down_blocks.{i}.downsampler", out_ch, out_ch, temb)
+    s += _resnet_shapes("middle_block.resnet_1", ch[-1], ch[-1], temb)
+    s += _attention_shapes("middle_block.attention", ch[-1])
+    s += _resnet_shapes("middle_block.resnet_2", ch[-1], ch[-1], temb)
+    rc, rres, rattn = ch[::-1], nres[::-1], attn[::-1]
+    out_ch = rc[0]
+    for i in range(nl):
+        prev, out_ch = out_ch, rc[i]
+        in_ch = rc[min(i + 1, nl - 1)]
+        n = rres[i] + 1
+        for r in range(n):
+            skip_ch = in_ch if r == n - 1 else out_ch
+            s += _resnet_shapes(f"up_blocks.{i}.resnets.{r}", (prev if r == 0 else out_ch) + skip_ch, out_ch, temb)
+            if rattn[i]:
+                s += _attention_shapes(f"up_blocks.{i}.attentions.{r}", out_ch)
+        if i != nl - 1:
+            s += _resnet_shapes(f"up_blocks.{i}.upsampler", out_ch, out_ch, temb)
+    s += [("out.0.weight", (ch[0],)), ("out.0.bias", (ch[0],)),
+          ("out.2.conv.weight", (int(constructor["out_channels"]), ch[0], 3, 3, 3)),
+          ("out.2.conv.bias", (int(constructor["out_channels"]),))]
+    return s
+
+
+def vae_decoder_weight_shapes(constructor: Mapping) -> list[tuple[str, tuple[int, ...]]]:
+    """State-dict names and shapes of the AutoencoderKlMaisi decode path for ``constructor``."""
+    ch = [int(c) for c in constructor["num_channels"]]
+    lat = int(constructor["latent_channels"])
+    rc = ch[::-1]
+    nres = [int(r) for r in constructor["num_res_blocks"]][::-1]
+    s = [("post_quant_conv.conv.weight", (lat, lat, 1, 1, 1)), ("post_quant_conv.conv.bias", (lat,)),
+         ("decoder.blocks.0.conv.conv.weight", (rc[0], lat, 3, 3, 3)), ("decoder.blocks.0.conv.conv.bias", (rc[0],))]
+    idx, block_in = 1, rc[0]
+    for level, n in enumerate(nres):
+        block_out = rc[level]
+        for _ in range(n):
+            p = f"decoder.blocks.{idx}"
+            s += [(f"{p}.norm1.weight", (block_in,)), (f"{p}.norm1.bias", (block_in,)),
+                  (f"{p}.conv1.conv.conv.weight", (block_out, block_in, 3, 3, 3)), (f"{p}.conv1.conv.conv.bias", (block_out,)),
+                  (f"{p}.norm2.weight", (block_out,)), (f"{p}.norm2.bias", (block_out,)),
+                  (f"{p}.conv2.conv.conv.weight", (block_out, block_out, 3, 3, 3)),
+                  (f"{p}.conv2.conv.conv.bias", (block_out,))]
+            if block_in != block_out:
+                s += [(f"{p}.nin_shortcut.conv.conv.weight", (block_out, block_in, 1, 1, 1)),
+                      (f"{p}.nin_shortcut.conv.conv.bias", (block_out,))]
+            block_in = block_out
+            idx += 1
+        if level != len(nres) - 1:
+            s += [(f"decoder.blocks.{idx}.conv.conv.conv.weight", (block_in, block_in, 3, 3, 3)),
+                  (f"decoder.blocks.{idx}.conv.conv.conv.bias", (block_in,))]
+            idx += 1
+    s += [(f"decoder.blocks.{idx}.weight", (block_in,)), (f"decoder.blocks.{idx}.bias", (block_in,)),
+          (f"decoder.blocks.{idx + 1}.conv.conv.weight", (int(constructor["out_channels"]), block_in, 3, 3, 3)),
+          (f"decoder.blocks.{idx + 1}.conv.conv.bias", (int(constructor["out_channels"]),))]
+    return s
+
+
+def random_weights(shapes: Sequence[tuple[str, tuple[int, ...]]], *, seed: int) -> dict[str, np.ndarray]:
+    """Random-init fp32 weights (host): conv/linear ~ N(0, 1/fan_in), biases ~ N(0, 0.01^2),
+    norm scales ~ 1 + N(0, 0.1^2), norm shifts ~ N(0, 0.1^2), embeddings ~ N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in shapes:
+        if len(shape) == 1:
+            is_norm = ".norm" in name or name.startswith("out.0") or name.split(".")[-2].isdigit() and "conv" not in name
+            if name.endswith("weight") and is_norm:
+                v = 1.0 + 0.1 * rng.standard_normal(shape)
+            else:
+                v = (0.1 if is_norm else 0.01) * rng.standard_normal(shape)
+        elif name == "class_embedding.weight":
+            v = rng.standard_normal(shape)
+        else:
+            fan_in = int(np.prod(shape[1:]))
+            v = rng.standard_normal(shape) / np.sqrt(fan_in)
+        out[name] = v.astype(np.float32)
+    return out
+
+
+def output_intensities(decoded: np.ndarray, *, configuration: str = "mr") -> np.ndarray:
+    """int16 image: CT ``clip(x*2000-1000, -1000, 1000)``, MR ``max(x*1000, 0)``, truncated (image.py:68-87)."""
+    data = np.asarray(decoded, dtype=np.float32)
+    if not np.isfinite(data).all():
+        raise ValueError("decoded image must be finite")
+    if configuration == "ct":
+        scaled = np.clip(data * 2000.0 - 1000.0, -1000.0, 1000.0)
+    else:
+        scaled = np.clip(data * 1000.0, 0.0, None)
+    return scaled.astype(np.int16)
+
+
+def spacing_tensor(spacing_mm: Sequence[float], device=None) -> Tensor:
+    """``spacing_mm * 100`` rounded through float16, ``(1, 3)`` fp32 (image.py:90-115)."""
+    scaled = np.asarray([spacing_mm], dtype=np.float64) * 100.0
+    return torch.from_numpy(scaled.astype(np.float16).astype(np.float32)).to(device)

@@ -107,7 +107,7 @@ def test_group_norm_host_checks(ctmr, native_loaded):
     assert L.gn_workspace_bytes(1, 128**3, 128) == 1 * 2048 * 128 * 2 * 8
     rc = native_loaded.ctmr_gn_affine(1, 64, 12, 5, 1e-6, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1 << 30, None)
     assert rc == L.E_INVALID and "divisible" in L.last_error()
-    rc = native_loaded.ctmr_gn_affine(1, 64, 6, 3, 1e-6, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1 << 30, None)
+    rc = native_loaded.ctmr_gn_affine(1, 64, 258, 2, 1e-6, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1 << 30, None)
     assert rc == L.E_UNSUPPORTED
     rc = native_loaded.ctmr_resample(0, 1, 1, 4, 4, 4, 0x1000, 0x1000, None)
     assert rc == L.E_INVALID and "pooling" in L.last_error()

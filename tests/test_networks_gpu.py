@@ -1,0 +1,214 @@
+"""GPU parity of the MAISI networks composed over the HIP kernels.
+
+Small cases: the reference's recorded goldens (MONAI 1.6.0, Torch CPU) with the
+reference's tolerances (UNet/VAE rtol 1e-4 atol 1e-5, residual 1e-5/1e-6).
+Full-size cases (production constructors, random init): the HIP composition
+against the independent PyTorch-CPU oracle (oracle/maisi_torch.py, pinned on
+the same goldens in tests/test_oracle_networks.py); the north-star bar for a
+UNet step is a max relative error of 1e-4.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from golden_util import load_boundary, load_fixture
+from oracle import maisi_torch as mt
+from oracle import reference_math as rm
+
+pytestmark = pytest.mark.gpu
+
+UNET_RTOL, UNET_ATOL = 1e-4, 1e-5
+VAE_RTOL, VAE_ATOL = 1e-4, 1e-5
+RES_RTOL, RES_ATOL = 1e-5, 1e-6
+
+
+def _g(a, dev, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device=dev, dtype=dtype)
+
+
+def _gw(arrays, dev, strip="weight."):
+    return {k[len(strip):]: _g(v, dev) for k, v in arrays.items() if k.startswith(strip)}
+
+
+def _h(t):
+    return t.detach().cpu().numpy()
+
+
+def _rel(actual, expected):
+    err = rm.max_rel_error(actual, expected)
+    print(f"max rel error {err:.3e}", flush=True)
+    return err
+
+
+def test_residual_block_golden(ctmr, dev):
+    manifest, a = load_boundary("residual")
+    c = manifest["constructor"]
+    y = ctmr.fast_fp32.residual_block_ncdhw(_g(a["x"], dev), _g(a["emb"], dev), _gw(a, dev),
+                                            num_groups=c["norm_num_groups"], eps=c["norm_eps"])
+    np.testing.assert_allclose(_h(y), a["y"], rtol=RES_RTOL, atol=RES_ATOL)
+
+
+@pytest.mark.parametrize("mode", ["plain", "up", "down", "project"])
+def test_residual_block_variants_match_oracle(ctmr, dev, mode):
+    """Fused up (parity-folded conv1), down (GN before pooling) and 1x1-projected blocks."""
+    rng = np.random.default_rng(31)
+    cin = 96 if mode == "project" else 64
+    cout, temb, g = 64, 48, 16
+    shapes = ctmr.maisi._resnet_shapes("b", cin, cout, temb)
+    w = {k[2:]: v for k, v in ctmr.maisi.random_weights(shapes, seed=5).items()}
+    x = (2 * rng.standard_normal((2, cin, 4, 6, 8)) + 0.5).astype(np.float32)
+    emb = rng.standard_normal((2, temb)).astype(np.float32)
+    kw = {"up": mode == "up", "down": mode == "down"}
+    y = ctmr.fast_fp32.residual_block_ncdhw(_g(x, dev), _g(emb, dev), {k: _g(v, dev) for k, v in w.items()},
+                                            num_groups=g, eps=1e-6, **kw)
+    ref = mt.residual_block(torch.from_numpy(x).double(), torch.from_numpy(emb).double(),
+                            {k: torch.from_numpy(v).double() for k, v in w.items()}, g, 1e-6, **kw)
+    assert _rel(_h(y), ref.numpy()) <= 1e-5
+
+
+def test_unet_goldens(ctmr, dev):
+    manifest, a = load_boundary("diffusion")
+    f = load_fixture("unet.npz")
+    w = _gw(f, dev)
+    m = ctmr.maisi
+    t_emb, y = m.denoise_unet_ncdhw(_g(a["x"], dev), _g(a["timesteps"], dev), _g(a["class_labels"], dev, torch.int64),
+                                    _g(a["spacing"], dev), w, constructor=manifest["constructor"])
+    np.testing.assert_allclose(_h(t_emb), a["t_emb"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(_h(y), a["y"], rtol=UNET_RTOL, atol=UNET_ATOL)
+    _, y = m.denoise_unet_ncdhw(_g(f["input.x"], dev), _g(f["input.timesteps"], dev),
+                                _g(f["input.class_labels"], dev, torch.int64), _g(f["input.spacing"], dev), w,
+                                constructor=f["__metadata__"]["constructor"])
+    np.testing.assert_allclose(_h(y), f["output.velocity"], rtol=UNET_RTOL, atol=UNET_ATOL)
+
+
+def test_unet_with_controlnet_mid_residual_matches_oracle(ctmr, dev):
+    manifest, a = load_boundary("diffusion")
+    f = load_fixture("unet.npz")
+    ctor = manifest["constructor"]
+    mid = np.full((1, ctor["num_channels"][-1], 2, 2, 2), 0.01, dtype=np.float32)
+    _, y = ctmr.maisi.denoise_unet_ncdhw(_g(a["x"], dev), _g(a["timesteps"], dev),
+                                         _g(a["class_labels"], dev, torch.int64), _g(a["spacing"], dev), _gw(f, dev),
+                                         constructor=ctor, mid_block_additional_residual=_g(mid, dev))
+    _, ref = mt.unet(torch.from_numpy(a["x"]).double(), torch.from_numpy(a["timesteps"]).double(),
+                     torch.from_numpy(a["class_labels"]), torch.from_numpy(a["spacing"]).double(), mt.to_torch(f),
+                     ctor, mid_residual=torch.from_numpy(mid).double())
+    np.testing.assert_allclose(_h(y), ref.numpy(), rtol=UNET_RTOL, atol=UNET_ATOL)
+
+
+def test_vae_goldens(ctmr, dev):
+    f = load_fixture("vae.npz")
+    ctor = f["__metadata__"]["constructor"]
+    w = _gw(f, dev)
+    m = ctmr.maisi
+    _, decoded = m.decode_vae_ncdhw(_g(f["input.z"], dev), w, constructor=ctor)
+    np.testing.assert_allclose(_h(decoded), f["output.decoded"], rtol=VAE_RTOL, atol=VAE_ATOL)
+    tiled = m.sliding_window_decode_ncdhw(_g(f["input.z"], dev), w, constructor=ctor, roi=(2, 2, 2), overlap=0.5,
+                                          scale_factor=1.25)
+    np.testing.assert_allclose(_h(tiled), f["output.tiled"], rtol=VAE_RTOL, atol=VAE_ATOL)
+    _, b = load_boundary("vae")
+    post, decoded = m.decode_vae_ncdhw(_g(b["z"], dev), w, constructor=ctor)
+    np.testing.assert_allclose(_h(post), b["post_quant"], rtol=VAE_RTOL, atol=VAE_ATOL)
+    np.testing.assert_allclose(_h(decoded), b["decoded"], rtol=VAE_RTOL, atol=VAE_ATOL)
+
+
+@pytest.mark.parametrize("name", ["mr.npz", "mr-brain.npz"])
+@pytest.mark.parametrize("execution", ["batched", "sequential"])
+def test_mr_pipeline_golden(ctmr, dev, name, execution):
+    """End-to-end golden of the fast path (reference test_mr.py:181-242): CFG velocity
+    batch, 30 rflow steps, the windowed decode and the int16 image."""
+    f = load_fixture(name)
+    meta = f["__metadata__"]
+    ctor = meta["constructor"]
+    m, ff = ctmr.maisi, ctmr.fast_fp32
+    uw = _gw(f, dev, "weight.unet.")
+    vw = _gw(f, dev, "weight.vae.")
+    x = ff.to_ndhwc(_g(f["input.latent"], dev))
+    spacing = _g(f["output.spacing"], dev)
+    classes = torch.tensor([int(meta["modality"])], device=dev)
+    _, vb = m.denoise_unet(torch.cat([x, x]), torch.full((2,), 1000.0, device=dev), torch.cat([classes, classes * 0]),
+                           spacing.repeat(2, 1), uw, constructor=ctor["unet"])
+    np.testing.assert_allclose(_h(ff.to_ncdhw(vb)), f["output.velocity_batch"], rtol=UNET_RTOL, atol=UNET_ATOL)
+    times, _ = m.set_timesteps_rflow(num_inference_steps=int(meta["num_inference_steps"]),
+                                     input_img_size_numel=int(np.prod(x.shape[1:4])))
+    np.testing.assert_array_equal(times, f["output.timesteps"])
+    g = float(meta["guidance_scale"])
+    velocity = lambda z, t: m.guided_velocity(z, t, class_labels=classes, spacing=spacing, weights=uw,
+                                              constructor=ctor["unet"], guidance_scale=g, guidance_execution=execution)
+    latent = m.sample_rflow(x, velocity, times)
+    np.testing.assert_allclose(_h(ff.to_ncdhw(latent)), f["output.latent"], rtol=UNET_RTOL, atol=UNET_ATOL)
+    decoded = m.sliding_window_decode(latent, vw, constructor=ctor["vae"], roi=(80, 80, 80), overlap=0.4,
+                                      scale_factor=1.25)
+    decoded = _h(ff.to_ncdhw(decoded))
+    np.testing.assert_allclose(decoded, f["output.decoded"], rtol=VAE_RTOL, atol=VAE_ATOL)
+    image = m.output_intensities(decoded, configuration="mr")
+    diff = np.abs(image.astype(np.int32) - f["output.image"].astype(np.int32))
+    # truncation flips by one count only where x*1000 sits within the decode tolerance of an integer
+    assert diff.max() <= 1 and (diff == 0).mean() >= 0.99
+
+
+def _production_unet(ctmr, dev, seed=7):
+    m = ctmr.maisi
+    host = m.random_weights(m.unet_weight_shapes(m.PRODUCTION_UNET_CONSTRUCTOR), seed=seed)
+    return host, {k: _g(v, dev) for k, v in host.items()}
+
+
+def test_config3_unet_step_matches_cpu_oracle(ctmr, dev):
+    """Config 3 at full size: production UNet, latent 64x64x32x4, batch 2 (CFG pair),
+    random init; max relative error vs the PyTorch-CPU fp32 oracle <= 1e-4."""
+    m = ctmr.maisi
+    host, w = _production_unet(ctmr, dev)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 64, 64, 32, 4)).astype(np.float32)
+    t = np.full(2, float(rng.uniform(0, 1000)), dtype=np.float32)
+    classes = np.array([9, 0])
+    spacing = np.repeat(np.asarray([[0.94, 0.94, 1.36]], np.float64) * 100, 2, 0).astype(np.float16).astype(np.float32)
+    ctor = m.PRODUCTION_UNET_CONSTRUCTOR
+    _, y = m.denoise_unet(_g(x, dev), _g(t, dev), _g(classes, dev, torch.int64), _g(spacing, dev), w, constructor=ctor)
+    y = _h(y)
+    torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
+    with torch.no_grad():
+        _, ref = mt.unet(torch.from_numpy(np.moveaxis(x, -1, 1).copy()), torch.from_numpy(t), torch.from_numpy(classes),
+                         torch.from_numpy(spacing), mt.to_torch(host, dtype=torch.float32, strip=""), ctor)
+    assert _rel(y, np.moveaxis(ref.numpy(), 1, -1)) <= 1e-4
+
+
+def test_config4_vae_decoder_window_matches_cpu_oracle(ctmr, dev):
+    """Config 4's decoder (production constructor, random init) on a reduced window."""
+    m = ctmr.maisi
+    ctor = m.PRODUCTION_VAE_CONSTRUCTOR
+    host = m.random_weights(m.vae_decoder_weight_shapes(ctor), seed=11)
+    w = {k: _g(v, dev) for k, v in host.items()}
+    z = np.random.default_rng(4).standard_normal((1, 6, 8, 10, 4)).astype(np.float32)
+    _, y = m.decode_vae(_g(z, dev), w, constructor=ctor)
+    with torch.no_grad():
+        _, ref = mt.vae_decode(torch.from_numpy(np.moveaxis(z, -1, 1).copy()), mt.to_torch(host, dtype=torch.float32,
+                                                                                             strip=""), ctor)
+    assert _rel(_h(y), np.moveaxis(ref.numpy(), 1, -1)) <= 1e-4
+
+
+def test_sliding_window_decode_matches_cpu_oracle(ctmr, dev):
+    """Four overlapping windows along D (overlap 0.25), Gaussian blend, production decoder."""
+    m = ctmr.maisi
+    ctor = m.PRODUCTION_VAE_CONSTRUCTOR
+    host = m.random_weights(m.vae_decoder_weight_shapes(ctor), seed=12)
+    w = {k: _g(v, dev) for k, v in host.items()}
+    z = np.random.default_rng(6).standard_normal((1, 16, 6, 6, 4)).astype(np.float32)
+    y = m.sliding_window_decode(_g(z, dev), w, constructor=ctor, roi=(5, 6, 6), overlap=0.25, scale_factor=1.0)
+    with torch.no_grad():
+        ref = mt.sliding_window_decode(torch.from_numpy(np.moveaxis(z, -1, 1).copy()),
+                                       mt.to_torch(host, dtype=torch.float32, strip=""), ctor, roi=(5, 6, 6),
+                                       overlap=0.25, scale_factor=1.0)
+    assert m.dense_patch_slices((16, 6, 6), (5, 6, 6), m.scan_interval((16, 6, 6), (5, 6, 6), 0.25))[-1][0].start == 11
+    assert _rel(_h(y), np.moveaxis(ref.numpy(), 1, -1)) <= 1e-4
+
+
+def test_unet_step_is_bitwise_reproducible(ctmr, dev):
+    m = ctmr.maisi
+    manifest, a = load_boundary("diffusion")
+    w = _gw(load_fixture("unet.npz"), dev)
+    args = (_g(a["x"], dev), _g(a["timesteps"], dev), _g(a["class_labels"], dev, torch.int64), _g(a["spacing"], dev), w)
+    first = m.denoise_unet_ncdhw(*args, constructor=manifest["constructor"])[1]
+    assert torch.equal(first, m.denoise_unet_ncdhw(*args, constructor=manifest["constructor"])[1])
