@@ -157,6 +157,186 @@ def secondary(pkg, dev, steps):
     return out
 
 
+def unet_flops(constructor, batch, d, h, w):
+    """Conv FLOPs of one UNet pass (8-tap folded upsample convs) and attention FLOPs."""
+    ch = list(constructor["num_channels"])
+    nl = len(ch)
+    nres = [constructor["num_res_blocks"]] * nl
+    attn = list(constructor["attention_levels"])
+    head = list(constructor["num_head_channels"])
+    conv = attn_f = 0.0
+    vox = [batch * d * h * w // 8**i for i in range(nl)]
+
+    def res(v, cin, cout, taps1=27):
+        f = 2.0 * v * cin * cout * taps1 + 2.0 * v * cout * cout * 27
+        return f + (2.0 * v * cin * cout if cin != cout else 0.0)
+
+    def att(v, c):
+        tokens = v // batch
+        return batch * (4 * 2.0 * tokens * c * c + 2 * 2.0 * tokens * tokens * c)
+
+    conv += 2.0 * vox[0] * constructor["in_channels"] * ch[0] * 27
+    prev = ch[0]
+    for i in range(nl):
+        for r in range(nres[i]):
+            conv += res(vox[i], prev if r == 0 else ch[i], ch[i])
+            attn_f += att(vox[i], ch[i]) if attn[i] else 0.0
+        prev = ch[i]
+        if i != nl - 1:
+            conv += res(vox[i + 1], ch[i], ch[i])  # down: convs at the pooled grid
+    conv += 2 * res(vox[-1], ch[-1], ch[-1])
+    attn_f += att(vox[-1], ch[-1])
+    rc = ch[::-1]
+    out = rc[0]
+    for i in range(nl):
+        li = nl - 1 - i
+        prev, out = out, rc[i]
+        cin_skip = rc[min(i + 1, nl - 1)]
+        n = nres[li] + 1
+        for r in range(n):
+            skip = cin_skip if r == n - 1 else out
+            conv += res(vox[li], (prev if r == 0 else out) + skip, out)
+            attn_f += att(vox[li], out) if attn[li] else 0.0
+        if i != nl - 1:
+            # up: conv1 on the source grid with 8 folded taps per parity (x8 outputs)
+            conv += 2.0 * vox[li] * out * out * 8 * 8 + 2.0 * vox[li - 1] * out * out * 27
+    conv += 2.0 * vox[0] * ch[0] * constructor["out_channels"] * 27
+    return conv, attn_f
+
+
+def vae_decoder_flops(constructor, d, h, w):
+    """Conv FLOPs of one decoder pass on a (d, h, w) latent (trilinear convs on the 2x grid)."""
+    ch = list(constructor["num_channels"])[::-1]
+    nres = list(constructor["num_res_blocks"])[::-1]
+    lat = constructor["latent_channels"]
+    v = d * h * w
+    f = 2.0 * v * lat * lat + 2.0 * v * lat * ch[0] * 27
+    block_in = ch[0]
+    for level, n in enumerate(nres):
+        for _ in range(n):
+            out = ch[level]
+            f += 2.0 * v * 27 * (block_in * out + out * out) + (2.0 * v * block_in * out if block_in != out else 0)
+            block_in = out
+        if level != len(nres) - 1:
+            v *= 8
+            f += 2.0 * v * 27 * block_in * block_in
+    return f + 2.0 * v * 27 * block_in * constructor["out_channels"]
+
+
+def networks(pkg, dev, steps, generation=True, cpu=False):
+    """Config 3 (UNet step), config 4 (256^3 windowed decode + int16) and the full
+    256^3 generation (30 CFG UNet steps at a 64^3 latent + decode)."""
+    import numpy as np
+    import torch
+
+    m = pkg.maisi
+    out = {}
+    uc, vc = m.PRODUCTION_UNET_CONSTRUCTOR, m.PRODUCTION_VAE_CONSTRUCTOR
+    uw = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.unet_weight_shapes(uc), seed=7).items()}
+    vw = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal((2, 64, 64, 32, 4), dtype=np.float32)).to(dev)
+    t = torch.full((2,), float(rng.uniform(0, 1000)), device=dev)
+    classes = torch.tensor([9, 0], device=dev)
+    spacing = m.spacing_tensor([0.94, 0.94, 1.36], device=dev).repeat(2, 1)
+    step = lambda: m.denoise_unet(x, t, classes, spacing, uw, constructor=uc)
+    for _ in range(2):
+        step()
+    ms = _wall_ms(step, max(3, steps // 2))
+    conv_f, attn_f = unet_flops(uc, 2, 64, 64, 32)
+    floor_ms = (conv_f + attn_f) / FP32_PEAK * 1e3
+    out["config3_unet_step_batch2_64x64x32"] = {
+        "ms": round(ms, 3), "conv_tflop": round(conv_f / 1e12, 4), "attention_tflop": round(attn_f / 1e12, 4),
+        "tflops": round((conv_f + attn_f) / ms / 1e9, 2), "roofline_ms": round(floor_ms, 3),
+        "frac_roofline": round(floor_ms / ms, 4)}
+    if cpu:
+        from oracle import maisi_torch as mt
+
+        host_w = {k: v.cpu() for k, v in uw.items()}
+        xc = x.cpu().permute(0, 4, 1, 2, 3).contiguous()
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            mt.unet(xc, t.cpu(), classes.cpu(), spacing.cpu(), host_w, uc)
+            out["config3_unet_step_batch2_64x64x32"]["cpu_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+            out["config3_unet_step_batch2_64x64x32"]["cpu_cores"] = torch.get_num_threads()
+    del x
+    # config 4: 64^3 latent -> 256^3, 4 windows along D (roi 20x64x64, overlap 0.25), int16
+    z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 64, 64, 64, 4), dtype=np.float32)).to(dev)
+
+    def decode():
+        y = m.sliding_window_decode(z, vw, constructor=vc, roi=(20, 64, 64), overlap=0.25, scale_factor=1.0)
+        img = torch.clamp(y * 1000.0, min=0.0).to(torch.int16)
+        return img
+
+    decode()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    img = decode()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    dec_f = 4 * vae_decoder_flops(vc, 20, 64, 64)
+    out["config4_vae_decode_256^3_4windows"] = {
+        "s": round(sec, 4), "tflop": round(dec_f / 1e12, 3), "tflops": round(dec_f / sec / 1e12, 2),
+        "roofline_s": round(dec_f / FP32_PEAK, 4), "frac_roofline": round(dec_f / FP32_PEAK / sec, 4),
+        "output": list(img.shape)}
+    del img
+    if generation:
+        # full 256^3 generation: 30 rflow steps with batched CFG at a 64^3 latent, then decode
+        lat = torch.from_numpy(np.random.default_rng(5).standard_normal((1, 64, 64, 64, 4), dtype=np.float32)).to(dev)
+        sp = m.spacing_tensor([1.0, 1.0, 1.0], device=dev)
+        cls = torch.tensor([9], device=dev)
+        times, _ = m.set_timesteps_rflow(num_inference_steps=30, input_img_size_numel=64**3)
+        vel = lambda s, tt: m.guided_velocity(s, tt, class_labels=cls, spacing=sp, weights=uw, constructor=uc,
+                                              guidance_scale=5.0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        final = m.sample_rflow(lat, vel, times)
+        torch.cuda.synchronize()
+        t_sample = time.perf_counter() - t0
+        y = m.sliding_window_decode(final, vw, constructor=vc, roi=(20, 64, 64), overlap=0.25, scale_factor=1.0)
+        img = torch.clamp(y * 1000.0, min=0.0).to(torch.int16).cpu()
+        total = time.perf_counter() - t0
+        gen_f = 30 * sum(unet_flops(uc, 2, 64, 64, 64)) + dec_f
+        out["generation_256^3_30steps_cfg"] = {
+            "s": round(total, 3), "sampling_s": round(t_sample, 3), "tflop": round(gen_f / 1e12, 2),
+            "roofline_s": round(gen_f / FP32_PEAK, 3), "frac_roofline": round(gen_f / FP32_PEAK / total, 4),
+            "target_s": 60, "image_dtype": str(img.dtype)}
+    return out
+
+
+def profile_only(pkg, dev, what, steps, warmup):
+    """Run one workload alone (for rocprofv3 traces) and print its mean time."""
+    import numpy as np
+    import torch
+
+    m, f = pkg.maisi, pkg.fast_fp32
+    if what == "unet":
+        uc = m.PRODUCTION_UNET_CONSTRUCTOR
+        w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.unet_weight_shapes(uc), seed=7).items()}
+        x = torch.from_numpy(np.random.default_rng(3).standard_normal((2, 64, 64, 32, 4), dtype=np.float32)).to(dev)
+        t = torch.full((2,), 500.0, device=dev)
+        cls = torch.tensor([9, 0], device=dev)
+        sp = m.spacing_tensor([0.94, 0.94, 1.36], device=dev).repeat(2, 1)
+        fn = lambda: m.denoise_unet(x, t, cls, sp, w, constructor=uc)
+    elif what == "decode":
+        vc = m.PRODUCTION_VAE_CONSTRUCTOR
+        w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
+        z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 20, 64, 64, 4), dtype=np.float32)).to(dev)
+        fn = lambda: m.decode_vae(z, w, constructor=vc)
+    else:
+        rng = np.random.default_rng(1)
+        x = torch.from_numpy(rng.standard_normal((1, 128, 128, 128, 128), dtype=np.float32)).to(dev)
+        w1 = torch.from_numpy((rng.standard_normal((128, 128, 3, 3, 3)) / np.sqrt(27 * 128)).astype(np.float32)).to(dev)
+        b = torch.zeros(128, device=dev)
+        g, z0 = torch.ones(128, device=dev), torch.zeros(128, device=dev)
+        fn = lambda: f.vae_resblock([x], (w1, b), (w1, b), (g, z0), (g, z0), None, num_groups=32, eps=1e-6)
+    for _ in range(warmup):
+        fn()
+    ms = _wall_ms(fn, steps)
+    print(json.dumps({"only": what, "ms": round(ms, 3), "steps": steps}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +344,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
+    ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
+    ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
+    ap.add_argument("--only", choices=["unet", "decode", "resblock"],
+                    help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -188,6 +372,8 @@ def main() -> int:
     pkg = importlib.import_module("mlx-generate-ctmr_amd")
     f = pkg.fast_fp32
     dev = torch.device("cuda:0")
+    if args.only:
+        return profile_only(pkg, dev, args.only, args.steps, args.warmup)
     rng = np.random.default_rng(0)
     n, s, cin, cout = 1, 64, 64, 64
     x = torch.from_numpy(rng.standard_normal((n, s, s, s, cin), dtype=np.float32)).to(dev)
@@ -247,6 +433,8 @@ def main() -> int:
                                  "frac_bf16_peak": round(flops / (bf16_ms * 1e-3) / BF16_PEAK, 4)}}
     if not args.no_secondary:
         sec.update(secondary(pkg, dev, args.steps))
+    if not args.no_networks:
+        sec.update(networks(pkg, dev, args.steps, generation=not args.no_generation, cpu=not args.no_cpu))
     result["secondary"] = sec
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

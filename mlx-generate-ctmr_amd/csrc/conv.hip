@@ -295,23 +295,43 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
 #pragma unroll
     for (int ns = 0; ns < NSUB; ++ns) B[ns] = *reinterpret_cast<const u4*>(bcol[ns] + bo);
   };
+  // K sub-step outermost: consecutive MFMAs always write different
+  // accumulators, so none waits for the previous one's result.
   auto compute = [&](const u4 (&A)[4], const u4 (&B)[NSUB]) {
+    if constexpr (DT == CTMR_F32) {
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int ns = 0; ns < NSUB; ++ns) mfma_step<DT>(acc[ms][ns], A[ms], B[ns]);
+        for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+          for (int ns = 0; ns < NSUB; ++ns)
+            acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(f4, A[ms])[j],
+                                                               __builtin_bit_cast(f4, B[ns])[j],
+                                                               acc[ms][ns], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns) mfma_step<DT>(acc[ms][ns], A[ms], B[ns]);
+    }
   };
 
   // Register double buffer: the next K block is in flight while this one
-  // multiplies.
+  // multiplies.  The scheduling barriers keep the prefetch loads ahead of the
+  // MFMAs that would otherwise be hoisted above them (the compiler's default
+  // order issues the loads after the MFMA burst and exposes their latency).
   u4 A0[4], B0[NSUB], A1[4], B1[NSUB];
   load(s_begin, A0, B0);
   for (int s = s_begin; s < s_end; s += 2) {
     if (s + 1 < s_end) load(s + 1, A1, B1);
+    __builtin_amdgcn_sched_barrier(0);
     compute(A0, B0);
+    __builtin_amdgcn_sched_barrier(0);
     if (s + 1 >= s_end) break;
     if (s + 2 < s_end) load(s + 2, A0, B0);
+    __builtin_amdgcn_sched_barrier(0);
     compute(A1, B1);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // Epilogue: D row 4*(lane/16)+r, column lane%16 of each 16x16 block.
