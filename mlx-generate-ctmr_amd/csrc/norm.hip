@@ -9,8 +9,8 @@
 // consumer computes x*scale + offset (fused into the conv input pack).
 //
 // Statistics are HBM-bound (4 bytes read per element).  Pass 1 splits the
-// voxels of each batch item into fixed-size chunks (the chunk size depends on
-// C only); each 256-thread workgroup streams one chunk with coalesced 16-byte
+// voxels of each batch item into chunks (the chunking depends on the shape
+// only: about 64 KiB of input per chunk, at most ~2048 workgroups per launch); each 256-thread workgroup streams one chunk with coalesced 16-byte
 // loads, every thread owning 4 channels, and accumulates sum and sum of
 // squares in fp64.  The per-thread partials are combined in a fixed order, so
 // the result is bit-identical run to run and independent of the device.
@@ -21,8 +21,18 @@
 
 namespace ctmr {
 
-// Voxels per statistics chunk: 512 KiB of fp32 input per chunk.
-static inline int64_t gn_chunk_voxels(int c) { return std::max<int64_t>(1, 131072 / c); }
+// Statistics chunking, a function of (n, s, c) only: chunks of about 64 KiB
+// of fp32 input, capped so one launch has at most ~2048 workgroups.
+struct GnChunks {
+  int64_t vox, count;
+};
+static inline GnChunks gn_chunks(int32_t n, int64_t s, int32_t c) {
+  const int64_t target_vox = std::max<int64_t>(1, 16384 / c);
+  const int64_t cap = std::max<int64_t>(1, 2048 / std::max<int32_t>(n, 1));
+  const int64_t count = std::min<int64_t>(ceil_div(s, target_vox), cap);
+  const int64_t vox = ceil_div(s, count);
+  return {vox, ceil_div(s, vox)};
+}
 
 // VEC channels per thread: 4 (16-byte loads) when c % 4 == 0, else 1.
 template <int VEC>
@@ -225,8 +235,7 @@ extern "C" {
 
 int64_t ctmr_gn_workspace_bytes(int32_t n, int64_t s, int32_t c) {
   if (n <= 0 || s <= 0 || c <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
-  const int64_t chunks = ceil_div(s, gn_chunk_voxels(c));
-  return (int64_t)n * chunks * c * 2 * (int64_t)sizeof(double);
+  return (int64_t)n * gn_chunks(n, s, c).count * c * 2 * (int64_t)sizeof(double);
 }
 
 int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, const float* x,
@@ -239,8 +248,8 @@ int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, c
     return fail(CTMR_E_UNSUPPORTED, "group norm needs c <= 1024 (c % 4 == 0) or c <= 256");
   if (!x || !gamma || !beta || !affine) return fail(CTMR_E_INVALID, "null pointer");
   if (vec && ((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
-  const int64_t chunk_vox = gn_chunk_voxels(c);
-  const int64_t chunks = ceil_div(s, chunk_vox);
+  const GnChunks ch = gn_chunks(n, s, c);
+  const int64_t chunk_vox = ch.vox, chunks = ch.count;
   const int64_t need = (int64_t)n * chunks * c * 2 * (int64_t)sizeof(double);
   if ((int64_t)workspace_bytes < need || !workspace) {
     set_error("group-norm workspace %zu bytes < required %lld", workspace_bytes, (long long)need);

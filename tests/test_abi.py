@@ -104,7 +104,8 @@ def test_conv_rejects_null_and_small_workspace_before_launch(ctmr, native_loaded
 
 def test_group_norm_host_checks(ctmr, native_loaded):
     L = ctmr._lib
-    assert L.gn_workspace_bytes(1, 128**3, 128) == 1 * 2048 * 128 * 2 * 8
+    assert L.gn_workspace_bytes(1, 128**3, 128) == 1 * 2048 * 128 * 2 * 8  # capped at 2048 chunks
+    assert L.gn_workspace_bytes(2, 64 * 64 * 32, 64) == 2 * 512 * 64 * 2 * 8  # 256-voxel chunks
     rc = native_loaded.ctmr_gn_affine(1, 64, 12, 5, 1e-6, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1 << 30, None)
     assert rc == L.E_INVALID and "divisible" in L.last_error()
     rc = native_loaded.ctmr_gn_affine(1, 64, 258, 2, 1e-6, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1 << 30, None)
