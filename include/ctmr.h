@@ -76,7 +76,9 @@ typedef struct ctmr_conv_desc {
   int32_t mode;         /* enum ctmr_conv_mode */
   int32_t flags;        /* enum ctmr_conv_flags, OR-ed */
   int32_t dtype;        /* enum ctmr_dtype */
-  int32_t split;        /* tap split for small grids: 0 = library policy, else 1, 3, 9, 27 */
+  int32_t split;        /* K split for small grids: 0 = library policy, else the number of
+                           contiguous ranges of the (tap, channel block) step sequence,
+                           1 .. taps * ceil(cin / K block) */
 } ctmr_conv_desc;
 
 /* Library identity; returns CTMR_ABI_VERSION. */
@@ -118,8 +120,10 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  *   residual output-shaped NDHWC with CTMR_F_RESIDUAL, else NULL
  *   y        (n, D', H', W', cout); must not alias x or residual
  * Accumulation order is fixed: taps kd*9+kh*3+kw ascending (outer), input
- * channels in ascending 16-wide blocks (inner); split partial planes are
- * added in ascending order.  Results are bit-identical run to run.
+ * channels in ascending 16-wide (fp32) / 32-wide (bf16) blocks (inner); with a
+ * split, each contiguous range of that sequence is summed separately and the
+ * partial planes are added in ascending order after the bias.  The split and
+ * tiling depend on the shape only, so results are bit-identical run to run.
  */
 int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed,
                 const float* bias, const float* affine, const float* residual, float* y,

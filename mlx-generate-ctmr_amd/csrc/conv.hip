@@ -15,9 +15,9 @@
 //      kd*9+kh*3+kw ascending, then 64-byte channel blocks ascending.  Bias,
 //      per-batch bias and residual join the fp32 sum before the single store
 //      (_nax_conv.py:282-317).
-//   3. split_reduce: when the grid is small the taps are split into equal
-//      ranges whose fp32 partial planes are added in ascending order with bias
-//      and residual (_nax_conv.py:320-332).
+//   3. split_reduce: when the grid is small the K steps are split into
+//      contiguous ranges whose fp32 partial planes are added in ascending
+//      order with bias and residual (_nax_conv.py:320-332).
 //
 // Wave tile: 64 output voxels (4 MFMA row blocks of 16) x NSUB*16 channels;
 // a 256-thread workgroup holds WM x WN waves.  Each lane loads 16 bytes per
@@ -277,9 +277,9 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
 #pragma unroll
     for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int taps_per = p.taps / p.split;
-  const int s_begin = split_id * taps_per * p.kb;
-  const int s_end = s_begin + taps_per * p.kb;
+  const int steps = p.taps * p.kb;
+  const int s_begin = (int)((int64_t)split_id * steps / p.split);
+  const int s_end = (int)((int64_t)(split_id + 1) * steps / p.split);
   const int64_t bstep = (int64_t)p.np * 64;
 
   auto a_offset = [&](int s) -> int64_t {
@@ -474,22 +474,22 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   else { g.nsub = 4; g.wm = 2; g.wn = 2; }
   g.m_tiles = (int)ceil_div(S, g.wm * 64);
   g.n_tiles = (int)ceil_div(g.np, g.wn * g.nsub * 16);
-  // Tap split: chosen from the shape only (never from the device), so each
-  // output's summation order is fixed for a given problem.
+  // K split: the (tap, channel-block) step sequence of every output is cut
+  // into `split` contiguous ranges whose fp32 partial planes are summed in
+  // ascending order.  Chosen from the shape only (never from the device), so
+  // each output's summation order is fixed for a given problem.  Small grids
+  // are split so the launch fills whole rounds of 512 resident workgroups
+  // (two per CU on 256 CUs), keeping at least 8 steps per range.
+  const int steps = g.taps * g.kblocks;
   if (d->split > 0) {
-    if (g.taps % d->split != 0) return fail(CTMR_E_INVALID, "split must divide the tap count");
+    if (d->split > steps) return fail(CTMR_E_INVALID, "split must not exceed the K step count");
     g.split = d->split;
   } else {
     const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases;
+    const int64_t slots = 512;
     g.split = 1;
-    const int64_t target = 512;  // two workgroups per CU on 256 CUs
-    if (g.taps > 1 && base < target && d->cin >= 64) {
-      static const int cands27[3] = {3, 9, 27}, cands8[3] = {2, 4, 8};
-      const int* cands = g.taps == 27 ? cands27 : cands8;
-      for (int i = 0; i < 3; ++i) {
-        g.split = cands[i];
-        if (base * g.split >= target) break;
-      }
+    if (base < slots && steps >= 16) {
+      g.split = (int)std::min<int64_t>(ceil_div(slots, base), std::max(1, steps / 8));
     }
   }
   const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases * g.split;

@@ -61,14 +61,17 @@ def test_workspace_and_packed_sizes(ctmr):
 
 def test_split_policy_is_shape_only(ctmr):
     L = ctmr._lib
-    # UNet deepest level (512 ch on 8x8x4, batch 2): few tiles -> full tap split
-    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512)) == 27
+    # UNet levels at a 64x64x32 latent, batch 2: the split fills 512 resident workgroups
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512)) == 32  # 16 tiles x 32
+    assert L.conv_split(L.conv_desc(2, 8, 16, 16, 256, 256)) == 8  # 64 tiles x 8
+    assert L.conv_split(L.conv_desc(2, 16, 32, 32, 128, 128)) == 2  # 256 tiles x 2
     # large grids never split
     assert L.conv_split(L.conv_desc(1, 128, 128, 128, 128, 128)) == 1
-    # explicit split must divide the tap count
-    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=3)) == 3
-    with pytest.raises(L.CtmrError, match="divide"):
-        L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=4))
+    assert L.conv_split(L.conv_desc(1, 64, 64, 64, 64, 64)) == 1
+    # an explicit split may be any count up to the step count (27 taps x 32 blocks here)
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=5)) == 5
+    with pytest.raises(L.CtmrError, match="step count"):
+        L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32 + 1))
 
 
 @pytest.mark.parametrize(
