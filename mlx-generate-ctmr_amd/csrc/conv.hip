@@ -193,6 +193,8 @@ struct ConvArgs {
   const float* bias;       // (cout) or (n, cout) or null
   const float* res;        // output-shaped residual or null
   float* y;                // output, or split partial planes
+  int64_t x_bytes;         // bytes of the packed input (buffer-descriptor range)
+  int64_t w_bytes;         // bytes of the packed weight
   int64_t rows_per_batch;  // rows of the packed input per batch item
   int64_t row_bytes;       // bytes per packed row (cp * element size)
   int64_t plane;           // elements per split plane (n * s_out * cout)
@@ -226,7 +228,9 @@ __device__ __forceinline__ void mfma_step<CTMR_BF16>(f4& acc, const u4& a, const
 template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
 __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   static_assert(WM * WN == 4, "four waves per workgroup");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // Wave index made provably uniform so every address base below lives in SGPRs.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wave_m = wave % WM, wave_n = wave / WM;
 
   // XCD-aware tile order: hardware deals consecutive workgroups round-robin
@@ -249,27 +253,33 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   const int m0 = m_tile * (WM * 64) + wave_m * 64;
   const int lrow = lane & 15, lgrp = lane >> 4;
 
-  // A: one window-start row per 16-voxel block; rows past the grid reuse the
-  // last voxel and are not stored.
-  const char* xb = p.xp + (int64_t)b * p.rows_per_batch * p.row_bytes + lgrp * 16;
-  const char* arow[4];
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms) {
-    const int v = min(m0 + ms * 16 + lrow, S - 1);
+  // Loads go through buffer descriptors: a wave-uniform base (SGPRs), a
+  // per-lane 32-bit offset fixed for the whole kernel, and one scalar offset
+  // per K step, so a step costs no vector address arithmetic.
+  auto window_row = [&](int v) -> int64_t {
     const int d = v / ghw, r = v - d * ghw;
     const int h = r / p.gw, w = r - h * p.gw;
-    const int64_t row =
-        (int64_t)(STRIDE * d + pd) * p.P + (int64_t)(STRIDE * h + ph) * p.Q + STRIDE * w + pw;
-    arow[ms] = xb + row * p.row_bytes;
-  }
+    return (int64_t)(STRIDE * d + pd) * p.P + (int64_t)(STRIDE * h + ph) * p.Q + STRIDE * w + pw;
+  };
+  // A: one window-start row per 16-voxel block; rows past the grid reuse the
+  // last voxel and are not stored.  Rows grow with the voxel index, so the
+  // wave's first voxel has the smallest row and every lane offset is >= 0.
+  const int64_t row0 = window_row(min(m0, S - 1));
+  const int64_t abase_off = ((int64_t)b * p.rows_per_batch + row0) * p.row_bytes;
+  const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.xp + abase_off), (short)0, (int)min(p.x_bytes - abase_off, (int64_t)0x7fffffff), 0x00020000);
+  int aoff[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+    aoff[ms] = (int)((window_row(min(m0 + ms * 16 + lrow, S - 1)) - row0) * p.row_bytes) + lgrp * 16;
   // B: one output column per lane per 16-column block.
   const int n0 = n_tile * (WN * NSUB * 16) + wave_n * (NSUB * 16);
-  const char* bcol[NSUB];
+  const int64_t bbase_off = (int64_t)phase * p.taps * p.kb * p.np * 64;
+  const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.wp + bbase_off), (short)0, (int)min(p.w_bytes - bbase_off, (int64_t)0x7fffffff), 0x00020000);
+  int boff[NSUB];
 #pragma unroll
-  for (int ns = 0; ns < NSUB; ++ns) {
-    const int col = min(n0 + ns * 16 + lrow, p.np - 1);
-    bcol[ns] = p.wp + ((int64_t)phase * p.taps * p.kb * p.np + col) * 64 + lgrp * 16;
-  }
+  for (int ns = 0; ns < NSUB; ++ns) boff[ns] = min(n0 + ns * 16 + lrow, p.np - 1) * 64 + lgrp * 16;
 
   f4 acc[4][NSUB];
 #pragma unroll
@@ -280,20 +290,22 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   const int steps = p.taps * p.kb;
   const int s_begin = (int)((int64_t)split_id * steps / p.split);
   const int s_end = (int)((int64_t)(split_id + 1) * steps / p.split);
-  const int64_t bstep = (int64_t)p.np * 64;
+  const int bstep = p.np * 64;
 
-  auto a_offset = [&](int s) -> int64_t {
+  auto a_offset = [&](int s) -> int {
     const int tap = s / p.kb, kb = s - tap * p.kb;
     const int td = tap / (KT * KT), th = (tap / KT) % KT, tw = tap % KT;
-    return ((int64_t)td * p.P + (int64_t)th * p.Q + tw) * p.row_bytes + kb * 64;
+    return (td * p.P + th * p.Q + tw) * (int)p.row_bytes + kb * 64;
   };
   auto load = [&](int s, u4 (&A)[4], u4 (&B)[NSUB]) {
-    const int64_t ao = a_offset(s);
-    const int64_t bo = (int64_t)s * bstep;
+    // readfirstlane: the step offsets are wave-uniform; saying so keeps them in
+    // SGPRs (buffer soffset) instead of a per-lane waterfall.
+    const int ao = __builtin_amdgcn_readfirstlane(a_offset(s));
+    const int bo = __builtin_amdgcn_readfirstlane(s * bstep);
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms) A[ms] = *reinterpret_cast<const u4*>(arow[ms] + ao);
+    for (int ms = 0; ms < 4; ++ms) A[ms] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, aoff[ms], ao, 0);
 #pragma unroll
-    for (int ns = 0; ns < NSUB; ++ns) B[ns] = *reinterpret_cast<const u4*>(bcol[ns] + bo);
+    for (int ns = 0; ns < NSUB; ++ns) B[ns] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, boff[ns], bo, 0);
   };
   // K sub-step outermost: consecutive MFMAs always write different
   // accumulators, so none waits for the previous one's result.
@@ -671,6 +683,8 @@ int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* pac
   a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
   a.rows_per_batch = g.rows_per_batch;
   a.row_bytes = (int64_t)g.cp * g.esize;
+  a.x_bytes = (int64_t)desc->n * g.rows_per_batch * a.row_bytes;
+  a.w_bytes = (int64_t)g.phases * g.taps * g.kblocks * g.np * 64;
   a.plane = (int64_t)desc->n * s_out * desc->cout;
   a.kb = g.kblocks;
   a.np = g.np;
