@@ -288,24 +288,47 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
     for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int steps = p.taps * p.kb;
-  const int s_begin = (int)((int64_t)split_id * steps / p.split);
-  const int s_end = (int)((int64_t)(split_id + 1) * steps / p.split);
+  // Wave-uniform (readfirstlane) so the loop counter and the load cursor
+  // derived from them stay in SGPRs.
+  const int s_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)split_id * steps / p.split));
+  const int s_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(split_id + 1) * steps / p.split));
   const int bstep = p.np * 64;
 
-  auto a_offset = [&](int s) -> int {
-    const int tap = s / p.kb, kb = s - tap * p.kb;
-    const int td = tap / (KT * KT), th = (tap / KT) % KT, tw = tap % KT;
-    return (td * p.P + th * p.Q + tw) * (int)p.row_bytes + kb * 64;
-  };
-  auto load = [&](int s, u4 (&A)[4], u4 (&B)[NSUB]) {
+  // Load cursor over the step sequence (tap-major, 64-byte channel block
+  // minor), advanced incrementally so a step costs a few scalar adds.
+  const int rb = (int)p.row_bytes;
+  int c_kb, c_tw, c_th, c_tapoff, c_bo;
+  {
+    const int tap = s_begin / p.kb;
+    c_kb = s_begin - tap * p.kb;
+    c_tw = tap % KT;
+    c_th = (tap / KT) % KT;
+    const int td = tap / (KT * KT);
+    c_tapoff = (td * p.P + c_th * p.Q + c_tw) * rb;
+    c_bo = s_begin * bstep;
+  }
+  auto load = [&](u4 (&A)[4], u4 (&B)[NSUB]) {
     // readfirstlane: the step offsets are wave-uniform; saying so keeps them in
     // SGPRs (buffer soffset) instead of a per-lane waterfall.
-    const int ao = __builtin_amdgcn_readfirstlane(a_offset(s));
-    const int bo = __builtin_amdgcn_readfirstlane(s * bstep);
+    const int ao = __builtin_amdgcn_readfirstlane(c_tapoff + c_kb * 64);
+    const int bo = __builtin_amdgcn_readfirstlane(c_bo);
 #pragma unroll
     for (int ms = 0; ms < 4; ++ms) A[ms] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, aoff[ms], ao, 0);
 #pragma unroll
     for (int ns = 0; ns < NSUB; ++ns) B[ns] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, boff[ns], bo, 0);
+    c_bo += bstep;
+    if (++c_kb == p.kb) {
+      c_kb = 0;
+      c_tapoff += rb;
+      if (++c_tw == KT) {
+        c_tw = 0;
+        c_tapoff += (p.Q - KT) * rb;
+        if (++c_th == KT) {
+          c_th = 0;
+          c_tapoff += (p.P - KT * p.Q) * rb;
+        }
+      }
+    }
   };
   // K sub-step outermost: consecutive MFMAs always write different
   // accumulators, so none waits for the previous one's result.
@@ -333,14 +356,14 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   // MFMAs that would otherwise be hoisted above them (the compiler's default
   // order issues the loads after the MFMA burst and exposes their latency).
   u4 A0[4], B0[NSUB], A1[4], B1[NSUB];
-  load(s_begin, A0, B0);
+  load(A0, B0);  // step s_begin; each load() fetches the cursor's step, then advances it
   for (int s = s_begin; s < s_end; s += 2) {
-    if (s + 1 < s_end) load(s + 1, A1, B1);
+    if (s + 1 < s_end) load(A1, B1);
     __builtin_amdgcn_sched_barrier(0);
     compute(A0, B0);
     __builtin_amdgcn_sched_barrier(0);
     if (s + 1 >= s_end) break;
-    if (s + 2 < s_end) load(s + 2, A0, B0);
+    if (s + 2 < s_end) load(A0, B0);
     __builtin_amdgcn_sched_barrier(0);
     compute(A1, B1);
     __builtin_amdgcn_sched_barrier(0);
