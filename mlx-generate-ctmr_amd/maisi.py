@@ -129,6 +129,42 @@ def spatial_attention(x: Tensor, weights: Mapping[str, Tensor], *, num_groups: i
 # ---------------------------------------------------------------------------
 # UNet (unet.py:42-487)
 # ---------------------------------------------------------------------------
+def _blocks(weights: Mapping[str, Tensor], emb: Tensor, groups: int, eps: float, include_fc: bool):
+    """Residual-block and attention callables bound to one embedding and weight dict."""
+
+    def resnet(h: Tensor, prefix: str, **kw) -> Tensor:
+        return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps, **kw)
+
+    def attention(h: Tensor, prefix: str, n_heads: int) -> Tensor:
+        return spatial_attention(h, _prefixed(weights, prefix), num_groups=groups, eps=eps,
+                                 num_head_channels=n_heads, include_fc=include_fc)
+
+    return resnet, attention
+
+
+def _down_path(hidden: Tensor, resnet, attention, res_blocks, attn_levels, heads) -> tuple[Tensor, list[Tensor]]:
+    """Encoder levels; returns the hidden state and every skip (unet.py:274-356)."""
+    skips = [hidden]
+    n_levels = len(res_blocks)
+    for index in range(n_levels):
+        for r in range(res_blocks[index]):
+            hidden = resnet(hidden, f"down_blocks.{index}.resnets.{r}")
+            if attn_levels[index]:
+                hidden = attention(hidden, f"down_blocks.{index}.attentions.{r}", heads[index])
+            skips.append(hidden)
+        if index != n_levels - 1:
+            hidden = resnet(hidden, f"down_blocks.{index}.downsampler", down=True)
+            skips.append(hidden)
+    return hidden, skips
+
+
+def _mid_block(hidden: Tensor, resnet, attention, n_heads: int) -> Tensor:
+    """resnet -> attention -> resnet (unet.py:359-399)."""
+    hidden = resnet(hidden, "middle_block.resnet_1")
+    hidden = attention(hidden, "middle_block.attention", n_heads)
+    return resnet(hidden, "middle_block.resnet_2")
+
+
 def denoise_unet(
     x: Tensor,
     timesteps: Tensor,
@@ -158,34 +194,17 @@ def denoise_unet(
         raise ValueError("resblock_updown=False (ddpm-ct) is not part of this path")
 
     t_emb, emb = condition_embedding(timesteps, class_labels, spacing, weights, constructor)
-
-    def resnet(h: Tensor, prefix: str, **kw) -> Tensor:
-        return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps, **kw)
-
-    def attention(h: Tensor, prefix: str, n_heads: int) -> Tensor:
-        return spatial_attention(h, _prefixed(weights, prefix), num_groups=groups, eps=eps,
-                                 num_head_channels=n_heads, include_fc=include_fc)
+    resnet, attention = _blocks(weights, emb, groups, eps, include_fc)
 
     hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1)
-    skips = [hidden]
-    for index in range(n_levels):
-        for r in range(res_blocks[index]):
-            hidden = resnet(hidden, f"down_blocks.{index}.resnets.{r}")
-            if attn_levels[index]:
-                hidden = attention(hidden, f"down_blocks.{index}.attentions.{r}", heads[index])
-            skips.append(hidden)
-        if index != n_levels - 1:
-            hidden = resnet(hidden, f"down_blocks.{index}.downsampler", down=True)
-            skips.append(hidden)
+    hidden, skips = _down_path(hidden, resnet, attention, res_blocks, attn_levels, heads)
     if down_block_additional_residuals is not None:
         extras = list(down_block_additional_residuals)
         if len(extras) != len(skips):
             raise ValueError(f"ControlNet residuals length {len(extras)} != UNet skip count {len(skips)}")
         skips = [s + e for s, e in zip(skips, extras)]
         hidden = skips[-1]
-    hidden = resnet(hidden, "middle_block.resnet_1")
-    hidden = attention(hidden, "middle_block.attention", heads[-1])
-    hidden = resnet(hidden, "middle_block.resnet_2")
+    hidden = _mid_block(hidden, resnet, attention, heads[-1])
     if mid_block_additional_residual is not None:
         hidden = hidden + mid_block_additional_residual
     rev_res, rev_attn, rev_heads = res_blocks[::-1], attn_levels[::-1], heads[::-1]
@@ -216,6 +235,105 @@ def denoise_unet_ncdhw(x: Tensor, timesteps: Tensor, class_labels, spacing, weig
     t_emb, y = denoise_unet(ff.to_ndhwc(x), timesteps, class_labels, spacing, weights, constructor=constructor,
                             down_block_additional_residuals=down, mid_block_additional_residual=mid)
     return t_emb, ff.to_ncdhw(y)
+
+
+# ---------------------------------------------------------------------------
+# ControlNet (controlnet.py:31-274)
+# ---------------------------------------------------------------------------
+def _check_controlnet(constructor: Mapping) -> tuple[int, ...]:
+    if int(constructor.get("spatial_dims", 3)) != 3 or constructor.get("use_flash_attention"):
+        raise ValueError("MAISI ControlNet destination is 3D without CUDA flash attention")
+    if not constructor.get("resblock_updown", True) or constructor.get("with_conditioning"):
+        raise ValueError("ddpm-ct / cross-attention ControlNet variants are not part of this path")
+    return tuple(int(c) for c in constructor["conditioning_embedding_num_channels"])
+
+
+def encode_controlnet_condition(cond: Tensor, weights: Mapping[str, Tensor], *, constructor: Mapping) -> Tensor:
+    """Conditioning encoder on an NDHWC label condition (controlnet.py:167-249):
+    conv_in -> SiLU, then per level a stride-1 conv -> SiLU and a stride-2 conv -> SiLU,
+    then conv_out; output ``(N, D/s, H/s, W/s, num_channels[0])``."""
+    channels = _check_controlnet(constructor)
+    cond_in = int(constructor["conditioning_embedding_in_channels"])
+    if cond.shape[-1] != cond_in:
+        raise ValueError(f"controlnet cond channels {cond.shape[-1]} != {cond_in}")
+    scale = 2 ** (len(channels) - 1)
+    if any(int(s) % scale for s in cond.shape[1:4]):
+        raise ValueError(f"controlnet cond spatial sizes must be multiples of {scale}")
+    p = "controlnet_cond_embedding"
+    hidden = ff.silu(ff.conv3d(cond, weights[f"{p}.conv_in.conv.weight"], weights[f"{p}.conv_in.conv.bias"], padding=1))
+    block = 0
+    for _ in range(len(channels) - 1):
+        for stride in (1, 2):
+            hidden = ff.silu(ff.conv3d(hidden, _need(weights, f"{p}.blocks.{block}.conv.weight"),
+                                       _need(weights, f"{p}.blocks.{block}.conv.bias"), padding=1, stride=stride))
+            block += 1
+    return ff.conv3d(hidden, _need(weights, f"{p}.conv_out.conv.weight"), _need(weights, f"{p}.conv_out.conv.bias"),
+                     padding=1)
+
+
+def _zero_conv(x: Tensor, weights: Mapping[str, Tensor], prefix: str) -> Tensor:
+    """1x1 zero convolution, wrapped (``.conv.weight``) or raw naming (controlnet.py:252-266)."""
+    for key in (f"{prefix}.conv", prefix):
+        if f"{key}.weight" in weights:
+            return ff.pointwise_conv(x, weights[f"{key}.weight"], _need(weights, f"{key}.bias"))
+    raise ValueError(f"ControlNet weights missing: {prefix}.conv.weight or {prefix}.weight")
+
+
+def controlnet_residuals(
+    x: Tensor,
+    timesteps: Tensor,
+    class_labels: Optional[Tensor],
+    cond: Tensor,
+    weights: Mapping[str, Tensor],
+    *,
+    constructor: Mapping,
+    conditioning_scale: float = 1.0,
+    conditioning_embedding: Optional[Tensor] = None,
+) -> tuple[list[Tensor], Tensor]:
+    """ControlNetMaisi on NDHWC ``x``/``cond``: ``(down, mid)`` residuals for the UNet (controlnet.py:31-164)."""
+    cond_channels = _check_controlnet(constructor)
+    if x.shape[-1] != int(constructor["in_channels"]):
+        raise ValueError(f"controlnet latent channels {x.shape[-1]} != in_channels {constructor['in_channels']}")
+    scale = 2 ** (len(cond_channels) - 1)
+    if conditioning_embedding is None:
+        expected = tuple(int(s) * scale for s in x.shape[1:4])
+        if tuple(int(s) for s in cond.shape[1:4]) != expected:
+            raise ValueError(f"controlnet cond spatial {tuple(cond.shape[1:4])} must be {scale}x latent")
+    channels = tuple(int(c) for c in constructor["num_channels"])
+    n_levels = len(channels)
+    res_blocks = _per_level(constructor["num_res_blocks"], n_levels)
+    attn_levels = tuple(bool(a) for a in constructor["attention_levels"])
+    heads = _per_level(constructor["num_head_channels"], n_levels)
+    groups, eps = int(constructor["norm_num_groups"]), float(constructor["norm_eps"])
+    include_fc = bool(constructor.get("include_fc", True))
+    t_emb = sinusoidal_timestep_embedding(timesteps, channels[0])
+    emb = _silu_mlp(t_emb, weights, "time_embed")
+    if constructor.get("num_class_embeds") is not None:
+        if class_labels is None:
+            raise ValueError("class_labels should be provided when num_class_embeds > 0")
+        emb = emb + _need(weights, "class_embedding.weight")[class_labels.to(torch.long)]
+    resnet, attention = _blocks(weights, emb, groups, eps, include_fc)
+    hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1)
+    embedding = (encode_controlnet_condition(cond, weights, constructor=constructor)
+                 if conditioning_embedding is None else conditioning_embedding)
+    hidden = hidden + embedding
+    hidden, skips = _down_path(hidden, resnet, attention, res_blocks, attn_levels, heads)
+    hidden = _mid_block(hidden, resnet, attention, heads[-1])
+    down = [_zero_conv(s, weights, f"controlnet_down_blocks.{i}") for i, s in enumerate(skips)]
+    mid = _zero_conv(hidden, weights, "controlnet_mid_block")
+    if conditioning_scale != 1.0:
+        down = [d * conditioning_scale for d in down]
+        mid = mid * conditioning_scale
+    return down, mid
+
+
+def controlnet_residuals_ncdhw(x, timesteps, class_labels, cond, weights, *, constructor, mx=None,
+                               conditioning_scale=1.0, conditioning_embedding=None):
+    emb = None if conditioning_embedding is None else ff.to_ndhwc(conditioning_embedding)
+    down, mid = controlnet_residuals(ff.to_ndhwc(x), timesteps, class_labels, ff.to_ndhwc(cond), weights,
+                                     constructor=constructor, conditioning_scale=conditioning_scale,
+                                     conditioning_embedding=emb)
+    return [ff.to_ncdhw(d) for d in down], ff.to_ncdhw(mid)
 
 
 # ---------------------------------------------------------------------------
@@ -536,6 +654,62 @@ def unet_weight_shapes(constructor: Mapping) -> list[tuple[str, tuple[int, ...]]
     s += [("out.0.weight", (ch[0],)), ("out.0.bias", (ch[0],)),
           ("out.2.conv.weight", (int(constructor["out_channels"]), ch[0], 3, 3, 3)),
           ("out.2.conv.bias", (int(constructor["out_channels"]),))]
+    return s
+
+
+PRODUCTION_CONTROLNET_CONSTRUCTOR = {
+    # maisi_mlx_from_mask.py:63-80 of the reference
+    "spatial_dims": 3, "in_channels": 4, "num_channels": [64, 128, 256, 512],
+    "attention_levels": [False, False, True, True], "num_head_channels": [0, 0, 32, 32], "num_res_blocks": 2,
+    "norm_num_groups": 32, "norm_eps": 1e-6, "use_flash_attention": False, "conditioning_embedding_in_channels": 8,
+    "conditioning_embedding_num_channels": [8, 32, 64], "num_class_embeds": 128, "resblock_updown": True,
+    "include_fc": True, "with_conditioning": False, "use_combined_linear": False,
+}
+
+
+def controlnet_weight_shapes(constructor: Mapping) -> list[tuple[str, tuple[int, ...]]]:
+    """State-dict names and shapes of ControlNetMaisi for ``constructor`` (the first zero
+    conv is a bare Conv3d, the others are wrapped, as in the released checkpoints)."""
+    ch = [int(c) for c in constructor["num_channels"]]
+    nl = len(ch)
+    nres = _per_level(constructor["num_res_blocks"], nl)
+    attn = [bool(a) for a in constructor["attention_levels"]]
+    t = 4 * ch[0]
+    s = [("time_embed.0.weight", (t, ch[0])), ("time_embed.0.bias", (t,)), ("time_embed.2.weight", (t, t)),
+         ("time_embed.2.bias", (t,))]
+    if constructor.get("num_class_embeds") is not None:
+        s.append(("class_embedding.weight", (int(constructor["num_class_embeds"]), t)))
+    s += [("conv_in.conv.weight", (ch[0], int(constructor["in_channels"]), 3, 3, 3)), ("conv_in.conv.bias", (ch[0],))]
+    cc = [int(c) for c in constructor["conditioning_embedding_num_channels"]]
+    p = "controlnet_cond_embedding"
+    s += [(f"{p}.conv_in.conv.weight", (cc[0], int(constructor["conditioning_embedding_in_channels"]), 3, 3, 3)),
+          (f"{p}.conv_in.conv.bias", (cc[0],))]
+    block = 0
+    for i in range(len(cc) - 1):
+        for cout in (cc[i], cc[i + 1]):
+            s += [(f"{p}.blocks.{block}.conv.weight", (cout, cc[i], 3, 3, 3)), (f"{p}.blocks.{block}.conv.bias", (cout,))]
+            block += 1
+    s += [(f"{p}.conv_out.conv.weight", (ch[0], cc[-1], 3, 3, 3)), (f"{p}.conv_out.conv.bias", (ch[0],))]
+    temb = t
+    out_ch = ch[0]
+    skip_ch = [ch[0]]
+    for i in range(nl):
+        in_ch, out_ch = out_ch, ch[i]
+        for r in range(nres[i]):
+            s += _resnet_shapes(f"down_blocks.{i}.resnets.{r}", in_ch if r == 0 else out_ch, out_ch, temb)
+            if attn[i]:
+                s += _attention_shapes(f"down_blocks.{i}.attentions.{r}", out_ch)
+            skip_ch.append(out_ch)
+        if i != nl - 1:
+            s += _resnet_shapes(f"down_blocks.{i}.downsampler", out_ch, out_ch, temb)
+            skip_ch.append(out_ch)
+    s += _resnet_shapes("middle_block.resnet_1", ch[-1], ch[-1], temb)
+    s += _attention_shapes("middle_block.attention", ch[-1])
+    s += _resnet_shapes("middle_block.resnet_2", ch[-1], ch[-1], temb)
+    for i, c in enumerate(skip_ch):
+        key = f"controlnet_down_blocks.{i}" + ("" if i == 0 else ".conv")
+        s += [(f"{key}.weight", (c, c, 1, 1, 1)), (f"{key}.bias", (c,))]
+    s += [("controlnet_mid_block.conv.weight", (ch[-1], ch[-1], 1, 1, 1)), ("controlnet_mid_block.conv.bias", (ch[-1],))]
     return s
 
 

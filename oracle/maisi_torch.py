@@ -8,7 +8,12 @@ HIP composition it checks:
   UNet             unet.py:42-487, embed.py:15-87
   VAE decoder      vae.py:29-62, 103-200, 273-379 (materialized trilinear upsampling)
   sliding window   decode.py:30-245
-Pinned by the reference goldens in tests/golden (tests/test_oracle_networks.py).
+  ControlNet       controlnet.py:31-274
+Pinned by the reference goldens in tests/golden (tests/test_oracle_networks.py).  The ControlNet
+has no recorded outputs in the reference fixtures (its boundary arrays live outside the repository);
+its shared down path is pinned through the UNet goldens and an identity invariant, its conditioning
+encoder and zero convolutions are plain conv/SiLU/1x1 compositions of pinned primitives — the
+ControlNet as a whole is "parity unpinned" against a recording.
 """
 
 from __future__ import annotations
@@ -86,23 +91,21 @@ def _mlp(x, w, prefix):
     return F.linear(h, w[f"{prefix}.2.weight"], w[f"{prefix}.2.bias"])
 
 
-def unet(x, t, class_labels, spacing, w, ctor, down_residuals=None, mid_residual=None):
-    """DiffusionModelUNetMaisi forward (unet.py:42-487); returns (t_emb, y), NCDHW."""
+def _levels(ctor):
     ch = list(ctor["num_channels"])
     nl = len(ch)
     nres = ctor["num_res_blocks"]
     nres = [nres] * nl if isinstance(nres, int) else list(nres)
-    attn = list(ctor["attention_levels"])
     heads = ctor["num_head_channels"]
     heads = [heads] * nl if isinstance(heads, int) else list(heads)
+    return ch, nl, nres, list(ctor["attention_levels"]), heads
+
+
+def down_path(h, emb, w, ctor):
+    """Encoder levels and mid block shared by UNet and ControlNet (unet.py:274-399);
+    returns (hidden after the mid block, skips)."""
+    ch, nl, nres, attn, heads = _levels(ctor)
     g, eps, fc = ctor["norm_num_groups"], ctor["norm_eps"], ctor.get("include_fc", True)
-    t_emb = timestep_embedding(t, ch[0])
-    emb = _mlp(t_emb, w, "time_embed")
-    if ctor.get("num_class_embeds") is not None:
-        emb = emb + w["class_embedding.weight"][class_labels.long()]
-    if ctor.get("include_spacing_input"):
-        emb = torch.cat([emb, _mlp(spacing, w, "spacing_layer")], dim=-1)
-    h = F.conv3d(x, w["conv_in.conv.weight"], w["conv_in.conv.bias"], padding=1)
     skips = [h]
     for i in range(nl):
         for r in range(nres[i]):
@@ -113,12 +116,33 @@ def unet(x, t, class_labels, spacing, w, ctor, down_residuals=None, mid_residual
         if i != nl - 1:
             h = residual_block(h, emb, _pre(w, f"down_blocks.{i}.downsampler"), g, eps, down=True)
             skips.append(h)
+    return h, skips
+
+
+def mid_block(h, emb, w, ctor):
+    _, _, _, _, heads = _levels(ctor)
+    g, eps, fc = ctor["norm_num_groups"], ctor["norm_eps"], ctor.get("include_fc", True)
+    h = residual_block(h, emb, _pre(w, "middle_block.resnet_1"), g, eps)
+    h = attention(h, _pre(w, "middle_block.attention"), g, eps, heads[-1], fc)
+    return residual_block(h, emb, _pre(w, "middle_block.resnet_2"), g, eps)
+
+
+def unet(x, t, class_labels, spacing, w, ctor, down_residuals=None, mid_residual=None):
+    """DiffusionModelUNetMaisi forward (unet.py:42-487); returns (t_emb, y), NCDHW."""
+    ch, nl, nres, attn, heads = _levels(ctor)
+    g, eps, fc = ctor["norm_num_groups"], ctor["norm_eps"], ctor.get("include_fc", True)
+    t_emb = timestep_embedding(t, ch[0])
+    emb = _mlp(t_emb, w, "time_embed")
+    if ctor.get("num_class_embeds") is not None:
+        emb = emb + w["class_embedding.weight"][class_labels.long()]
+    if ctor.get("include_spacing_input"):
+        emb = torch.cat([emb, _mlp(spacing, w, "spacing_layer")], dim=-1)
+    h = F.conv3d(x, w["conv_in.conv.weight"], w["conv_in.conv.bias"], padding=1)
+    h, skips = down_path(h, emb, w, ctor)
     if down_residuals is not None:
         skips = [s + e for s, e in zip(skips, down_residuals)]
         h = skips[-1]
-    h = residual_block(h, emb, _pre(w, "middle_block.resnet_1"), g, eps)
-    h = attention(h, _pre(w, "middle_block.attention"), g, eps, heads[-1], fc)
-    h = residual_block(h, emb, _pre(w, "middle_block.resnet_2"), g, eps)
+    h = mid_block(h, emb, w, ctor)
     if mid_residual is not None:
         h = h + mid_residual
     for i in range(nl):
@@ -134,6 +158,38 @@ def unet(x, t, class_labels, spacing, w, ctor, down_residuals=None, mid_residual
             h = residual_block(h, emb, _pre(w, f"up_blocks.{i}.upsampler"), g, eps, up=True)
     h = F.silu(_gn(h, w["out.0.weight"], w["out.0.bias"], g, eps))
     return t_emb, F.conv3d(h, w["out.2.conv.weight"], w["out.2.conv.bias"], padding=1)
+
+
+def controlnet_condition(cond, w, ctor):
+    """Conditioning encoder (controlnet.py:167-249): conv_in, SiLU; per level conv s1 SiLU,
+    conv s2 SiLU; conv_out."""
+    p = "controlnet_cond_embedding"
+    h = F.silu(F.conv3d(cond, w[f"{p}.conv_in.conv.weight"], w[f"{p}.conv_in.conv.bias"], padding=1))
+    block = 0
+    for _ in range(len(ctor["conditioning_embedding_num_channels"]) - 1):
+        for stride in (1, 2):
+            h = F.silu(F.conv3d(h, w[f"{p}.blocks.{block}.conv.weight"], w[f"{p}.blocks.{block}.conv.bias"],
+                                padding=1, stride=stride))
+            block += 1
+    return F.conv3d(h, w[f"{p}.conv_out.conv.weight"], w[f"{p}.conv_out.conv.bias"], padding=1)
+
+
+def _zero_conv(x, w, prefix):
+    key = f"{prefix}.conv" if f"{prefix}.conv.weight" in w else prefix
+    return F.conv3d(x, w[f"{key}.weight"], w[f"{key}.bias"])
+
+
+def controlnet(x, t, class_labels, cond, w, ctor, scale=1.0):
+    """ControlNetMaisi (controlnet.py:31-164); returns (down residuals, mid residual), NCDHW."""
+    ch = list(ctor["num_channels"])
+    emb = _mlp(timestep_embedding(t, ch[0]), w, "time_embed")
+    if ctor.get("num_class_embeds") is not None:
+        emb = emb + w["class_embedding.weight"][class_labels.long()]
+    h = F.conv3d(x, w["conv_in.conv.weight"], w["conv_in.conv.bias"], padding=1) + controlnet_condition(cond, w, ctor)
+    h, skips = down_path(h, emb, w, ctor)
+    h = mid_block(h, emb, w, ctor)
+    down = [_zero_conv(s, w, f"controlnet_down_blocks.{i}") * scale for i, s in enumerate(skips)]
+    return down, _zero_conv(h, w, "controlnet_mid_block") * scale
 
 
 def _cw(w, prefix):
@@ -224,5 +280,5 @@ def to_torch(weights: Mapping[str, np.ndarray], dtype=torch.float64, strip: str 
             for k, v in weights.items() if k.startswith(strip)}
 
 
-__all__ = ["residual_block", "attention", "unet", "vae_decode", "sliding_window_decode", "rflow_timesteps",
-           "to_torch", "rm"]
+__all__ = ["residual_block", "attention", "unet", "down_path", "mid_block", "controlnet", "controlnet_condition",
+           "vae_decode", "sliding_window_decode", "rflow_timesteps", "to_torch", "rm"]

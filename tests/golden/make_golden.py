@@ -24,6 +24,7 @@ FILES = (
     "mr.npz",  # end-to-end MR: velocity batch, 30-step latent, decoded, int16
     "mr-brain.npz",
     "rflow.npz",
+    "controlnet.npz",  # tiny ControlNet weight recipe + constructor (no recorded outputs)
     "maisi/residual.json",
     "maisi/residual.npz",
     "maisi/diffusion.json",
@@ -34,6 +35,7 @@ FILES = (
     "maisi/scheduler.npz",
     "maisi/attention.json",
     "maisi/attention.npz",
+    "maisi/controlnet.json",
 )
 
 

@@ -8,6 +8,7 @@ recorded recipe (numpy default_rng(seed), discard ``skip`` normals, then
 
 from __future__ import annotations
 
+import ast
 import json
 from pathlib import Path
 
@@ -34,6 +35,8 @@ def load_fixture(name: str) -> dict[str, np.ndarray]:
         arrays = {k: np.array(archive[k]) for k in archive.files}
     if "metadata" in arrays:
         meta = json.loads(str(arrays["metadata"]))
+        # some recordings store nested fields as Python literals (data only)
+        meta = {k: (ast.literal_eval(v) if isinstance(v, str) and v[:1] in "{[" else v) for k, v in meta.items()}
         arrays["__metadata__"] = meta  # type: ignore[assignment]
         recipe = meta.get("weight_recipe")
         if recipe is not None:

@@ -98,6 +98,49 @@ def test_unet_with_controlnet_mid_residual_matches_oracle(ctmr, dev):
     np.testing.assert_allclose(_h(y), ref.numpy(), rtol=UNET_RTOL, atol=UNET_ATOL)
 
 
+def _controlnet_case():
+    f = load_fixture("controlnet.npz")
+    cond = np.random.default_rng(11).standard_normal((1, 8, 16, 16, 16)).astype(np.float32)
+    return f, f["__metadata__"]["constructor"], cond
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.5])
+def test_controlnet_residuals_match_oracle(ctmr, dev, scale):
+    """ControlNetMaisi (controlnet.py:31-164) on the recorded recipe network, cond at 4x the
+    latent, against the float64 CPU oracle at the UNet tolerance."""
+    f, ctor, cond = _controlnet_case()
+    down, mid = ctmr.maisi.controlnet_residuals_ncdhw(
+        _g(f["input.x"], dev), _g(f["input.timesteps"], dev), _g(f["input.class_labels"], dev, torch.int64),
+        _g(cond, dev), _gw(f, dev), constructor=ctor, conditioning_scale=scale)
+    rdown, rmid = mt.controlnet(torch.from_numpy(f["input.x"]).double(), torch.from_numpy(f["input.timesteps"]).double(),
+                                torch.from_numpy(f["input.class_labels"]), torch.from_numpy(cond).double(),
+                                mt.to_torch(f), ctor, scale=scale)
+    assert len(down) == len(rdown)
+    for d, r in zip(down, rdown):
+        np.testing.assert_allclose(_h(d), r.numpy(), rtol=UNET_RTOL, atol=UNET_ATOL)
+    np.testing.assert_allclose(_h(mid), rmid.numpy(), rtol=UNET_RTOL, atol=UNET_ATOL)
+
+
+def test_unet_step_with_controlnet_matches_oracle(ctmr, dev):
+    """ControlNet residuals added into the UNet's skips and mid block (unet.py:392-399)."""
+    f, cctor, cond = _controlnet_case()
+    u = load_fixture("unet.npz")
+    uctor = u["__metadata__"]["constructor"]
+    args = [u["input.x"], u["input.timesteps"], u["input.class_labels"]]
+    down, mid = ctmr.maisi.controlnet_residuals_ncdhw(_g(args[0], dev), _g(args[1], dev), _g(args[2], dev, torch.int64),
+                                                      _g(cond, dev), _gw(f, dev), constructor=cctor)
+    _, y = ctmr.maisi.denoise_unet_ncdhw(_g(args[0], dev), _g(args[1], dev), _g(args[2], dev, torch.int64),
+                                         _g(u["input.spacing"], dev), _gw(u, dev), constructor=uctor,
+                                         down_block_additional_residuals=down, mid_block_additional_residual=mid)
+    t64 = [torch.from_numpy(args[0]).double(), torch.from_numpy(args[1]).double(), torch.from_numpy(args[2])]
+    rdown, rmid = mt.controlnet(*t64, torch.from_numpy(cond).double(), mt.to_torch(f), cctor)
+    _, ref = mt.unet(*t64, torch.from_numpy(u["input.spacing"]).double(), mt.to_torch(u), uctor,
+                     down_residuals=rdown, mid_residual=rmid)
+    np.testing.assert_allclose(_h(y), ref.numpy(), rtol=UNET_RTOL, atol=UNET_ATOL)
+    _, plain = mt.unet(*t64, torch.from_numpy(u["input.spacing"]).double(), mt.to_torch(u), uctor)
+    assert np.abs(ref.numpy() - plain.numpy()).max() > 1e-3
+
+
 def test_vae_goldens(ctmr, dev):
     f = load_fixture("vae.npz")
     ctor = f["__metadata__"]["constructor"]

@@ -144,3 +144,56 @@ def test_rflow_schedule_and_step(ctmr):
     assert dt == (float(times[1]) - int(float(nxt[1]))) / 1000.0
     sample = m.sample_rflow(x, lambda cur, t: cur * 0.125 + t * 0.0001, times)
     np.testing.assert_allclose(sample.numpy(), f["output.sample"], rtol=1e-5, atol=1e-6)
+
+
+def test_controlnet_oracle_identity_invariant(ctmr):
+    """With identity 1x1 zero convs and a zero conditioning encoder, the ControlNet's down
+    residuals are the UNet encoder's skips (golden-pinned blocks) and its mid residual is the
+    mid-block output; the 3x down-blocks and mid block are the UNet's own, so this ties the
+    ControlNet composition to the UNet goldens.  (No recorded ControlNet outputs ship with
+    the reference, so this is the available pin.)"""
+    f = load_fixture("controlnet.npz")
+    ctor = f["__metadata__"]["constructor"]
+    w = mt.to_torch(f)
+    for k in list(w):
+        if k.startswith("controlnet_down_blocks.") or k.startswith("controlnet_mid_block."):
+            if k.endswith("weight"):
+                c = w[k].shape[0]
+                w[k] = torch.eye(c, dtype=D).reshape(c, c, 1, 1, 1)
+            else:
+                w[k] = torch.zeros_like(w[k])
+        if k == "controlnet_cond_embedding.conv_out.conv.weight" or k == "controlnet_cond_embedding.conv_out.conv.bias":
+            w[k] = torch.zeros_like(w[k])
+    x = _t(f["input.x"])
+    cond = torch.from_numpy(np.random.default_rng(2).standard_normal((1, 8, 16, 16, 16)))
+    t = _t(f["input.timesteps"])
+    labels = torch.from_numpy(f["input.class_labels"])
+    down, mid = mt.controlnet(x, t, labels, cond, w, ctor)
+    emb = mt._mlp(mt.timestep_embedding(t, ctor["num_channels"][0]), w, "time_embed") + w["class_embedding.weight"][labels.long()]
+    h = torch.nn.functional.conv3d(x, w["conv_in.conv.weight"], w["conv_in.conv.bias"], padding=1)
+    h, skips = mt.down_path(h, emb, w, ctor)
+    assert len(down) == len(skips)
+    for d, s in zip(down, skips):
+        np.testing.assert_allclose(d.numpy(), s.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(mid.numpy(), mt.mid_block(h, emb, w, ctor).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_controlnet_catalog_matches_recorded_recipe(ctmr):
+    f = load_fixture("controlnet.npz")
+    meta = f["__metadata__"]
+    recorded = {n[len("weight."):]: tuple(s) for n, s in meta["weight_recipe"]["shapes"]}
+    assert dict(ctmr.maisi.controlnet_weight_shapes(meta["constructor"])) == recorded
+
+
+def test_controlnet_rejects_bad_condition_shapes(ctmr):
+    """Host-side validation runs before any kernel: cond channels and the 4x spatial ratio."""
+    f = load_fixture("controlnet.npz")
+    ctor = f["__metadata__"]["constructor"]
+    x = torch.zeros(1, 4, 4, 4, 4)
+    with pytest.raises(ValueError, match="cond channels"):
+        ctmr.maisi.encode_controlnet_condition(torch.zeros(1, 16, 16, 16, 3), {}, constructor=ctor)
+    with pytest.raises(ValueError, match="4x latent"):
+        ctmr.maisi.controlnet_residuals(x, torch.zeros(1), torch.zeros(1, dtype=torch.long),
+                                        torch.zeros(1, 8, 8, 8, 8), {}, constructor=ctor)
+    with pytest.raises(ValueError, match="ddpm-ct"):
+        ctmr.maisi.controlnet_residuals(x, None, None, x, {}, constructor={**ctor, "resblock_updown": False})
