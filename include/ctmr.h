@@ -26,6 +26,9 @@
  *   ctmr_resample             <- medmlx_core.ops.avg_pool3d_ncdhw / upsample_nearest_ncdhw
  *                                (fast_fp32.py:48-59) and source_vae.upsample_trilinear_ncdhw
  *                                (fast_fp32.py:66-68; formula at _nax_conv.py:115-142)
+ *   ctmr_flash_attention      <- _flash_attention.flash_attention (_flash_attention.py:320-360),
+ *                                selected by flash_eligible (_flash_attention.py:276-289) from
+ *                                fast_fp32.self_attention_tokens (fast_fp32.py:352-392)
  */
 #ifndef CTMR_H
 #define CTMR_H
@@ -167,6 +170,24 @@ enum ctmr_resample_op {
 };
 int ctmr_resample(int32_t op, int32_t n, int32_t d, int32_t h, int32_t w, int32_t c,
                   const float* x, float* y, void* stream);
+
+/* Multi-head softmax(Q K^T * scale) V in FP32 on head-interleaved projections,
+ * without materialising the scores.  q is (n, lq, heads * head_dim) with row
+ * stride ldq floats (batch stride lq * ldq); head h is columns
+ * [h * head_dim, (h + 1) * head_dim).  k and v are (n, lk, ...) with row strides
+ * ldk / ldv; out is (n, lq, heads * head_dim) with row stride ldo.  q, k and v
+ * may be column slices of one fused (n, l, 3C) projection.  head_dim must be
+ * 32 (the MAISI UNet's num_head_channels).  Any lq, lk >= 1.  query_tiles
+ * picks 16 (1) or 32 (2) queries per wave, 0 = the library's policy; results
+ * are bit-identical either way (keys are visited in the same fixed order). */
+typedef struct ctmr_attn_desc {
+  int32_t n, lq, lk, heads, head_dim, query_tiles;
+  int64_t ldq, ldk, ldv, ldo;
+  float scale;
+} ctmr_attn_desc;
+
+int ctmr_flash_attention(const ctmr_attn_desc* desc, const float* q, const float* k, const float* v,
+                         float* out, void* stream);
 
 #ifdef __cplusplus
 }

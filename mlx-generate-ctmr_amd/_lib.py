@@ -33,6 +33,14 @@ class ConvDesc(ctypes.Structure):
     ]
 
 
+class AttnDesc(ctypes.Structure):
+    """``ctmr_attn_desc``."""
+
+    _fields_ = [(name, ctypes.c_int32) for name in ("n", "lq", "lk", "heads", "head_dim", "query_tiles")] + [
+        (name, ctypes.c_int64) for name in ("ldq", "ldk", "ldv", "ldo")
+    ] + [("scale", ctypes.c_float)]
+
+
 _c_int, _c_i32, _c_i64 = ctypes.c_int, ctypes.c_int32, ctypes.c_int64
 _vp, _sz, _f = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
 _desc_p = ctypes.POINTER(ConvDesc)
@@ -54,6 +62,7 @@ _PROTOTYPES = {
     "ctmr_gn_apply": (_c_int, [_c_i32, _c_i64, _c_i32, _vp, _vp, _c_i32, _vp, _vp]),
     "ctmr_silu": (_c_int, [_c_i64, _vp, _vp, _vp]),
     "ctmr_resample": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp]),
+    "ctmr_flash_attention": (_c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lock = threading.Lock()

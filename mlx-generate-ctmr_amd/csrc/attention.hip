@@ -1,0 +1,245 @@
+// FP32 flash attention for 32-wide heads on gfx950 matrix cores.
+//
+// Computes softmax(Q K^T * scale) V per (batch item, head) without writing the
+// scores, as _flash_attention.flash_attention does (_flash_attention.py:1-27,
+// 320-360): an online softmax over key blocks with a running row maximum and
+// sum, exp2 of log2(e)-scaled scores (the scale is folded into Q once).
+//
+// MI355X layout.  One wave owns QT x 16 queries and walks all keys in blocks of
+// 64.  Both products run on v_mfma_f32_16x16x4_f32 in the transposed form:
+//   S^T = K Q^T   (rows = keys, columns = queries; k runs over the 32 head dims)
+//   O^T += V^T P^T (rows = head dims, columns = queries; k runs over keys)
+// With the MFMA result layout (lane l, register r -> row 4*(l/16)+r, column
+// l%16) a lane's S^T registers are 4 keys of ONE query, so
+//   * the per-query max/sum need only 2 cross-lane steps (lanes l^16, l^32),
+//   * the S^T registers are already P^T's B operand for the next product
+//     (step r of a 16-key tile pairs lane group g with key 4g+r), and
+//   * the running-output rescale is one scalar per lane.
+// The head-dim order inside Q K^T is permuted the same way in both operands
+// (step s, lane group g -> dim 8g+s) so each lane loads 8 contiguous floats.
+// Everything accumulates in FP32; keys are visited in ascending blocks, so the
+// result does not depend on the launch shape or on other work on the device.
+#include "ctmr_common.hpp"
+
+#include <cmath>
+
+namespace ctmr {
+namespace {
+
+constexpr int kHeadDim = 32;
+constexpr int kWaves = 4;     // waves per workgroup (independent; no LDS, no barriers)
+constexpr int kKeyTiles = 4;  // 16-key tiles per key block
+
+struct AttnArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* out;
+  int64_t ldq, ldk, ldv, ldo;
+  int lq, lk, heads;
+  float qscale;  // scale * log2(e)
+};
+
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Keys and values of one 64-key block in MFMA operand order.
+struct KeyBlock {
+  f4 k[kKeyTiles][2];      // K row (tile*16 + l%16), dims 8g .. 8g+7
+  float v[kKeyTiles][4][2];  // V row (tile*16 + 4g + r), dims (l%16) and (16 + l%16)
+};
+
+template <int QT>
+__global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, g = lane >> 4;
+  const int b = blockIdx.y / a.heads, h = blockIdx.y % a.heads;
+  const int q0 = (blockIdx.x * kWaves + wave) * (QT * 16);
+  if (q0 >= a.lq) return;  // wave-uniform; the kernel has no barriers
+
+  const float* Q = a.q + (int64_t)b * a.lq * a.ldq + h * kHeadDim;
+  const float* K = a.k + (int64_t)b * a.lk * a.ldk + h * kHeadDim;
+  const float* V = a.v + (int64_t)b * a.lk * a.ldv + h * kHeadDim;
+
+  f4 qa[QT][2];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int row = min(q0 + t * 16 + col, a.lq - 1);
+    const f4* p = reinterpret_cast<const f4*>(Q + (int64_t)row * a.ldq + 8 * g);
+    qa[t][0] = p[0] * a.qscale;
+    qa[t][1] = p[1] * a.qscale;
+  }
+
+  f4 o[QT][2];
+  float m[QT], l[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    o[t][0] = f4{0.f, 0.f, 0.f, 0.f};
+    o[t][1] = f4{0.f, 0.f, 0.f, 0.f};
+    m[t] = -INFINITY;
+    l[t] = 0.f;
+  }
+
+  // Rows past the end are clamped to the last key (in bounds) and masked below.
+  auto load = [&](KeyBlock& kb, int k0) {
+#pragma unroll
+    for (int u = 0; u < kKeyTiles; ++u) {
+      const int row = min(k0 + u * 16 + col, a.lk - 1);
+      const f4* p = reinterpret_cast<const f4*>(K + (int64_t)row * a.ldk + 8 * g);
+      kb.k[u][0] = p[0];
+      kb.k[u][1] = p[1];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vr = V + (int64_t)min(k0 + u * 16 + 4 * g + r, a.lk - 1) * a.ldv;
+        kb.v[u][r][0] = vr[col];
+        kb.v[u][r][1] = vr[16 + col];
+      }
+    }
+  };
+
+  auto compute = [&](const KeyBlock& kb, int k0) {
+    f4 s[kKeyTiles][QT];
+#pragma unroll
+    for (int u = 0; u < kKeyTiles; ++u)
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = mfma4(kb.k[u][j][e], qa[t][j][e], acc);
+        s[u][t] = acc;
+      }
+    if (k0 + 16 * kKeyTiles > a.lk) {  // wave-uniform: only the last block is ragged
+#pragma unroll
+      for (int u = 0; u < kKeyTiles; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (k0 + u * 16 + 4 * g + r >= a.lk)
+#pragma unroll
+            for (int t = 0; t < QT; ++t) s[u][t][r] = -INFINITY;
+    }
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      float bm = s[0][t][0];
+#pragma unroll
+      for (int u = 0; u < kKeyTiles; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bm = fmaxf(bm, s[u][t][r]);
+      bm = fmaxf(bm, __shfl_xor(bm, 16));
+      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      // Every block holds at least one real key, so mn is finite and the first
+      // block's alpha is exp2(-inf) = 0.
+      const float mn = fmaxf(m[t], bm);
+      const float alpha = exp2f(m[t] - mn);
+      m[t] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int u = 0; u < kKeyTiles; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = exp2f(s[u][t][r] - mn);
+          s[u][t][r] = p;
+          ps += p;
+        }
+      l[t] = l[t] * alpha + ps;
+      o[t][0] *= alpha;
+      o[t][1] *= alpha;
+    }
+#pragma unroll
+    for (int u = 0; u < kKeyTiles; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+          o[t][0] = mfma4(kb.v[u][r][0], s[u][t][r], o[t][0]);
+          o[t][1] = mfma4(kb.v[u][r][1], s[u][t][r], o[t][1]);
+        }
+  };
+
+  // Register double buffer: the next block's loads are in flight while the
+  // current block's products run.
+  constexpr int kBlock = 16 * kKeyTiles;
+  KeyBlock b0, b1;
+  load(b0, 0);
+  for (int k0 = 0; k0 < a.lk; k0 += 2 * kBlock) {
+    if (k0 + kBlock < a.lk) load(b1, k0 + kBlock);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b0, k0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (k0 + kBlock >= a.lk) break;
+    if (k0 + 2 * kBlock < a.lk) load(b0, k0 + 2 * kBlock);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b1, k0 + kBlock);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  float* O = a.out + (int64_t)b * a.lq * a.ldo + h * kHeadDim;
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    // The four lane groups hold partial sums of the same query; xor pairs add
+    // commutatively, so every lane ends with the same bits.
+    float lt = l[t];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    const float inv = 1.0f / lt;
+    const int query = q0 + t * 16 + col;
+    if (query < a.lq) {
+      f4* dst = reinterpret_cast<f4*>(O + (int64_t)query * a.ldo + 4 * g);
+      dst[0] = o[t][0] * inv;  // dims 4g .. 4g+3
+      dst[4] = o[t][1] * inv;  // dims 16 + 4g .. 16 + 4g+3
+    }
+  }
+}
+
+template <int QT>
+int launch_attention(const AttnArgs& a, int n, hipStream_t stream) {
+  const int64_t per_block = (int64_t)kWaves * QT * 16;
+  dim3 grid((unsigned)ceil_div(a.lq, per_block), (unsigned)(n * a.heads));
+  hipLaunchKernelGGL(flash_attention_kernel<QT>, grid, dim3(256), 0, stream, a);
+  return check_launch("flash_attention_kernel");
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+// Query tiles per wave: two (more reuse of each key block) when that still
+// gives at least one wave per SIMD of the 256-CU device, else one.
+int attention_query_tiles(int n, int lq, int heads) {
+  const int64_t waves2 = ceil_div(lq, 32) * (int64_t)n * heads;
+  return waves2 >= 1024 ? 2 : 1;
+}
+
+}  // namespace ctmr
+
+extern "C" int ctmr_flash_attention(const ctmr_attn_desc* d, const float* q, const float* k, const float* v,
+                                    float* out, void* stream) {
+  using namespace ctmr;
+  if (!d || !q || !k || !v || !out) return fail(CTMR_E_INVALID, "ctmr_flash_attention: null argument");
+  if (d->head_dim != kHeadDim) {
+    set_error("ctmr_flash_attention: head_dim %d unsupported (32 only)", d->head_dim);
+    return CTMR_E_UNSUPPORTED;
+  }
+  if (d->query_tiles < 0 || d->query_tiles > 2)
+    return fail(CTMR_E_INVALID, "ctmr_flash_attention: query_tiles must be 0, 1 or 2");
+  if (d->n < 1 || d->lq < 1 || d->lk < 1 || d->heads < 1)
+    return fail(CTMR_E_INVALID, "ctmr_flash_attention: n, lq, lk and heads must be >= 1");
+  if ((int64_t)d->n * d->heads > 65535)
+    return fail(CTMR_E_INVALID, "ctmr_flash_attention: n * heads exceeds 65535");
+  const int64_t width = (int64_t)d->heads * kHeadDim;
+  if (d->ldq < width || d->ldk < width || d->ldv < width || d->ldo < width)
+    return fail(CTMR_E_INVALID, "ctmr_flash_attention: row stride below heads * head_dim");
+  if ((d->ldq | d->ldk | d->ldv | d->ldo) & 3)
+    return fail(CTMR_E_INVALID, "ctmr_flash_attention: row strides must be multiples of 4 floats");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(CTMR_E_INVALID, "ctmr_flash_attention: q, k, v and out must be 16-byte aligned");
+  if (!std::isfinite(d->scale)) return fail(CTMR_E_INVALID, "ctmr_flash_attention: scale must be finite");
+  AttnArgs a{q, k, v, out, d->ldq, d->ldk, d->ldv, d->ldo, d->lq, d->lk, d->heads,
+             (float)((double)d->scale * 1.4426950408889634)};
+  hipStream_t st = (hipStream_t)stream;
+  const int qt = d->query_tiles ? d->query_tiles : attention_query_tiles(d->n, d->lq, d->heads);
+  return qt == 2 ? launch_attention<2>(a, d->n, st) : launch_attention<1>(a, d->n, st);
+}

@@ -291,6 +291,89 @@ def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
     return F.linear(x, weight, bias)
 
 
+# ---------------------------------------------------------------------------
+# attention (fast_fp32.py:352-392, _flash_attention.py:276-360)
+# ---------------------------------------------------------------------------
+FLASH_HEAD_DIM = 32
+
+
+def flash_eligible(q: Tensor, k: Tensor, heads: int) -> bool:
+    """Whether ``(B, L, heads * 32)`` FP32 projections fit the HIP kernel
+    (``_flash_attention.flash_eligible``, :276-289; any L here, ragged key blocks are masked)."""
+    return (q.dtype == torch.float32 and k.dtype == torch.float32
+            and int(q.shape[-1]) == heads * FLASH_HEAD_DIM and int(k.shape[-1]) == heads * FLASH_HEAD_DIM)
+
+
+def _rows(t: Tensor, name: str) -> Tensor:
+    if t.dim() != 3 or t.dtype != torch.float32:
+        raise ValueError(f"{name} must be a 3-D float32 (B, L, C) tensor; got {tuple(t.shape)} {t.dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU (there is no CPU path); got {t.device}")
+    if t.stride(2) != 1 or t.stride(1) % 4 or t.stride(0) != t.shape[1] * t.stride(1) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def flash_attention(q: Tensor, k: Tensor, v: Tensor, *, heads: int, scale: float, mx=None,
+                    query_tiles: int = 0) -> Tensor:
+    """``softmax(q k^T * scale) v`` on head-interleaved ``(B, L, heads * 32)`` projections
+    (``_flash_attention.flash_attention``, :320-360); FP32 throughout, output in the same layout."""
+    q, k, v = _rows(q, "q"), _rows(k, "k"), _rows(v, "v")
+    if not flash_eligible(q, k, heads) or v.shape != k.shape or q.shape[0] != k.shape[0]:
+        raise ValueError(f"flash attention needs (B, L, heads*32) q/k/v with heads={heads}; got "
+                         f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    return ops.flash_attention(q, k, v, int(heads), float(scale), int(query_tiles))
+
+
+# Fused (3C, C) Q/K/V projection weights, keyed by the three weights' ids and
+# validated by weak references like the packed conv weights.
+_qkv: dict[tuple[int, int, int], tuple[tuple[weakref.ref, ...], Tensor, Optional[Tensor]]] = {}
+
+
+def _fused_qkv(wq: Tensor, wk: Tensor, wv: Tensor, biases) -> tuple[Tensor, Optional[Tensor]]:
+    key = (id(wq), id(wk), id(wv))
+    with _packed_lock:
+        hit = _qkv.get(key)
+        if hit is not None and all(r() is t for r, t in zip(hit[0], (wq, wk, wv))):
+            return hit[1], hit[2]
+    weight = torch.cat([wq, wk, wv], dim=0).to(torch.float32).contiguous()
+    bias = None if biases is None else torch.cat(list(biases), dim=0).to(torch.float32).contiguous()
+
+    def _evict(_ref, key=key):
+        with _packed_lock:
+            _qkv.pop(key, None)
+
+    with _packed_lock:
+        _qkv[key] = (tuple(weakref.ref(t, _evict) for t in (wq, wk, wv)), weight, bias)
+    return weight, bias
+
+
+def self_attention_tokens(tokens: Tensor, weights: Mapping[str, Tensor], *, heads: int, scale: float,
+                          include_fc: bool, mx=None, prefix: str = "attn", qkv_bias: bool = True) -> Tensor:
+    """Q/K/V projections, multi-head self-attention and optional ``out_proj`` on ``(B, L, C)``
+    tokens (``fast_fp32.self_attention_tokens``, :352-392).  32-wide heads run the HIP flash
+    kernel on one fused Q/K/V projection; other head widths use PyTorch's attention on the
+    GPU, as the reference falls back to ``mx.fast.scaled_dot_product_attention``."""
+    tokens = _rows(tokens, "tokens")
+    n, length, c = (int(s) for s in tokens.shape)
+    names = ("q", "k", "v")
+    biases = tuple(weights[f"{prefix}.to_{m}.bias"] for m in names) if qkv_bias else None
+    w, b = _fused_qkv(*(weights[f"{prefix}.to_{m}.weight"] for m in names), biases)
+    qkv = F.linear(tokens, w, b)
+    q, k, v = qkv[..., :c], qkv[..., c:2 * c], qkv[..., 2 * c:]
+    if c == heads * FLASH_HEAD_DIM:
+        merged = ops.flash_attention(q, k, v, int(heads), float(scale), 0)
+    else:
+        def split(t: Tensor) -> Tensor:
+            return t.reshape(n, length, heads, c // heads).transpose(1, 2).contiguous()
+
+        att = F.scaled_dot_product_attention(split(q), split(k), split(v), scale=scale)
+        merged = att.transpose(1, 2).reshape(n, length, c)
+    if include_fc:
+        merged = F.linear(merged, weights[f"{prefix}.out_proj.weight"], weights[f"{prefix}.out_proj.bias"])
+    return merged
+
+
 def residual_block(
     x: Tensor,
     emb: Tensor,

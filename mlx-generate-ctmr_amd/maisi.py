@@ -105,24 +105,16 @@ def condition_embedding(timesteps: Tensor, class_labels: Optional[Tensor], spaci
 # ---------------------------------------------------------------------------
 def spatial_attention(x: Tensor, weights: Mapping[str, Tensor], *, num_groups: int, eps: float,
                       num_head_channels: int, include_fc: bool) -> Tensor:
+    """Residual self-attention over all voxels of NDHWC ``x`` (attention.py:92-160): group
+    norm (HIP), tokens are the NDHWC rows as they lie, Q/K/V + flash attention + out_proj."""
     n, d, h, w, c = x.shape
     if c % num_head_channels != 0:
         raise ValueError("num_channels must be divisible by num_head_channels")
     heads = c // num_head_channels
     scale = float(num_head_channels) ** -0.5
     hidden = ff.group_norm(x, weights["norm.weight"], weights["norm.bias"], num_groups=num_groups, eps=eps)
-    tokens = hidden.reshape(n, d * h * w, c)
-
-    def split(t: Tensor) -> Tensor:
-        return t.reshape(n, -1, heads, num_head_channels).transpose(1, 2).contiguous()
-
-    q = split(F.linear(tokens, weights["attn.to_q.weight"], weights["attn.to_q.bias"]))
-    k = split(F.linear(tokens, weights["attn.to_k.weight"], weights["attn.to_k.bias"]))
-    v = split(F.linear(tokens, weights["attn.to_v.weight"], weights["attn.to_v.bias"]))
-    att = F.scaled_dot_product_attention(q, k, v, scale=scale)
-    merged = att.transpose(1, 2).reshape(n, -1, c)
-    if include_fc:
-        merged = F.linear(merged, weights["attn.out_proj.weight"], weights["attn.out_proj.bias"])
+    merged = ff.self_attention_tokens(hidden.reshape(n, d * h * w, c), weights, heads=heads, scale=scale,
+                                      include_fc=include_fc)
     return x + merged.reshape(n, d, h, w, c)
 
 

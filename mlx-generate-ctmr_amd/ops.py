@@ -211,3 +211,32 @@ def _(x, op):
     if op == _lib.AVGPOOL2:
         return x.new_empty((n, d // 2, h // 2, w // 2, c))
     return x.new_empty((n, 2 * d, 2 * h, 2 * w, c))
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("ctmr::flash_attention", mutates_args=())
+def flash_attention(q: Tensor, k: Tensor, v: Tensor, heads: int, scale: float, query_tiles: int = 0) -> Tensor:
+    """``softmax(q k^T * scale) v`` per head on ``(B, L, heads * 32)`` projections.
+
+    ``q``/``k``/``v`` may be column slices of one fused projection: the last
+    dimension must be unit-stride and the batch stride ``L * row stride``.
+    """
+    _require_device(q, k, v)
+    n, lq, c = (int(s) for s in q.shape)
+    lk = int(k.shape[1])
+    out = torch.empty((n, lq, c), device=q.device, dtype=torch.float32)
+    desc = _lib.AttnDesc(n, lq, lk, int(heads), c // int(heads), int(query_tiles),
+                         q.stride(1), k.stride(1), v.stride(1), c, float(scale))
+    _lib.check(
+        _lib.lib().ctmr_flash_attention(ctypes.byref(desc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                        out.data_ptr(), _stream(q.device)),
+        "ctmr_flash_attention",
+    )
+    return out
+
+
+@flash_attention.register_fake
+def _(q, k, v, heads, scale, query_tiles=0):
+    return q.new_empty(q.shape)

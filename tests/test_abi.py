@@ -115,3 +115,39 @@ def test_group_norm_host_checks(ctmr, native_loaded):
     assert rc == L.E_UNSUPPORTED
     rc = native_loaded.ctmr_resample(0, 1, 1, 4, 4, 4, 0x1000, 0x1000, None)
     assert rc == L.E_INVALID and "pooling" in L.last_error()
+
+
+def test_attention_desc_layout_matches_header(ctmr):
+    """ctmr_attn_desc: six int32, four int64 strides, one float (natural alignment)."""
+    D = ctmr._lib.AttnDesc
+    assert D.ldq.offset == 24 and D.ldo.offset == 48 and D.scale.offset == 56
+    assert ctypes.sizeof(D) == 64
+
+
+@pytest.mark.parametrize(
+    ("kw", "status", "message"),
+    [
+        ({"head_dim": 16}, -2, "head_dim 16 unsupported"),
+        ({"query_tiles": 3}, -1, "query_tiles"),
+        ({"lk": 0}, -1, ">= 1"),
+        ({"n": 300, "heads": 256}, -1, "65535"),
+        ({"ldk": 60}, -1, "below heads"),
+        ({"ldv": 66}, -1, "multiples of 4"),
+        ({"scale": float("inf")}, -1, "finite"),
+    ],
+)
+def test_attention_host_checks(ctmr, native_loaded, kw, status, message):
+    """Every rejection happens on the host, before any launch (fake pointers are never touched)."""
+    base = dict(n=2, lq=64, lk=64, heads=2, head_dim=32, query_tiles=0, ldq=64, ldk=64, ldv=64, ldo=64, scale=0.17)
+    base.update(kw)
+    d = ctmr._lib.AttnDesc(**base)
+    fake = ctypes.c_void_p(1 << 20)
+    rc = native_loaded.ctmr_flash_attention(ctypes.byref(d), fake, fake, fake, fake, None)
+    assert rc == status
+    assert message in ctmr._lib.last_error()
+    assert native_loaded.ctmr_flash_attention(ctypes.byref(d), None, fake, fake, fake, None) == -1
+    good = ctmr._lib.AttnDesc(**{**base, **dict(head_dim=32, query_tiles=0, lk=64, n=2, heads=2, ldk=64,
+                                                 ldv=64, scale=0.17)})
+    misaligned = ctypes.c_void_p((1 << 20) + 4)
+    assert native_loaded.ctmr_flash_attention(ctypes.byref(good), misaligned, fake, fake, fake, None) == -1
+    assert "16-byte aligned" in ctmr._lib.last_error()

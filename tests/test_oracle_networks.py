@@ -197,3 +197,29 @@ def test_controlnet_rejects_bad_condition_shapes(ctmr):
                                         torch.zeros(1, 8, 8, 8, 8), {}, constructor=ctor)
     with pytest.raises(ValueError, match="ddpm-ct"):
         ctmr.maisi.controlnet_residuals(x, None, None, x, {}, constructor={**ctor, "resblock_updown": False})
+
+
+def test_attention_oracle_golden():
+    """Residual spatial self-attention (attention.py:92-160) against the recorded MONAI block."""
+    manifest, a = load_boundary("attention")
+    c = manifest["constructor"]
+    y = mt.attention(_t(a["x"]), mt.to_torch(a), c["norm_num_groups"], c["norm_eps"], c["num_head_channels"],
+                     c["include_fc"])
+    np.testing.assert_allclose(y.numpy(), a["y"], rtol=RES_RTOL, atol=RES_ATOL)
+
+
+def test_planted_unscaled_scores_fail_attention_golden():
+    """Dropping the 1/sqrt(head_dim) score scale (head_dim 1 -> scale 1) must fail the golden."""
+    manifest, a = load_boundary("attention")
+    c = manifest["constructor"]
+    w = mt.to_torch(a)
+    x = _t(a["x"])
+    n = x.shape[0]
+    h = torch.nn.functional.group_norm(x, c["norm_num_groups"], w["norm.weight"], w["norm.bias"], c["norm_eps"])
+    tok = h.reshape(n, x.shape[1], -1).transpose(1, 2)
+    q, k, v = (torch.nn.functional.linear(tok, w[f"attn.to_{m}.weight"], w[f"attn.to_{m}.bias"]) for m in "qkv")
+    out = torch.softmax(q @ k.transpose(1, 2), dim=-1) @ v
+    out = torch.nn.functional.linear(out, w["attn.out_proj.weight"], w["attn.out_proj.bias"])
+    y = x + out.transpose(1, 2).reshape(x.shape)
+    with pytest.raises(AssertionError):
+        np.testing.assert_allclose(y.numpy(), a["y"], rtol=RES_RTOL, atol=RES_ATOL)
