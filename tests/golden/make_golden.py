@@ -7,12 +7,18 @@ the reference regenerates weights from a recipe recorded in each file's
 metadata (``tests/fixture_parameters.py:15-25`` of the reference), which
 ``tests/golden_util.py`` restates.
 
+It also extracts the production weight inventory (tensor name, Torch shape,
+on-disk layout) of the from-mask checkpoints from the reference's data file
+``src/mlx_generate_ctmr/data/maisi_mlx_from_mask_weight_catalog.json`` into
+``from_mask_catalog.json``.
+
 Run once in a container that has the reference checkout:
     python tests/golden/make_golden.py /root/reference
 """
 
 from __future__ import annotations
 
+import json
 import shutil
 import sys
 from pathlib import Path
@@ -47,6 +53,18 @@ def main(reference: Path) -> None:
         dst.parent.mkdir(parents=True, exist_ok=True)
         shutil.copyfile(src_dir / name, dst)
         print(f"copied {name} ({dst.stat().st_size} bytes)")
+    catalog = json.loads((reference / "src" / "mlx_generate_ctmr" / "data" /
+                          "maisi_mlx_from_mask_weight_catalog.json").read_text())
+    slim = {
+        "source": "maisi_mlx_from_mask_weight_catalog.json (name, torch_shape, layout per tensor)",
+        "networks": {
+            net: [[t["name"], t["torch_shape"], t["layout"].rsplit(".", 1)[-1]] for t in spec["tensors"]]
+            for net, spec in catalog["networks"].items()
+        },
+    }
+    out = dst_dir / "from_mask_catalog.json"
+    out.write_text(json.dumps(slim, separators=(",", ":")) + "\n")
+    print(f"wrote {out.name} ({out.stat().st_size} bytes)")
 
 
 if __name__ == "__main__":

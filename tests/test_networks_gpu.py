@@ -255,3 +255,19 @@ def test_unet_step_is_bitwise_reproducible(ctmr, dev):
     args = (_g(a["x"], dev), _g(a["timesteps"], dev), _g(a["class_labels"], dev, torch.int64), _g(a["spacing"], dev), w)
     first = m.denoise_unet_ncdhw(*args, constructor=manifest["constructor"])[1]
     assert torch.equal(first, m.denoise_unet_ncdhw(*args, constructor=manifest["constructor"])[1])
+
+
+def test_unet_golden_through_safetensors_checkpoint(ctmr, dev, tmp_path):
+    """Weights written in the on-disk layout (channels-last convs) and loaded back onto the
+    GPU reproduce the recorded UNet golden."""
+    f = load_fixture("unet.npz")
+    w = {k[len("weight."):]: v for k, v in f.items() if k.startswith("weight.")}
+    path = tmp_path / "model.safetensors"
+    ctmr.weights.save_network(path, w, scale_factor=0.75, prefix="unet.")
+    loaded, scale = ctmr.weights.load_network(path, network="unet", device=dev,
+                                              catalog=[(k, np.shape(v)) for k, v in w.items()])
+    assert scale == 0.75
+    _, y = ctmr.maisi.denoise_unet_ncdhw(_g(f["input.x"], dev), _g(f["input.timesteps"], dev),
+                                         _g(f["input.class_labels"], dev, torch.int64), _g(f["input.spacing"], dev),
+                                         loaded, constructor=f["__metadata__"]["constructor"])
+    np.testing.assert_allclose(_h(y), f["output.velocity"], rtol=UNET_RTOL, atol=UNET_ATOL)
