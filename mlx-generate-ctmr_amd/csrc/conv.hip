@@ -123,6 +123,99 @@ __global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
   }
 }
 
+// Small-cin packing (cin below one K block): one row per output voxel holding
+// every tap's channels, K index tap*cin + c (tap = kd*9 + kh*3 + kw), so the
+// GEMM runs ceil(27*cin / K block) steps instead of 27 padded ones.  Values
+// outside the volume are zero; inside ones get pack_input's affine + SiLU, or
+// its trilinear-2x sample (same helper, so both packings agree bitwise).
+struct Im2colArgs {
+  const float* x;
+  void* out;
+  const float* affine;
+  int64_t total4;        // n * output voxels * cp / 4
+  int d, h, w, c, cp;    // convolved grid (2x the source for trilinear), channels, packed channels
+  int od, oh, ow, stride;
+  int sd, sh, sw;        // source grid
+  int affine_on, silu_on, trilinear, bf16;
+};
+
+__global__ __launch_bounds__(256) void im2col_kernel(Im2colArgs a) {
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total4;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int c4n = a.cp >> 2;
+    const int k0 = (int)(idx % c4n) * 4;
+    int64_t v = idx / c4n;
+    const int ox = (int)(v % a.ow);
+    v /= a.ow;
+    const int oy = (int)(v % a.oh);
+    v /= a.oh;
+    const int oz = (int)(v % a.od);
+    const int b = (int)(v / a.od);
+    f4 val = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = k0 + j;
+      if (k >= 27 * a.c) continue;
+      const int tap = k / a.c, ch = k - tap * a.c;
+      const int z = oz * a.stride + tap / 9 - 1, y = oy * a.stride + (tap / 3) % 3 - 1,
+                x = ox * a.stride + tap % 3 - 1;
+      if (z < 0 || z >= a.d || y < 0 || y >= a.h || x < 0 || x >= a.w) continue;
+      float t;
+      if (a.trilinear)
+        t = trilinear_sample1(a.x + (int64_t)b * a.sd * a.sh * a.sw * a.c, a.sd, a.sh, a.sw, a.c, ch, z, y, x);
+      else
+        t = a.x[((((int64_t)b * a.d + z) * a.h + y) * a.w + x) * a.c + ch];
+      if (a.affine_on) {
+        const float* q = a.affine + ((int64_t)b * a.c + ch) * 2;
+        t = fmaf(t, q[0], q[1]);
+      }
+      if (a.silu_on) t = silu_f(t);
+      val[j] = t;
+    }
+    if (a.bf16) {
+      uint2 packed;
+      packed.x = (unsigned)f32_to_bf16_bits(val[0]) | ((unsigned)f32_to_bf16_bits(val[1]) << 16);
+      packed.y = (unsigned)f32_to_bf16_bits(val[2]) | ((unsigned)f32_to_bf16_bits(val[3]) << 16);
+      reinterpret_cast<uint2*>(a.out)[idx] = packed;
+    } else {
+      reinterpret_cast<f4*>(a.out)[idx] = val;
+    }
+  }
+}
+
+// Small-cout convolution, second stage: the tap-expanded GEMM left, for every
+// padded input row r and column tap*cout + o, z[(tap*cout + o) * zstride + r]
+// = sum_c xpad[r, c] * W[o, c, tap].  Output voxel v sums the 27 taps of its
+// window (top-left padded row stride * v) in ascending tap order after the
+// bias, then adds the residual.  At stride 1 the window rows of consecutive
+// voxels are consecutive for a fixed tap, so each z element is read once and
+// every load is coalesced.
+__global__ __launch_bounds__(256) void tap_sum_kernel(const float* __restrict__ z, int64_t zstride,
+                                                      int64_t rows_per_batch, int P, int Q, int stride, int n,
+                                                      int d, int h, int w, int cout, const float* __restrict__ bias,
+                                                      int batch_bias, const float* __restrict__ res,
+                                                      float* __restrict__ y) {
+  const int64_t S = (int64_t)d * h * w;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < (int64_t)n * S;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int b = (int)(idx / S);
+    const int v = (int)(idx - (int64_t)b * S);
+    const int dd = v / (h * w), r = v - dd * (h * w);
+    const int hh = r / w, ww = r - hh * w;
+    const int64_t row = (int64_t)b * rows_per_batch + (int64_t)stride * dd * P + (int64_t)stride * hh * Q +
+                        stride * ww;
+    for (int o = 0; o < cout; ++o) {
+      float sum = bias ? bias[(batch_bias ? (int64_t)b * cout : 0) + o] : 0.f;
+      const float* zc = z + (int64_t)o * zstride + row;
+#pragma unroll
+      for (int tap = 0; tap < 27; ++tap)
+        sum += zc[(int64_t)tap * cout * zstride + (tap / 9) * P + ((tap / 3) % 3) * Q + tap % 3];
+      if (res) sum += res[idx * cout + o];
+      y[idx * cout + o] = sum;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 2. Weight packing (reference: _nax_conv.py:372-445)
 // ---------------------------------------------------------------------------
@@ -134,7 +227,13 @@ struct WPackArgs {
   void* out;
   int64_t total;
   int cout, cin, ks, np, kblocks, kstep, taps, up, bf16;
+  int layout;      // WL_TAPS, or WL_EXPAND / WL_IM2COL with taps = 1
 };
+
+// Packed-weight layouts.  WL_TAPS: K = (tap, channel).  WL_EXPAND (cout <= 4):
+// one 1x1 GEMM whose column tap*cout + o holds W[o, :, tap].  WL_IM2COL
+// (cin below one K block): K index tap*cin + c holds W[:, c, tap].
+enum { WL_TAPS = 0, WL_EXPAND = 1, WL_IM2COL = 2 };
 
 // Nearest-2x parity fold: tap t of parity p on one axis merges the 3x3x3
 // taps k in [lo, hi]: p=0 -> t0:{0}, t1:{1,2}; p=1 -> t0:{0,1}, t1:{2}
@@ -158,7 +257,11 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(WPackArgs a) {
   const int phase = (int)(t / a.taps);
   const int c = kb * a.kstep + e;
   float val = 0.f;
-  if (col < a.cout && c < a.cin) {
+  if (a.layout == WL_EXPAND) {
+    if (col < 27 * a.cout && c < a.cin) val = a.w[((int64_t)(col % a.cout) * a.cin + c) * 27 + col / a.cout];
+  } else if (a.layout == WL_IM2COL) {
+    if (col < a.cout && c < 27 * a.cin) val = a.w[((int64_t)col * a.cin + c % a.cin) * 27 + c / a.cin];
+  } else if (col < a.cout && c < a.cin) {
     const float* wc = a.w + ((int64_t)col * a.cin + c) * a.ks * a.ks * a.ks;
     if (!a.up) {
       const int kd = tap / (a.ks * a.ks), kh = (tap / a.ks) % a.ks, kw = tap % a.ks;
@@ -204,6 +307,8 @@ struct ConvArgs {
   int oh, ow, s_out;       // output H, W and voxel count (UP remap)
   int taps, split, m_tiles, n_tiles;
   int batch_bias, has_res, has_bias;
+  int planar;              // store column c of voxel v at y[c * zstride + v] (tap-expanded GEMM)
+  int64_t zstride;
 };
 
 template <int DT>
@@ -385,7 +490,8 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
         const int h = rr / p.gw, w = rr - h * p.gw;
         o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
       }
-      const int64_t base = ((int64_t)b * p.s_out + o) * p.cout;
+      const int64_t vox = (int64_t)b * p.s_out + o;
+      const int64_t base = vox * p.cout;
 #pragma unroll
       for (int ns = 0; ns < NSUB; ++ns) {
         const int col = n0 + ns * 16 + lrow;
@@ -395,7 +501,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
           if (p.has_bias) sum += bias_b[col];
           if (p.has_res) sum += p.res[base + col];
         }
-        out[base + col] = sum;
+        out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
       }
     }
   }
@@ -435,7 +541,9 @@ struct Geometry {
   int64_t rows_per_batch;
   int split;
   int nsub, wm, wn, m_tiles, n_tiles;
-  int64_t pack_bytes, part_bytes;
+  int layout;            // WL_TAPS, WL_EXPAND (cout <= 4) or WL_IM2COL (small cin)
+  int ncols;             // GEMM columns: cout, or 27 * cout for WL_EXPAND
+  int64_t pack_bytes, part_bytes, z_bytes;
 };
 
 static int geometry(const ctmr_conv_desc* d, Geometry& g) {
@@ -498,14 +606,43 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     g.P = g.th * g.tw;
     g.rows_per_batch = (int64_t)g.td * g.P;
   }
+  // Shape-selected GEMM formulations of a plain 3x3x3 conv (same results to
+  // fp32 rounding; each keeps a fixed summation order):
+  //  * WL_IM2COL, cin below one K block: K = 27 * cin packed per output voxel
+  //    instead of 27 zero-padded channel blocks (the 4-channel input convs);
+  //  * WL_EXPAND, cout <= 4: a 1x1 GEMM over every padded input
+  //    row with 27 * cout columns, then a 27-tap gather sum (the 1- and
+  //    4-channel output convs, where 16-column MFMA tiles would idle).
+  g.layout = WL_TAPS;
+  g.ncols = d->cout;
+  g.z_bytes = 0;
+  const bool plain_weights = d->mode == CTMR_MODE_PLAIN || d->mode == CTMR_MODE_TRILINEAR2X;
+  if (d->ksize == 3 && plain_weights && d->cin < g.kstep) {
+    g.layout = WL_IM2COL;
+    g.KT = 1;
+    g.taps = 1;
+    g.halo = 0;  // td/th/tw stay the convolved grid: the window bounds of the im2col pack
+    g.cp = (int)round_up(27 * d->cin, g.kstep);
+    g.kblocks = g.cp / g.kstep;
+    g.Q = g.gw;
+    g.P = g.gh * g.gw;
+    g.rows_per_batch = (int64_t)g.gd * g.P;
+  } else if (d->ksize == 3 && plain_weights && d->cout <= 4) {
+    g.layout = WL_EXPAND;
+    g.KT = 1;
+    g.taps = 1;
+    g.ncols = 27 * d->cout;
+    g.np = (int)round_up(g.ncols, 16);
+    g.gd = g.td + 2; g.gh = g.th + 2; g.gw = g.tw + 2;  // GEMM rows: every padded row
+  }
   const int64_t S = (int64_t)g.gd * g.gh * g.gw;
   const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
   if (S > (1ll << 30) || s_out * d->cout > (1ll << 40))
     return fail(CTMR_E_UNSUPPORTED, "volume too large for 32-bit voxel indexing");
-  // Tile shape by output width.
-  if (d->cout <= 16) { g.nsub = 1; g.wm = 4; g.wn = 1; }
-  else if (d->cout <= 32) { g.nsub = 2; g.wm = 4; g.wn = 1; }
-  else if (d->cout <= 64) { g.nsub = 4; g.wm = 4; g.wn = 1; }
+  // Tile shape by GEMM width.
+  if (g.ncols <= 16) { g.nsub = 1; g.wm = 4; g.wn = 1; }
+  else if (g.ncols <= 32) { g.nsub = 2; g.wm = 4; g.wn = 1; }
+  else if (g.ncols <= 64) { g.nsub = 4; g.wm = 4; g.wn = 1; }
   else { g.nsub = 4; g.wm = 2; g.wn = 2; }
   g.m_tiles = (int)ceil_div(S, g.wm * 64);
   g.n_tiles = (int)ceil_div(g.np, g.wn * g.nsub * 16);
@@ -516,7 +653,10 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // are split so the launch fills whole rounds of 512 resident workgroups
   // (two per CU on 256 CUs), keeping at least 8 steps per range.
   const int steps = g.taps * g.kblocks;
-  if (d->split > 0) {
+  if (g.layout == WL_EXPAND) {
+    if (d->split > 1) return fail(CTMR_E_INVALID, "split must be 1 for the cout <= 4 tap-expanded GEMM");
+    g.split = 1;
+  } else if (d->split > 0) {
     if (d->split > steps) return fail(CTMR_E_INVALID, "split must not exceed the K step count");
     g.split = d->split;
   } else {
@@ -531,6 +671,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
   g.pack_bytes = g.pack ? round_up((int64_t)d->n * g.rows_per_batch * g.cp * g.esize, 256) : 0;
   g.part_bytes = g.split > 1 ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
+  if (g.layout == WL_EXPAND) g.z_bytes = (int64_t)g.ncols * d->n * g.rows_per_batch * 4;
   return CTMR_OK;
 }
 
@@ -588,7 +729,7 @@ int64_t ctmr_packed_weight_elems(const ctmr_conv_desc* desc) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
-  const int kblocks = (int)ceil_div(desc->cin, g.kstep);
+  const int kblocks = g.layout == WL_IM2COL ? g.kblocks : (int)ceil_div(desc->cin, g.kstep);
   return (int64_t)g.phases * g.taps * kblocks * g.np * g.kstep;
 }
 
@@ -596,7 +737,7 @@ int64_t ctmr_conv3d_workspace_bytes(const ctmr_conv_desc* desc) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
-  return g.pack_bytes + g.part_bytes;
+  return g.pack_bytes + g.part_bytes + g.z_bytes;
 }
 
 int ctmr_conv3d_split(const ctmr_conv_desc* desc) {
@@ -623,10 +764,11 @@ static int pack_weight_impl(const ctmr_conv_desc* desc, const float* weight, voi
   a.ks = desc->ksize;
   a.np = g.np;
   a.kstep = g.kstep;
-  a.kblocks = (int)ceil_div(desc->cin, g.kstep);
+  a.kblocks = g.layout == WL_IM2COL ? g.kblocks : (int)ceil_div(desc->cin, g.kstep);
   a.taps = g.taps;
   a.up = up ? 1 : 0;
   a.bf16 = desc->dtype == CTMR_BF16;
+  a.layout = g.layout;
   a.total = (int64_t)g.phases * g.taps * a.kblocks * g.np * g.kstep;
   hipLaunchKernelGGL(pack_weight_kernel, dim3(elementwise_blocks(a.total)), dim3(256), 0,
                      (hipStream_t)stream, a);
@@ -643,7 +785,7 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
 }
 
 static int check_workspace(const Geometry& g, const void* workspace, size_t workspace_bytes) {
-  const int64_t need = g.pack_bytes + g.part_bytes;
+  const int64_t need = g.pack_bytes + g.part_bytes + g.z_bytes;
   if ((int64_t)workspace_bytes < need || (need > 0 && !workspace)) {
     set_error("workspace %zu bytes < required %lld", workspace_bytes, (long long)need);
     return CTMR_E_WORKSPACE;
@@ -660,6 +802,26 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
   if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
   if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
   if (!g.pack) return CTMR_OK;
+  if (g.layout == WL_IM2COL) {
+    Im2colArgs ia;
+    ia.x = x;
+    ia.out = workspace;
+    ia.affine = affine;
+    ia.d = g.td; ia.h = g.th; ia.w = g.tw;
+    ia.sd = desc->d; ia.sh = desc->h; ia.sw = desc->w;
+    ia.trilinear = desc->mode == CTMR_MODE_TRILINEAR2X;
+    ia.c = desc->cin;
+    ia.cp = g.cp;
+    ia.od = g.od; ia.oh = g.oh; ia.ow = g.ow;
+    ia.stride = desc->stride;
+    ia.affine_on = (desc->flags & CTMR_F_AFFINE) != 0;
+    ia.silu_on = (desc->flags & CTMR_F_SILU) != 0;
+    ia.bf16 = desc->dtype == CTMR_BF16;
+    ia.total4 = (int64_t)desc->n * g.rows_per_batch * (g.cp / 4);
+    hipLaunchKernelGGL(im2col_kernel, dim3(elementwise_blocks(ia.total4)), dim3(256), 0,
+                       (hipStream_t)stream, ia);
+    return check_launch("im2col");
+  }
   if ((desc->cin & 3) == 0 && ((uintptr_t)x & 15) != 0)
     return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
   PackArgs pa;
@@ -719,13 +881,39 @@ int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* pac
   a.split = g.split;
   a.m_tiles = g.m_tiles;
   a.n_tiles = g.n_tiles;
+  a.planar = 0;
+  a.zstride = 0;
   float* part = (float*)((char*)workspace + g.pack_bytes);
   a.y = g.split > 1 ? part : y;
   if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
+  float* z = (float*)((char*)workspace + g.pack_bytes + g.part_bytes);
+  if (g.layout == WL_EXPAND) {
+    // GEMM over every padded row into planar tap columns; bias and residual
+    // join in the tap sum.
+    a.cout = g.ncols;
+    a.s_out = (int)g.rows_per_batch;
+    a.plane = 0;
+    a.planar = 1;
+    a.zstride = (int64_t)desc->n * g.rows_per_batch;
+    a.y = z;
+    a.bias = nullptr;
+    a.has_bias = 0;
+    a.batch_bias = 0;
+    a.res = nullptr;
+    a.has_res = 0;
+  }
   const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
   ConvFn fn = pick(desc, g);
   fn(dim3((unsigned)blocks), dim3(256), st, a);
   if ((rc = check_launch("conv"))) return rc;
+  if (g.layout == WL_EXPAND) {
+    hipLaunchKernelGGL(tap_sum_kernel, dim3(elementwise_blocks((int64_t)desc->n * s_out)), dim3(256), 0, st,
+                       z, (int64_t)desc->n * g.rows_per_batch, g.rows_per_batch, g.P, g.Q, desc->stride,
+                       desc->n, g.od,
+                       g.oh, g.ow, desc->cout, bias, (desc->flags & CTMR_F_BATCH_BIAS) ? 1 : 0,
+                       (desc->flags & CTMR_F_RESIDUAL) ? residual : nullptr, y);
+    return check_launch("tap_sum");
+  }
   if (g.split > 1) {
     hipLaunchKernelGGL(split_reduce_kernel, dim3(elementwise_blocks(a.plane)), dim3(256), 0, st,
                        part, a.plane, g.split, bias, bias != nullptr ? 1 : 0, a.batch_bias,

@@ -383,6 +383,7 @@ def residual_block(
     eps: float,
     up: bool = False,
     down: bool = False,
+    conv1_bias: Optional[Tensor] = None,
 ) -> Tensor:
     """Fused ``DiffusionUNetResnetBlock`` on NDHWC ``x`` (``fast_fp32.residual_block_ncdhw``, :214-291).
 
@@ -390,10 +391,16 @@ def residual_block(
     path (after its optional 1x1x1 projection) joins conv2's accumulator.
     ``down`` normalizes separately before pooling (pooling does not commute
     with SiLU); ``up`` folds the nearest-2x upsampling into conv1's weights and
-    projects the skip before upsampling it.
+    projects the skip before upsampling it.  ``conv1_bias`` (``(N, O)``) is
+    ``conv1.bias + time_emb_proj(silu(emb))`` when the caller has computed it
+    already (the UNet batches every block's projection into one GEMM); ``emb``
+    is then unused.
     """
-    temb = linear(F.silu(emb), weights["time_emb_proj.weight"], weights["time_emb_proj.bias"])
-    bias1 = weights["conv1.conv.bias"].reshape(1, -1) + temb
+    if conv1_bias is None:
+        temb = linear(F.silu(emb), weights["time_emb_proj.weight"], weights["time_emb_proj.bias"])
+        bias1 = weights["conv1.conv.bias"].reshape(1, -1) + temb
+    else:
+        bias1 = conv1_bias
     norm1 = (weights["norm1.weight"], weights["norm1.bias"])
     project = int(x.shape[-1]) != int(weights["conv1.conv.weight"].shape[0])
 

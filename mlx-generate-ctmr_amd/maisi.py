@@ -20,6 +20,8 @@ on the GPU.  Each public ``*_ncdhw`` function takes and returns NCDHW.
 from __future__ import annotations
 
 import math
+import threading
+import weakref
 from collections.abc import Callable, Mapping, Sequence
 from itertools import product
 from typing import Optional
@@ -121,11 +123,49 @@ def spatial_attention(x: Tensor, weights: Mapping[str, Tensor], *, num_groups: i
 # ---------------------------------------------------------------------------
 # UNet (unet.py:42-487)
 # ---------------------------------------------------------------------------
+# Every residual block's time-embedding projection stacked into one GEMM, with
+# conv1's bias folded into the GEMM bias: keyed by the projection weights' ids
+# and validated by weak references (evicted when a weight is collected).
+_TIME_SUFFIX = ".time_emb_proj.weight"
+_time_proj: dict[tuple[int, ...], tuple] = {}
+_time_proj_lock = threading.Lock()
+
+
+def _time_projections(weights: Mapping[str, Tensor]) -> tuple[Tensor, Tensor, dict[str, tuple[int, int]]]:
+    prefixes = sorted(k[: -len(_TIME_SUFFIX)] for k in weights if k.endswith(_TIME_SUFFIX))
+    mats = [weights[p + _TIME_SUFFIX] for p in prefixes]
+    key = tuple(id(m) for m in mats)
+    with _time_proj_lock:
+        hit = _time_proj.get(key)
+        if hit is not None and all(r() is m for r, m in zip(hit[0], mats)):
+            return hit[1], hit[2], hit[3]
+    weight = torch.cat(mats, dim=0).to(torch.float32).contiguous()
+    bias = torch.cat([_need(weights, f"{p}.time_emb_proj.bias") + _need(weights, f"{p}.conv1.conv.bias")
+                      for p in prefixes]).to(torch.float32).contiguous()
+    spans, start = {}, 0
+    for p, m in zip(prefixes, mats):
+        spans[p] = (start, start + int(m.shape[0]))
+        start += int(m.shape[0])
+
+    def _evict(_ref, key=key):
+        with _time_proj_lock:
+            _time_proj.pop(key, None)
+
+    with _time_proj_lock:
+        _time_proj[key] = (tuple(weakref.ref(m, _evict) for m in mats), weight, bias, spans)
+    return weight, bias, spans
+
+
 def _blocks(weights: Mapping[str, Tensor], emb: Tensor, groups: int, eps: float, include_fc: bool):
-    """Residual-block and attention callables bound to one embedding and weight dict."""
+    """Residual-block and attention callables bound to one embedding and weight dict.  The
+    per-block conv1 biases (``conv1.bias + time_emb_proj(silu(emb))``) come from one GEMM."""
+    proj_w, proj_b, spans = _time_projections(weights)
+    conv1_bias = F.linear(F.silu(emb), proj_w, proj_b)
 
     def resnet(h: Tensor, prefix: str, **kw) -> Tensor:
-        return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps, **kw)
+        lo, hi = spans[prefix]
+        return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps,
+                                 conv1_bias=conv1_bias[:, lo:hi].contiguous(), **kw)
 
     def attention(h: Tensor, prefix: str, n_heads: int) -> Tensor:
         return spatial_attention(h, _prefixed(weights, prefix), num_groups=groups, eps=eps,

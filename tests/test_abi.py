@@ -48,9 +48,19 @@ def test_workspace_and_packed_sizes(ctmr):
     assert L.workspace_bytes(d) == ((66**3 * 64 * 4 + 255) // 256) * 256
     assert L.packed_weight_elems(d) == 27 * 64 * 64
     assert L.conv_split(d) == 1
-    # bf16 halves the copy and rounds channels to 32
+    # cin below one K block packs im2col rows: K = 27 * cin rounded to the block
+    d4 = L.conv_desc(1, 8, 8, 8, 4, 64)
+    assert L.packed_weight_elems(d4) == 112 * 64
+    assert L.workspace_bytes(d4) == 8**3 * 112 * 4
     d16 = L.conv_desc(1, 8, 8, 8, 4, 4, dtype=L.DT_BF16)
-    assert L.packed_weight_elems(d16) == 27 * 32 * 16
+    assert L.packed_weight_elems(d16) == 128 * 16
+    # cout <= 4: one GEMM with 27 * cout columns (padded to 16) over every
+    # padded row, plus the planar tap columns it writes
+    d1 = L.conv_desc(1, 8, 8, 8, 64, 1)
+    assert L.packed_weight_elems(d1) == 4 * 32 * 16
+    assert L.workspace_bytes(d1) == ((10**3 * 64 * 4 + 255) // 256) * 256 + 27 * 10**3 * 4
+    assert L.conv_split(d1) == 1
+    assert L.packed_weight_elems(L.conv_desc(1, 8, 8, 8, 64, 4, stride=2)) == 4 * 112 * 16
     # nearest-2x parity weights: 8 phases x 8 taps
     du = L.conv_desc(1, 4, 4, 4, 32, 48, mode=L.MODE_NEAREST2X)
     assert L.packed_weight_elems(du) == 8 * 8 * 32 * 48

@@ -84,6 +84,21 @@ def test_fused_norm_conv_matches_float64(ctmr, dev, upsample):
     _assert_rel(_h(y), rm.ndhwc_to_ncdhw(expected), REF_REL, f"fused norm conv up={upsample}")
 
 
+@pytest.mark.parametrize(("cin", "cout"), [(3, 8), (32, 2)])
+def test_trilinear_small_channel_layouts_match_materialized(ctmr, dev, cin, cout):
+    """The im2col (small cin) and tap-expanded (small cout) packings sample trilinear-2x with the
+    same helper as the padded packing: bitwise equal to convolving the materialized upsampling."""
+    rng = np.random.default_rng(37)
+    x = _t(rng.standard_normal((2, cin, 3, 4, 5)).astype(np.float32), dev)
+    w = _t((rng.standard_normal((cout, cin, 3, 3, 3)) / np.sqrt(27 * cin)).astype(np.float32), dev)
+    b = _t(rng.standard_normal(cout).astype(np.float32), dev)
+    f = ctmr.fast_fp32
+    fused = f.trilinear_conv3d_ncdhw(x, w, b)
+    assert torch.equal(fused, f.conv3d_ncdhw(f.upsample_trilinear_ncdhw(x), w, b, padding=1))
+    expected = rm.conv3d(rm.upsample_trilinear(rm.ncdhw_to_ndhwc(_h(x))), _h(w), _h(b))
+    _assert_rel(_h(fused), rm.ndhwc_to_ncdhw(expected), FP32_REL, f"trilinear {cin}->{cout}")
+
+
 def test_trilinear_conv_matches_materialized_upsampling(ctmr, dev):
     """Reference test_trilinear_conv_matches_materialized_upsampling (test_fast_fp32.py:130-150): bitwise."""
     rng = np.random.default_rng(7)
@@ -140,7 +155,69 @@ def test_pointwise_conv_matches_matmul(ctmr, dev, cin, cout):
     _assert_rel(_h(y), x.astype(np.float64) @ w[:, :, 0, 0, 0].T.astype(np.float64) + b, REF_REL, f"1x1 {cin}->{cout}")
 
 
+@pytest.mark.parametrize(("shape", "cout", "stride", "fused"), [
+    ((2, 64, 6, 7, 9), 1, 1, True),     # VAE output conv shape class (64 -> 1)
+    ((1, 64, 8, 16, 16), 4, 1, True),   # UNet output conv shape class (64 -> 4)
+    ((2, 20, 7, 6, 5), 3, 1, False),    # channels off the K block
+    ((1, 48, 7, 6, 5), 2, 2, False),    # stride 2
+])
+def test_small_cout_tap_expanded_conv(ctmr, dev, shape, cout, stride, fused):
+    """cout <= 4 runs as a 27*cout-column GEMM plus a fixed-order tap sum; same bar as every conv."""
+    rng = np.random.default_rng(23)
+    n, c = shape[0], shape[1]
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal((n, cout)).astype(np.float32)
+    f = ctmr.fast_fp32
+    xn = rm.ncdhw_to_ndhwc(x)
+    if fused:
+        gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+        res = rng.standard_normal((n, *shape[2:], cout)).astype(np.float32)
+        run = lambda: f.norm_conv3d(_t(xn, dev), _t(w, dev), _t(bias, dev), norm=(_t(gw, dev), _t(gb, dev)),
+                                    num_groups=4, eps=1e-6, apply_silu=True, residual=_t(res, dev))
+        expected = rm.conv3d(rm.group_norm(xn, gw, gb, 4, 1e-6, apply_silu=True), w) + bias[:, None, None, None, :] + res
+    else:
+        run = lambda: f.conv3d(_t(xn, dev), _t(w, dev), _t(bias[0], dev), padding=1, stride=stride)
+        expected = rm.conv3d(xn, w, bias[0], stride=stride)
+    y = run()
+    assert torch.equal(y, run())
+    _assert_rel(_h(y), expected, FP32_REL, f"tap-expanded {shape}->{cout} s{stride}")
+
+
+@pytest.mark.parametrize(("cin", "cout", "stride", "fused"), [
+    (4, 64, 1, False),   # UNet input conv shape class (4 -> 64)
+    (4, 256, 1, False),  # VAE decoder input conv shape class (4 -> 256)
+    (3, 16, 2, True),
+    (1, 4, 1, True),     # small cin and small cout together
+    (8, 40, 1, True),
+])
+def test_small_cin_im2col_conv(ctmr, dev, cin, cout, stride, fused):
+    """cin below one K block packs 27*cin im2col rows (one GEMM step per 16 of them)."""
+    rng = np.random.default_rng(29)
+    n, sp = 2, (6, 9, 7)
+    x = (2 * rng.standard_normal((n, *sp, cin)) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, cin, 3, 3, 3)) / np.sqrt(27 * cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    f = ctmr.fast_fp32
+    if fused:
+        gw = (1 + 0.1 * rng.standard_normal(cin)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(cin)).astype(np.float32)
+        affine = f.group_norm_affine(_t(x, dev), _t(gw, dev), _t(gb, dev), groups=1, eps=1e-6)
+        y = f.implicit_gemm_conv3d(_t(x, dev), f.pack_weight(_t(w, dev)), _t(b, dev), cout=cout, affine=affine,
+                                   silu=True, stride=stride)
+        expected = rm.conv3d(rm.group_norm(x, gw, gb, 1, 1e-6, apply_silu=True), w, b, stride=stride)
+    else:
+        y = f.conv3d(_t(x, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
+        expected = rm.conv3d(x, w, b, stride=stride)
+    _assert_rel(_h(y), expected, FP32_REL, f"im2col {cin}->{cout} s{stride}")
+    with f.precision("bf16"):
+        y16 = f.conv3d(_t(x, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
+    _assert_rel(_h(y16), rm.conv3d(x, w, b, stride=stride), BF16_REL, f"bf16 im2col {cin}->{cout}")
+
+
 @pytest.mark.parametrize(("shape", "cout", "stride", "mode"), [
+    ((1, 64, 6, 7, 9), 1, 1, "plain"),
     ((2, 64, 8, 16, 16), 64, 1, "plain"),
     ((1, 32, 8, 12, 16), 64, 2, "plain"),
     ((2, 64, 4, 8, 8), 32, 1, "nearest"),
