@@ -62,7 +62,9 @@ enum ctmr_conv_flags {
   CTMR_F_AFFINE = 1,     /* y = x*affine[b,c,0] + affine[b,c,1] before the conv */
   CTMR_F_SILU = 2,       /* SiLU after the affine (or on x) before the conv */
   CTMR_F_BATCH_BIAS = 4, /* bias is (N, Cout) instead of (Cout) */
-  CTMR_F_RESIDUAL = 8    /* residual (output-shaped, NDHWC) added before the store */
+  CTMR_F_RESIDUAL = 8,   /* residual (output-shaped, NDHWC) added before the store */
+  CTMR_F_STREAM = 16     /* use the register-streaming GEMM even where the LDS-staged
+                            one applies (comparisons and tests) */
 };
 
 enum ctmr_dtype {
@@ -122,11 +124,16 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  *   affine   (n, cin, 2) fp32 (scale, offset) pairs with CTMR_F_AFFINE, else NULL
  *   residual output-shaped NDHWC with CTMR_F_RESIDUAL, else NULL
  *   y        (n, D', H', W', cout); must not alias x or residual
- * Accumulation order is fixed: taps kd*9+kh*3+kw ascending (outer), input
- * channels in ascending 16-wide (fp32) / 32-wide (bf16) blocks (inner); with a
- * split, each contiguous range of that sequence is summed separately and the
- * partial planes are added in ascending order after the bias.  The split and
- * tiling depend on the shape only, so results are bit-identical run to run.
+ * Accumulation order is fixed for a given desc.  The register-streaming GEMM
+ * visits taps kd*9+kh*3+kw ascending (outer) and input channels in ascending
+ * 16-wide (fp32) / 32-wide (bf16) blocks (inner).  The LDS-staged GEMM, chosen
+ * by shape for large stride-1 fp32 volumes (cin >= 128 and a multiple of 16,
+ * cout % 64 == 0, no resampling, CTMR_F_STREAM not set), stages 16-channel chunks of the input
+ * with their halo (affine + SiLU and zero padding applied while staging) and
+ * visits chunks ascending (outer), taps ascending (inner).  With a split, each
+ * contiguous range of the sequence is summed separately and the partial planes
+ * are added in ascending order after the bias.  Kernel, split and tiling depend
+ * on the desc only, so results are bit-identical run to run.
  */
 int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed,
                 const float* bias, const float* affine, const float* residual, float* y,
@@ -140,7 +147,8 @@ int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed,
  * implicit GEMM (and split reduce) reading it (_nax_conv.py:200-332).  A
  * packed input may be reused by several _gemm calls with the same desc.
  * For a 1x1x1 fp32 conv with cin % 16 == 0 and no affine/SiLU nothing is
- * packed and _gemm reads x directly.
+ * packed and _gemm reads x directly; for the LDS-staged GEMM _pack only keeps
+ * the affine table in `workspace` and _gemm reads x directly.
  */
 int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* affine,
                      void* workspace, size_t workspace_bytes, void* stream);

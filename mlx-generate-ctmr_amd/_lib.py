@@ -18,7 +18,7 @@ HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "ctmr.h"
 OK = 0
 E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_LAUNCH = -1, -2, -3, -4
 MODE_PLAIN, MODE_NEAREST2X, MODE_TRILINEAR2X = 0, 1, 2
-F_AFFINE, F_SILU, F_BATCH_BIAS, F_RESIDUAL = 1, 2, 4, 8
+F_AFFINE, F_SILU, F_BATCH_BIAS, F_RESIDUAL, F_STREAM = 1, 2, 4, 8, 16
 DT_F32, DT_BF16 = 0, 1
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2
 ABI_VERSION = 1

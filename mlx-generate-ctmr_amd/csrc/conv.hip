@@ -460,17 +460,28 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   // multiplies.  The scheduling barriers keep the prefetch loads ahead of the
   // MFMAs that would otherwise be hoisted above them (the compiler's default
   // order issues the loads after the MFMA burst and exposes their latency).
+  //
+  // The prefetch loads are unconditional: under a branch the compiler cannot
+  // count the loads in flight and waits for all of them (vmcnt(0)) before the
+  // current block's MFMAs, i.e. for the prefetch too.  A prefetch past the
+  // last step reads through the buffer descriptors -- in range it is data
+  // that is never used, out of range the hardware returns zeros -- so it is
+  // harmless.
   u4 A0[4], B0[NSUB], A1[4], B1[NSUB];
   load(A0, B0);  // step s_begin; each load() fetches the cursor's step, then advances it
   for (int s = s_begin; s < s_end; s += 2) {
-    if (s + 1 < s_end) load(A1, B1);
+    load(A1, B1);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);  // MFMA bursts win issue slots over address/load code
     compute(A0, B0);
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
     if (s + 1 >= s_end) break;
-    if (s + 2 < s_end) load(A0, B0);
+    load(A0, B0);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
     compute(A1, B1);
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -502,6 +513,222 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
           if (p.has_res) sum += p.res[base + col];
         }
         out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3b. LDS-staged implicit GEMM (large stride-1 fp32 volumes)
+// ---------------------------------------------------------------------------
+// A workgroup owns a 4x8x8 brick of output voxels (256 GEMM rows: wave m holds
+// depth m, MFMA row block ms holds brick rows 2ms and 2ms+1, lane%16 -> (row
+// parity, column)) and 64 output channels.  For each 16-channel chunk it
+// stages the brick's 6x10x10 halo from the unpadded NDHWC input into LDS --
+// zero outside the volume, group-norm affine + SiLU applied on the way, so the
+// streaming path's separate pack pass disappears -- then runs all 27 taps with
+// A read from LDS at compile-time offsets and B (packed weight) fetched one tap
+// ahead through buffer loads.  The next chunk's halo is in flight in registers
+// while the current chunk multiplies.  A staged voxel row is 80 bytes (16
+// channels + 16 bytes of padding), which spreads the 8 rows of each
+// ds_read_b128 quarter-wave over distinct banks.
+constexpr int kBD = 4, kBH = 8, kBW = 8;
+constexpr int kHD = kBD + 2, kHH = kBH + 2, kHW = kBW + 2;
+constexpr int kHaloVox = kHD * kHH * kHW;                 // 600
+constexpr int kLdsRow = 80;
+constexpr int kStageIters = (kHaloVox * 4 + 255) / 256;  // 16-byte pieces per thread
+
+struct LdsArgs {
+  const float* x;       // unpadded NDHWC input
+  const float* affine;  // (n, cin, 2) or null
+  const char* wp;       // packed weight [tap][kblock][np][64 bytes]
+  const float* bias;
+  const float* res;
+  float* y;             // output, or split partial planes
+  int64_t x_bytes, w_bytes, plane;
+  int n, d, h, w, cin, cout, np, kb;
+  int tz, ty, tx;       // bricks per axis
+  int n_tiles, split;
+  int affine_on, silu_on, batch_bias, has_res, has_bias;
+};
+
+__global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
+  __shared__ __attribute__((aligned(16))) char lds[kHaloVox * kLdsRow];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-aware order (as conv_kernel): neighbouring bricks share halo planes.
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int xcd = bid & 7, slot = bid >> 3, per = nb >> 3, rem = nb & 7;
+  const int tile = (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int n_tile = tile % p.n_tiles;
+  int rest = tile / p.n_tiles;
+  const int bx = rest % p.tx;
+  rest /= p.tx;
+  const int by = rest % p.ty;
+  rest /= p.ty;
+  const int bz = rest % p.tz;
+  rest /= p.tz;
+  const int b = rest % p.n;
+  const int split_id = rest / p.n;
+  const int z0 = bz * kBD, y0 = by * kBH, x0 = bx * kBW;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+
+  // Staging: piece i of thread t is channels 4*(t&3)..+3 of the chunk at halo
+  // voxel (t>>2) + 64i.  Offsets are relative to the first staged plane, so
+  // they stay within 32 bits (the host checks 6 planes fit).
+  const int part = tid & 3;
+  const int zb = max(z0 - 1, 0);
+  const int64_t xbase = ((int64_t)b * p.d + zb) * p.h * p.w * p.cin * 4;
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const char*)p.x + xbase), (short)0, (int)min(p.x_bytes - xbase, (int64_t)0x7fffffff),
+      0x00020000);
+  int goff[kStageIters];
+  unsigned valid = 0;
+#pragma unroll
+  for (int i = 0; i < kStageIters; ++i) {
+    const int hv = (tid >> 2) + 64 * i;
+    goff[i] = 0;
+    if (hv < kHaloVox) {
+      const int hz = hv / (kHH * kHW), hr = hv - hz * (kHH * kHW);
+      const int hy = hr / kHW, hx = hr - hy * kHW;
+      const int gz = z0 - 1 + hz, gy = y0 - 1 + hy, gx = x0 - 1 + hx;
+      if (gz >= 0 && gz < p.d && gy >= 0 && gy < p.h && gx >= 0 && gx < p.w) {
+        valid |= 1u << i;
+        goff[i] = (int)((((int64_t)(gz - zb) * p.h + gy) * p.w + gx) * p.cin * 4) + part * 16;
+      }
+    }
+  }
+
+  // A: LDS byte address of this lane's voxel at tap (0,0,0) per row block.
+  int abase[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+    abase[ms] = ((wave * kHH + 2 * ms + (lrow >> 3)) * kHW + (lrow & 7)) * kLdsRow + lgrp * 16;
+  // B: one output column per lane per 16-column block.
+  const int n0 = n_tile * 64;
+  const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wp, (short)0, (int)min(p.w_bytes, (int64_t)0x7fffffff), 0x00020000);
+  int boff[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) boff[ns] = min(n0 + ns * 16 + lrow, p.np - 1) * 64 + lgrp * 16;
+  const int bchunk = p.np * 64;
+
+  f4 acc[4][4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int c_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)split_id * p.kb / p.split));
+  const int c_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(split_id + 1) * p.kb / p.split));
+
+  u4 stage[kStageIters];
+  auto fetch = [&](int chunk) {
+    const int so = __builtin_amdgcn_readfirstlane(chunk * 64);
+#pragma unroll
+    for (int i = 0; i < kStageIters; ++i) stage[i] = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, goff[i], so, 0);
+  };
+  auto commit = [&](int chunk) {
+    f4 sc = {1.f, 1.f, 1.f, 1.f}, of = {0.f, 0.f, 0.f, 0.f};
+    if (p.affine_on) {
+      const f4* q = reinterpret_cast<const f4*>(p.affine + ((int64_t)b * p.cin + chunk * 16 + part * 4) * 2);
+      const f4 a0 = q[0], a1 = q[1];
+      sc = f4{a0[0], a0[2], a1[0], a1[2]};
+      of = f4{a0[1], a0[3], a1[1], a1[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < kStageIters; ++i) {
+      const int hv = (tid >> 2) + 64 * i;
+      if (hv >= kHaloVox) continue;
+      f4 v = __builtin_bit_cast(f4, stage[i]);
+      const bool in = (valid >> i) & 1u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float t = v[j];
+        if (p.affine_on) t = fmaf(t, sc[j], of[j]);
+        if (p.silu_on) t = silu_f(t);
+        v[j] = in ? t : 0.f;
+      }
+      *reinterpret_cast<f4*>(lds + hv * kLdsRow + part * 16) = v;
+    }
+  };
+  auto load_a = [&](f4 (&A)[4], int tap) {
+    const int off = (((tap / 9) * kHH + (tap / 3) % 3) * kHW + tap % 3) * kLdsRow;
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) A[ms] = *reinterpret_cast<const f4*>(lds + abase[ms] + off);
+  };
+  auto load_b = [&](u4 (&B)[4], int tap, int chunk) {
+    const int so = __builtin_amdgcn_readfirstlane((tap * p.kb + chunk) * bchunk);
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) B[ns] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, boff[ns], so, 0);
+  };
+  auto mma = [&](const f4 (&A)[4], const u4 (&B)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns)
+          acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x4f32(A[ms][j], __builtin_bit_cast(f4, B[ns])[j],
+                                                             acc[ms][ns], 0, 0, 0);
+  };
+
+  fetch(c_begin);
+  for (int chunk = c_begin; chunk < c_end; ++chunk) {
+    __syncthreads();  // every wave has finished reading the previous chunk
+    commit(chunk);
+    __syncthreads();
+    f4 A[2][4];
+    u4 B[2][4];
+    load_b(B[0], 0, chunk);
+    load_a(A[0], 0);
+    // Unconditional (see conv_kernel): the last chunk re-reads itself.
+    const int next_so = __builtin_amdgcn_readfirstlane(min(chunk + 1, c_end - 1) * 64);
+#pragma unroll
+    for (int t = 0; t < 27; ++t) {
+      if (t + 1 < 27) {
+        load_b(B[(t + 1) & 1], t + 1, chunk);
+        load_a(A[(t + 1) & 1], t + 1);
+      }
+      // The next chunk's halo, one 16-byte piece every other tap: loads
+      // retire in order, so each piece has two taps of products to arrive
+      // before a later weight load has to wait for it.
+      if ((t & 1) && (t >> 1) < kStageIters)
+        stage[t >> 1] = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, goff[t >> 1], next_so, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      // Raised priority while this wave's MFMAs issue, so a wave whose
+      // operands are ready wins issue slots over waves in their staging code.
+      __builtin_amdgcn_s_setprio(1);
+      mma(A[t & 1], B[t & 1]);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Epilogue: D row 4*(lane/16)+r of block ms is brick row 2ms + lane/32,
+  // column 4*((lane/16)&1) + r.
+  const bool partial = p.split > 1;
+  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
+  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
+  const int z = z0 + wave;
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+    const int y = y0 + 2 * ms + (lgrp >> 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int x = x0 + 4 * (lgrp & 1) + r;
+      if (z >= p.d || y >= p.h || x >= p.w) continue;
+      const int64_t base = ((((int64_t)b * p.d + z) * p.h + y) * p.w + x) * p.cout;
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) {
+        const int col = n0 + ns * 16 + lrow;
+        if (col >= p.cout) continue;
+        float sum = acc[ms][ns][r];
+        if (!partial) {
+          if (p.has_bias) sum += bias_b[col];
+          if (p.has_res) sum += p.res[base + col];
+        }
+        out[base + col] = sum;
       }
     }
   }
@@ -541,6 +768,8 @@ struct Geometry {
   int64_t rows_per_batch;
   int split;
   int nsub, wm, wn, m_tiles, n_tiles;
+  bool lds;              // LDS-staged GEMM (conv_lds_kernel)
+  int tz, ty, tx;        // its bricks per axis
   int layout;            // WL_TAPS, WL_EXPAND (cout <= 4) or WL_IM2COL (small cin)
   int ncols;             // GEMM columns: cout, or 27 * cout for WL_EXPAND
   int64_t pack_bytes, part_bytes, z_bytes;
@@ -639,6 +868,43 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
   if (S > (1ll << 30) || s_out * d->cout > (1ll << 40))
     return fail(CTMR_E_UNSUPPORTED, "volume too large for 32-bit voxel indexing");
+  // LDS-staged GEMM: stride-1 fp32 volumes whose 4x8x8 bricks are at least
+  // 3/4 full, with at least 128 input channels (8 staged chunks; below that
+  // the per-chunk staging and barriers cost more than the pack pass they
+  // replace, measured on MI355X), 64-wide column tiles, and 6 staged planes
+  // within 32-bit buffer offsets.
+  g.lds = false;
+  if (g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 && d->stride == 1 &&
+      d->mode == CTMR_MODE_PLAIN && d->cin % 16 == 0 && d->cin >= 128 && d->cout % 64 == 0 &&
+      !(d->flags & CTMR_F_STREAM)) {
+    g.tz = (int)ceil_div(d->d, kBD);
+    g.ty = (int)ceil_div(d->h, kBH);
+    g.tx = (int)ceil_div(d->w, kBW);
+    const int64_t slots = (int64_t)g.tz * g.ty * g.tx * kBD * kBH * kBW;
+    const int64_t planes = (int64_t)kHD * d->h * d->w * d->cin * 4;
+    if (4 * S >= 3 * slots && planes < (1ll << 31)) g.lds = true;
+  }
+  if (g.lds) {
+    g.pack = false;
+    g.cp = d->cin;
+    g.kblocks = d->cin / 16;
+    g.nsub = 4; g.wm = 4; g.wn = 1;
+    g.m_tiles = g.tz * g.ty * g.tx;
+    g.n_tiles = d->cout / 64;
+    const int chunks = g.kblocks;
+    if (d->split > 0) {
+      if (d->split > chunks) return fail(CTMR_E_INVALID, "split must not exceed the 16-channel chunk count");
+      g.split = d->split;
+    } else {
+      const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n;
+      g.split = base < 512 ? (int)std::min<int64_t>(ceil_div(512, base), chunks) : 1;
+    }
+    g.pack_bytes = (d->flags & CTMR_F_AFFINE) ? round_up((int64_t)d->n * d->cin * 2 * 4, 256) : 0;
+    g.part_bytes = g.split > 1 ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * g.split;
+    if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
+    return CTMR_OK;
+  }
   // Tile shape by GEMM width.
   if (g.ncols <= 16) { g.nsub = 1; g.wm = 4; g.wn = 1; }
   else if (g.ncols <= 32) { g.nsub = 2; g.wm = 4; g.wn = 1; }
@@ -801,6 +1067,13 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
   if (!x) return fail(CTMR_E_INVALID, "null input");
   if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
   if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
+  if (g.lds) {
+    if (!(desc->flags & CTMR_F_AFFINE)) return CTMR_OK;
+    if (hipMemcpyAsync(workspace, affine, (size_t)desc->n * desc->cin * 2 * 4, hipMemcpyDeviceToDevice,
+                       (hipStream_t)stream) != hipSuccess)
+      return fail(CTMR_E_LAUNCH, "affine copy failed");
+    return CTMR_OK;
+  }
   if (!g.pack) return CTMR_OK;
   if (g.layout == WL_IM2COL) {
     Im2colArgs ia;
@@ -858,6 +1131,40 @@ int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* pac
   if (!g.pack && ((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
+  if (g.lds) {
+    LdsArgs a;
+    a.x = x;
+    a.affine = (desc->flags & CTMR_F_AFFINE) ? (const float*)workspace : nullptr;
+    a.wp = (const char*)packed;
+    a.bias = bias;
+    a.res = residual;
+    a.x_bytes = (int64_t)desc->n * desc->d * desc->h * desc->w * desc->cin * 4;
+    a.w_bytes = (int64_t)27 * g.kblocks * g.np * 64;
+    a.plane = (int64_t)desc->n * s_out * desc->cout;
+    a.n = desc->n; a.d = desc->d; a.h = desc->h; a.w = desc->w;
+    a.cin = desc->cin; a.cout = desc->cout; a.np = g.np; a.kb = g.kblocks;
+    a.tz = g.tz; a.ty = g.ty; a.tx = g.tx;
+    a.n_tiles = g.n_tiles;
+    a.split = g.split;
+    a.affine_on = (desc->flags & CTMR_F_AFFINE) != 0;
+    a.silu_on = (desc->flags & CTMR_F_SILU) != 0;
+    a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
+    a.has_bias = bias != nullptr;
+    a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
+    float* part = (float*)((char*)workspace + g.pack_bytes);
+    a.y = g.split > 1 ? part : y;
+    if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.split;
+    hipLaunchKernelGGL(conv_lds_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    if ((rc = check_launch("conv_lds"))) return rc;
+    if (g.split > 1) {
+      hipLaunchKernelGGL(split_reduce_kernel, dim3(elementwise_blocks(a.plane)), dim3(256), 0, st, part,
+                         a.plane, g.split, bias, bias != nullptr ? 1 : 0, a.batch_bias,
+                         (desc->flags & CTMR_F_RESIDUAL) ? residual : nullptr, y, desc->cout, s_out);
+      if ((rc = check_launch("split_reduce"))) return rc;
+    }
+    return CTMR_OK;
+  }
   ConvArgs a;
   a.xp = xp;
   a.wp = (const char*)packed;

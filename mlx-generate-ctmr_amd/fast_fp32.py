@@ -158,6 +158,7 @@ def implicit_gemm_conv3d(
     trilinear: bool = False,
     residual: Optional[Tensor] = None,
     split: int = 0,
+    stream_gemm: bool = False,
 ) -> Tensor:
     """Padding-1 3x3x3 (or 1x1x1) convolution of NDHWC ``x`` (``_nax_conv.nax_conv3d``).
 
@@ -166,7 +167,10 @@ def implicit_gemm_conv3d(
     pairs applied before SiLU; ``upsample`` convolves the nearest-2x upsampling
     with weights from ``pack_upsample_weight``; ``trilinear`` convolves the
     half-pixel trilinear-2x upsampling (plain stride-1 only); ``residual`` has
-    the output's shape.  ``split`` forces a tap split (0: library policy).
+    the output's shape.  ``split`` forces a K split (0: library policy).
+    ``stream_gemm`` keeps the register-streaming GEMM where the library would
+    pick the LDS-staged one (large stride-1 fp32 volumes); both are exact to
+    fp32 rounding with different fixed summation orders.
 
     Raises:
         ValueError: on a packed weight that does not fit, unsupported option
@@ -182,7 +186,8 @@ def implicit_gemm_conv3d(
         raise ValueError("1x1x1 convolution supports only stride 1 without resampling")
     mode = _lib.MODE_NEAREST2X if upsample else (_lib.MODE_TRILINEAR2X if trilinear else _lib.MODE_PLAIN)
     code = _lib.DT_BF16 if packed.dtype == torch.bfloat16 else _lib.DT_F32
-    desc = ops.make_desc(tuple(x.shape), cout, ksize, stride, mode, 0, code, split)
+    desc = ops.make_desc(tuple(x.shape), cout, ksize, stride, mode, _lib.F_STREAM if stream_gemm else 0, code,
+                         split)
     if packed.numel() != _lib.packed_weight_elems(desc):
         raise ValueError(
             f"packed weight of {packed.numel()} elements does not fit {cin} input / {cout} output "
@@ -200,7 +205,8 @@ def implicit_gemm_conv3d(
         residual = _require(residual, "residual")
         if tuple(residual.shape) != out_shape:
             raise ValueError(f"residual shape {tuple(residual.shape)} != output {out_shape}")
-    return ops.conv3d(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split)
+    return ops.conv3d(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split,
+                      stream_gemm)
 
 
 def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, stride: int = 1) -> Tensor:

@@ -97,11 +97,15 @@ def conv3d(
     silu: bool,
     dtype: int,
     split: int,
+    stream_gemm: bool = False,
 ) -> Tensor:
-    """``ctmr_conv3d`` on an NDHWC fp32 tensor; returns the NDHWC output."""
+    """``ctmr_conv3d`` on an NDHWC fp32 tensor; returns the NDHWC output.  ``stream_gemm``
+    forces the register-streaming GEMM where the LDS-staged one would be chosen."""
     _require_device(x, packed, bias, affine, residual)
     batch_bias = bias is not None and bias.dim() == 2
     flags = _flags(affine is not None, silu, batch_bias, residual is not None)
+    if stream_gemm:
+        flags |= _lib.F_STREAM
     desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split)
     od, oh, ow = _lib.output_dims(desc)
     y = torch.empty((x.shape[0], od, oh, ow, cout), device=x.device, dtype=torch.float32)
@@ -118,7 +122,7 @@ def conv3d(
 
 
 @conv3d.register_fake
-def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split):
+def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split, stream_gemm=False):
     desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, 0, dtype, split)
     od, oh, ow = _lib.output_dims(desc)
     return x.new_empty((x.shape[0], od, oh, ow, cout))

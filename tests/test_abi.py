@@ -44,10 +44,18 @@ def test_output_dims(ctmr, dims, kw, expected):
 def test_workspace_and_packed_sizes(ctmr):
     L = ctmr._lib
     d = L.conv_desc(1, 64, 64, 64, 64, 64)
-    # padded copy: 66^3 rows x 64 fp32 channels, 256-byte aligned; no split
+    # streaming GEMM (cin < 128): padded copy, 66^3 rows x 64 fp32 channels, 256-byte aligned
     assert L.workspace_bytes(d) == ((66**3 * 64 * 4 + 255) // 256) * 256
     assert L.packed_weight_elems(d) == 27 * 64 * 64
     assert L.conv_split(d) == 1
+    # the LDS-staged GEMM (cin >= 128) reads x directly: no workspace without affine or
+    # split, just the (n, cin, 2) affine table with one; same packed weight
+    d128 = L.conv_desc(1, 64, 64, 64, 128, 128)
+    assert L.workspace_bytes(d128) == 0
+    assert L.workspace_bytes(L.conv_desc(1, 64, 64, 64, 128, 128, flags=L.F_AFFINE)) == 1024
+    assert L.packed_weight_elems(d128) == 27 * 128 * 128
+    ds = L.conv_desc(1, 64, 64, 64, 128, 128, flags=L.F_STREAM)
+    assert L.workspace_bytes(ds) == ((66**3 * 128 * 4 + 255) // 256) * 256
     # cin below one K block packs im2col rows: K = 27 * cin rounded to the block
     d4 = L.conv_desc(1, 8, 8, 8, 4, 64)
     assert L.packed_weight_elems(d4) == 112 * 64
@@ -75,13 +83,19 @@ def test_split_policy_is_shape_only(ctmr):
     assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512)) == 32  # 16 tiles x 32
     assert L.conv_split(L.conv_desc(2, 8, 16, 16, 256, 256)) == 8  # 64 tiles x 8
     assert L.conv_split(L.conv_desc(2, 16, 32, 32, 128, 128)) == 2  # 256 tiles x 2
+    assert L.conv_split(L.conv_desc(2, 16, 32, 32, 64, 64)) == 4  # streaming: 128 tiles x 4
     # large grids never split
     assert L.conv_split(L.conv_desc(1, 128, 128, 128, 128, 128)) == 1
     assert L.conv_split(L.conv_desc(1, 64, 64, 64, 64, 64)) == 1
-    # an explicit split may be any count up to the step count (27 taps x 32 blocks here)
+    # an explicit split may be any count up to the K step count: 16-channel
+    # chunks for the LDS-staged GEMM, (27 taps x 32 blocks) for the streaming one
     assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=5)) == 5
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=32)) == 32
+    with pytest.raises(L.CtmrError, match="chunk count"):
+        L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=33))
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32, flags=L.F_STREAM)) == 27 * 32
     with pytest.raises(L.CtmrError, match="step count"):
-        L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32 + 1))
+        L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32 + 1, flags=L.F_STREAM))
 
 
 @pytest.mark.parametrize(

@@ -134,6 +134,44 @@ def test_forced_tap_split_matches_float64(ctmr, dev, split):
     _assert_rel(_h(y1), rm.conv3d(x, w, b) + res, FP32_REL, f"split {split}")
 
 
+@pytest.mark.parametrize(("shape", "cout", "fused", "split"), [
+    ((2, 8, 16, 16, 128), 128, True, 0),   # whole bricks, GN affine + SiLU, batch bias, residual
+    ((2, 7, 16, 15, 128), 64, True, 0),    # ragged bricks (masked rows)
+    ((1, 4, 8, 8, 512), 512, False, 0),    # one brick: chunk split filling the device
+    ((1, 12, 16, 8, 128), 128, False, 3),  # forced uneven chunk split
+])
+def test_lds_staged_and_streaming_gemms_match_float64(ctmr, dev, shape, cout, fused, split):
+    """The LDS-staged GEMM (halo bricks in LDS, affine + SiLU applied while staging) and the
+    register-streaming GEMM over the packed copy both meet the bar; each is deterministic."""
+    rng = np.random.default_rng(41)
+    n, c = shape[0], shape[-1]
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal((n, cout)).astype(np.float32)
+    res = rng.standard_normal((*shape[:-1], cout)).astype(np.float32)
+    f = ctmr.fast_fp32
+    packed = f.pack_weight(_t(w, dev))
+    if fused:
+        gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+        affine = f.group_norm_affine(_t(x, dev), _t(gw, dev), _t(gb, dev), groups=8, eps=1e-6)
+        expected = (rm.conv3d(rm.group_norm(x, gw, gb, 8, 1e-6, apply_silu=True), w)
+                    + bias[:, None, None, None, :] + res)
+    else:
+        affine = None
+        expected = rm.conv3d(x, w) + bias[:, None, None, None, :] + res
+    outs = []
+    for stream_gemm in (False, True):
+        run = lambda: f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), cout=cout, affine=affine,
+                                             silu=fused, residual=_t(res, dev), split=split,
+                                             stream_gemm=stream_gemm)
+        y = run()
+        assert torch.equal(y, run())
+        _assert_rel(_h(y), expected, FP32_REL, f"{'streaming' if stream_gemm else 'lds'} {shape}->{cout}")
+        outs.append(_h(y))
+    assert rm.max_rel_error(outs[0], outs[1]) <= 2 * FP32_REL
+
+
 def test_repeat_runs_are_bitwise_identical(ctmr, dev):
     rng = np.random.default_rng(13)
     x = _t(rng.standard_normal((2, 12, 10, 9, 48)).astype(np.float32), dev)
