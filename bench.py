@@ -14,6 +14,10 @@ parity tests compare against), timed on this host's cores.
 ``secondary`` reports the other configs' GPU numbers (config 1 residual
 block, config 2 resolution-change convs, bf16 variant of config 0).
 
+Warm-up before the headline timed region: W untimed steps, continued until 1 s
+has passed so the GPU clock settles (a cold device runs ~10 % slower for its
+first several hundred milliseconds of work).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
 """
 
@@ -38,6 +42,26 @@ HBM_PEAK = 8.0e12
 
 def conv_flops(n, d, h, w, cin, cout, taps=27):
     return 2.0 * n * d * h * w * cin * cout * taps
+
+
+SETTLE_S = 1.0
+
+
+def warm_up(fn, steps, settle_s=SETTLE_S):
+    """Untimed warm-up: `steps` calls, continued until `settle_s` seconds have passed so the
+    GPU clock reaches its steady state (measured on MI355X: config 0 runs ~10 % slower until
+    several hundred milliseconds of work have passed).  Returns the number of calls made."""
+    import torch
+
+    t0 = time.perf_counter()
+    done = 0
+    while done < steps or time.perf_counter() - t0 < settle_s:
+        fn()
+        done += 1
+        if done % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return done
 
 
 def _wall_ms(fn, steps):
@@ -329,6 +353,12 @@ def profile_only(pkg, dev, what, steps, warmup):
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
         z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 20, 64, 64, 4), dtype=np.float32)).to(dev)
         fn = lambda: m.decode_vae(z, w, constructor=vc)
+    elif what == "attention":
+        # production UNet level-2 attention: 16x16x8 latent = 2048 tokens, 256 channels = 8 heads, batch 2
+        g = torch.Generator(device=dev).manual_seed(0)
+        qkv = torch.randn(2, 2048, 3 * 256, device=dev, generator=g)
+        q, k, v = qkv[..., :256], qkv[..., 256:512], qkv[..., 512:]
+        fn = lambda: f.flash_attention(q, k, v, heads=8, scale=32 ** -0.5)
     else:
         rng = np.random.default_rng(1)
         x = torch.from_numpy(rng.standard_normal((1, 128, 128, 128, 128), dtype=np.float32)).to(dev)
@@ -336,8 +366,7 @@ def profile_only(pkg, dev, what, steps, warmup):
         b = torch.zeros(128, device=dev)
         g, z0 = torch.ones(128, device=dev), torch.zeros(128, device=dev)
         fn = lambda: f.vae_resblock([x], (w1, b), (w1, b), (g, z0), (g, z0), None, num_groups=32, eps=1e-6)
-    for _ in range(warmup):
-        fn()
+    warm_up(fn, warmup)
     ms = _wall_ms(fn, steps)
     print(json.dumps({"only": what, "ms": round(ms, 3), "steps": steps}), flush=True)
     return 0
@@ -352,7 +381,7 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "decode", "resblock"],
+    ap.add_argument("--only", choices=["unet", "decode", "resblock", "attention"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
@@ -388,9 +417,7 @@ def main() -> int:
     flops = conv_flops(n, s, s, s, cin, cout)
 
     step = lambda: f.conv3d(x, w, b, padding=1)
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_up(step, args.warmup)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()

@@ -1116,9 +1116,21 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
   return check_launch("pack_input");
 }
 
+static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                            const float* affine_direct, const float* residual, float* y, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* packed,
                      const float* bias, const float* residual, float* y, void* workspace,
                      size_t workspace_bytes, void* stream) {
+  return conv3d_gemm_impl(desc, x, packed, bias, nullptr, residual, y, workspace, workspace_bytes, stream);
+}
+
+// affine_direct: the caller's (n, cin, 2) table when the pack stage was skipped
+// (ctmr_conv3d on the LDS path); null means "read it from the workspace".
+static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                            const float* affine_direct, const float* residual, float* y, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
@@ -1134,7 +1146,7 @@ int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* pac
   if (g.lds) {
     LdsArgs a;
     a.x = x;
-    a.affine = (desc->flags & CTMR_F_AFFINE) ? (const float*)workspace : nullptr;
+    a.affine = (desc->flags & CTMR_F_AFFINE) ? (affine_direct ? affine_direct : (const float*)workspace) : nullptr;
     a.wp = (const char*)packed;
     a.bias = bias;
     a.res = residual;
@@ -1237,6 +1249,10 @@ int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed, 
   int rc = geometry(desc, g);
   if (rc) return rc;
   if (!x || !packed || !y) return fail(CTMR_E_INVALID, "null input, weight or output");
+  if (g.lds) {  // no pack stage: the LDS GEMM reads x and the caller's affine table directly
+    if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
+    return conv3d_gemm_impl(desc, x, packed, bias, affine, residual, y, workspace, workspace_bytes, stream);
+  }
   if ((rc = ctmr_conv3d_pack(desc, x, affine, workspace, workspace_bytes, stream))) return rc;
   return ctmr_conv3d_gemm(desc, x, packed, bias, residual, y, workspace, workspace_bytes, stream);
 }

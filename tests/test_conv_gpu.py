@@ -328,3 +328,51 @@ def test_validation_errors(ctmr, dev):
         f.implicit_gemm_conv3d(x, packed, None, cout=16, residual=torch.zeros((1, 4, 4, 4, 8), device=dev))
     with pytest.raises(ValueError, match="does not fit"):
         f.implicit_gemm_conv3d(torch.zeros((1, 4, 4, 4, 32), device=dev), packed, None, cout=16)
+
+
+@pytest.mark.parametrize(("shape", "cout", "flags_extra"), [
+    ((2, 8, 16, 16, 128), 128, 0),                 # LDS-staged GEMM: _pack keeps the affine table
+    ((2, 8, 16, 16, 64), 64, 0),                   # streaming GEMM: _pack writes the padded copy
+    ((2, 8, 16, 16, 128), 128, 16),                # CTMR_F_STREAM on an LDS-eligible shape
+])
+def test_two_stage_abi_equals_combined_call(ctmr, dev, shape, cout, flags_extra):
+    """ctmr_conv3d_pack + ctmr_conv3d_gemm on one stream == ctmr_conv3d, bitwise, with the GN
+    affine + SiLU, per-batch bias and residual flags set (include/ctmr.h contract)."""
+    import ctypes
+
+    L = ctmr._lib
+    rng = np.random.default_rng(43)
+    n, c = shape[0], shape[-1]
+    f = ctmr.fast_fp32
+    x = _t((2 * rng.standard_normal(shape) + 0.5).astype(np.float32), dev)
+    w = _t((rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32), dev)
+    bias = _t(rng.standard_normal((n, cout)).astype(np.float32), dev)
+    res = _t(rng.standard_normal((*shape[:-1], cout)).astype(np.float32), dev)
+    affine = f.group_norm_affine(x, _t(np.ones(c, np.float32), dev), _t(np.zeros(c, np.float32), dev),
+                                 groups=8, eps=1e-6)
+    flags = L.F_AFFINE | L.F_SILU | L.F_BATCH_BIAS | L.F_RESIDUAL | flags_extra
+    d = L.conv_desc(*shape[:4], c, cout, flags=flags)
+    packed = f.pack_weight(w)
+    ws_bytes = L.workspace_bytes(d)
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = L.lib()
+    outs = []
+    for staged in (False, True):
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        y = torch.empty((*shape[:-1], cout), device=dev)
+        if staged:
+            L.check(lib.ctmr_conv3d_pack(ctypes.byref(d), x.data_ptr(), affine.data_ptr(), ws.data_ptr(), ws_bytes,
+                                         stream), "pack")
+            L.check(lib.ctmr_conv3d_gemm(ctypes.byref(d), x.data_ptr(), packed.data_ptr(), bias.data_ptr(),
+                                         res.data_ptr(), y.data_ptr(), ws.data_ptr(), ws_bytes, stream), "gemm")
+        else:
+            L.check(lib.ctmr_conv3d(ctypes.byref(d), x.data_ptr(), packed.data_ptr(), bias.data_ptr(),
+                                    affine.data_ptr(), res.data_ptr(), y.data_ptr(), ws.data_ptr(), ws_bytes,
+                                    stream), "conv3d")
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    xn = _h(x)
+    expected = (rm.conv3d(rm.group_norm(xn, np.ones(c), np.zeros(c), 8, 1e-6, apply_silu=True), _h(w))
+                + _h(bias)[:, None, None, None, :] + _h(res))
+    _assert_rel(_h(outs[0]), expected, FP32_REL, f"two-stage {shape}->{cout} flags {flags}")
