@@ -530,8 +530,9 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
 // A read from LDS at compile-time offsets and B (packed weight) fetched one tap
 // ahead through buffer loads.  The next chunk's halo is in flight in registers
 // while the current chunk multiplies.  A staged voxel row is 80 bytes (16
-// channels + 16 bytes of padding), which spreads the 8 rows of each
-// ds_read_b128 quarter-wave over distinct banks.
+// channels + 16 bytes of padding), which spreads the 8 rows of one brick line
+// over distinct banks (a 16-lane group also reads the next line: some
+// conflicts remain, hidden behind the MFMAs).
 constexpr int kBD = 4, kBH = 8, kBW = 8;
 constexpr int kHD = kBD + 2, kHH = kBH + 2, kHW = kBW + 2;
 constexpr int kHaloVox = kHD * kHH * kHW;                 // 600
