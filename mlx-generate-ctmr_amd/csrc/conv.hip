@@ -872,8 +872,8 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // LDS-staged GEMM: stride-1 fp32 volumes whose 4x8x8 bricks are at least
   // 3/4 full, with at least 128 input channels (8 staged chunks; below that
   // the per-chunk staging and barriers cost more than the pack pass they
-  // replace, measured on MI355X), 64-wide column tiles, and 6 staged planes
-  // within 32-bit buffer offsets.
+  // replace, measured on MI355X), 64-wide column tiles, at least 4 chunks per
+  // split, and 6 staged planes within 32-bit buffer offsets.
   g.lds = false;
   if (g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 && d->stride == 1 &&
       d->mode == CTMR_MODE_PLAIN && d->cin % 16 == 0 && d->cin >= 128 && d->cout % 64 == 0 &&
@@ -883,7 +883,13 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     g.tx = (int)ceil_div(d->w, kBW);
     const int64_t slots = (int64_t)g.tz * g.ty * g.tx * kBD * kBH * kBW;
     const int64_t planes = (int64_t)kHD * d->h * d->w * d->cin * 4;
-    if (4 * S >= 3 * slots && planes < (1ll << 31)) g.lds = true;
+    // The policy split (below) must leave each workgroup at least 4 chunks:
+    // with fewer, the exposed first-chunk staging outweighs the saved pack
+    // (measured on the UNet's 16x16x8 level: streaming 68 % vs LDS 63 %).
+    const int64_t base = (int64_t)g.tz * g.ty * g.tx * (d->cout / 64) * d->n;
+    const int64_t policy_split = base < 512 ? std::min<int64_t>(ceil_div(512, base), d->cin / 16) : 1;
+    const int64_t split = d->split > 0 ? d->split : policy_split;
+    if (4 * S >= 3 * slots && planes < (1ll << 31) && (d->cin / 16) / split >= 4) g.lds = true;
   }
   if (g.lds) {
     g.pack = false;

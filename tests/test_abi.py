@@ -87,12 +87,16 @@ def test_split_policy_is_shape_only(ctmr):
     # large grids never split
     assert L.conv_split(L.conv_desc(1, 128, 128, 128, 128, 128)) == 1
     assert L.conv_split(L.conv_desc(1, 64, 64, 64, 64, 64)) == 1
-    # an explicit split may be any count up to the K step count: 16-channel
-    # chunks for the LDS-staged GEMM, (27 taps x 32 blocks) for the streaming one
-    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=5)) == 5
-    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=32)) == 32
-    with pytest.raises(L.CtmrError, match="chunk count"):
-        L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=33))
+    # an explicit split may be any count up to the K step count (27 taps x 32
+    # blocks here); the LDS-staged GEMM takes a split only while each range keeps
+    # at least 4 of its 16-channel chunks (5 here: no packed copy in the
+    # workspace), larger splits go to the streaming GEMM (packed copy)
+    d5 = L.conv_desc(2, 4, 8, 8, 512, 512, split=5)
+    assert L.conv_split(d5) == 5
+    assert L.workspace_bytes(d5) == 5 * 2 * 256 * 512 * 4
+    d33 = L.conv_desc(2, 4, 8, 8, 512, 512, split=33)
+    assert L.conv_split(d33) == 33
+    assert L.workspace_bytes(d33) > 33 * 2 * 256 * 512 * 4
     assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32, flags=L.F_STREAM)) == 27 * 32
     with pytest.raises(L.CtmrError, match="step count"):
         L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32 + 1, flags=L.F_STREAM))

@@ -137,8 +137,8 @@ def test_forced_tap_split_matches_float64(ctmr, dev, split):
 @pytest.mark.parametrize(("shape", "cout", "fused", "split"), [
     ((2, 8, 16, 16, 128), 128, True, 0),   # whole bricks, GN affine + SiLU, batch bias, residual
     ((2, 7, 16, 15, 128), 64, True, 0),    # ragged bricks (masked rows)
-    ((1, 4, 8, 8, 512), 512, False, 0),    # one brick: chunk split filling the device
-    ((1, 12, 16, 8, 128), 128, False, 3),  # forced uneven chunk split
+    ((1, 4, 8, 8, 512), 512, False, 8),    # one brick, chunk split (4 chunks per range)
+    ((1, 12, 16, 8, 256), 128, False, 3),  # forced uneven chunk split (5/5/6 chunks)
 ])
 def test_lds_staged_and_streaming_gemms_match_float64(ctmr, dev, shape, cout, fused, split):
     """The LDS-staged GEMM (halo bricks in LDS, affine + SiLU applied while staging) and the
