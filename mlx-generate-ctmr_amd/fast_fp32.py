@@ -25,6 +25,7 @@ linear ``(O, I)``.
 from __future__ import annotations
 
 import contextlib
+import math
 import threading
 import weakref
 from collections.abc import Iterable, Iterator, Mapping
@@ -115,6 +116,8 @@ def pack_upsample_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tens
 
 
 def _pack(weight: Tensor, mode: int) -> Tensor:
+    if not isinstance(weight, Tensor) or weight.device.type != "cuda":
+        raise ValueError("conv weight must be a torch.Tensor on the GPU (there is no CPU path)")
     code = _dtype_code()
     key = (id(weight), mode, code)
     with _packed_lock:
@@ -209,6 +212,9 @@ def implicit_gemm_conv3d(
                       stream_gemm)
 
 
+nax_conv3d = implicit_gemm_conv3d  # the reference orchestrator's name (_nax_conv.py:475)
+
+
 def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, stride: int = 1) -> Tensor:
     """NDHWC convolution with a Torch ``(O, C, k, k, k)`` weight (``fast_fp32.conv3d_ncdhw``, :133-154)."""
     k = int(weight.shape[2])
@@ -292,9 +298,42 @@ def trilinear_conv3d(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
                                 trilinear=True)
 
 
-def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
-    """FP32 ``x @ weight.T + bias`` (embedding MLPs; not on the conv hot path)."""
+def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor], mx=None) -> Tensor:
+    """FP32 ``x @ weight.T + bias`` (``medmlx_core.ops.linear``, re-exported by the reference's
+    fast_fp32.py:48-53; embedding MLPs and attention projections, not on the conv hot path)."""
     return F.linear(x, weight, bias)
+
+
+def sinusoidal_timestep_embedding(timesteps: Tensor, embedding_dim: int, *, mx=None,
+                                  max_period: int = 10000) -> Tensor:
+    """``[cos, sin]`` sinusoidal embedding of ``(N,)`` timesteps (embed.py:15-40), padded with one
+    zero column for odd ``embedding_dim``."""
+    if timesteps.dim() != 1:
+        raise ValueError("Timesteps should be a 1d-array")
+    half = embedding_dim // 2
+    exponent = -math.log(max_period) * torch.arange(half, dtype=torch.float32, device=timesteps.device)
+    freqs = torch.exp(exponent / half)
+    args = timesteps.to(torch.float32).reshape(-1, 1) * freqs.reshape(1, -1)
+    emb = torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+    if embedding_dim % 2 == 1:
+        emb = F.pad(emb, (0, 1))
+    return emb
+
+
+def kernels_available(mx=None) -> bool:
+    """Whether the HIP kernels can run here (the reference's ``nax_available`` gate,
+    _nax_conv.py:352-363): the library loads and the current device is a gfx950 GPU.  Nothing
+    falls back when this is False -- the operators raise."""
+    try:
+        _lib.lib()
+    except _lib.CtmrError:
+        return False
+    if not torch.cuda.is_available():
+        return False
+    return torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName.startswith("gfx950")
+
+
+nax_available = kernels_available
 
 
 # ---------------------------------------------------------------------------
@@ -303,7 +342,7 @@ def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
 FLASH_HEAD_DIM = 32
 
 
-def flash_eligible(q: Tensor, k: Tensor, heads: int) -> bool:
+def flash_eligible(q: Tensor, k: Tensor, heads: int, mx=None) -> bool:
     """Whether ``(B, L, heads * 32)`` FP32 projections fit the HIP kernel
     (``_flash_attention.flash_eligible``, :276-289; any L here, ragged key blocks are masked)."""
     return (q.dtype == torch.float32 and k.dtype == torch.float32
@@ -352,6 +391,27 @@ def _fused_qkv(wq: Tensor, wk: Tensor, wv: Tensor, biases) -> tuple[Tensor, Opti
     with _packed_lock:
         _qkv[key] = (tuple(weakref.ref(t, _evict) for t in (wq, wk, wv)), weight, bias)
     return weight, bias
+
+
+def attention(query: Tensor, key: Tensor, value: Tensor, *, scale: float, mx=None) -> Tensor:
+    """Scaled dot-product attention on ``(B, H, L, D)`` heads (the ``AttentionArithmetic``
+    surface, reference fast_fp32.py:399-401).  32-wide heads run the HIP flash kernel, each
+    (batch, head) pair as one single-head item; other widths use PyTorch's attention on the GPU."""
+    if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+        raise ValueError("attention expects (B, H, L, D) query, key and value")
+    b, h, lq, d = (int(v) for v in query.shape)
+    if d == FLASH_HEAD_DIM and query.dtype == key.dtype == value.dtype == torch.float32:
+        q = query.contiguous().reshape(b * h, lq, d)
+        k = key.contiguous().reshape(b * h, -1, d)
+        v = value.contiguous().reshape(b * h, -1, d)
+        return ops.flash_attention(_rows(q, "query"), _rows(k, "key"), _rows(v, "value"), 1, float(scale),
+                                   0).reshape(b, h, lq, d)
+    return F.scaled_dot_product_attention(query, key, value, scale=scale)
+
+
+def attention_projection(array: Tensor, weight: Tensor, bias: Tensor, mx=None) -> Tensor:
+    """Attention output projection, the same FP32 GEMM as ``linear`` (reference fast_fp32.py:404-406)."""
+    return F.linear(array, weight, bias)
 
 
 def self_attention_tokens(tokens: Tensor, weights: Mapping[str, Tensor], *, heads: int, scale: float,

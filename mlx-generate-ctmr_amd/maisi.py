@@ -64,16 +64,7 @@ def _per_level(value, n: int) -> tuple[int, ...]:
 # ---------------------------------------------------------------------------
 def sinusoidal_timestep_embedding(timesteps: Tensor, dim: int, max_period: int = 10000) -> Tensor:
     """``[cos, sin]`` sinusoidal embedding of ``(N,)`` timesteps (embed.py:15-40)."""
-    if timesteps.dim() != 1:
-        raise ValueError("Timesteps should be a 1d-array")
-    half = dim // 2
-    exponent = -math.log(max_period) * torch.arange(half, dtype=torch.float32, device=timesteps.device)
-    freqs = torch.exp(exponent / half)
-    args = timesteps.to(torch.float32).reshape(-1, 1) * freqs.reshape(1, -1)
-    emb = torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
-    if dim % 2 == 1:
-        emb = F.pad(emb, (0, 1))
-    return emb
+    return ff.sinusoidal_timestep_embedding(timesteps, dim, max_period=max_period)
 
 
 def _silu_mlp(x: Tensor, weights: Mapping[str, Tensor], prefix: str) -> Tensor:

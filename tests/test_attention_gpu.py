@@ -120,3 +120,20 @@ def test_spatial_attention_production_shapes_match_oracle(ctmr, dev, shape, grou
     err = rm.max_rel_error(y.cpu().numpy(), ref)
     print(f"spatial attention {shape}: max rel error {err:.3e}", flush=True)
     assert err <= FP32_REL
+
+
+@pytest.mark.parametrize(("b", "h", "lq", "lk", "d"), [(2, 4, 96, 80, 32), (1, 2, 40, 40, 16)])
+def test_attention_protocol_on_head_major_inputs(ctmr, dev, b, h, lq, lk, d):
+    """``fast_fp32.attention`` on (B, H, L, D) heads (the AttentionArithmetic surface): 32-wide heads
+    through the flash kernel, other widths through PyTorch's attention, both against float64."""
+    rng = np.random.default_rng(b * 100 + d)
+    q = rng.standard_normal((b, h, lq, d)).astype(np.float32)
+    k = rng.standard_normal((b, h, lk, d)).astype(np.float32)
+    v = rng.standard_normal((b, h, lk, d)).astype(np.float32)
+    scale = d ** -0.5
+    out = ctmr.fast_fp32.attention(torch.from_numpy(q).to(dev), torch.from_numpy(k).to(dev),
+                                   torch.from_numpy(v).to(dev), scale=scale)
+    s = torch.from_numpy(q).double() @ torch.from_numpy(k).double().transpose(-1, -2).contiguous() * scale
+    ref = (torch.softmax(s, dim=-1) @ torch.from_numpy(v).double()).numpy()
+    assert rm.max_rel_error(out.cpu().numpy(), ref) <= FP32_REL
+    assert ctmr.fast_fp32.kernels_available()

@@ -200,7 +200,9 @@ def _production_unet(ctmr, dev, seed=7):
 
 def test_config3_unet_step_matches_cpu_oracle(ctmr, dev):
     """Config 3 at full size: production UNet, latent 64x64x32x4, batch 2 (CFG pair),
-    random init; max relative error vs the PyTorch-CPU fp32 oracle <= 1e-4."""
+    random init; max relative error vs the PyTorch-CPU fp32 oracle <= 1e-4.  The same step with
+    every conv in bf16 (bf16 operands, fp32 accumulation) stays within the per-layer bf16 bar,
+    2e-2, end to end (measured 5.8e-3 on MI355X)."""
     m = ctmr.maisi
     host, w = _production_unet(ctmr, dev)
     rng = np.random.default_rng(3)
@@ -209,13 +211,19 @@ def test_config3_unet_step_matches_cpu_oracle(ctmr, dev):
     classes = np.array([9, 0])
     spacing = np.repeat(np.asarray([[0.94, 0.94, 1.36]], np.float64) * 100, 2, 0).astype(np.float16).astype(np.float32)
     ctor = m.PRODUCTION_UNET_CONSTRUCTOR
-    _, y = m.denoise_unet(_g(x, dev), _g(t, dev), _g(classes, dev, torch.int64), _g(spacing, dev), w, constructor=ctor)
+    args = (_g(x, dev), _g(t, dev), _g(classes, dev, torch.int64), _g(spacing, dev), w)
+    _, y = m.denoise_unet(*args, constructor=ctor)
     y = _h(y)
+    with ctmr.fast_fp32.precision("bf16"):
+        _, y16 = m.denoise_unet(*args, constructor=ctor)
+    y16 = _h(y16)
     torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
     with torch.no_grad():
         _, ref = mt.unet(torch.from_numpy(np.moveaxis(x, -1, 1).copy()), torch.from_numpy(t), torch.from_numpy(classes),
                          torch.from_numpy(spacing), mt.to_torch(host, dtype=torch.float32, strip=""), ctor)
-    assert _rel(y, np.moveaxis(ref.numpy(), 1, -1)) <= 1e-4
+    ref = np.moveaxis(ref.numpy(), 1, -1)
+    assert _rel(y, ref) <= 1e-4
+    assert _rel(y16, ref) <= 2e-2
 
 
 def test_config4_vae_decoder_window_matches_cpu_oracle(ctmr, dev):

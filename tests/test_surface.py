@@ -1,0 +1,56 @@
+"""The arithmetic-module surface (CPU): fast_fp32 provides every method of the reference's
+arithmetic protocols with the same parameter names, so it can be returned from
+``unet_arithmetic()`` / ``vae_arithmetic()`` (reference _types.py:216-286, fast_fp32.py:30-68)."""
+
+from __future__ import annotations
+
+import inspect
+
+import pytest
+
+# protocol method -> keyword parameters the reference's callers pass by name
+PROTOCOLS = {
+    "MlpArithmetic": {"linear": ["mx"], "silu": ["mx"]},
+    "ConvArithmetic": {
+        "silu": ["mx"],
+        "group_norm_ncdhw": ["num_groups", "eps", "mx"],
+        "conv3d_ncdhw": ["padding", "mx", "stride"],
+    },
+    "VaeArithmetic": {"upsample_trilinear_ncdhw": ["mx", "scale"]},
+    "ResidualArithmetic": {"avg_pool3d_ncdhw": ["mx"], "upsample_nearest_ncdhw": ["mx"]},
+    "AttentionArithmetic": {"attention_projection": ["mx"], "attention": ["scale", "mx"]},
+    "UnetArithmetic": {"sinusoidal_timestep_embedding": ["mx", "max_period"]},
+}
+# other module-level names the reference's networks use from fast_fp32 (fast_fp32.py:30-68, 102-406)
+EXTRA = ["norm_conv3d_ncdhw", "pointwise_conv_ncdhw", "residual_block_ncdhw", "vae_resblock_ncdhw",
+         "trilinear_conv3d_ncdhw", "self_attention_tokens", "flash_attention", "flash_eligible",
+         "pack_weight", "pack_upsample_weight", "drop_packed_weights", "group_norm_affine", "nax_conv3d",
+         "nax_available"]
+
+
+@pytest.mark.parametrize("protocol", sorted(PROTOCOLS))
+def test_fast_fp32_satisfies_reference_protocols(ctmr, protocol):
+    ff = ctmr.fast_fp32
+    for name, keywords in PROTOCOLS[protocol].items():
+        fn = getattr(ff, name, None)
+        assert callable(fn), f"{protocol}.{name} missing"
+        params = inspect.signature(fn).parameters
+        for kw in keywords:
+            assert kw in params, f"{protocol}.{name} lacks keyword {kw!r}"
+
+
+def test_fast_fp32_exports_reference_names(ctmr):
+    missing = [n for n in EXTRA if not callable(getattr(ctmr.fast_fp32, n, None))]
+    assert not missing, missing
+
+
+def test_operators_reject_cpu_tensors_without_fallback(ctmr):
+    import torch
+
+    x = torch.zeros(1, 4, 4, 4, 4)
+    w = torch.zeros(4, 4, 3, 3, 3)
+    with pytest.raises(ValueError, match="GPU"):
+        ctmr.fast_fp32.conv3d_ncdhw(x, w, None, padding=1)
+    with pytest.raises(ValueError, match="GPU"):
+        ctmr.fast_fp32.flash_attention(torch.zeros(1, 8, 32), torch.zeros(1, 8, 32), torch.zeros(1, 8, 32),
+                                       heads=1, scale=1.0)
