@@ -486,22 +486,41 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   }
 
   // Epilogue: D row 4*(lane/16)+r, column lane%16 of each 16x16 block.
+  // Residual values are all loaded before the first store: interleaved, each
+  // load would wait for the stores before it (the compiler cannot prove the
+  // output and the residual apart).  Indices past the grid are clamped for
+  // the loads and masked for the stores.
   const bool partial = p.split > 1;
   const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
+  auto out_voxel = [&](int v) -> int64_t {
+    int o = v;
+    if (UP) {
+      const int d = v / ghw, rr = v - d * ghw;
+      const int h = rr / p.gw, w = rr - h * p.gw;
+      o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
+    }
+    return (int64_t)b * p.s_out + o;
+  };
+  float rv[4][4][NSUB];
+  const bool add_res = !partial && p.has_res;
+  if (add_res) {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t base = out_voxel(min(m0 + ms * 16 + lgrp * 4 + r, S - 1)) * p.cout;
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns) rv[ms][r][ns] = p.res[base + min(n0 + ns * 16 + lrow, p.cout - 1)];
+      }
+  }
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int v = m0 + ms * 16 + lgrp * 4 + r;
       if (v >= S) continue;
-      int o = v;
-      if (UP) {
-        const int d = v / ghw, rr = v - d * ghw;
-        const int h = rr / p.gw, w = rr - h * p.gw;
-        o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
-      }
-      const int64_t vox = (int64_t)b * p.s_out + o;
+      const int64_t vox = out_voxel(v);
       const int64_t base = vox * p.cout;
 #pragma unroll
       for (int ns = 0; ns < NSUB; ++ns) {
@@ -510,7 +529,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
         float sum = acc[ms][ns][r];
         if (!partial) {
           if (p.has_bias) sum += bias_b[col];
-          if (p.has_res) sum += p.res[base + col];
+          if (add_res) sum += rv[ms][r][ns];
         }
         out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
       }
@@ -708,10 +727,26 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 
   // Epilogue: D row 4*(lane/16)+r of block ms is brick row 2ms + lane/32,
   // column 4*((lane/16)&1) + r.
+  // (Residual values loaded before the first store, as in conv_kernel.)
   const bool partial = p.split > 1;
   const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
   const int z = z0 + wave;
+  auto out_base = [&](int y, int x) -> int64_t {
+    return ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout;
+  };
+  float rv[4][4][4];
+  const bool add_res = !partial && p.has_res;
+  if (add_res) {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t base = out_base(y0 + 2 * ms + (lgrp >> 1), x0 + 4 * (lgrp & 1) + r);
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) rv[ms][r][ns] = p.res[base + n0 + ns * 16 + lrow];
+      }
+  }
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
     const int y = y0 + 2 * ms + (lgrp >> 1);
@@ -719,15 +754,14 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
     for (int r = 0; r < 4; ++r) {
       const int x = x0 + 4 * (lgrp & 1) + r;
       if (z >= p.d || y >= p.h || x >= p.w) continue;
-      const int64_t base = ((((int64_t)b * p.d + z) * p.h + y) * p.w + x) * p.cout;
+      const int64_t base = out_base(y, x);
 #pragma unroll
       for (int ns = 0; ns < 4; ++ns) {
         const int col = n0 + ns * 16 + lrow;
-        if (col >= p.cout) continue;
         float sum = acc[ms][ns][r];
         if (!partial) {
           if (p.has_bias) sum += bias_b[col];
-          if (p.has_res) sum += p.res[base + col];
+          if (add_res) sum += rv[ms][r][ns];
         }
         out[base + col] = sum;
       }
