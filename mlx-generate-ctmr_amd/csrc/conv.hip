@@ -486,10 +486,10 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   }
 
   // Epilogue: D row 4*(lane/16)+r, column lane%16 of each 16x16 block.
-  // Residual values are all loaded before the first store: interleaved, each
-  // load would wait for the stores before it (the compiler cannot prove the
-  // output and the residual apart).  Indices past the grid are clamped for
-  // the loads and masked for the stores.
+  // Bias and residual values are all loaded before the first store:
+  // interleaved, each load would wait for the stores before it (the compiler
+  // cannot prove the output and its inputs apart).  Indices past the grid are
+  // clamped for the loads and masked for the stores.
   const bool partial = p.split > 1;
   const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
@@ -502,6 +502,10 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
     }
     return (int64_t)b * p.s_out + o;
   };
+  float bv[NSUB];
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns)
+    bv[ns] = (!partial && p.has_bias) ? bias_b[min(n0 + ns * 16 + lrow, p.cout - 1)] : 0.f;
   float rv[4][4][NSUB];
   const bool add_res = !partial && p.has_res;
   if (add_res) {
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
         if (col >= p.cout) continue;
         float sum = acc[ms][ns][r];
         if (!partial) {
-          if (p.has_bias) sum += bias_b[col];
+          if (p.has_bias) sum += bv[ns];
           if (add_res) sum += rv[ms][r][ns];
         }
         out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
@@ -727,7 +731,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 
   // Epilogue: D row 4*(lane/16)+r of block ms is brick row 2ms + lane/32,
   // column 4*((lane/16)&1) + r.
-  // (Residual values loaded before the first store, as in conv_kernel.)
+  // (Bias and residual values loaded before the first store, as in conv_kernel.)
   const bool partial = p.split > 1;
   const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
@@ -735,6 +739,9 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
   auto out_base = [&](int y, int x) -> int64_t {
     return ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout;
   };
+  float bv[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) bv[ns] = (!partial && p.has_bias) ? bias_b[n0 + ns * 16 + lrow] : 0.f;
   float rv[4][4][4];
   const bool add_res = !partial && p.has_res;
   if (add_res) {
@@ -760,7 +767,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
         const int col = n0 + ns * 16 + lrow;
         float sum = acc[ms][ns][r];
         if (!partial) {
-          if (p.has_bias) sum += bias_b[col];
+          if (p.has_bias) sum += bv[ns];
           if (add_res) sum += rv[ms][r][ns];
         }
         out[base + col] = sum;
