@@ -353,6 +353,19 @@ def profile_only(pkg, dev, what, steps, warmup):
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
         z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 20, 64, 64, 4), dtype=np.float32)).to(dev)
         fn = lambda: m.decode_vae(z, w, constructor=vc)
+    elif what == "gemms":
+        # config-0 fp32 and bf16 GEMM kernels alone (one pack each), for counter passes
+        rng = np.random.default_rng(0)
+        x = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 64), dtype=np.float32)).to(dev)
+        w = torch.from_numpy((rng.standard_normal((64, 64, 3, 3, 3)) / np.sqrt(27 * 64)).astype(np.float32)).to(dev)
+        b = torch.zeros(64, device=dev)
+        stages = [staged_op(pkg, x, w, b, code) for code in (pkg._lib.DT_F32, pkg._lib.DT_BF16)]
+        for pack, _, _ in stages:
+            pack()
+
+        def fn():
+            for _, gemm, _ in stages:
+                gemm()
     elif what == "attention":
         # production UNet level-2 attention: 16x16x8 latent = 2048 tokens, 256 channels = 8 heads, batch 2
         g = torch.Generator(device=dev).manual_seed(0)
@@ -381,7 +394,7 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "decode", "resblock", "attention"],
+    ap.add_argument("--only", choices=["unet", "decode", "resblock", "attention", "gemms"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
