@@ -156,6 +156,33 @@ int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* pac
                      const float* bias, const float* residual, float* y, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/*
+ * Group-norm statistics of a convolution's output, produced by its epilogue so a
+ * following group norm needs no read pass (the reference computes them in a
+ * separate medmlx-core pass, fast_fp32.py:185-189).  No counterpart entry point
+ * exists in the reference; these replace group_norm_affine on a conv output.
+ *   ctmr_conv3d_stats_tiles: the per-batch-item partial count ("tiles") that
+ *     ctmr_conv3d_gn writes for `groups`, or 0 when this descriptor cannot
+ *     produce them (cout <= 4, groups not dividing cout, a group that does not
+ *     divide the GEMM's column tile; on a K split, cout not a multiple of 64 or
+ *     a group wider than 64 channels); use ctmr_gn_affine on the output then.
+ *     A tile is a GEMM output tile, or on a K split a chunk of output voxels
+ *     of the reduction.
+ *   ctmr_conv3d_gn: ctmr_conv3d that also writes fp64 (sum, sum of squares) of
+ *     the stored output per (batch item, tile, group), each summed in a fixed
+ *     order, into stats[((b * tiles + tile) * groups + g) * 2 + {0, 1}].  The
+ *     output is bit-identical to ctmr_conv3d's.
+ *   ctmr_gn_affine_from_stats: the (n, c, 2) affine from those partials with the
+ *     semantics of ctmr_gn_affine (count = output voxels * c / groups).
+ */
+int32_t ctmr_conv3d_stats_tiles(const ctmr_conv_desc* desc, int32_t groups);
+int ctmr_conv3d_gn(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                   const float* affine, const float* residual, float* y, void* workspace,
+                   size_t workspace_bytes, int32_t groups, double* stats, void* stream);
+int ctmr_gn_affine_from_stats(int32_t n, int32_t tiles, int32_t c, int32_t groups, int64_t count, float eps,
+                              const double* stats, const float* gamma, const float* beta, float* affine,
+                              void* stream);
+
 /* Group-norm statistics: affine (n, c, 2) = (gamma*rstd, beta - mean*gamma*rstd)
  * over (c/groups channels) x s voxels, biased variance, fp64 accumulation in a
  * fixed-order tree.  Needs ctmr_gn_workspace_bytes(n, s, c) of scratch. */

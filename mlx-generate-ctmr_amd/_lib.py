@@ -57,8 +57,11 @@ _PROTOTYPES = {
     "ctmr_conv3d": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ctmr_conv3d_pack": (_c_int, [_desc_p, _vp, _vp, _vp, _sz, _vp]),
     "ctmr_conv3d_gemm": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ctmr_conv3d_stats_tiles": (_c_i32, [_desc_p, _c_i32]),
+    "ctmr_conv3d_gn": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _c_i32, _vp, _vp]),
     "ctmr_gn_workspace_bytes": (_c_i64, [_c_i32, _c_i64, _c_i32]),
     "ctmr_gn_affine": (_c_int, [_c_i32, _c_i64, _c_i32, _c_i32, _f, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ctmr_gn_affine_from_stats": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _f, _vp, _vp, _vp, _vp, _vp]),
     "ctmr_gn_apply": (_c_int, [_c_i32, _c_i64, _c_i32, _vp, _vp, _c_i32, _vp, _vp]),
     "ctmr_silu": (_c_int, [_c_i64, _vp, _vp, _vp]),
     "ctmr_resample": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp]),

@@ -309,7 +309,52 @@ struct ConvArgs {
   int batch_bias, has_res, has_bias;
   int planar;              // store column c of voxel v at y[c * zstride + v] (tap-expanded GEMM)
   int64_t zstride;
+  double* stats;           // group-norm partials of the output (ctmr_conv3d_gn) or null
+  int gn_groups, gn_cpg, stats_tiles;
 };
+
+// Group-norm partials of a stored tile (ctmr_conv3d_gn).  On entry each lane
+// holds, per 16-column block ns, the fp64 sum and sum of squares of its rows'
+// stored values in column ns*16 + lane%16 of its wave's tile.  The four lane
+// groups are combined with xor butterflies (every lane ends with the same
+// bits), the waves through `red`, and each group's columns and waves are added
+// in ascending order -- a fixed order for a given shape.
+template <int NSUB, int WM, int WN>
+__device__ __forceinline__ void write_gn_partials(double (&s1)[NSUB], double (&s2)[NSUB], double (*red)[64][2],
+                                                  int wave, int lane, int col0, int cout, int cpg, int groups,
+                                                  double* __restrict__ stats_tile) {
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) {
+    s1[ns] += __shfl_xor(s1[ns], 16);
+    s1[ns] += __shfl_xor(s1[ns], 32);
+    s2[ns] += __shfl_xor(s2[ns], 16);
+    s2[ns] += __shfl_xor(s2[ns], 32);
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) {
+      red[wave][ns * 16 + lane][0] = s1[ns];
+      red[wave][ns * 16 + lane][1] = s2[ns];
+    }
+  }
+  __syncthreads();
+  constexpr int kWaveCols = NSUB * 16;
+  const int groups_here = (WN * kWaveCols) / cpg;
+  for (int gl = threadIdx.x; gl < groups_here; gl += 256) {
+    const int g = col0 / cpg + gl;
+    if (g >= groups || g * cpg >= cout) continue;
+    double a = 0.0, q = 0.0;
+    for (int wm = 0; wm < WM; ++wm)
+      for (int cc = 0; cc < cpg; ++cc) {
+        const int col = gl * cpg + cc;
+        const int wv = (col / kWaveCols) * WM + wm;
+        a += red[wv][col % kWaveCols][0];
+        q += red[wv][col % kWaveCols][1];
+      }
+    stats_tile[(int64_t)g * 2] = a;
+    stats_tile[(int64_t)g * 2 + 1] = q;
+  }
+}
 
 template <int DT>
 __device__ __forceinline__ void mfma_step(f4& acc, const u4& a, const u4& b);
@@ -518,6 +563,9 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
         for (int ns = 0; ns < NSUB; ++ns) rv[ms][r][ns] = p.res[base + min(n0 + ns * 16 + lrow, p.cout - 1)];
       }
   }
+  double s1[NSUB], s2[NSUB];
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) s1[ns] = s2[ns] = 0.0;
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
 #pragma unroll
@@ -536,8 +584,19 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
           if (add_res) sum += rv[ms][r][ns];
         }
         out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
+        if (p.stats) {
+          s1[ns] += (double)sum;
+          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
+        }
       }
     }
+  }
+  if (p.stats) {  // wave-uniform (a kernel argument): every thread reaches the barrier inside
+    __shared__ double red[WM * WN][64][2];
+    const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
+    write_gn_partials<NSUB, WM, WN>(s1, s2, red, wave, lane, n_tile * (WN * NSUB * 16), p.cout, p.gn_cpg,
+                                    p.gn_groups,
+                                    p.stats + ((int64_t)b * p.stats_tiles + tile_id) * p.gn_groups * 2);
   }
 }
 
@@ -574,6 +633,8 @@ struct LdsArgs {
   int tz, ty, tx;       // bricks per axis
   int n_tiles, split;
   int affine_on, silu_on, batch_bias, has_res, has_bias;
+  double* stats;        // group-norm partials of the output (ctmr_conv3d_gn) or null
+  int gn_groups, gn_cpg;
 };
 
 __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
@@ -754,6 +815,9 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
         for (int ns = 0; ns < 4; ++ns) rv[ms][r][ns] = p.res[base + n0 + ns * 16 + lrow];
       }
   }
+  double s1[4], s2[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) s1[ns] = s2[ns] = 0.0;
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
     const int y = y0 + 2 * ms + (lgrp >> 1);
@@ -771,8 +835,18 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
           if (add_res) sum += rv[ms][r][ns];
         }
         out[base + col] = sum;
+        if (p.stats) {
+          s1[ns] += (double)sum;
+          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
+        }
       }
     }
+  }
+  if (p.stats) {  // a kernel argument: every thread reaches the barrier inside
+    __shared__ double red[4][64][2];
+    const int tile_id = (bz * p.ty + by) * p.tx + bx;
+    write_gn_partials<4, 4, 1>(s1, s2, red, wave, lane, n0, p.cout, p.gn_cpg, p.gn_groups,
+                               p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
   }
 }
 
@@ -793,6 +867,69 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
     for (int k = 0; k < split; ++k) v += part[(int64_t)k * plane + i];
     if (res) v += res[i];
     y[i] = v;
+  }
+}
+
+// The same reduction (same order per element, so the same output bits) that
+// also writes group-norm partials (ctmr_conv3d_gn on a K split).  Block
+// (chunk, 64-column tile) of batch item blockIdx.y: thread t sums columns
+// 4*(t%16)..+3 of voxels chunk*16*rows + 16*j + t/16, keeping fp64 sums; the
+// 16 voxel lanes and each group's columns are then added in ascending order.
+// Partials: stats[((b * chunks + chunk) * groups + g) * 2 + {0, 1}].
+__global__ __launch_bounds__(256) void split_reduce_gn_kernel(const float* __restrict__ part,
+                                                              int64_t plane, int split,
+                                                              const float* __restrict__ bias,
+                                                              int has_bias, int batch_bias,
+                                                              const float* __restrict__ res,
+                                                              float* __restrict__ y, int cout,
+                                                              int64_t s_out, int rows, int chunks,
+                                                              int cpg, int groups,
+                                                              double* __restrict__ stats) {
+  const int ctiles = cout / 64;
+  const int chunk = blockIdx.x / ctiles, ct = blockIdx.x % ctiles, b = blockIdx.y;
+  const int t = threadIdx.x, cv = t & 15, vl = t >> 4;
+  const int c0 = ct * 64 + cv * 4;
+  float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (has_bias) bv = *(const float4*)(bias + (batch_bias ? (int64_t)b * cout : 0) + c0);
+  double s1[4] = {0.0, 0.0, 0.0, 0.0}, s2[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int j = 0; j < rows; ++j) {
+    const int64_t v = ((int64_t)chunk * rows + j) * 16 + vl;
+    if (v >= s_out) break;
+    const int64_t i = ((int64_t)b * s_out + v) * cout + c0;
+    float4 a = bv;
+    for (int k = 0; k < split; ++k) {
+      const float4 q = *(const float4*)(part + (int64_t)k * plane + i);
+      a.x += q.x; a.y += q.y; a.z += q.z; a.w += q.w;
+    }
+    if (res) {
+      const float4 r = *(const float4*)(res + i);
+      a.x += r.x; a.y += r.y; a.z += r.z; a.w += r.w;
+    }
+    *(float4*)(y + i) = a;
+    const float e[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      s1[k] += (double)e[k];
+      s2[k] = fma((double)e[k], (double)e[k], s2[k]);
+    }
+  }
+  __shared__ double red[16][64][2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    red[vl][cv * 4 + k][0] = s1[k];
+    red[vl][cv * 4 + k][1] = s2[k];
+  }
+  __syncthreads();
+  if (t < 64 / cpg) {
+    double a = 0.0, q = 0.0;
+    for (int l = 0; l < 16; ++l)
+      for (int cc = 0; cc < cpg; ++cc) {
+        a += red[l][t * cpg + cc][0];
+        q += red[l][t * cpg + cc][1];
+      }
+    double* out = stats + (((int64_t)b * chunks + chunk) * groups + ct * (64 / cpg) + t) * 2;
+    out[0] = a;
+    out[1] = q;
   }
 }
 
@@ -989,6 +1126,49 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   return CTMR_OK;
 }
 
+// Per-batch-item partial count of ctmr_conv3d_gn for `groups`, or 0 when the
+// epilogue cannot produce them: a K split (partial planes, not outputs), the
+// tap-expanded cout <= 4 GEMM (outputs come from the tap sum), or a group that
+// does not divide the workgroup's column tile.
+// On a K split the partials come from split_reduce_gn_kernel, one per chunk of
+// 16 * split_gn_rows() output voxels; the row count keeps about 1024 blocks.
+static int split_gn_rows(const ctmr_conv_desc* d, const Geometry& g) {
+  const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
+  const int64_t rows = s_out * (d->cout / 64) * d->n / (16 * 1024);
+  return (int)std::min<int64_t>(std::max<int64_t>(rows, 1), 16);
+}
+
+static int gn_stats_tiles(const ctmr_conv_desc* d, const Geometry& g, int groups) {
+  if (groups <= 0 || d->cout % groups != 0) return 0;
+  if (g.layout == WL_EXPAND) return 0;
+  const int cpg = d->cout / groups;
+  if (g.split > 1) {
+    if (d->cout % 64 != 0 || 64 % cpg != 0) return 0;
+    const int64_t s_out = (int64_t)g.od * g.oh * g.ow, per = 16 * (int64_t)split_gn_rows(d, g);
+    const int64_t chunks = (s_out + per - 1) / per;
+    return chunks > 65535 ? 0 : (int)chunks;
+  }
+  const int width = g.lds ? 64 : g.wn * g.nsub * 16;
+  if (cpg > width || width % cpg != 0) return 0;
+  return g.lds ? g.tz * g.ty * g.tx : g.m_tiles * g.phases;
+}
+
+// The K-split reduction, with group-norm partials when `stats` is set.
+static void launch_split_reduce(const ctmr_conv_desc* d, const Geometry& g, const float* part, int64_t plane,
+                                const float* bias, int batch_bias, const float* residual, float* y,
+                                int64_t s_out, int groups, double* stats, hipStream_t st) {
+  const float* res = (d->flags & CTMR_F_RESIDUAL) ? residual : nullptr;
+  if (!stats) {
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(elementwise_blocks(plane)), dim3(256), 0, st, part, plane,
+                       g.split, bias, bias != nullptr ? 1 : 0, batch_bias, res, y, d->cout, s_out);
+    return;
+  }
+  const int rows = split_gn_rows(d, g), chunks = gn_stats_tiles(d, g, groups);
+  hipLaunchKernelGGL(split_reduce_gn_kernel, dim3((unsigned)chunks * (d->cout / 64), d->n), dim3(256), 0, st,
+                     part, plane, g.split, bias, bias != nullptr ? 1 : 0, batch_bias, res, y, d->cout, s_out,
+                     rows, chunks, d->cout / groups, groups, stats);
+}
+
 typedef void (*ConvFn)(dim3, dim3, hipStream_t, const ConvArgs&);
 
 template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
@@ -1166,22 +1346,26 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
 
 static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
                             const float* affine_direct, const float* residual, float* y, void* workspace,
-                            size_t workspace_bytes, void* stream);
+                            size_t workspace_bytes, int groups, double* stats, void* stream);
 
 int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* packed,
                      const float* bias, const float* residual, float* y, void* workspace,
                      size_t workspace_bytes, void* stream) {
-  return conv3d_gemm_impl(desc, x, packed, bias, nullptr, residual, y, workspace, workspace_bytes, stream);
+  return conv3d_gemm_impl(desc, x, packed, bias, nullptr, residual, y, workspace, workspace_bytes, 0, nullptr,
+                          stream);
 }
 
 // affine_direct: the caller's (n, cin, 2) table when the pack stage was skipped
 // (ctmr_conv3d on the LDS path); null means "read it from the workspace".
+// stats: group-norm partials for `groups` (validated by the caller) or null.
 static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
                             const float* affine_direct, const float* residual, float* y, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+                            size_t workspace_bytes, int groups, double* stats, void* stream) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
+  const int tiles = stats ? gn_stats_tiles(desc, g, groups) : 0;
+  if (stats && tiles == 0) return fail(CTMR_E_UNSUPPORTED, "this convolution cannot produce group-norm partials");
   if (!packed || !y || (!g.pack && !x)) return fail(CTMR_E_INVALID, "null input, weight or output");
   if ((desc->flags & CTMR_F_RESIDUAL) && !residual)
     return fail(CTMR_E_INVALID, "residual flag without residual");
@@ -1211,6 +1395,9 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
     a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
     a.has_bias = bias != nullptr;
     a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
+    a.stats = g.split > 1 ? nullptr : stats;  // a split's partial planes: the reduce writes them
+    a.gn_groups = stats ? groups : 0;
+    a.gn_cpg = stats ? desc->cout / groups : 1;
     float* part = (float*)((char*)workspace + g.pack_bytes);
     a.y = g.split > 1 ? part : y;
     if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
@@ -1218,9 +1405,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
     hipLaunchKernelGGL(conv_lds_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
     if ((rc = check_launch("conv_lds"))) return rc;
     if (g.split > 1) {
-      hipLaunchKernelGGL(split_reduce_kernel, dim3(elementwise_blocks(a.plane)), dim3(256), 0, st, part,
-                         a.plane, g.split, bias, bias != nullptr ? 1 : 0, a.batch_bias,
-                         (desc->flags & CTMR_F_RESIDUAL) ? residual : nullptr, y, desc->cout, s_out);
+      launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
       if ((rc = check_launch("split_reduce"))) return rc;
     }
     return CTMR_OK;
@@ -1250,6 +1435,10 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
   a.n_tiles = g.n_tiles;
   a.planar = 0;
   a.zstride = 0;
+  a.stats = g.split > 1 ? nullptr : stats;
+  a.gn_groups = stats ? groups : 0;
+  a.gn_cpg = stats ? desc->cout / groups : 1;
+  a.stats_tiles = tiles;
   float* part = (float*)((char*)workspace + g.pack_bytes);
   a.y = g.split > 1 ? part : y;
   if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
@@ -1282,9 +1471,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
     return check_launch("tap_sum");
   }
   if (g.split > 1) {
-    hipLaunchKernelGGL(split_reduce_kernel, dim3(elementwise_blocks(a.plane)), dim3(256), 0, st,
-                       part, a.plane, g.split, bias, bias != nullptr ? 1 : 0, a.batch_bias,
-                       (desc->flags & CTMR_F_RESIDUAL) ? residual : nullptr, y, desc->cout, s_out);
+    launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
     if ((rc = check_launch("split_reduce"))) return rc;
   }
   return CTMR_OK;
@@ -1299,10 +1486,36 @@ int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed, 
   if (!x || !packed || !y) return fail(CTMR_E_INVALID, "null input, weight or output");
   if (g.lds) {  // no pack stage: the LDS GEMM reads x and the caller's affine table directly
     if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
-    return conv3d_gemm_impl(desc, x, packed, bias, affine, residual, y, workspace, workspace_bytes, stream);
+    return conv3d_gemm_impl(desc, x, packed, bias, affine, residual, y, workspace, workspace_bytes, 0, nullptr,
+                            stream);
   }
   if ((rc = ctmr_conv3d_pack(desc, x, affine, workspace, workspace_bytes, stream))) return rc;
   return ctmr_conv3d_gemm(desc, x, packed, bias, residual, y, workspace, workspace_bytes, stream);
+}
+
+int32_t ctmr_conv3d_stats_tiles(const ctmr_conv_desc* desc, int32_t groups) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  return gn_stats_tiles(desc, g, groups);
+}
+
+int ctmr_conv3d_gn(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                   const float* affine, const float* residual, float* y, void* workspace,
+                   size_t workspace_bytes, int32_t groups, double* stats, void* stream) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  if (!x || !packed || !y || !stats) return fail(CTMR_E_INVALID, "null input, weight, output or stats");
+  if (gn_stats_tiles(desc, g, groups) == 0)
+    return fail(CTMR_E_UNSUPPORTED, "this convolution cannot produce group-norm partials");
+  if (g.lds) {
+    if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
+  } else if ((rc = ctmr_conv3d_pack(desc, x, affine, workspace, workspace_bytes, stream))) {
+    return rc;
+  }
+  return conv3d_gemm_impl(desc, x, packed, bias, g.lds ? affine : nullptr, residual, y, workspace,
+                          workspace_bytes, groups, stats, stream);
 }
 
 }  // extern "C"

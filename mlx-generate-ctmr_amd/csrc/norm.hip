@@ -91,6 +91,12 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict
   }
 }
 
+// Fixed-order combine of the 256 per-thread (sum, sum of squares) of group g of
+// batch item b, then that group's (scale, offset) pairs.
+__device__ void gn_group_affine(double sm, double sq, int g, int b, int c, int groups, int64_t count,
+                                const float* __restrict__ gamma, const float* __restrict__ beta,
+                                float eps, float* __restrict__ affine);
+
 __global__ __launch_bounds__(256) void gn_finalize_kernel(const double* __restrict__ part,
                                                           int chunks, int c, int groups,
                                                           int64_t count,
@@ -107,6 +113,32 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(const double* __restri
     sm += p[0];
     sq += p[1];
   }
+  gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
+}
+
+// Affine from per-(batch item, tile, group) partials written by a conv
+// epilogue (ctmr_conv3d_gn): tiles strided over the threads, then the same
+// fixed-order combine.
+__global__ __launch_bounds__(256) void gn_tiles_finalize_kernel(const double* __restrict__ part, int tiles,
+                                                                int c, int groups, int64_t count,
+                                                                const float* __restrict__ gamma,
+                                                                const float* __restrict__ beta, float eps,
+                                                                float* __restrict__ affine) {
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  double sm = 0, sq = 0;
+  for (int i = t; i < tiles; i += 256) {
+    const double* p = part + (((int64_t)b * tiles + i) * groups + g) * 2;
+    sm += p[0];
+    sq += p[1];
+  }
+  gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
+}
+
+__device__ void gn_group_affine(double sm, double sq, int g, int b, int c, int groups, int64_t count,
+                                const float* __restrict__ gamma, const float* __restrict__ beta,
+                                float eps, float* __restrict__ affine) {
+  const int t = threadIdx.x;
+  const int cpg = c / groups;
   __shared__ double rs[256], rq[256];
   __shared__ double stat[2];
   rs[t] = sm;
@@ -269,6 +301,19 @@ int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, c
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups, n), dim3(256), 0, st, part, (int)chunks, c,
                      groups, s * (c / groups), gamma, beta, eps, affine);
   return check_launch("gn_finalize");
+}
+
+int ctmr_gn_affine_from_stats(int32_t n, int32_t tiles, int32_t c, int32_t groups, int64_t count, float eps,
+                              const double* stats, const float* gamma, const float* beta, float* affine,
+                              void* stream) {
+  if (n <= 0 || tiles <= 0 || c <= 0 || groups <= 0 || count <= 0)
+    return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (c % groups != 0) return fail(CTMR_E_INVALID, "channels must be divisible by groups");
+  if (n > 65535 || groups > 65535) return fail(CTMR_E_UNSUPPORTED, "too many batch items or groups");
+  if (!stats || !gamma || !beta || !affine) return fail(CTMR_E_INVALID, "null pointer");
+  hipLaunchKernelGGL(gn_tiles_finalize_kernel, dim3(groups, n), dim3(256), 0, (hipStream_t)stream, stats, tiles,
+                     c, groups, count, gamma, beta, eps, affine);
+  return check_launch("gn_tiles_finalize");
 }
 
 int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,

@@ -162,6 +162,7 @@ def implicit_gemm_conv3d(
     residual: Optional[Tensor] = None,
     split: int = 0,
     stream_gemm: bool = False,
+    gn_groups: int = 0,
 ) -> Tensor:
     """Padding-1 3x3x3 (or 1x1x1) convolution of NDHWC ``x`` (``_nax_conv.nax_conv3d``).
 
@@ -173,7 +174,11 @@ def implicit_gemm_conv3d(
     the output's shape.  ``split`` forces a K split (0: library policy).
     ``stream_gemm`` keeps the register-streaming GEMM where the library would
     pick the LDS-staged one (large stride-1 fp32 volumes); both are exact to
-    fp32 rounding with different fixed summation orders.
+    fp32 rounding with different fixed summation orders.  ``gn_groups`` asks
+    the epilogue for the group-norm statistics of the output over that many
+    groups (``ctmr_conv3d_gn``; same output bits); a later ``group_norm_affine``
+    of the unmodified output with the same groups uses them instead of reading
+    the output again.  Shapes that cannot produce them are computed without.
 
     Raises:
         ValueError: on a packed weight that does not fit, unsupported option
@@ -208,15 +213,32 @@ def implicit_gemm_conv3d(
         residual = _require(residual, "residual")
         if tuple(residual.shape) != out_shape:
             raise ValueError(f"residual shape {tuple(residual.shape)} != output {out_shape}")
+    if gn_groups > 0 and ops.conv_stats_tiles(tuple(x.shape), cout, ksize, stride, mode, code, split,
+                                              stream_gemm, int(gn_groups)) > 0:
+        y, stats = ops.conv3d_gn(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split,
+                                 stream_gemm, int(gn_groups))
+        y._ctmr_gn_stats = (int(gn_groups), stats, y._version)
+        return y
     return ops.conv3d(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split,
                       stream_gemm)
+
+
+def conv_output_stats(x: Tensor, groups: int) -> Optional[Tensor]:
+    """The ``(N, tiles, groups, 2)`` group-norm partials a conv epilogue wrote for ``x``, or None if
+    ``x`` carries none for ``groups`` or was modified in place since."""
+    info = getattr(x, "_ctmr_gn_stats", None)
+    if info is None or info[0] != groups or info[2] != x._version:
+        return None
+    return info[1]
 
 
 nax_conv3d = implicit_gemm_conv3d  # the reference orchestrator's name (_nax_conv.py:475)
 
 
-def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, stride: int = 1) -> Tensor:
-    """NDHWC convolution with a Torch ``(O, C, k, k, k)`` weight (``fast_fp32.conv3d_ncdhw``, :133-154)."""
+def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, stride: int = 1,
+           gn_groups: int = 0) -> Tensor:
+    """NDHWC convolution with a Torch ``(O, C, k, k, k)`` weight (``fast_fp32.conv3d_ncdhw``, :133-154);
+    ``gn_groups`` as in ``implicit_gemm_conv3d``."""
     k = int(weight.shape[2])
     if tuple(weight.shape[2:]) != (k, k, k) or (k, padding) not in ((3, 1), (1, 0)):
         raise ValueError(f"supported kernels: 3x3x3 padding 1 and 1x1x1 padding 0; got k={k}, padding={padding}")
@@ -225,7 +247,7 @@ def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, s
     if int(weight.shape[1]) != int(x.shape[-1]):
         raise ValueError(f"weight expects {int(weight.shape[1])} input channels; x has {int(x.shape[-1])}")
     return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_PLAIN), bias, cout=int(weight.shape[0]),
-                                ksize=k, stride=stride)
+                                ksize=k, stride=stride, gn_groups=gn_groups)
 
 
 def pointwise_conv(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
@@ -236,13 +258,18 @@ def pointwise_conv(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
 
 
 def group_norm_affine(x: Tensor, weight: Tensor, bias: Tensor, *, groups: int, eps: float) -> Tensor:
-    """``(N, C, 2)`` scale/offset pairs of a group norm of NDHWC ``x`` (``medmlx_core.group_norm_affine``)."""
+    """``(N, C, 2)`` scale/offset pairs of a group norm of NDHWC ``x`` (``medmlx_core.group_norm_affine``).
+    Uses the statistics a convolution epilogue wrote for ``x`` when there are any."""
     x = _require(x, "x")
     c = int(x.shape[-1])
     if c % groups != 0:
         raise ValueError(f"{c} channels are not divisible by {groups} groups")
     gamma = _vec(weight, c, "norm weight", x.device)
     beta = _vec(bias, c, "norm bias", x.device)
+    stats = conv_output_stats(x, int(groups))
+    if stats is not None:
+        count = (x.numel() // (int(x.shape[0]) * c)) * (c // int(groups))
+        return ops.gn_affine_from_stats(stats, gamma, beta, count, float(eps))
     return ops.gn_affine(x, gamma, beta, int(groups), float(eps))
 
 
@@ -283,19 +310,21 @@ def norm_conv3d(
     apply_silu: bool,
     upsample: bool = False,
     residual: Optional[Tensor] = None,
+    out_gn_groups: int = 0,
 ) -> Tensor:
-    """``conv(upsample?(silu?(norm?(x)))) + bias (+ residual)`` for 3x3x3 kernels (:162-211)."""
+    """``conv(upsample?(silu?(norm?(x)))) + bias (+ residual)`` for 3x3x3 kernels (:162-211);
+    ``out_gn_groups`` asks for the output's group-norm statistics (``implicit_gemm_conv3d``)."""
     x = _require(x, "x")
     affine = None if norm is None else group_norm_affine(x, norm[0], norm[1], groups=num_groups, eps=eps)
     mode = _lib.MODE_NEAREST2X if upsample else _lib.MODE_PLAIN
     return implicit_gemm_conv3d(x, _pack(weight, mode), bias, cout=int(weight.shape[0]), affine=affine,
-                                silu=apply_silu, upsample=upsample, residual=residual)
+                                silu=apply_silu, upsample=upsample, residual=residual, gn_groups=out_gn_groups)
 
 
-def trilinear_conv3d(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+def trilinear_conv3d(x: Tensor, weight: Tensor, bias: Tensor, *, gn_groups: int = 0) -> Tensor:
     """Padding-1 3x3x3 conv of the trilinear 2x upsampling, sampled while packing (:339-349)."""
     return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_PLAIN), bias, cout=int(weight.shape[0]),
-                                trilinear=True)
+                                trilinear=True, gn_groups=gn_groups)
 
 
 def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor], mx=None) -> Tensor:
@@ -450,6 +479,7 @@ def residual_block(
     up: bool = False,
     down: bool = False,
     conv1_bias: Optional[Tensor] = None,
+    out_gn_groups: int = 0,
 ) -> Tensor:
     """Fused ``DiffusionUNetResnetBlock`` on NDHWC ``x`` (``fast_fp32.residual_block_ncdhw``, :214-291).
 
@@ -460,7 +490,9 @@ def residual_block(
     projects the skip before upsampling it.  ``conv1_bias`` (``(N, O)``) is
     ``conv1.bias + time_emb_proj(silu(emb))`` when the caller has computed it
     already (the UNet batches every block's projection into one GEMM); ``emb``
-    is then unused.
+    is then unused.  conv1's epilogue writes norm2's statistics; conv2's writes
+    them for the block's output when ``out_gn_groups`` is set (the next
+    consumer is a group norm with that many groups).
     """
     if conv1_bias is None:
         temb = linear(F.silu(emb), weights["time_emb_proj.weight"], weights["time_emb_proj.bias"])
@@ -479,16 +511,16 @@ def residual_block(
         skip = project_skip(avg_pool3d(x))
         hidden = avg_pool3d(group_norm(x, *norm1, num_groups=num_groups, eps=eps, apply_silu=True))
         hidden = norm_conv3d(hidden, weights["conv1.conv.weight"], bias1, norm=None, num_groups=num_groups,
-                             eps=eps, apply_silu=False)
+                             eps=eps, apply_silu=False, out_gn_groups=num_groups)
     else:
         skip = project_skip(x)
         if up:
             skip = upsample_nearest(skip)
         hidden = norm_conv3d(x, weights["conv1.conv.weight"], bias1, norm=norm1, num_groups=num_groups,
-                             eps=eps, apply_silu=True, upsample=up)
+                             eps=eps, apply_silu=True, upsample=up, out_gn_groups=num_groups)
     return norm_conv3d(hidden, weights["conv2.conv.weight"], weights["conv2.conv.bias"],
                        norm=(weights["norm2.weight"], weights["norm2.bias"]), num_groups=num_groups,
-                       eps=eps, apply_silu=True, residual=skip)
+                       eps=eps, apply_silu=True, residual=skip, out_gn_groups=out_gn_groups)
 
 
 def vae_resblock(
@@ -501,18 +533,21 @@ def vae_resblock(
     *,
     num_groups: int,
     eps: float,
+    out_gn_groups: int = 0,
 ) -> Tensor:
     """Fused ``MaisiResBlock``: GN-SiLU-conv twice, skip in conv2's accumulator (:294-336).
+    Group-norm statistics as in ``residual_block``.
 
     ``state`` holds the block input and is emptied so the caller's reference
     does not keep a multi-gigabyte input alive past its last use.
     """
     x = state.pop()
-    hidden = norm_conv3d(x, *conv1, norm=norm1, num_groups=num_groups, eps=eps, apply_silu=True)
+    hidden = norm_conv3d(x, *conv1, norm=norm1, num_groups=num_groups, eps=eps, apply_silu=True,
+                         out_gn_groups=num_groups)
     skip = x if shortcut is None else pointwise_conv(x, *shortcut)
     del x
     return norm_conv3d(hidden, *conv2, norm=norm2, num_groups=num_groups, eps=eps, apply_silu=True,
-                       residual=skip)
+                       residual=skip, out_gn_groups=out_gn_groups)
 
 
 # ---------------------------------------------------------------------------

@@ -153,10 +153,12 @@ def _blocks(weights: Mapping[str, Tensor], emb: Tensor, groups: int, eps: float,
     proj_w, proj_b, spans = _time_projections(weights)
     conv1_bias = F.linear(F.silu(emb), proj_w, proj_b)
 
-    def resnet(h: Tensor, prefix: str, **kw) -> Tensor:
+    def resnet(h: Tensor, prefix: str, *, normed_next: bool = True, **kw) -> Tensor:
+        """``normed_next``: a group norm reads the output next (its statistics come from conv2)."""
         lo, hi = spans[prefix]
         return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps,
-                                 conv1_bias=conv1_bias[:, lo:hi].contiguous(), **kw)
+                                 conv1_bias=conv1_bias[:, lo:hi].contiguous(),
+                                 out_gn_groups=groups if normed_next else 0, **kw)
 
     def attention(h: Tensor, prefix: str, n_heads: int) -> Tensor:
         return spatial_attention(h, _prefixed(weights, prefix), num_groups=groups, eps=eps,
@@ -185,7 +187,7 @@ def _mid_block(hidden: Tensor, resnet, attention, n_heads: int) -> Tensor:
     """resnet -> attention -> resnet (unet.py:359-399)."""
     hidden = resnet(hidden, "middle_block.resnet_1")
     hidden = attention(hidden, "middle_block.attention", n_heads)
-    return resnet(hidden, "middle_block.resnet_2")
+    return resnet(hidden, "middle_block.resnet_2", normed_next=False)  # concatenated with a skip next
 
 
 def denoise_unet(
@@ -219,7 +221,8 @@ def denoise_unet(
     t_emb, emb = condition_embedding(timesteps, class_labels, spacing, weights, constructor)
     resnet, attention = _blocks(weights, emb, groups, eps, include_fc)
 
-    hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1)
+    hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1,
+                       gn_groups=groups)
     hidden, skips = _down_path(hidden, resnet, attention, res_blocks, attn_levels, heads)
     if down_block_additional_residuals is not None:
         extras = list(down_block_additional_residuals)
@@ -237,7 +240,7 @@ def denoise_unet(
         for r in range(n_res):
             skip = samples.pop()
             hidden = torch.cat([hidden, skip], dim=-1)
-            hidden = resnet(hidden, f"up_blocks.{index}.resnets.{r}")
+            hidden = resnet(hidden, f"up_blocks.{index}.resnets.{r}", normed_next=rev_attn[index] or r == n_res - 1)
             if rev_attn[index]:
                 hidden = attention(hidden, f"up_blocks.{index}.attentions.{r}", rev_heads[index])
         if index != n_levels - 1:
@@ -379,11 +382,11 @@ def run_vae_decoder(x: Tensor, weights: Mapping[str, Tensor], *, constructor: Ma
     if constructor.get("use_convtranspose"):
         raise ValueError("transposed-convolution upsampling is not part of this path")
     groups, eps = int(constructor["norm_num_groups"]), float(constructor["norm_eps"])
-    hidden = ff.conv3d(x, *_conv_weights(weights, "decoder.blocks.0"), padding=1)
+    hidden = ff.conv3d(x, *_conv_weights(weights, "decoder.blocks.0"), padding=1, gn_groups=groups)
     index = 1
     rev = channels[::-1]
     for level, n_res in enumerate(res_blocks[::-1]):
-        for _ in range(n_res):
+        for r in range(n_res):
             p = f"decoder.blocks.{index}"
             shortcut = _conv_weights(weights, f"{p}.nin_shortcut") if any(
                 k.startswith(f"{p}.nin_shortcut.") for k in weights) else None
@@ -392,11 +395,12 @@ def run_vae_decoder(x: Tensor, weights: Mapping[str, Tensor], *, constructor: Ma
             hidden = ff.vae_resblock(state, _conv_weights(weights, f"{p}.conv1"), _conv_weights(weights, f"{p}.conv2"),
                                      (_need(weights, f"{p}.norm1.weight"), _need(weights, f"{p}.norm1.bias")),
                                      (_need(weights, f"{p}.norm2.weight"), _need(weights, f"{p}.norm2.bias")),
-                                     shortcut, num_groups=groups, eps=eps)
+                                     shortcut, num_groups=groups, eps=eps,
+                                     out_gn_groups=groups if r < n_res - 1 or level == len(rev) - 1 else 0)
             index += 1
         if level != len(rev) - 1:
             w, b = _conv_weights(weights, f"decoder.blocks.{index}.conv")
-            hidden = ff.trilinear_conv3d(hidden, w, b)
+            hidden = ff.trilinear_conv3d(hidden, w, b, gn_groups=groups)
             index += 1
     norm = (_need(weights, f"decoder.blocks.{index}.weight"), _need(weights, f"decoder.blocks.{index}.bias"))
     return ff.norm_conv3d(hidden, *_conv_weights(weights, f"decoder.blocks.{index + 1}"), norm=norm,

@@ -128,9 +128,92 @@ def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype,
     return x.new_empty((x.shape[0], od, oh, ow, cout))
 
 
+def conv_stats_tiles(x_shape: tuple[int, ...], cout: int, ksize: int, stride: int, mode: int, dtype: int,
+                     split: int, stream_gemm: bool, groups: int) -> int:
+    """Group-norm partials per batch item that ``conv3d_gn`` writes for this shape, 0 if it cannot."""
+    flags = _lib.F_STREAM if stream_gemm else 0
+    desc = make_desc(tuple(x_shape), cout, ksize, stride, mode, flags, dtype, split)
+    return max(int(_lib.lib().ctmr_conv3d_stats_tiles(ctypes.byref(desc), groups)), 0)
+
+
+@torch.library.custom_op("ctmr::conv3d_gn", mutates_args=())
+def conv3d_gn(
+    x: Tensor,
+    packed: Tensor,
+    bias: Optional[Tensor],
+    affine: Optional[Tensor],
+    residual: Optional[Tensor],
+    cout: int,
+    ksize: int,
+    stride: int,
+    mode: int,
+    silu: bool,
+    dtype: int,
+    split: int,
+    stream_gemm: bool,
+    groups: int,
+) -> tuple[Tensor, Tensor]:
+    """``ctmr_conv3d_gn``: the ``conv3d`` output plus float64 group-norm partials of it, shape
+    ``(N, tiles, groups, 2)`` holding (sum, sum of squares) per output tile and group."""
+    _require_device(x, packed, bias, affine, residual)
+    batch_bias = bias is not None and bias.dim() == 2
+    flags = _flags(affine is not None, silu, batch_bias, residual is not None)
+    if stream_gemm:
+        flags |= _lib.F_STREAM
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split)
+    tiles = _lib.check(_lib.lib().ctmr_conv3d_stats_tiles(ctypes.byref(desc), groups), "ctmr_conv3d_stats_tiles")
+    if tiles == 0:
+        raise ValueError("this convolution cannot produce group-norm partials")
+    od, oh, ow = _lib.output_dims(desc)
+    y = torch.empty((x.shape[0], od, oh, ow, cout), device=x.device, dtype=torch.float32)
+    stats = torch.empty((x.shape[0], tiles, groups, 2), device=x.device, dtype=torch.float64)
+    ws_bytes = _lib.workspace_bytes(desc)
+    ws = torch.empty(max(ws_bytes, 1), device=x.device, dtype=torch.uint8)
+    _lib.check(
+        _lib.lib().ctmr_conv3d_gn(
+            ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
+            _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, groups, stats.data_ptr(),
+            _stream(x.device),
+        ),
+        "ctmr_conv3d_gn",
+    )
+    return y, stats
+
+
+@conv3d_gn.register_fake
+def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split, stream_gemm, groups):
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, _lib.F_STREAM if stream_gemm else 0, dtype, split)
+    od, oh, ow = _lib.output_dims(desc)
+    tiles = max(int(_lib.lib().ctmr_conv3d_stats_tiles(ctypes.byref(desc), groups)), 1)
+    return (x.new_empty((x.shape[0], od, oh, ow, cout)),
+            x.new_empty((x.shape[0], tiles, groups, 2), dtype=torch.float64))
+
+
 # ---------------------------------------------------------------------------
 # group norm
 # ---------------------------------------------------------------------------
+@torch.library.custom_op("ctmr::gn_affine_from_stats", mutates_args=())
+def gn_affine_from_stats(stats: Tensor, gamma: Tensor, beta: Tensor, count: int, eps: float) -> Tensor:
+    """``ctmr_gn_affine_from_stats``: (N, C, 2) (scale, offset) pairs from ``conv3d_gn`` partials
+    ``(N, tiles, groups, 2)``; ``count`` is the number of values in one (batch item, group)."""
+    _require_device(stats, gamma, beta)
+    n, tiles, groups = (int(v) for v in stats.shape[:3])
+    c = int(gamma.numel())
+    out = torch.empty((n, c, 2), device=stats.device, dtype=torch.float32)
+    _lib.check(
+        _lib.lib().ctmr_gn_affine_from_stats(n, tiles, c, groups, count, float(eps), stats.data_ptr(),
+                                             gamma.data_ptr(), beta.data_ptr(), out.data_ptr(),
+                                             _stream(stats.device)),
+        "ctmr_gn_affine_from_stats",
+    )
+    return out
+
+
+@gn_affine_from_stats.register_fake
+def _(stats, gamma, beta, count, eps):
+    return stats.new_empty((stats.shape[0], gamma.numel(), 2), dtype=torch.float32)
+
+
 @torch.library.custom_op("ctmr::gn_affine", mutates_args=())
 def gn_affine(x: Tensor, gamma: Tensor, beta: Tensor, groups: int, eps: float) -> Tensor:
     """Per-(batch, channel) (scale, offset) pairs, shape ``(N, C, 2)``."""

@@ -179,3 +179,40 @@ def test_attention_host_checks(ctmr, native_loaded, kw, status, message):
     misaligned = ctypes.c_void_p((1 << 20) + 4)
     assert native_loaded.ctmr_flash_attention(ctypes.byref(good), misaligned, fake, fake, fake, None) == -1
     assert "16-byte aligned" in ctmr._lib.last_error()
+
+
+def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
+    """``ctmr_conv3d_stats_tiles``: partials per batch item, or 0 where the epilogue cannot write them."""
+    L = ctmr._lib
+
+    def tiles(groups, *dims, **kw):
+        return native_loaded.ctmr_conv3d_stats_tiles(ctypes.byref(L.conv_desc(*dims, **kw)), groups)
+
+    assert tiles(32, 1, 64, 64, 64, 128, 128) == 16 * 8 * 8  # LDS-staged: one per 4x8x8 brick
+    assert tiles(32, 1, 64, 64, 64, 64, 64) == 64**3 // 256  # streaming: one per 256-voxel M tile
+    # K split: the reduction writes them, one per chunk of 16 * rows output voxels (rows keeps ~1024 blocks)
+    assert tiles(32, 2, 4, 8, 8, 512, 512) == 256 // 16
+    assert tiles(32, 2, 16, 32, 32, 128, 128) == 16 * 32 * 32 // (16 * 4)
+    assert tiles(3, 1, 8, 8, 8, 256, 96, split=4) == 0  # split reduce works on 64-column tiles
+    assert tiles(2, 1, 8, 8, 8, 256, 256, split=4) == 0  # 128-wide groups
+    assert tiles(1, 1, 8, 8, 8, 64, 1) == 0  # cout <= 4: outputs come from the tap sum
+    assert tiles(3, 1, 8, 8, 8, 64, 128) == 0  # groups must divide cout
+    # 256 columns in two 128-wide workgroup tiles: a group may not straddle them
+    assert tiles(1, 1, 16, 16, 16, 256, 256, flags=L.F_STREAM, split=1) == 0
+    assert tiles(2, 1, 16, 16, 16, 256, 256, flags=L.F_STREAM, split=1) == 16**3 // 128
+    # nearest-2x upsample: one tile per (parity phase, source M tile)
+    assert tiles(3, 1, 4, 4, 4, 32, 48, mode=L.MODE_NEAREST2X, split=1) == 8
+    assert tiles(2, 1, 4, 4, 4, 32, 48, mode=L.MODE_NEAREST2X, split=1) == 0  # 24-wide groups vs 64 columns
+    d = L.conv_desc(1, 8, 8, 8, 64, 1)
+    fake = 0x1000  # never dereferenced: the checks fail first
+    rc = native_loaded.ctmr_conv3d_gn(ctypes.byref(d), fake, fake, None, None, None, fake, fake, 1 << 40, 1, fake,
+                                      None)
+    assert rc == L.E_UNSUPPORTED and "partials" in L.last_error()
+    d = L.conv_desc(1, 8, 8, 8, 64, 64)
+    rc = native_loaded.ctmr_conv3d_gn(ctypes.byref(d), fake, fake, None, None, None, fake, fake, 1 << 40, 32, None,
+                                      None)
+    assert rc == L.E_INVALID
+    rc = native_loaded.ctmr_gn_affine_from_stats(1, 4, 12, 5, 64, 1e-6, fake, fake, fake, fake, None)
+    assert rc == L.E_INVALID and "divisible" in L.last_error()
+    rc = native_loaded.ctmr_gn_affine_from_stats(1, 0, 12, 4, 64, 1e-6, fake, fake, fake, fake, None)
+    assert rc == L.E_INVALID
