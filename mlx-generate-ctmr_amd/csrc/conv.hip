@@ -850,6 +850,284 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 3c. LDS-staged bf16 implicit GEMM (stride-1 bf16 volumes)
+// ---------------------------------------------------------------------------
+// The bf16 MFMA (16x16x32, 16 cycles) consumes operands 8x faster per cycle
+// than the fp32 one, more than the texture path can feed from L2 (the
+// register-streaming bf16 GEMM saturates it at ~15 % of the bf16 peak).  Here
+// both operands come from LDS, filled by direct-to-LDS buffer loads (no
+// register staging): per 32-channel chunk the 6x10x10 halo of a 4x8x8 output
+// brick from the bf16 packed copy (already zero-padded, affine + SiLU or the
+// trilinear sample applied by the pack), and per tap row (kd, kh) the three
+// taps' 64-column weight tiles, double buffered one row ahead.  A lane's
+// 16-byte slot s of a fill lands at LDS byte 16 s; 80-byte voxel / column rows
+// (64 data bytes + one skipped slot) keep a 16-lane read on distinct banks.
+// Tiles, wave layout and epilogue are those of conv_lds_kernel.
+constexpr int kB16Row = 80;
+constexpr int kB16HaloSlots = kHaloVox * 5;                  // 3000
+constexpr int kB16HaloIters = (kB16HaloSlots + 255) / 256;   // 12
+constexpr int kB16TapBytes = 64 * kB16Row;                   // one tap's 64 columns
+constexpr int kB16RowSlots = 3 * 64 * 5;                     // 960
+constexpr int kB16RowIters = (kB16RowSlots + 255) / 256;     // 4
+
+struct Lds16Args {
+  const char* xp;       // bf16 packed copy (n, d+2, h+2, w+2, cp)
+  const char* wp;       // packed bf16 weight [tap][kblock][np][64 bytes]
+  const float* bias;
+  const float* res;
+  float* y;             // output, or split partial planes
+  int64_t x_bytes, w_bytes, plane, rows_per_batch;
+  int d, h, w;          // output grid = packed interior
+  int P, Q;             // padded plane / row pitch in voxels
+  int vbytes;           // bytes per packed voxel (cp * 2)
+  int cout, np, kb, n;
+  int tz, ty, tx, n_tiles, split;
+  int batch_bias, has_res, has_bias;
+  double* stats;
+  int gn_groups, gn_cpg;
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Direct-to-LDS 16-byte load of lane i into LDS byte `lds_addr + 16 i` (a
+// wave-uniform address).  Written as inline assembly because the compiler
+// cannot tell this LDS target apart from the buffers being read meanwhile and
+// would wait for the load before every following ds_read; callers wait for
+// it themselves (s_waitcnt vmcnt(0) before the barrier that publishes it).
+__device__ __forceinline__ void lds_dma16(const void* gptr, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(gptr)
+               : "memory", "m0");
+}
+
+// One tap row (kd, kh) of conv_lds_bf16_kernel: starts the fill of the next
+// weight row into `fill` (when `do_fill`), then runs the row's three taps with
+// A from `halo_p` and B from `brow`.  The restrict qualifiers state that the
+// fill target, the weight row being read and the halo are distinct LDS
+// buffers, so the compiler keeps the fill in flight across the reads instead
+// of waiting for it before the first ds_read.
+template <int KD, int KH>
+__device__ __forceinline__ void lds16_row(f4 (&acc)[4][4], char* __restrict__ fill,
+                                          const char* __restrict__ wsrc, const char* __restrict__ brow,
+                                          const char* __restrict__ halo_p, bool do_fill, const int (&woff)[4],
+                                          unsigned wload, int wave, const int (&abase)[4],
+                                          const int (&bbase)[4]) {
+  if (do_fill) {
+#pragma unroll
+    for (int j = 0; j < kB16RowIters; ++j)
+      if ((wload >> j) & 1u)
+        lds_dma16(wsrc + woff[j], (unsigned)(uintptr_t)(lds_ptr_t)(fill + (j * 256 + wave * 64) * 16));
+  }
+  u4 A[2][4], B[2][4];
+  auto load = [&](int slot, int kw) {
+    const int off = ((KD * kHH + KH) * kHW + kw) * kB16Row;
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) A[slot][ms] = *reinterpret_cast<const u4*>(halo_p + abase[ms] + off);
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns)
+      B[slot][ns] = *reinterpret_cast<const u4*>(brow + kw * kB16TapBytes + bbase[ns]);
+  };
+  load(0, 0);
+#pragma unroll
+  for (int kw = 0; kw < 3; ++kw) {
+    if (kw < 2) load((kw + 1) & 1, kw + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) mfma_step<CTMR_BF16>(acc[ms][ns], A[kw & 1][ms], B[kw & 1][ns]);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
+  __shared__ __attribute__((aligned(16))) char halo[kHaloVox * kB16Row];
+  __shared__ __attribute__((aligned(16))) char bbuf[2][3 * kB16TapBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int xcd = bid & 7, slot = bid >> 3, per = nb >> 3, rem = nb & 7;
+  const int tile = (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int n_tile = tile % p.n_tiles;
+  int rest = tile / p.n_tiles;
+  const int bx = rest % p.tx;
+  rest /= p.tx;
+  const int by = rest % p.ty;
+  rest /= p.ty;
+  const int bz = rest % p.tz;
+  rest /= p.tz;
+  const int b = rest % p.n;
+  const int split_id = rest / p.n;
+  const int z0 = bz * kBD, y0 = by * kBH, x0 = bx * kBW;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int n0 = n_tile * 64;
+
+  // Halo fill: slot s = tid + 256 i is 16-byte piece s % 5 of halo voxel s / 5
+  // (piece 4 is the row's padding, not loaded).  The brick's halo origin in
+  // padded coordinates is (z0, y0, x0); coordinates past the padded volume
+  // (ragged bricks) are clamped -- they feed only masked output rows.
+  const int64_t xbase = ((int64_t)b * p.rows_per_batch + (int64_t)z0 * p.P) * p.vbytes;
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.xp + xbase), (short)0, (int)min(p.x_bytes - xbase, (int64_t)0x7fffffff), 0x00020000);
+  const int pd_max = p.d + 1 - z0, ph_max = p.h + 1, pw_max = p.w + 1;
+  int hoff[kB16HaloIters];
+  unsigned hload = 0;
+#pragma unroll
+  for (int i = 0; i < kB16HaloIters; ++i) {
+    const int sl = tid + 256 * i;
+    const int v = sl / 5, q = sl - 5 * (sl / 5);
+    hoff[i] = 0;
+    if (sl < kB16HaloSlots && q < 4) {
+      hload |= 1u << i;
+      const int hz = v / (kHH * kHW), hr = v - hz * (kHH * kHW);
+      const int hy = hr / kHW, hx = hr - hy * kHW;
+      const int pz = min(hz, pd_max), py = min(y0 + hy, ph_max), px = min(x0 + hx, pw_max);
+      hoff[i] = ((pz * p.P + py * p.Q + px) * p.vbytes) + q * 16;
+    }
+  }
+  // Weight-row fill: slot s = tid + 256 j is piece s % 5 of column (s % 320) / 5
+  // of tap s / 320 of the row.
+  const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wp, (short)0, (int)min(p.w_bytes, (int64_t)0x7fffffff), 0x00020000);
+  const int tap_bytes = p.kb * p.np * 64;  // packed bytes between consecutive taps
+  int woff[kB16RowIters];
+  unsigned wload = 0;
+#pragma unroll
+  for (int j = 0; j < kB16RowIters; ++j) {
+    const int sl = tid + 256 * j;
+    const int t = sl / 320, r = sl - 320 * (sl / 320);
+    const int col = r / 5, q = r - 5 * (r / 5);
+    woff[j] = 0;
+    if (sl < kB16RowSlots && q < 4) {
+      wload |= 1u << j;
+      woff[j] = t * tap_bytes + (n0 + col) * 64 + q * 16;
+    }
+  }
+  auto fill_halo = [&](int chunk) {
+    const int so = __builtin_amdgcn_readfirstlane(chunk * 64);
+#pragma unroll
+    for (int i = 0; i < kB16HaloIters; ++i)
+      if ((hload >> i) & 1u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (lds_ptr_t)(halo + (i * 256 + wave * 64) * 16), 16,
+                                                 hoff[i], so, 0, 0);
+  };
+  auto row_so = [&](int chunk, int row) {
+    return __builtin_amdgcn_readfirstlane((row * 3 * p.kb + chunk) * p.np * 64);
+  };
+
+  int abase[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+    abase[ms] = ((wave * kHH + 2 * ms + (lrow >> 3)) * kHW + (lrow & 7)) * kB16Row + lgrp * 16;
+  int bbase[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) bbase[ns] = (ns * 16 + lrow) * kB16Row + lgrp * 16;
+
+  f4 acc[4][4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int c_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)split_id * p.kb / p.split));
+  const int c_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(split_id + 1) * p.kb / p.split));
+
+  int k = 0;  // running tap-row count: weight buffer k & 1
+  fill_halo(c_begin);
+  {
+    const int so0 = row_so(c_begin, 0);
+#pragma unroll
+    for (int j = 0; j < kB16RowIters; ++j)
+      if ((wload >> j) & 1u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, (lds_ptr_t)(&bbuf[0][0] + (j * 256 + wave * 64) * 16), 16,
+                                                 woff[j], so0, 0, 0);
+  }
+  for (int chunk = c_begin; chunk < c_end; ++chunk) {
+    const bool more = chunk + 1 < c_end;
+#define CTMR_LDS16_ROW(R)                                                                                   \
+    {                                                                                                      \
+      /* This wave's fills have landed; the barrier makes every wave's visible and ends every read of   \
+         the buffer the next fill overwrites. */                                                           \
+      __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */                                                   \
+      __syncthreads();                                                                                     \
+      const int so = (R) < 8 ? row_so(chunk, (R) + 1) : row_so(more ? chunk + 1 : chunk, 0);              \
+      lds16_row<(R) / 3, (R) % 3>(acc, &bbuf[(k + 1) & 1][0], p.wp + so, &bbuf[k & 1][0], halo,            \
+                                  (R) < 8 || more, woff, wload, wave, abase, bbase);                       \
+      ++k;                                                                                                 \
+    }
+    CTMR_LDS16_ROW(0) CTMR_LDS16_ROW(1) CTMR_LDS16_ROW(2)
+    CTMR_LDS16_ROW(3) CTMR_LDS16_ROW(4) CTMR_LDS16_ROW(5)
+    CTMR_LDS16_ROW(6) CTMR_LDS16_ROW(7) CTMR_LDS16_ROW(8)
+#undef CTMR_LDS16_ROW
+    if (more) {
+      __syncthreads();  // every wave is done with this chunk's halo
+      fill_halo(chunk + 1);
+    }
+  }
+
+  // Epilogue (as conv_lds_kernel).
+  const bool partial = p.split > 1;
+  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
+  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
+  const int z = z0 + wave;
+  auto out_base = [&](int y, int x) -> int64_t {
+    return ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout;
+  };
+  float bv[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) bv[ns] = (!partial && p.has_bias) ? bias_b[n0 + ns * 16 + lrow] : 0.f;
+  float rv[4][4][4];
+  const bool add_res = !partial && p.has_res;
+  if (add_res) {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t base = out_base(y0 + 2 * ms + (lgrp >> 1), x0 + 4 * (lgrp & 1) + r);
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) rv[ms][r][ns] = p.res[base + n0 + ns * 16 + lrow];
+      }
+  }
+  double s1[4], s2[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) s1[ns] = s2[ns] = 0.0;
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+    const int y = y0 + 2 * ms + (lgrp >> 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int x = x0 + 4 * (lgrp & 1) + r;
+      if (z >= p.d || y >= p.h || x >= p.w) continue;
+      const int64_t base = out_base(y, x);
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) {
+        const int col = n0 + ns * 16 + lrow;
+        float sum = acc[ms][ns][r];
+        if (!partial) {
+          if (p.has_bias) sum += bv[ns];
+          if (add_res) sum += rv[ms][r][ns];
+        }
+        out[base + col] = sum;
+        if (p.stats) {
+          s1[ns] += (double)sum;
+          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
+        }
+      }
+    }
+  }
+  if (p.stats) {  // a kernel argument: every thread reaches both barriers
+    __syncthreads();  // the reduction buffer reuses the halo
+    double (*red)[64][2] = reinterpret_cast<double (*)[64][2]>(halo);
+    const int tile_id = (bz * p.ty + by) * p.tx + bx;
+    write_gn_partials<4, 4, 1>(s1, s2, red, wave, lane, n0, p.cout, p.gn_cpg, p.gn_groups,
+                               p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
+  }
+}
+
 // Sum of split partial planes in ascending order, then residual; bias first
 // as in the reference reduce (_nax_conv.py:320-332).
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
@@ -948,6 +1226,7 @@ struct Geometry {
   int split;
   int nsub, wm, wn, m_tiles, n_tiles;
   bool lds;              // LDS-staged GEMM (conv_lds_kernel)
+  bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
   int tz, ty, tx;        // its bricks per axis
   int layout;            // WL_TAPS, WL_EXPAND (cout <= 4) or WL_IM2COL (small cin)
   int ncols;             // GEMM columns: cout, or 27 * cout for WL_EXPAND
@@ -1053,6 +1332,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // replace, measured on MI355X), 64-wide column tiles, at least 4 chunks per
   // split, and 6 staged planes within 32-bit buffer offsets.
   g.lds = false;
+  g.lds16 = false;
   if (g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 && d->stride == 1 &&
       d->mode == CTMR_MODE_PLAIN && d->cin % 16 == 0 && d->cin >= 128 && d->cout % 64 == 0 &&
       !(d->flags & CTMR_F_STREAM)) {
@@ -1090,12 +1370,28 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
     return CTMR_OK;
   }
+  // LDS-staged bf16 GEMM: stride-1 bf16 convs (plain or trilinear-2x, both
+  // sampled by the pack) with 64-wide column tiles whose 4x8x8 bricks are at
+  // least 3/4 full; the halo fill's 32-bit offsets span 6 packed planes.
+  g.lds16 = false;
+  if (g.layout == WL_TAPS && d->dtype == CTMR_BF16 && d->ksize == 3 && d->stride == 1 && plain_weights &&
+      d->cout % 64 == 0 && !(d->flags & CTMR_F_STREAM)) {
+    const int tz = (int)ceil_div(g.gd, kBD), ty = (int)ceil_div(g.gh, kBH), tx = (int)ceil_div(g.gw, kBW);
+    const int64_t slots = (int64_t)tz * ty * tx * kBD * kBH * kBW;
+    const int64_t planes = (int64_t)kHD * g.P * g.cp * 2;
+    const int64_t w_bytes = (int64_t)27 * g.kblocks * g.np * 64;
+    if (4 * S >= 3 * slots && planes < (1ll << 31) && w_bytes < (1ll << 31)) {
+      g.lds16 = true;
+      g.tz = tz; g.ty = ty; g.tx = tx;
+    }
+  }
   // Tile shape by GEMM width.
-  if (g.ncols <= 16) { g.nsub = 1; g.wm = 4; g.wn = 1; }
+  if (g.lds16) { g.nsub = 4; g.wm = 4; g.wn = 1; }
+  else if (g.ncols <= 16) { g.nsub = 1; g.wm = 4; g.wn = 1; }
   else if (g.ncols <= 32) { g.nsub = 2; g.wm = 4; g.wn = 1; }
   else if (g.ncols <= 64) { g.nsub = 4; g.wm = 4; g.wn = 1; }
   else { g.nsub = 4; g.wm = 2; g.wn = 2; }
-  g.m_tiles = (int)ceil_div(S, g.wm * 64);
+  g.m_tiles = g.lds16 ? g.tz * g.ty * g.tx : (int)ceil_div(S, g.wm * 64);
   g.n_tiles = (int)ceil_div(g.np, g.wn * g.nsub * 16);
   // K split: the (tap, channel-block) step sequence of every output is cut
   // into `split` contiguous ranges whose fp32 partial planes are summed in
@@ -1107,6 +1403,11 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   if (g.layout == WL_EXPAND) {
     if (d->split > 1) return fail(CTMR_E_INVALID, "split must be 1 for the cout <= 4 tap-expanded GEMM");
     g.split = 1;
+  } else if (g.lds16) {  // chunk-range split, as the fp32 LDS GEMM
+    if (d->split > g.kblocks) return fail(CTMR_E_INVALID, "split must not exceed the 32-channel chunk count");
+    const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n;
+    g.split = d->split > 0 ? d->split
+                           : (base < 512 ? (int)std::min<int64_t>(ceil_div(512, base), g.kblocks) : 1);
   } else if (d->split > 0) {
     if (d->split > steps) return fail(CTMR_E_INVALID, "split must not exceed the K step count");
     g.split = d->split;
@@ -1150,7 +1451,7 @@ static int gn_stats_tiles(const ctmr_conv_desc* d, const Geometry& g, int groups
   }
   const int width = g.lds ? 64 : g.wn * g.nsub * 16;
   if (cpg > width || width % cpg != 0) return 0;
-  return g.lds ? g.tz * g.ty * g.tx : g.m_tiles * g.phases;
+  return (g.lds || g.lds16) ? g.tz * g.ty * g.tx : g.m_tiles * g.phases;
 }
 
 // The K-split reduction, with group-norm partials when `stats` is set.
@@ -1404,6 +1705,41 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
     const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.split;
     hipLaunchKernelGGL(conv_lds_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
     if ((rc = check_launch("conv_lds"))) return rc;
+    if (g.split > 1) {
+      launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
+      if ((rc = check_launch("split_reduce"))) return rc;
+    }
+    return CTMR_OK;
+  }
+  if (g.lds16) {
+    Lds16Args a;
+    a.xp = xp;
+    a.wp = (const char*)packed;
+    a.bias = bias;
+    a.res = residual;
+    a.rows_per_batch = g.rows_per_batch;
+    a.x_bytes = (int64_t)desc->n * g.rows_per_batch * g.cp * 2;
+    a.w_bytes = (int64_t)27 * g.kblocks * g.np * 64;
+    a.plane = (int64_t)desc->n * s_out * desc->cout;
+    a.d = g.gd; a.h = g.gh; a.w = g.gw;
+    a.P = g.P; a.Q = g.Q;
+    a.vbytes = g.cp * 2;
+    a.cout = desc->cout; a.np = g.np; a.kb = g.kblocks; a.n = desc->n;
+    a.tz = g.tz; a.ty = g.ty; a.tx = g.tx;
+    a.n_tiles = g.n_tiles;
+    a.split = g.split;
+    a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
+    a.has_bias = bias != nullptr;
+    a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
+    a.stats = g.split > 1 ? nullptr : stats;
+    a.gn_groups = stats ? groups : 0;
+    a.gn_cpg = stats ? desc->cout / groups : 1;
+    float* part = (float*)((char*)workspace + g.pack_bytes);
+    a.y = g.split > 1 ? part : y;
+    if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.split;
+    hipLaunchKernelGGL(conv_lds_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    if ((rc = check_launch("conv_lds_bf16"))) return rc;
     if (g.split > 1) {
       launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
       if ((rc = check_launch("split_reduce"))) return rc;

@@ -84,6 +84,10 @@ def test_split_policy_is_shape_only(ctmr):
     assert L.conv_split(L.conv_desc(2, 8, 16, 16, 256, 256)) == 8  # 64 tiles x 8
     assert L.conv_split(L.conv_desc(2, 16, 32, 32, 128, 128)) == 2  # 256 tiles x 2
     assert L.conv_split(L.conv_desc(2, 16, 32, 32, 64, 64)) == 4  # streaming: 128 tiles x 4
+    # bf16 stride-1 convs with 64-wide column tiles use the LDS-staged bf16 GEMM: its split divides the
+    # 32-channel chunks (2 here) over 4x8x8 bricks; the streaming bf16 GEMM splits the 54 K steps
+    assert L.conv_split(L.conv_desc(2, 8, 16, 16, 64, 64, dtype=L.DT_BF16)) == 2  # 16 bricks x 2 chunks
+    assert L.conv_split(L.conv_desc(2, 8, 16, 16, 64, 64, dtype=L.DT_BF16, flags=L.F_STREAM)) == 6
     # large grids never split
     assert L.conv_split(L.conv_desc(1, 128, 128, 128, 128, 128)) == 1
     assert L.conv_split(L.conv_desc(1, 64, 64, 64, 64, 64)) == 1

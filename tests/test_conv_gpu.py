@@ -172,6 +172,51 @@ def test_lds_staged_and_streaming_gemms_match_float64(ctmr, dev, shape, cout, fu
     assert rm.max_rel_error(outs[0], outs[1]) <= 2 * FP32_REL
 
 
+@pytest.mark.parametrize(("shape", "cout", "kw"), [
+    ((2, 8, 16, 16, 64), 64, {}),                               # config-0 channels, policy chunk split
+    ((1, 7, 16, 15, 128), 128, {"split": 1}),                   # ragged bricks (clamped halo, masked rows)
+    ((1, 4, 8, 8, 512), 512, {"split": 8}),                     # one brick, 8-way chunk split
+    ((2, 8, 8, 8, 48), 64, {"split": 1}),                       # 48 channels packed to 64 (zero chunk half)
+    ((1, 4, 8, 8, 32), 64, {"trilinear": True, "split": 1}),    # trilinear-2x sampled by the pack
+    ((2, 8, 16, 16, 128), 128, {"fused": True, "split": 1}),    # GN affine + SiLU, batch bias, residual
+])
+def test_bf16_lds_gemm_matches_streaming_bf16(ctmr, dev, shape, cout, kw):
+    """The LDS-staged bf16 GEMM (direct-to-LDS halo and weight fills) against the register-streaming bf16
+    GEMM: same bf16 operands from the same pack, fp32 accumulation in two fixed orders, so they agree to
+    fp32 rounding (1e-5); both within the bf16 bar of float64; repeat runs bit-identical."""
+    print(f"bf16 lds {shape}->{cout} {kw}", flush=True)
+    kw = dict(kw)
+    fused = kw.pop("fused", False)
+    rng = np.random.default_rng(sum(shape) + cout)
+    n, c = shape[0], shape[-1]
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal((n, cout)).astype(np.float32)
+    f = ctmr.fast_fp32
+    packed = f.pack_weight(_t(w, dev), dtype="bf16")
+    xin = rm.upsample_trilinear(x) if kw.get("trilinear") else x
+    affine = res = None
+    if fused:
+        gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+        affine = f.group_norm_affine(_t(x, dev), _t(gw, dev), _t(gb, dev), groups=8, eps=1e-6)
+        xin = rm.group_norm(x, gw, gb, 8, 1e-6, apply_silu=True)
+        res = rng.standard_normal((*shape[:-1], cout)).astype(np.float32)
+    expected = rm.conv3d(xin, w) + bias[:, None, None, None, :] + (0 if res is None else res)
+    outs = []
+    for stream_gemm in (False, True):
+        run = lambda: f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), cout=cout, affine=affine,
+                                             silu=fused, residual=None if res is None else _t(res, dev),
+                                             stream_gemm=stream_gemm, **kw)
+        y = run()
+        assert torch.equal(y, run())
+        _assert_rel(_h(y), expected, BF16_REL, f"bf16 {'streaming' if stream_gemm else 'lds'} {shape}->{cout}")
+        outs.append(_h(y))
+    err = rm.max_rel_error(outs[0], outs[1])
+    print(f"bf16 lds vs streaming: {err:.3e}", flush=True)
+    assert err <= FP32_REL
+
+
 def test_repeat_runs_are_bitwise_identical(ctmr, dev):
     rng = np.random.default_rng(13)
     x = _t(rng.standard_normal((2, 12, 10, 9, 48)).astype(np.float32), dev)
