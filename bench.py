@@ -279,6 +279,15 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         "ms": round(ms, 3), "conv_tflop": round(conv_f / 1e12, 4), "attention_tflop": round(attn_f / 1e12, 4),
         "tflops": round((conv_f + attn_f) / ms / 1e9, 2), "roofline_ms": round(floor_ms, 3),
         "frac_roofline": round(floor_ms / ms, 4)}
+    # the bf16-in / fp32-accumulate variant of the same step (convolutions on bf16 MFMA; attention,
+    # norms and projections stay fp32): floor = convs at the bf16 peak + attention at the fp32 peak
+    with pkg.fast_fp32.precision("bf16"):
+        for _ in range(2):
+            step()
+        ms16 = _wall_ms(step, max(3, steps // 2))
+    floor16 = (conv_f / BF16_PEAK + attn_f / FP32_PEAK) * 1e3
+    out["config3_unet_step_batch2_64x64x32"].update(
+        {"bf16_ms": round(ms16, 3), "bf16_roofline_ms": round(floor16, 3), "bf16_frac_roofline": round(floor16 / ms16, 4)})
     if cpu:
         from oracle import maisi_torch as mt
 
@@ -309,6 +318,17 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         "s": round(sec, 4), "tflop": round(dec_f / 1e12, 3), "tflops": round(dec_f / sec / 1e12, 2),
         "roofline_s": round(dec_f / FP32_PEAK, 4), "frac_roofline": round(dec_f / FP32_PEAK / sec, 4),
         "output": list(img.shape)}
+    del img
+    with pkg.fast_fp32.precision("bf16"):
+        decode()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        img = decode()
+        torch.cuda.synchronize()
+        sec16 = time.perf_counter() - t0
+    out["config4_vae_decode_256^3_4windows"].update(
+        {"bf16_s": round(sec16, 4), "bf16_roofline_s": round(dec_f / BF16_PEAK, 4),
+         "bf16_frac_roofline": round(dec_f / BF16_PEAK / sec16, 4)})
     del img
     if generation:
         # full 256^3 generation: 30 rflow steps with batched CFG at a 64^3 latent, then decode
