@@ -75,14 +75,15 @@ def _wall_ms(fn, steps):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def staged_op(pkg, x, w, b, dtype_code):
+def staged_op(pkg, x, w, b, dtype_code, stream_gemm=False):
     """The operator as its two C-ABI stages (ctmr_conv3d_pack, ctmr_conv3d_gemm) for timing
-    the GEMM kernel in context: every GEMM reads a freshly packed input, as in the full op."""
+    the GEMM kernel in context: every GEMM reads a freshly packed input, as in the full op.
+    ``stream_gemm`` forces the register-streaming GEMM (CTMR_F_STREAM)."""
     import torch
 
     L, ops = pkg._lib, pkg.ops
     cin, cout = int(x.shape[-1]), int(w.shape[0])
-    desc = ops.make_desc(tuple(x.shape), cout, 3, 1, L.MODE_PLAIN, 0, dtype_code, 0)
+    desc = ops.make_desc(tuple(x.shape), cout, 3, 1, L.MODE_PLAIN, L.F_STREAM if stream_gemm else 0, dtype_code, 0)
     ws_bytes = L.workspace_bytes(desc)
     ws = torch.empty(max(ws_bytes, 1), device=x.device, dtype=torch.uint8)
     packed_w = ops.pack_weight(w, cin, cout, 3, L.MODE_PLAIN, dtype_code)
@@ -373,13 +374,15 @@ def profile_only(pkg, dev, what, steps, warmup):
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
         z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 20, 64, 64, 4), dtype=np.float32)).to(dev)
         fn = lambda: m.decode_vae(z, w, constructor=vc)
-    elif what == "gemms":
-        # config-0 fp32 and bf16 GEMM kernels alone (one pack each), for counter passes
+    elif what in ("gemms", "gemms_stream"):
+        # config-0 fp32 and bf16 GEMM kernels alone (one pack each), for counter passes; gemms_stream
+        # forces the register-streaming GEMM for the bf16 stage too (the LDS-staged one otherwise)
         rng = np.random.default_rng(0)
         x = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 64), dtype=np.float32)).to(dev)
         w = torch.from_numpy((rng.standard_normal((64, 64, 3, 3, 3)) / np.sqrt(27 * 64)).astype(np.float32)).to(dev)
         b = torch.zeros(64, device=dev)
-        stages = [staged_op(pkg, x, w, b, code) for code in (pkg._lib.DT_F32, pkg._lib.DT_BF16)]
+        stages = [staged_op(pkg, x, w, b, code, stream_gemm=what == "gemms_stream")
+                  for code in (pkg._lib.DT_F32, pkg._lib.DT_BF16)]
         for pack, _, _ in stages:
             pack()
 
@@ -414,7 +417,7 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "decode", "resblock", "attention", "gemms"],
+    ap.add_argument("--only", choices=["unet", "decode", "resblock", "attention", "gemms", "gemms_stream"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")

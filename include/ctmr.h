@@ -130,7 +130,11 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  * by shape for large stride-1 fp32 volumes (cin >= 128 and a multiple of 16,
  * cout % 64 == 0, no resampling, CTMR_F_STREAM not set), stages 16-channel chunks of the input
  * with their halo (affine + SiLU and zero padding applied while staging) and
- * visits chunks ascending (outer), taps ascending (inner).  With a split, each
+ * visits chunks ascending (outer), taps ascending (inner).  The LDS-staged
+ * bf16 GEMM, chosen for stride-1 bf16 convs (plain or trilinear-2x) with
+ * cout % 64 == 0 and bricks at least 3/4 full (CTMR_F_STREAM not set), reads the
+ * bf16 packed copy and visits 32-channel chunks ascending (outer), taps
+ * ascending (inner).  With a split, each
  * contiguous range of the sequence is summed separately and the partial planes
  * are added in ascending order after the bias.  Kernel, split and tiling depend
  * on the desc only, so results are bit-identical run to run.
