@@ -279,3 +279,59 @@ def test_unet_golden_through_safetensors_checkpoint(ctmr, dev, tmp_path):
                                          _g(f["input.class_labels"], dev, torch.int64), _g(f["input.spacing"], dev),
                                          loaded, constructor=f["__metadata__"]["constructor"])
     np.testing.assert_allclose(_h(y), f["output.velocity"], rtol=UNET_RTOL, atol=UNET_ATOL)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_unet_graph_replays_match_eager(ctmr, dev, precision):
+    """A recorded UNet pass (HIP graph) replayed on new inputs equals the eager pass bit for bit; eager
+    steps and synchronisations run between the replays (production UNet, 16^3 latent, batch 2)."""
+    m, f = ctmr.maisi, ctmr.fast_fp32
+    uc = m.PRODUCTION_UNET_CONSTRUCTOR
+    _, w = _production_unet(ctmr, dev)
+    rng = np.random.default_rng(11)
+
+    def inputs(i):
+        x = torch.from_numpy(rng.standard_normal((2, 16, 16, 16, 4), dtype=np.float32)).to(dev)
+        t = torch.tensor([100.0 + 300 * i, 900.0 - 200 * i], device=dev)
+        sp = m.spacing_tensor([1.0, 1.0, 1.2 + 0.1 * i], device=dev).repeat(2, 1)
+        return x, t, torch.tensor([9, i], device=dev), sp
+
+    with f.precision(precision):
+        graph = m.UNetGraph(*inputs(0), w, constructor=uc)
+        assert graph.precision == precision
+        for i in range(1, 4):
+            print(f"{precision} replay {i}", flush=True)
+            args = inputs(i)
+            t_emb, y = m.denoise_unet(*args, w, constructor=uc)
+            torch.cuda.synchronize()
+            g_emb, g_y = graph(*args)
+            torch.cuda.synchronize()
+            assert torch.equal(g_y, y) and torch.equal(g_emb, t_emb)
+        with pytest.raises(ValueError, match="does not match"):
+            graph(torch.zeros((1, 16, 16, 16, 4), device=dev), *inputs(0)[1:])
+
+
+def test_mr_pipeline_with_recorded_unet_equals_eager(ctmr, dev):
+    """The MR golden pipeline's 30-step batched-CFG sampling with the UNet pass replayed from a HIP graph
+    gives the eager latent bit for bit (and so the golden latent)."""
+    f = load_fixture("mr.npz")
+    meta = f["__metadata__"]
+    ctor = meta["constructor"]
+    m, ff = ctmr.maisi, ctmr.fast_fp32
+    uw = _gw(f, dev, "weight.unet.")
+    x = ff.to_ndhwc(_g(f["input.latent"], dev))
+    spacing = _g(f["output.spacing"], dev)
+    classes = torch.tensor([int(meta["modality"])], device=dev)
+    times, _ = m.set_timesteps_rflow(num_inference_steps=int(meta["num_inference_steps"]),
+                                     input_img_size_numel=int(np.prod(x.shape[1:4])))
+    g = float(meta["guidance_scale"])
+    t0 = torch.full((2,), float(times[0]), device=dev)
+    graph = m.UNetGraph(torch.cat([x, x]), t0, torch.cat([classes, classes * 0]), spacing.repeat(2, 1), uw,
+                        constructor=ctor["unet"])
+    runs = {}
+    for name, unet in (("eager", None), ("graph", graph)):
+        velocity = lambda z, t, unet=unet: m.guided_velocity(z, t, class_labels=classes, spacing=spacing, weights=uw,
+                                                             constructor=ctor["unet"], guidance_scale=g, unet=unet)
+        runs[name] = m.sample_rflow(x, velocity, times)
+    assert torch.equal(runs["graph"], runs["eager"])
+    np.testing.assert_allclose(_h(ff.to_ncdhw(runs["graph"])), f["output.latent"], rtol=UNET_RTOL, atol=UNET_ATOL)

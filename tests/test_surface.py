@@ -54,3 +54,10 @@ def test_operators_reject_cpu_tensors_without_fallback(ctmr):
     with pytest.raises(ValueError, match="GPU"):
         ctmr.fast_fp32.flash_attention(torch.zeros(1, 8, 32), torch.zeros(1, 8, 32), torch.zeros(1, 8, 32),
                                        heads=1, scale=1.0)
+
+
+def test_unet_graph_rejects_cpu_inputs(ctmr):
+    import torch
+
+    with pytest.raises(ValueError, match="CUDA"):
+        ctmr.maisi.UNetGraph(torch.zeros(1, 4, 4, 4, 4), torch.zeros(1), None, None, {}, constructor={})
