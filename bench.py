@@ -371,7 +371,7 @@ def profile_only(pkg, dev, what, steps, warmup):
     import torch
 
     m, f = pkg.maisi, pkg.fast_fp32
-    if what == "unet":
+    if what in ("unet", "unet_bf16"):
         uc = m.PRODUCTION_UNET_CONSTRUCTOR
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.unet_weight_shapes(uc), seed=7).items()}
         x = torch.from_numpy(np.random.default_rng(3).standard_normal((2, 64, 64, 32, 4), dtype=np.float32)).to(dev)
@@ -412,8 +412,9 @@ def profile_only(pkg, dev, what, steps, warmup):
         b = torch.zeros(128, device=dev)
         g, z0 = torch.ones(128, device=dev), torch.zeros(128, device=dev)
         fn = lambda: f.vae_resblock([x], (w1, b), (w1, b), (g, z0), (g, z0), None, num_groups=32, eps=1e-6)
-    warm_up(fn, warmup)
-    ms = _wall_ms(fn, steps)
+    with f.precision("bf16" if what == "unet_bf16" else "fp32"):
+        warm_up(fn, warmup)
+        ms = _wall_ms(fn, steps)
     print(json.dumps({"only": what, "ms": round(ms, 3), "steps": steps}), flush=True)
     return 0
 
@@ -427,7 +428,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "decode", "resblock", "attention", "gemms", "gemms_stream"],
+    ap.add_argument("--only", choices=["unet", "unet_bf16", "decode", "resblock", "attention", "gemms",
+                                       "gemms_stream"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
