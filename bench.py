@@ -157,7 +157,7 @@ def secondary(pkg, dev, steps):
     xa = torch.from_numpy(rng.standard_normal((1, 128, 128, 128, 64), dtype=np.float32)).to(dev)
     wa, ba = mk(128, 64), torch.zeros(128, device=dev)
     run = lambda: f.conv3d(xa, wa, ba, padding=1, stride=2)
-    run()
+    warm_up(run, 2, settle_s=0.5)  # the device idled while the input was drawn on the CPU
     ms = _wall_ms(run, steps)
     flops = conv_flops(1, 64, 64, 64, 64, 128)
     out["config2a_down_s2_64to128"] = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 2),
@@ -167,7 +167,7 @@ def secondary(pkg, dev, steps):
     xb = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 256), dtype=np.float32)).to(dev)
     wb, bb = mk(128, 256), torch.zeros(128, device=dev)
     run = lambda: f.norm_conv3d(xb, wb, bb, norm=None, num_groups=1, eps=1e-6, apply_silu=False, upsample=True)
-    run()
+    warm_up(run, 2, settle_s=0.5)  # the device idled while the input was drawn on the CPU
     ms = _wall_ms(run, max(2, steps // 2))
     flops = conv_flops(8, 64, 64, 64, 256, 128, taps=8)
     out["config2b_nearest_up_256to128"] = {"ms": round(ms, 3), "tflops_folded": round(flops / ms / 1e9, 2),
@@ -177,7 +177,7 @@ def secondary(pkg, dev, steps):
     xc = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 128), dtype=np.float32)).to(dev)
     wc, bc = mk(256, 128, 1), torch.zeros(256, device=dev)
     run = lambda: f.pointwise_conv(xc, wc, bc)
-    run()
+    warm_up(run, 2, settle_s=0.5)  # the device idled while the input was drawn on the CPU
     ms = _wall_ms(run, steps)
     flops = 2.0 * 64**3 * 128 * 256
     nbytes = 4.0 * 64**3 * (128 + 256)
@@ -399,6 +399,13 @@ def profile_only(pkg, dev, what, steps, warmup):
         def fn():
             for _, gemm, _ in stages:
                 gemm()
+    elif what == "pointwise":
+        # config 2c: 1x1x1 128 -> 256 at 64^3 (persistent pointwise GEMM)
+        rng = np.random.default_rng(1)
+        x = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 128), dtype=np.float32)).to(dev)
+        w = torch.from_numpy((rng.standard_normal((256, 128, 1, 1, 1)) / np.sqrt(128)).astype(np.float32)).to(dev)
+        b = torch.zeros(256, device=dev)
+        fn = lambda: f.pointwise_conv(x, w, b)
     elif what == "attention":
         # production UNet level-2 attention: 16x16x8 latent = 2048 tokens, 256 channels = 8 heads, batch 2
         g = torch.Generator(device=dev).manual_seed(0)
@@ -428,8 +435,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "unet_bf16", "decode", "resblock", "attention", "gemms",
-                                       "gemms_stream"],
+    ap.add_argument("--only", choices=["unet", "unet_bf16", "decode", "resblock", "attention", "pointwise",
+                                       "gemms", "gemms_stream"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")

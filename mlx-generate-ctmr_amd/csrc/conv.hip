@@ -311,6 +311,7 @@ struct ConvArgs {
   int64_t zstride;
   double* stats;           // group-norm partials of the output (ctmr_conv3d_gn) or null
   int gn_groups, gn_cpg, stats_tiles;
+  int items;               // pointwise_kernel: row tiles x batch items x split ranges
 };
 
 // Group-norm partials of a stored tile (ctmr_conv3d_gn).  On entry each lane
@@ -319,6 +320,36 @@ struct ConvArgs {
 // groups are combined with xor butterflies (every lane ends with the same
 // bits), the waves through `red`, and each group's columns and waves are added
 // in ascending order -- a fixed order for a given shape.
+// Final step of the group-norm partials of a stored tile: red[wave][c] holds
+// the fp64 (sum, sum of squares) of column c of each wave's 64 x (NSUB*16)
+// block over its rows (published by a barrier); each group's columns and
+// waves are added in ascending order -- a fixed order for a given shape.
+template <int NSUB, int WM, int WN>
+__device__ __forceinline__ void combine_gn_partials(const double (*red)[64][2], int col0, int cout, int cpg,
+                                                    int groups, double* __restrict__ stats_tile) {
+  constexpr int kWaveCols = NSUB * 16;
+  const int groups_here = (WN * kWaveCols) / cpg;
+  for (int gl = threadIdx.x; gl < groups_here; gl += 256) {
+    const int g = col0 / cpg + gl;
+    if (g >= groups || g * cpg >= cout) continue;
+    double a = 0.0, q = 0.0;
+    for (int wm = 0; wm < WM; ++wm)
+      for (int cc = 0; cc < cpg; ++cc) {
+        const int col = gl * cpg + cc;
+        const int wv = (col / kWaveCols) * WM + wm;
+        a += red[wv][col % kWaveCols][0];
+        q += red[wv][col % kWaveCols][1];
+      }
+    stats_tile[(int64_t)g * 2] = a;
+    stats_tile[(int64_t)g * 2 + 1] = q;
+  }
+}
+
+// Group-norm partials of a stored tile (ctmr_conv3d_gn).  On entry each lane
+// holds, per 16-column block ns, the fp64 sum and sum of squares of its rows'
+// stored values in column ns*16 + lane%16 of its wave's tile.  The four lane
+// groups are combined with xor butterflies (every lane ends with the same
+// bits), then the waves through `red`.
 template <int NSUB, int WM, int WN>
 __device__ __forceinline__ void write_gn_partials(double (&s1)[NSUB], double (&s2)[NSUB], double (*red)[64][2],
                                                   int wave, int lane, int col0, int cout, int cpg, int groups,
@@ -338,22 +369,7 @@ __device__ __forceinline__ void write_gn_partials(double (&s1)[NSUB], double (&s
     }
   }
   __syncthreads();
-  constexpr int kWaveCols = NSUB * 16;
-  const int groups_here = (WN * kWaveCols) / cpg;
-  for (int gl = threadIdx.x; gl < groups_here; gl += 256) {
-    const int g = col0 / cpg + gl;
-    if (g >= groups || g * cpg >= cout) continue;
-    double a = 0.0, q = 0.0;
-    for (int wm = 0; wm < WM; ++wm)
-      for (int cc = 0; cc < cpg; ++cc) {
-        const int col = gl * cpg + cc;
-        const int wv = (col / kWaveCols) * WM + wm;
-        a += red[wv][col % kWaveCols][0];
-        q += red[wv][col % kWaveCols][1];
-      }
-    stats_tile[(int64_t)g * 2] = a;
-    stats_tile[(int64_t)g * 2 + 1] = q;
-  }
+  combine_gn_partials<NSUB, WM, WN>(red, col0, cout, cpg, groups, stats_tile);
 }
 
 template <int DT>
@@ -373,6 +389,110 @@ template <>
 __device__ __forceinline__ void mfma_step<CTMR_BF16>(f4& acc, const u4& a, const u4& b) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a),
                                                  __builtin_bit_cast(bf8, b), acc, 0, 0, 0);
+}
+
+// One K block of a wave's 64 x (NSUB*16) tile: A[ms] holds rows ms*16 + lane%16,
+// B[ns] columns ns*16 + lane%16, each 16 bytes of K per lane group.  fp32: the
+// K sub-step is outermost, so consecutive MFMAs always write different
+// accumulators and none waits for the previous one's result.
+// TRANSPOSED multiplies B^T A^T instead: the same products summed in the same
+// K order (each output is the same dot product), but the result block holds
+// row lane%16 and columns 4*(lane/16) .. +3 in a lane's four registers.
+template <int DT, int NSUB, bool TRANSPOSED = false>
+__device__ __forceinline__ void mma_block(f4 (&acc)[4][NSUB], const u4 (&A)[4], const u4 (&B)[NSUB]) {
+  if constexpr (DT == CTMR_F32) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns) {
+          const float a = __builtin_bit_cast(f4, A[ms])[j], b = __builtin_bit_cast(f4, B[ns])[j];
+          acc[ms][ns] = TRANSPOSED ? __builtin_amdgcn_mfma_f32_16x16x4f32(b, a, acc[ms][ns], 0, 0, 0)
+                                   : __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[ms][ns], 0, 0, 0);
+        }
+  } else {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) {
+        if constexpr (TRANSPOSED)
+          mfma_step<DT>(acc[ms][ns], B[ns], A[ms]);
+        else
+          mfma_step<DT>(acc[ms][ns], A[ms], B[ns]);
+      }
+  }
+}
+
+// Epilogue of one wave's 64 x (NSUB*16) tile: D row 4*(lane/16)+r, column
+// lane%16 of each 16x16 block; output voxel v of batch item b is stored at
+// out_voxel(v) (the nearest-2x remap, or b * s_out + v).
+// Residual values (and, by the caller, bias values) are loaded before the first store:
+// interleaved, each load would wait for the stores before it (the compiler
+// cannot prove the output and its inputs apart).  Indices past the grid are
+// clamped for the loads and masked for the stores.
+// Bias of the lane's columns n0 + ns*16 + lane%16 for batch item b (zero for a
+// split's partial planes or without bias).
+template <int NSUB>
+__device__ __forceinline__ void load_bias(const ConvArgs& p, int b, int n0, int lane, float (&bv)[NSUB]) {
+  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns)
+    bv[ns] = (p.split == 1 && p.has_bias) ? bias_b[min(n0 + ns * 16 + (lane & 15), p.cout - 1)] : 0.f;
+}
+
+template <int NSUB, int WM, int WN, typename OutVoxel>
+__device__ __forceinline__ void store_tile(const ConvArgs& p, const f4 (&acc)[4][NSUB], const float (&bv)[NSUB],
+                                           int b, int m0, int n0, int S, int split_id, int wave, int lane,
+                                           int col0, int tile_id, OutVoxel out_voxel) {
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const bool partial = p.split > 1;
+  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
+  float rv[4][4][NSUB];
+  const bool add_res = !partial && p.has_res;
+  if (add_res) {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t base = out_voxel(min(m0 + ms * 16 + lgrp * 4 + r, S - 1)) * p.cout;
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns) rv[ms][r][ns] = p.res[base + min(n0 + ns * 16 + lrow, p.cout - 1)];
+      }
+  }
+  double s1[NSUB], s2[NSUB];
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) s1[ns] = s2[ns] = 0.0;
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int v = m0 + ms * 16 + lgrp * 4 + r;
+      if (v >= S) continue;
+      const int64_t vox = out_voxel(v);
+      const int64_t base = vox * p.cout;
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) {
+        const int col = n0 + ns * 16 + lrow;
+        if (col >= p.cout) continue;
+        float sum = acc[ms][ns][r];
+        if (!partial) {
+          if (p.has_bias) sum += bv[ns];
+          if (add_res) sum += rv[ms][r][ns];
+        }
+        out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
+        if (p.stats) {
+          s1[ns] += (double)sum;
+          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
+        }
+      }
+    }
+  }
+  if (p.stats) {  // wave-uniform (a kernel argument): every thread reaches the barrier inside
+    __shared__ double red[WM * WN][64][2];
+    write_gn_partials<NSUB, WM, WN>(s1, s2, red, wave, lane, col0, p.cout, p.gn_cpg, p.gn_groups,
+                                    p.stats + ((int64_t)b * p.stats_tiles + tile_id) * p.gn_groups * 2);
+  }
 }
 
 template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
@@ -480,26 +600,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
       }
     }
   };
-  // K sub-step outermost: consecutive MFMAs always write different
-  // accumulators, so none waits for the previous one's result.
-  auto compute = [&](const u4 (&A)[4], const u4 (&B)[NSUB]) {
-    if constexpr (DT == CTMR_F32) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-          for (int ns = 0; ns < NSUB; ++ns)
-            acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(f4, A[ms])[j],
-                                                               __builtin_bit_cast(f4, B[ns])[j],
-                                                               acc[ms][ns], 0, 0, 0);
-    } else {
-#pragma unroll
-      for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-        for (int ns = 0; ns < NSUB; ++ns) mfma_step<DT>(acc[ms][ns], A[ms], B[ns]);
-    }
-  };
+  auto compute = [&](const u4 (&A)[4], const u4 (&B)[NSUB]) { mma_block<DT, NSUB>(acc, A, B); };
 
   // Register double buffer: the next K block is in flight while this one
   // multiplies.  The scheduling barriers keep the prefetch loads ahead of the
@@ -530,74 +631,19 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // Epilogue: D row 4*(lane/16)+r, column lane%16 of each 16x16 block.
-  // Bias and residual values are all loaded before the first store:
-  // interleaved, each load would wait for the stores before it (the compiler
-  // cannot prove the output and its inputs apart).  Indices past the grid are
-  // clamped for the loads and masked for the stores.
-  const bool partial = p.split > 1;
-  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
-  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
-  auto out_voxel = [&](int v) -> int64_t {
-    int o = v;
-    if (UP) {
-      const int d = v / ghw, rr = v - d * ghw;
-      const int h = rr / p.gw, w = rr - h * p.gw;
-      o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
-    }
-    return (int64_t)b * p.s_out + o;
-  };
+  const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
   float bv[NSUB];
-#pragma unroll
-  for (int ns = 0; ns < NSUB; ++ns)
-    bv[ns] = (!partial && p.has_bias) ? bias_b[min(n0 + ns * 16 + lrow, p.cout - 1)] : 0.f;
-  float rv[4][4][NSUB];
-  const bool add_res = !partial && p.has_res;
-  if (add_res) {
-#pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t base = out_voxel(min(m0 + ms * 16 + lgrp * 4 + r, S - 1)) * p.cout;
-#pragma unroll
-        for (int ns = 0; ns < NSUB; ++ns) rv[ms][r][ns] = p.res[base + min(n0 + ns * 16 + lrow, p.cout - 1)];
-      }
-  }
-  double s1[NSUB], s2[NSUB];
-#pragma unroll
-  for (int ns = 0; ns < NSUB; ++ns) s1[ns] = s2[ns] = 0.0;
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int v = m0 + ms * 16 + lgrp * 4 + r;
-      if (v >= S) continue;
-      const int64_t vox = out_voxel(v);
-      const int64_t base = vox * p.cout;
-#pragma unroll
-      for (int ns = 0; ns < NSUB; ++ns) {
-        const int col = n0 + ns * 16 + lrow;
-        if (col >= p.cout) continue;
-        float sum = acc[ms][ns][r];
-        if (!partial) {
-          if (p.has_bias) sum += bv[ns];
-          if (add_res) sum += rv[ms][r][ns];
-        }
-        out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
-        if (p.stats) {
-          s1[ns] += (double)sum;
-          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
-        }
-      }
-    }
-  }
-  if (p.stats) {  // wave-uniform (a kernel argument): every thread reaches the barrier inside
-    __shared__ double red[WM * WN][64][2];
-    const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
-    write_gn_partials<NSUB, WM, WN>(s1, s2, red, wave, lane, n_tile * (WN * NSUB * 16), p.cout, p.gn_cpg,
-                                    p.gn_groups,
-                                    p.stats + ((int64_t)b * p.stats_tiles + tile_id) * p.gn_groups * 2);
-  }
+  load_bias<NSUB>(p, b, n0, lane, bv);
+  store_tile<NSUB, WM, WN>(p, acc, bv, b, m0, n0, S, split_id, wave, lane, n_tile * (WN * NSUB * 16), tile_id,
+                           [&](int v) -> int64_t {
+                             int o = v;
+                             if (UP) {
+                               const int d = v / ghw, rr = v - d * ghw;
+                               const int h = rr / p.gw, w = rr - h * p.gw;
+                               o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
+                             }
+                             return (int64_t)b * p.s_out + o;
+                           });
 }
 
 // ---------------------------------------------------------------------------
@@ -885,7 +931,7 @@ constexpr int kB16RowIters = 3;                              // 768 slots of a 3
 __host__ __device__ constexpr int lds16_halo_swizzle(int hx, int hy) {
   return ((hx >> 2) & 1) | (((hy >> 2) & 1) << 1);
 }
-__host__ __device__ constexpr int lds16_col_swizzle(int c) { return ((c >> 2) & 1) | (((c >> 3) & 1) << 1); }
+__host__ __device__ constexpr int row64_swizzle(int c) { return ((c >> 2) & 1) | (((c >> 3) & 1) << 1); }
 
 struct Lds16Args {
   const char* xp;       // bf16 packed copy (n, d+2, h+2, w+2, cp)
@@ -1029,7 +1075,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   const unsigned wload = (1u << kB16RowIters) - 1;
 #pragma unroll
   for (int j = 0; j < kB16RowIters; ++j)
-    woff[j] = j * tap_bytes + (n0 + (tid >> 2)) * 64 + 16 * ((tid & 3) ^ lds16_col_swizzle((tid >> 2) & 15));
+    woff[j] = j * tap_bytes + (n0 + (tid >> 2)) * 64 + 16 * ((tid & 3) ^ row64_swizzle((tid >> 2) & 15));
   auto fill_halo = [&](int chunk) {
     const int so = __builtin_amdgcn_readfirstlane(chunk * 64);
 #pragma unroll
@@ -1048,7 +1094,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
     abase[ms] = ((wave * kHH + ms + 4 * (lrow >> 3)) * kHW + (lrow & 7)) * 64;
   int bbase[4];
 #pragma unroll
-  for (int ns = 0; ns < 4; ++ns) bbase[ns] = (ns * 16 + lrow) * 64 + 16 * (lgrp ^ lds16_col_swizzle(lrow));
+  for (int ns = 0; ns < 4; ++ns) bbase[ns] = (ns * 16 + lrow) * 64 + 16 * (lgrp ^ row64_swizzle(lrow));
 
   f4 acc[4][4];
 #pragma unroll
@@ -1152,6 +1198,279 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 3d. Persistent pointwise GEMM over an LDS ring (one K tap: 1x1x1 convs and
+// the im2col and tap-expanded formulations)
+// ---------------------------------------------------------------------------
+// These GEMMs read their A rows from HBM once, with only 4-32 K blocks per
+// tile; a one-step register prefetch does not cover HBM latency, and a launch
+// of one tile per workgroup also exposes every tile's first loads.  Here:
+//  * operands go straight from memory into a ring of kStages LDS stages
+//    (buffer_load_dwordx4 ... lds), kStages - 1 K blocks ahead of the MFMAs,
+//    one barrier per K block;
+//  * a grid of as many workgroups as the device holds walks the tiles: a
+//    workgroup keeps one column tile and visits row items l, l + L, l + 2L, ...
+//    (an item is a WM*64-row tile of one batch item and one K range), and the
+//    ring runs straight across items, so the next item's first blocks land
+//    while this item's epilogue stores.
+// A stage holds the tile's A rows (WM*64 voxels) then its B columns (WN*64),
+// 64 bytes (one K block) each, the four 16-byte pieces of row r in slots
+// piece ^ row64_swizzle(r) -- the layout conflict-free for ds_read_b128 that
+// the bf16 LDS GEMM uses.  Each wave multiplies exactly the fragments
+// conv_kernel<DT, 4, WM, WN, 1, 1, false> loads, in the same order, with the
+// two MFMA operands exchanged (B^T A^T: every output is the same dot product,
+// and a lane ends with four adjacent columns of one row, stored as 16 bytes),
+// so the outputs are bit-identical to it.  Rows past the volume are outside
+// the A descriptor's range and stage as zeros (their outputs are not stored).
+template <int WM, int WN>
+struct PwRing {
+  static constexpr int kRows = (WM + WN) * 64;           // A rows + B columns of a stage
+  static constexpr int kStageBytes = kRows * 64;
+  static constexpr int kStages = kStageBytes <= 16384 ? 4 : 3;  // <= 64 KiB: two workgroups per CU
+  static constexpr int kDma = kRows / 64;                 // 1 KiB loads per wave per stage
+};
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor (raw, 32-bit range) with wave-uniform fields.
+__device__ __forceinline__ u32x4 raw_rsrc(const void* base, int64_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((unsigned)a);
+  r.y = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+  r.z = __builtin_amdgcn_readfirstlane((unsigned)min(max(bytes, (int64_t)0), (int64_t)0x7fffffff));
+  r.w = 0x00020000u;
+  return r;
+}
+
+// Direct-to-LDS 16-byte buffer load of lane i (offset voff + soff, zero out
+// of range) into LDS byte lds_addr + 16 i.  Inline assembly for the reason
+// given at lds_dma16; callers wait with wait_vmcnt.
+__device__ __forceinline__ void lds_dma_buf16(u32x4 rsrc, int voff, int soff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) (other counters unconstrained).  Vector-memory loads,
+// direct-to-LDS ones included, complete in issue order, so with N loads
+// issued after a given one this returns once that one has landed.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int DT, int WM, int WN>
+__global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
+  static_assert(WM * WN == 4, "four waves per workgroup");
+  using R = PwRing<WM, WN>;
+  constexpr int NSUB = 4, TM = WM * 64, TN = WN * 64;
+  __shared__ __attribute__((aligned(16))) char ring[R::kStages * R::kStageBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_m = wave % WM, wave_n = wave / WM;
+  // XCD-aware order (as conv_kernel): consecutive ids share an XCD, so the
+  // column tiles of one row lane, which read the same input rows, share an L2.
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int xcd = bid & 7, slot8 = bid >> 3, per = nb >> 3, rem = nb & 7;
+  const int vid = (xcd < rem) ? xcd * (per + 1) + slot8 : rem * (per + 1) + (xcd - rem) * per + slot8;
+  const int n_tile = vid % p.n_tiles;
+  const int lanes = nb / p.n_tiles;  // the host launches lanes * n_tiles workgroups
+  const int first = vid / p.n_tiles;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int S = p.gd * p.gh * p.gw;
+  const int rb = (int)p.row_bytes;
+  const int steps = p.kb;
+  const int bstep = p.np * 64;
+  const int n0 = n_tile * TN + wave_n * 64;
+
+  // Item r: split range r % split of row tile (r / split) % m_tiles of batch
+  // item r / (split * m_tiles), K blocks [s_begin, s_end).
+  struct Item {
+    int b, m_tile, split_id, s_begin, s_end;
+  };
+  auto item = [&](int r) {
+    Item it;
+    it.split_id = r % p.split;
+    const int rest = r / p.split;
+    it.m_tile = rest % p.m_tiles;
+    it.b = rest / p.m_tiles;
+    it.s_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)it.split_id * steps / p.split));
+    it.s_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(it.split_id + 1) * steps / p.split));
+    return it;
+  };
+
+  // Load t of this wave fills stage rows 16 * (wave * kDma + t) + lane / 4,
+  // slot lane % 4 -- piece (lane % 4) ^ swizzle of that row: an A row (voxel)
+  // or a B column.  The lane offsets are fixed; items move the A base only.
+  int voff[R::kDma];
+#pragma unroll
+  for (int t = 0; t < R::kDma; ++t) {
+    const int row = 16 * (wave * R::kDma + t) + (lane >> 2);
+    const int piece = (lane & 3) ^ row64_swizzle(row);
+    voff[t] = row < TM ? row * rb + piece * 16 : (n_tile * TN + row - TM) * 64 + piece * 16;
+  }
+  const u32x4 brsrc = raw_rsrc(p.wp, p.w_bytes);
+  const unsigned ring_lds = (unsigned)(uintptr_t)(lds_ptr_t)ring;
+
+  // Load cursor: item d_r, K block d_s of [.., d_end), the item's A rows.
+  int d_r = first, d_s, d_end;
+  u32x4 arsrc;
+  auto start_item = [&](int r) {
+    const Item it = item(r);
+    d_s = it.s_begin;
+    d_end = it.s_end;
+    const int64_t row = (int64_t)it.b * p.rows_per_batch + (int64_t)it.m_tile * TM;
+    arsrc = raw_rsrc(p.xp + row * rb, (int64_t)(S - it.m_tile * TM) * rb);
+  };
+  start_item(d_r);
+  auto fill = [&](int st) {
+    const unsigned lds = ring_lds + st * R::kStageBytes + wave * R::kDma * 1024;
+    const int sa = __builtin_amdgcn_readfirstlane(d_s * 64);
+    const int sb = __builtin_amdgcn_readfirstlane(d_s * bstep);
+#pragma unroll
+    for (int t = 0; t < R::kDma; ++t) {
+      const bool a_rows = 16 * (wave * R::kDma + t) < TM;  // wave-uniform: a scalar select, no branch
+      lds_dma_buf16(a_rows ? arsrc : brsrc, voff[t], a_rows ? sa : sb, lds + t * 1024);
+    }
+    if (++d_s == d_end) {
+      if (d_r + lanes < p.items) {
+        d_r += lanes;
+        start_item(d_r);
+      } else {
+        d_s = d_end - 1;  // past the last item: re-read its last block into a stage never read
+      }
+    }
+  };
+
+  f4 acc[4][NSUB];
+  auto clear = [&]() {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
+  };
+  clear();
+  // The accumulators hold B^T A^T blocks (mma_block<.., true>): lane l of
+  // block (ms, ns) has row ms*16 + l%16, columns ns*16 + 4*(l/16) .. +3.  The
+  // column tile is fixed, so those columns' bias is loaded once, before any
+  // ring load is in flight.
+  f4 bq[NSUB];
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) {
+    const float* bias = p.bias;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      bq[ns][r] = (p.split == 1 && p.has_bias) ? bias[min(n0 + ns * 16 + 4 * lgrp + r, p.cout - 1)] : 0.f;
+  }
+  int c_r = first, left;
+  {
+    const Item it = item(c_r);
+    left = it.s_end - it.s_begin;
+  }
+  // Epilogue: one 16-byte store per block and lane, through a buffer
+  // descriptor over the wave's output rows.  Rows past the volume fall
+  // outside its range and column quads past cout (a multiple of 4 here) get
+  // an offset outside it, so the hardware drops both without branches.  No
+  // global load happens here (per-batch bias and residual stay on
+  // conv_kernel): a load would make the compiler wait for every ring load in
+  // flight.
+  int q_off[NSUB];
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) {
+    const int col = n0 + ns * 16 + 4 * lgrp;
+    q_off[ns] = col < p.cout ? (lrow * p.cout + col) * 4 : 0x40000000;
+  }
+  __shared__ double red[4][64][2];
+  auto finish = [&]() -> bool {
+    const Item it = item(c_r);
+    const int m0 = it.m_tile * TM + wave_m * 64;
+    const int valid_rows = min(max(S - m0, 0), 64);
+    float* out = p.y + (p.split > 1 ? (int64_t)it.split_id * p.plane : 0) + ((int64_t)it.b * p.s_out + m0) * p.cout;
+    const __amdgpu_buffer_rsrc_t orsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out, (short)0, valid_rows * p.cout * 4, 0x00020000);
+    const bool add_bias = p.split == 1 && p.has_bias;
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) {
+      double q1[4] = {0.0, 0.0, 0.0, 0.0}, q2[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) {
+        f4 v = acc[ms][ns];
+        if (add_bias) v += bq[ns];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), orsrc, q_off[ns] + ms * 16 * p.cout * 4, 0,
+                                               0);
+        if (p.stats) {
+          const bool ok = ms * 16 + lrow < valid_rows && q_off[ns] < 0x40000000;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const double d = ok ? (double)v[r] : 0.0;
+            q1[r] += d;
+            q2[r] = fma(d, d, q2[r]);
+          }
+        }
+      }
+      if (p.stats) {  // column sums over the wave's rows: xor butterflies over lane%16
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int m = 1; m < 16; m <<= 1) {
+            q1[r] += __shfl_xor(q1[r], m);
+            q2[r] += __shfl_xor(q2[r], m);
+          }
+        if (lrow == 0) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            red[wave][ns * 16 + 4 * lgrp + r][0] = q1[r];
+            red[wave][ns * 16 + 4 * lgrp + r][1] = q2[r];
+          }
+        }
+      }
+    }
+    if (p.stats) {  // a kernel argument: every thread reaches the barriers
+      __syncthreads();
+      combine_gn_partials<NSUB, WM, WN>(red, n_tile * TN, p.cout, p.gn_cpg, p.gn_groups,
+                                        p.stats + ((int64_t)it.b * p.stats_tiles + it.m_tile) * p.gn_groups * 2);
+      __syncthreads();  // the next item's partials reuse `red`
+    }
+    c_r += lanes;
+    if (c_r >= p.items) return false;
+    const Item nx = item(c_r);
+    left = nx.s_end - nx.s_begin;
+    clear();
+    return true;
+  };
+
+  // Fragment addresses in a stage: A row wave_m*64 + ms*16 + lane%16, B column
+  // wave_n*64 + ns*16 + lane%16, K piece lane/16 (swizzle bits 2-3 of the row
+  // are those of lane%16).
+  const int sw = lgrp ^ row64_swizzle(lrow);
+  const int a_lds = (wave_m * 64 + lrow) * 64 + sw * 16;
+  const int b_lds = (TM + wave_n * 64 + lrow) * 64 + sw * 16;
+
+#pragma unroll
+  for (int st = 0; st < R::kStages - 1; ++st) fill(st);
+  int cur = 0;
+  for (;;) {
+    wait_vmcnt<R::kDma * (R::kStages - 2)>();  // this wave's loads of stage `cur`
+    __syncthreads();  // everyone's loads of `cur` landed; everyone is done reading the stage before it
+    fill(cur == 0 ? R::kStages - 1 : cur - 1);
+    const char* stage = ring + cur * R::kStageBytes;
+    u4 A[4], B[NSUB];
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) A[ms] = *reinterpret_cast<const u4*>(stage + a_lds + ms * 1024);
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) B[ns] = *reinterpret_cast<const u4*>(stage + b_lds + ns * 1024);
+    __builtin_amdgcn_s_setprio(1);
+    mma_block<DT, NSUB, true>(acc, A, B);
+    __builtin_amdgcn_s_setprio(0);
+    cur = cur + 1 == R::kStages ? 0 : cur + 1;
+    if (--left == 0 && !finish()) break;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no ring load may land after the workgroup ends
+}
+
 // Sum of split partial planes in ascending order, then residual; bias first
 // as in the reference reduce (_nax_conv.py:320-332).
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
@@ -1251,6 +1570,7 @@ struct Geometry {
   int nsub, wm, wn, m_tiles, n_tiles;
   bool lds;              // LDS-staged GEMM (conv_lds_kernel)
   bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
+  bool pointwise;        // one-tap GEMM on the persistent pointwise_kernel
   int tz, ty, tx;        // its bricks per axis
   int layout;            // WL_TAPS, WL_EXPAND (cout <= 4) or WL_IM2COL (small cin)
   int ncols;             // GEMM columns: cout, or 27 * cout for WL_EXPAND
@@ -1445,6 +1765,11 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   }
   const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases * g.split;
   if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
+  // One-tap GEMMs (1x1x1, im2col) with 64-column wave tiles walk their tiles
+  // persistently over an LDS ring; per-batch bias, residual and the planar
+  // tap-expanded output stay on conv_kernel.
+  g.pointwise = g.KT == 1 && g.nsub == 4 && g.layout != WL_EXPAND && d->cout % 4 == 0 &&
+                !(d->flags & (CTMR_F_STREAM | CTMR_F_BATCH_BIAS | CTMR_F_RESIDUAL));
   g.pack_bytes = g.pack ? round_up((int64_t)d->n * g.rows_per_batch * g.cp * g.esize, 256) : 0;
   g.part_bytes = g.split > 1 ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
   if (g.layout == WL_EXPAND) g.z_bytes = (int64_t)g.ncols * d->n * g.rows_per_batch * 4;
@@ -1501,6 +1826,37 @@ static void launch_conv(dim3 grid, dim3 block, hipStream_t st, const ConvArgs& a
   hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP>), grid, block, 0, st, a);
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  static int cache[64];
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// The persistent pointwise GEMM runs as many row lanes of n_tiles workgroups
+// as the device holds at once (capped by the item count).  Each tile is summed
+// by one wave in a fixed order whatever the grid, so the grid may follow the
+// device without changing a bit of the output.
+template <int DT, int WM, int WN>
+static void launch_pointwise(dim3, dim3 block, hipStream_t st, const ConvArgs& a) {
+  static const int per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pointwise_kernel<DT, WM, WN>, 256, 0) !=
+            hipSuccess ||
+        n <= 0)
+      n = 2;
+    return n;
+  }();
+  const int64_t lanes = std::min<int64_t>(a.items, std::max(1, per_cu * device_cus() / a.n_tiles));
+  hipLaunchKernelGGL((pointwise_kernel<DT, WM, WN>), dim3((unsigned)(lanes * a.n_tiles)), block, 0, st, a);
+}
+
 template <int DT, int NSUB, int WM, int WN>
 static ConvFn pick_kind(int KT, int stride, bool up) {
   if (up) return launch_conv<DT, NSUB, WM, WN, 2, 1, true>;
@@ -1509,14 +1865,22 @@ static ConvFn pick_kind(int KT, int stride, bool up) {
   return launch_conv<DT, NSUB, WM, WN, 3, 1, false>;
 }
 
+template <int DT, int NSUB, int WM, int WN>
+static ConvFn pick_kind(const Geometry& g, int stride, bool up) {
+  if constexpr (NSUB == 4) {
+    if (g.pointwise) return launch_pointwise<DT, WM, WN>;
+  }
+  return pick_kind<DT, NSUB, WM, WN>(g.KT, stride, up);
+}
+
 static ConvFn pick(const ctmr_conv_desc* d, const Geometry& g) {
   const bool up = d->mode == CTMR_MODE_NEAREST2X;
   const int st = d->stride;
 #define CTMR_PICK(DT)                                                            \
-  if (g.nsub == 1) return pick_kind<DT, 1, 4, 1>(g.KT, st, up);                  \
-  if (g.nsub == 2) return pick_kind<DT, 2, 4, 1>(g.KT, st, up);                  \
-  if (g.wn == 1) return pick_kind<DT, 4, 4, 1>(g.KT, st, up);                    \
-  return pick_kind<DT, 4, 2, 2>(g.KT, st, up);
+  if (g.nsub == 1) return pick_kind<DT, 1, 4, 1>(g, st, up);                     \
+  if (g.nsub == 2) return pick_kind<DT, 2, 4, 1>(g, st, up);                     \
+  if (g.wn == 1) return pick_kind<DT, 4, 4, 1>(g, st, up);                       \
+  return pick_kind<DT, 4, 2, 2>(g, st, up);
   if (d->dtype == CTMR_F32) {
     CTMR_PICK(CTMR_F32)
   } else {
@@ -1819,6 +2183,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
     a.has_res = 0;
   }
   const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
+  a.items = g.pointwise ? (int)((int64_t)g.m_tiles * desc->n * g.split) : 0;  // launch_pointwise sizes its grid
   ConvFn fn = pick(desc, g);
   fn(dim3((unsigned)blocks), dim3(256), st, a);
   if ((rc = check_launch("conv"))) return rc;

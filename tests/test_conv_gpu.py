@@ -238,6 +238,96 @@ def test_pointwise_conv_matches_matmul(ctmr, dev, cin, cout):
     _assert_rel(_h(y), x.astype(np.float64) @ w[:, :, 0, 0, 0].T.astype(np.float64) + b, REF_REL, f"1x1 {cin}->{cout}")
 
 
+PERSISTENT_CASES = [
+    # (name, x shape NDHWC, cout, ksize, options); the large shapes give every
+    # workgroup of the persistent grid several row items
+    ("config 2c", (1, 64, 64, 64, 128), 256, 1, {}),
+    ("64 columns, 2 items per lane", (1, 64, 64, 64, 32), 64, 1, {"gn": 32}),
+    ("ragged rows, 2 batch items", (2, 33, 47, 61, 64), 64, 1, {"gn": 16}),
+    ("3 column tiles", (2, 24, 32, 32, 128), 384, 1, {}),
+    ("batch bias + residual (one-tile route)", (2, 24, 32, 32, 128), 384, 1,
+     {"batch_bias": True, "residual": True}),
+    ("ragged 16-column tile", (1, 40, 40, 40, 48), 40, 1, {}),
+    ("cout not a multiple of 4 (one-tile route)", (1, 20, 20, 20, 48), 42, 1, {}),
+    ("K split", (1, 8, 8, 8, 512), 256, 1, {"split": 3, "gn": 32}),
+    ("affine + SiLU pack", (1, 32, 32, 32, 64), 128, 1, {"fused": True, "gn": 32}),
+    ("bf16", (1, 48, 48, 48, 128), 256, 1, {"bf16": True}),
+    ("im2col 3x3", (2, 32, 64, 64, 4), 64, 3, {"gn": 32}),
+    ("tap-expanded 3x3 -> 1", (1, 40, 64, 64, 64), 1, 3, {}),
+]
+
+
+@pytest.mark.parametrize(("name", "shape", "cout", "ksize", "opts"), PERSISTENT_CASES,
+                         ids=[c[0] for c in PERSISTENT_CASES])
+def test_persistent_pointwise_gemm_equals_one_tile_gemm(ctmr, dev, name, shape, cout, ksize, opts):
+    """One-tap GEMMs (1x1x1, im2col) run on a persistent grid whose workgroups walk the row tiles
+    over an LDS ring; each output keeps the one-tile-per-workgroup GEMM's summation order, so outputs
+    are bit-identical to it (CTMR_F_STREAM), epilogue group-norm partials agree to fp64 rounding, and
+    a sample of output voxels meets the float64 bar.  (Per-batch bias, residual and the tap-expanded
+    GEMM stay on the one-tile kernel: those cases check the routing.)"""
+    print(f"persistent pointwise {name}: {shape} -> {cout} k{ksize} {opts}", flush=True)
+    f = ctmr.fast_fp32
+    rng = np.random.default_rng(sum(shape) + cout + ksize)
+    n, c = shape[0], shape[-1]
+    x = rng.standard_normal(shape, dtype=np.float32)
+    w = (rng.standard_normal((cout, c, ksize, ksize, ksize)) / np.sqrt(c * ksize ** 3)).astype(np.float32)
+    bias = rng.standard_normal((n, cout) if opts.get("batch_bias") else (cout,)).astype(np.float32)
+    dtype = "bf16" if opts.get("bf16") else "fp32"
+    packed = f.pack_weight(_t(w, dev), dtype=dtype)
+    xt = _t(x, dev)
+    affine = None
+    if opts.get("fused"):
+        gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+        affine = f.group_norm_affine(xt, _t(gw, dev), _t(gb, dev), groups=8, eps=1e-6)
+    out_shape = (*shape[:-1], cout)
+    res = _t(rng.standard_normal(out_shape, dtype=np.float32), dev) if opts.get("residual") else None
+    groups = opts.get("gn", 0)
+    run = lambda stream: f.implicit_gemm_conv3d(xt, packed, _t(bias, dev), cout=cout, ksize=ksize, affine=affine,
+                                                silu=affine is not None, residual=res, split=opts.get("split", 0),
+                                                stream_gemm=stream, gn_groups=groups)
+    y = run(False)
+    y1 = run(True)
+    assert torch.equal(y, y1), f"{name}: persistent and one-tile GEMMs differ"
+    assert torch.equal(run(False), y)
+    if groups:
+        # same per-(tile, group) partials; the persistent epilogue adds a tile's rows in another fixed
+        # fp64 order, so they agree to fp64 rounding (and repeat bit for bit)
+        st, st1 = f.conv_output_stats(y, groups), f.conv_output_stats(y1, groups)
+        assert st is not None and st1 is not None and st.shape == st1.shape
+        assert rm.max_rel_error(_h(st), _h(st1)) <= 1e-12, f"{name}: epilogue partials differ"
+        assert torch.equal(f.conv_output_stats(run(False), groups), st)
+
+    # float64 check on a sample of output voxels (every voxel of the first and last rows of the grid
+    # and 512 random ones), computed from the same inputs
+    xin = x.astype(np.float64)
+    if affine is not None:
+        a = _h(affine)
+        xin = xin * a[:, None, None, None, :, 0] + a[:, None, None, None, :, 1]
+        xin = xin / (1 + np.exp(-xin))
+    flat = [(b, v) for b in range(n) for v in range(64)]
+    flat += [(n - 1, int(np.prod(shape[1:4])) - 1 - v) for v in range(64)]
+    flat += [(int(rng.integers(n)), int(rng.integers(np.prod(shape[1:4])))) for _ in range(512)]
+    d_, h_, w_ = shape[1:4]
+    xp = np.pad(xin, ((0, 0), (1, 1), (1, 1), (1, 1), (0, 0))) if ksize == 3 else xin
+    wk = w.astype(np.float64).transpose(2, 3, 4, 1, 0).reshape(-1, cout)  # (taps * cin, cout)
+    bias2 = bias.reshape(-1, cout).astype(np.float64)
+    yh = _h(y)
+    resh = None if res is None else _h(res)
+    got, want = [], []
+    for b, v in flat:
+        dd, rr = divmod(v, h_ * w_)
+        hh, ww = divmod(rr, w_)
+        patch = xp[b, dd:dd + ksize, hh:hh + ksize, ww:ww + ksize, :].reshape(-1)
+        ref = patch @ wk + bias2[b % bias2.shape[0]]
+        if resh is not None:
+            ref = ref + resh[b, dd, hh, ww]
+        want.append(ref)
+        got.append(yh[b, dd, hh, ww])
+    bound = BF16_REL if dtype == "bf16" else FP32_REL
+    _assert_rel(np.array(got), np.array(want), bound, f"persistent {name} (sampled voxels)")
+
+
 @pytest.mark.parametrize(("shape", "cout", "stride", "fused"), [
     ((2, 64, 6, 7, 9), 1, 1, True),     # VAE output conv shape class (64 -> 1)
     ((1, 64, 8, 16, 16), 4, 1, True),   # UNet output conv shape class (64 -> 4)
