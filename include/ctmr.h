@@ -63,8 +63,9 @@ enum ctmr_conv_flags {
   CTMR_F_SILU = 2,       /* SiLU after the affine (or on x) before the conv */
   CTMR_F_BATCH_BIAS = 4, /* bias is (N, Cout) instead of (Cout) */
   CTMR_F_RESIDUAL = 8,   /* residual (output-shaped, NDHWC) added before the store */
-  CTMR_F_STREAM = 16     /* use the register-streaming GEMM even where the LDS-staged
-                            one applies (comparisons and tests) */
+  CTMR_F_STREAM = 16     /* use the one-tile-per-workgroup register-streaming GEMM even
+                            where the LDS-staged or the persistent pointwise one
+                            applies (comparisons and tests) */
 };
 
 enum ctmr_dtype {
@@ -134,7 +135,10 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  * bf16 GEMM, chosen for stride-1 bf16 convs (plain or trilinear-2x) with
  * cout % 64 == 0 and bricks at least 3/4 full (CTMR_F_STREAM not set), reads the
  * bf16 packed copy and visits 32-channel chunks ascending (outer), taps
- * ascending (inner).  With a split, each
+ * ascending (inner).  One-tap GEMMs (1x1x1, im2col rows) with cout % 4 == 0 and
+ * no per-batch bias or residual run on a persistent grid with the streaming
+ * GEMM's per-output order, so their outputs equal the CTMR_F_STREAM ones bit
+ * for bit.  With a split, each
  * contiguous range of the sequence is summed separately and the partial planes
  * are added in ascending order after the bias.  Kernel, split and tiling depend
  * on the desc only, so results are bit-identical run to run.
