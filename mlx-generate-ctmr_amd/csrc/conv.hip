@@ -987,13 +987,15 @@ __device__ __forceinline__ void lds16_load(Lds16Frag& f, const char* brow, const
   for (int ns = 0; ns < 4; ++ns) f.b[ns] = *reinterpret_cast<const u4*>(brow + KW * kB16TapBytes + bbase[ns]);
 }
 
+// B^T A^T (operands exchanged: the same dot products) so that a lane's result
+// registers are four adjacent output columns of one voxel.
 __device__ __forceinline__ void lds16_mma(f4 (&acc)[4][4], const Lds16Frag& f) {
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-    for (int ns = 0; ns < 4; ++ns) mfma_step<CTMR_BF16>(acc[ms][ns], f.a[ms], f.b[ns]);
+    for (int ns = 0; ns < 4; ++ns) mfma_step<CTMR_BF16>(acc[ms][ns], f.b[ns], f.a[ms]);
   __builtin_amdgcn_s_setprio(0);
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -1139,62 +1141,84 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
 #undef CTMR_LDS16_ROW
   }
 
-  // Epilogue (as conv_lds_kernel).
+  // Epilogue.  Lane l of accumulator block (ms, ns) holds voxel (z0 + wave,
+  // y0 + ms + 4 * ((l / 8) % 2), x0 + l % 8) and output columns n0 + ns * 16 +
+  // 4 * (l / 16) .. +3, stored (with bias and residual) as 16 bytes.
   const bool partial = p.split > 1;
   const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
-  const int z = z0 + wave;
-  auto out_base = [&](int y, int x) -> int64_t {
+  const int z = z0 + wave, x = x0 + (lrow & 7);
+  auto out_base = [&](int y) -> int64_t {
     return ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout;
   };
-  float bv[4];
+  f4 bq[4];
 #pragma unroll
-  for (int ns = 0; ns < 4; ++ns) bv[ns] = (!partial && p.has_bias) ? bias_b[n0 + ns * 16 + lrow] : 0.f;
-  float rv[4][4][4];
+  for (int ns = 0; ns < 4; ++ns)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bq[ns][r] = (!partial && p.has_bias) ? bias_b[n0 + ns * 16 + 4 * lgrp + r] : 0.f;
+  f4 rq[4][4];
   const bool add_res = !partial && p.has_res;
   if (add_res) {
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
+    for (int ms = 0; ms < 4; ++ms) {
+      const int64_t base = out_base(y0 + ms + 4 * (lrow >> 3)) + n0 + 4 * lgrp;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t base = out_base(y0 + ms + 4 * (lgrp >> 1), x0 + 4 * (lgrp & 1) + r);
-#pragma unroll
-        for (int ns = 0; ns < 4; ++ns) rv[ms][r][ns] = p.res[base + n0 + ns * 16 + lrow];
-      }
+      for (int ns = 0; ns < 4; ++ns) rq[ms][ns] = *reinterpret_cast<const f4*>(p.res + base + ns * 16);
+    }
   }
-  double s1[4], s2[4];
-#pragma unroll
-  for (int ns = 0; ns < 4; ++ns) s1[ns] = s2[ns] = 0.0;
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
-    const int y = y0 + ms + 4 * (lgrp >> 1);
+    const int y = y0 + ms + 4 * (lrow >> 3);
+    const bool ok = z < p.d && y < p.h && x < p.w;
+    const int64_t base = out_base(y) + n0 + 4 * lgrp;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int x = x0 + 4 * (lgrp & 1) + r;
-      if (z >= p.d || y >= p.h || x >= p.w) continue;
-      const int64_t base = out_base(y, x);
+    for (int ns = 0; ns < 4; ++ns) {
+      f4 v = acc[ms][ns];
+      if (!partial) {
+        if (p.has_bias) v += bq[ns];
+        if (add_res) v += rq[ms][ns];
+      }
+      acc[ms][ns] = v;
+      if (ok) *reinterpret_cast<f4*>(out + base + ns * 16) = v;
+    }
+  }
+  if (p.stats) {  // a kernel argument: every thread reaches the barriers
+    __syncthreads();  // the reduction buffer reuses the halo
+    double (*red)[64][2] = reinterpret_cast<double (*)[64][2]>(halo);
 #pragma unroll
-      for (int ns = 0; ns < 4; ++ns) {
-        const int col = n0 + ns * 16 + lrow;
-        float sum = acc[ms][ns][r];
-        if (!partial) {
-          if (p.has_bias) sum += bv[ns];
-          if (add_res) sum += rv[ms][r][ns];
+    for (int ns = 0; ns < 4; ++ns) {
+      // column sums over the wave's 64 voxels: its 4 row blocks, then xor butterflies over lane % 16
+      double q1[4] = {0.0, 0.0, 0.0, 0.0}, q2[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) {
+        const int y = y0 + ms + 4 * (lrow >> 3);
+        const bool ok = z < p.d && y < p.h && x < p.w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const double d = ok ? (double)acc[ms][ns][r] : 0.0;
+          q1[r] += d;
+          q2[r] = fma(d, d, q2[r]);
         }
-        out[base + col] = sum;
-        if (p.stats) {
-          s1[ns] += (double)sum;
-          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) {
+          q1[r] += __shfl_xor(q1[r], m);
+          q2[r] += __shfl_xor(q2[r], m);
+        }
+      if (lrow == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          red[wave][ns * 16 + 4 * lgrp + r][0] = q1[r];
+          red[wave][ns * 16 + 4 * lgrp + r][1] = q2[r];
         }
       }
     }
-  }
-  if (p.stats) {  // a kernel argument: every thread reaches both barriers
-    __syncthreads();  // the reduction buffer reuses the halo
-    double (*red)[64][2] = reinterpret_cast<double (*)[64][2]>(halo);
+    __syncthreads();
     const int tile_id = (bz * p.ty + by) * p.tx + bx;
-    write_gn_partials<4, 4, 1>(s1, s2, red, wave, lane, n0, p.cout, p.gn_cpg, p.gn_groups,
-                               p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
+    combine_gn_partials<4, 4, 1>(red, n0, p.cout, p.gn_cpg, p.gn_groups,
+                                 p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
   }
 }
 
@@ -2062,6 +2086,11 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
   if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
   const char* xp = g.pack ? (const char*)workspace : (const char*)x;
   if (!g.pack && ((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
+  // The bf16 LDS GEMM and the pointwise GEMM store (and read the residual) 16 bytes at a time.
+  const uintptr_t wide = (uintptr_t)y | ((desc->flags & CTMR_F_RESIDUAL) ? (uintptr_t)residual : 0) |
+                         (g.split > 1 ? (uintptr_t)workspace : 0);
+  if ((g.lds16 || g.pointwise) && (wide & 15) != 0)
+    return fail(CTMR_E_INVALID, "y, residual and workspace must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
   if (g.lds) {

@@ -32,6 +32,14 @@ def _require_device(*tensors: Optional[Tensor]) -> None:
             raise RuntimeError("ctmr operators run only on the GPU (HIP); got a CPU tensor")
 
 
+def _aligned16(t: Optional[Tensor]) -> Optional[Tensor]:
+    """``t`` itself when its data starts on a 16-byte boundary (the kernels read and store 16 bytes
+    at a time), else a fresh contiguous copy (a view with an odd storage offset)."""
+    if t is None or t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def _flags(affine: bool, silu: bool, batch_bias: bool, residual: bool) -> int:
     return (
         (_lib.F_AFFINE if affine else 0)
@@ -102,6 +110,7 @@ def conv3d(
     """``ctmr_conv3d`` on an NDHWC fp32 tensor; returns the NDHWC output.  ``stream_gemm``
     forces the register-streaming GEMM where the LDS-staged one would be chosen."""
     _require_device(x, packed, bias, affine, residual)
+    x, residual = _aligned16(x), _aligned16(residual)
     batch_bias = bias is not None and bias.dim() == 2
     flags = _flags(affine is not None, silu, batch_bias, residual is not None)
     if stream_gemm:
@@ -156,6 +165,7 @@ def conv3d_gn(
     """``ctmr_conv3d_gn``: the ``conv3d`` output plus float64 group-norm partials of it, shape
     ``(N, tiles, groups, 2)`` holding (sum, sum of squares) per output tile and group."""
     _require_device(x, packed, bias, affine, residual)
+    x, residual = _aligned16(x), _aligned16(residual)
     batch_bias = bias is not None and bias.dim() == 2
     flags = _flags(affine is not None, silu, batch_bias, residual is not None)
     if stream_gemm:

@@ -465,6 +465,35 @@ def test_validation_errors(ctmr, dev):
         f.implicit_gemm_conv3d(torch.zeros((1, 4, 4, 4, 32), device=dev), packed, None, cout=16)
 
 
+def test_sixteen_byte_alignment_contract(ctmr, dev):
+    """The pointwise and bf16 LDS GEMMs store 16 bytes at a time: the C ABI rejects a misaligned output
+    (no launch), and the operator copies a misaligned residual view, giving the aligned result."""
+    import ctypes
+
+    f, ops, L = ctmr.fast_fp32, ctmr.ops, ctmr._lib
+    rng = np.random.default_rng(43)
+    x = _t(rng.standard_normal((1, 8, 8, 8, 64), dtype=np.float32), dev)
+    w = _t((rng.standard_normal((64, 64, 1, 1, 1)) / 8).astype(np.float32), dev)
+    packed = f.pack_weight(w)
+    desc = ops.make_desc(tuple(x.shape), 64, 1, 1, L.MODE_PLAIN, 0, L.DT_F32, 0)
+    buf = torch.zeros(8 * 8 * 8 * 64 + 4, device=dev)
+    y_odd = buf[1:]  # 4 bytes past a 16-byte boundary
+    ws = torch.empty(max(L.workspace_bytes(desc), 1), device=dev, dtype=torch.uint8)
+    rc = L.lib().ctmr_conv3d(ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), None, None, None,
+                             y_odd.data_ptr(), ws.data_ptr(), L.workspace_bytes(desc),
+                             torch.cuda.current_stream().cuda_stream)
+    assert rc != 0 and b"16-byte" in L.lib().ctmr_last_error()
+    assert not buf.any()
+    res = _t(rng.standard_normal((1, 8, 8, 8, 64), dtype=np.float32), dev)
+    res_odd = torch.zeros(res.numel() + 1, device=dev)[1:].view_as(res)
+    res_odd.copy_(res)
+    assert res_odd.data_ptr() % 16 != 0
+    w3 = _t((rng.standard_normal((64, 64, 3, 3, 3)) / 40).astype(np.float32), dev)
+    packed3 = f.pack_weight(w3, dtype="bf16")  # the bf16 LDS GEMM reads the residual 16 bytes at a time
+    y_ref = f.implicit_gemm_conv3d(x, packed3, None, cout=64, residual=res)
+    assert torch.equal(f.implicit_gemm_conv3d(x, packed3, None, cout=64, residual=res_odd), y_ref)
+
+
 @pytest.mark.parametrize(("shape", "cout", "flags_extra"), [
     ((2, 8, 16, 16, 128), 128, 0),                 # LDS-staged GEMM: _pack keeps the affine table
     ((2, 8, 16, 16, 64), 64, 0),                   # streaming GEMM: _pack writes the padded copy
