@@ -125,6 +125,9 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  *   affine   (n, cin, 2) fp32 (scale, offset) pairs with CTMR_F_AFFINE, else NULL
  *   residual output-shaped NDHWC with CTMR_F_RESIDUAL, else NULL
  *   y        (n, D', H', W', cout); must not alias x or residual
+ * y, residual and workspace must start on 16-byte boundaries where the
+ * persistent pointwise GEMM or the bf16 LDS GEMM is chosen (16-byte stores);
+ * CTMR_E_INVALID otherwise.
  * Accumulation order is fixed for a given desc.  The register-streaming GEMM
  * visits taps kd*9+kh*3+kw ascending (outer) and input channels in ascending
  * 16-wide (fp32) / 32-wide (bf16) blocks (inner).  The LDS-staged GEMM, chosen
