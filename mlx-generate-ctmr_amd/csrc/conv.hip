@@ -314,12 +314,6 @@ struct ConvArgs {
   int items;               // pointwise_kernel: row tiles x batch items x split ranges
 };
 
-// Group-norm partials of a stored tile (ctmr_conv3d_gn).  On entry each lane
-// holds, per 16-column block ns, the fp64 sum and sum of squares of its rows'
-// stored values in column ns*16 + lane%16 of its wave's tile.  The four lane
-// groups are combined with xor butterflies (every lane ends with the same
-// bits), the waves through `red`, and each group's columns and waves are added
-// in ascending order -- a fixed order for a given shape.
 // Final step of the group-norm partials of a stored tile: red[wave][c] holds
 // the fp64 (sum, sum of squares) of column c of each wave's 64 x (NSUB*16)
 // block over its rows (published by a barrier); each group's columns and
@@ -343,33 +337,6 @@ __device__ __forceinline__ void combine_gn_partials(const double (*red)[64][2], 
     stats_tile[(int64_t)g * 2] = a;
     stats_tile[(int64_t)g * 2 + 1] = q;
   }
-}
-
-// Group-norm partials of a stored tile (ctmr_conv3d_gn).  On entry each lane
-// holds, per 16-column block ns, the fp64 sum and sum of squares of its rows'
-// stored values in column ns*16 + lane%16 of its wave's tile.  The four lane
-// groups are combined with xor butterflies (every lane ends with the same
-// bits), then the waves through `red`.
-template <int NSUB, int WM, int WN>
-__device__ __forceinline__ void write_gn_partials(double (&s1)[NSUB], double (&s2)[NSUB], double (*red)[64][2],
-                                                  int wave, int lane, int col0, int cout, int cpg, int groups,
-                                                  double* __restrict__ stats_tile) {
-#pragma unroll
-  for (int ns = 0; ns < NSUB; ++ns) {
-    s1[ns] += __shfl_xor(s1[ns], 16);
-    s1[ns] += __shfl_xor(s1[ns], 32);
-    s2[ns] += __shfl_xor(s2[ns], 16);
-    s2[ns] += __shfl_xor(s2[ns], 32);
-  }
-  if (lane < 16) {
-#pragma unroll
-    for (int ns = 0; ns < NSUB; ++ns) {
-      red[wave][ns * 16 + lane][0] = s1[ns];
-      red[wave][ns * 16 + lane][1] = s2[ns];
-    }
-  }
-  __syncthreads();
-  combine_gn_partials<NSUB, WM, WN>(red, col0, cout, cpg, groups, stats_tile);
 }
 
 template <int DT>
@@ -424,74 +391,144 @@ __device__ __forceinline__ void mma_block(f4 (&acc)[4][NSUB], const u4 (&A)[4], 
   }
 }
 
-// Epilogue of one wave's 64 x (NSUB*16) tile: D row 4*(lane/16)+r, column
-// lane%16 of each 16x16 block; output voxel v of batch item b is stored at
-// out_voxel(v) (the nearest-2x remap, or b * s_out + v).
-// Residual values (and, by the caller, bias values) are loaded before the first store:
-// interleaved, each load would wait for the stores before it (the compiler
-// cannot prove the output and its inputs apart).  Indices past the grid are
-// clamped for the loads and masked for the stores.
-// Bias of the lane's columns n0 + ns*16 + lane%16 for batch item b (zero for a
-// split's partial planes or without bias).
+// Column sums over a wave's 64 rows of a transposed accumulator block set
+// (lane l of block (ms, ns): row ms*16 + l%16, columns ns*16 + 4*(l/16) .. +3),
+// masked by row_ok[ms] and col_ok[ns]: per block ns the 4 row blocks in the
+// lane, then xor butterflies over l%16; lanes l%16 == 0 publish the fp64
+// (sum, sum of squares) of their 4 columns in red[wave][column].  A fixed order.
 template <int NSUB>
-__device__ __forceinline__ void load_bias(const ConvArgs& p, int b, int n0, int lane, float (&bv)[NSUB]) {
-  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
-#pragma unroll
-  for (int ns = 0; ns < NSUB; ++ns)
-    bv[ns] = (p.split == 1 && p.has_bias) ? bias_b[min(n0 + ns * 16 + (lane & 15), p.cout - 1)] : 0.f;
-}
-
-template <int NSUB, int WM, int WN, typename OutVoxel>
-__device__ __forceinline__ void store_tile(const ConvArgs& p, const f4 (&acc)[4][NSUB], const float (&bv)[NSUB],
-                                           int b, int m0, int n0, int S, int split_id, int wave, int lane,
-                                           int col0, int tile_id, OutVoxel out_voxel) {
+__device__ __forceinline__ void column_sums(const f4 (&acc)[4][NSUB], const bool (&row_ok)[4],
+                                            const bool (&col_ok)[NSUB], double (*red)[64][2], int wave, int lane) {
   const int lrow = lane & 15, lgrp = lane >> 4;
-  const bool partial = p.split > 1;
-  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
-  float rv[4][4][NSUB];
-  const bool add_res = !partial && p.has_res;
-  if (add_res) {
 #pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
+  for (int ns = 0; ns < NSUB; ++ns) {
+    double q1[4] = {0.0, 0.0, 0.0, 0.0}, q2[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) {
+      const bool ok = row_ok[ms] && col_ok[ns];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t base = out_voxel(min(m0 + ms * 16 + lgrp * 4 + r, S - 1)) * p.cout;
-#pragma unroll
-        for (int ns = 0; ns < NSUB; ++ns) rv[ms][r][ns] = p.res[base + min(n0 + ns * 16 + lrow, p.cout - 1)];
+        const double d = ok ? (double)acc[ms][ns][r] : 0.0;
+        q1[r] += d;
+        q2[r] = fma(d, d, q2[r]);
       }
-  }
-  double s1[NSUB], s2[NSUB];
+    }
 #pragma unroll
-  for (int ns = 0; ns < NSUB; ++ns) s1[ns] = s2[ns] = 0.0;
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-  for (int ms = 0; ms < 4; ++ms) {
+      for (int m = 1; m < 16; m <<= 1) {
+        q1[r] += __shfl_xor(q1[r], m);
+        q2[r] += __shfl_xor(q2[r], m);
+      }
+    if (lrow == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int v = m0 + ms * 16 + lgrp * 4 + r;
-      if (v >= S) continue;
-      const int64_t vox = out_voxel(v);
-      const int64_t base = vox * p.cout;
-#pragma unroll
-      for (int ns = 0; ns < NSUB; ++ns) {
-        const int col = n0 + ns * 16 + lrow;
-        if (col >= p.cout) continue;
-        float sum = acc[ms][ns][r];
-        if (!partial) {
-          if (p.has_bias) sum += bv[ns];
-          if (add_res) sum += rv[ms][r][ns];
-        }
-        out[p.planar ? (int64_t)col * p.zstride + vox : base + col] = sum;
-        if (p.stats) {
-          s1[ns] += (double)sum;
-          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
-        }
+      for (int r = 0; r < 4; ++r) {
+        red[wave][ns * 16 + 4 * lgrp + r][0] = q1[r];
+        red[wave][ns * 16 + 4 * lgrp + r][1] = q2[r];
       }
     }
   }
-  if (p.stats) {  // wave-uniform (a kernel argument): every thread reaches the barrier inside
+}
+
+// Bias of the lane's output columns n0 + ns*16 + 4*(lane/16) + r (transposed
+// accumulator layout) for batch item b; zero for a split's partial planes or
+// without bias.
+template <int NSUB>
+__device__ __forceinline__ void load_bias(const ConvArgs& p, int b, int n0, int lane, f4 (&bq)[NSUB]) {
+  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      bq[ns][r] = (p.split == 1 && p.has_bias) ? bias_b[min(n0 + ns * 16 + 4 * (lane >> 4) + r, p.cout - 1)] : 0.f;
+}
+
+// Epilogue of one wave's 64 x (NSUB*16) tile from transposed accumulators
+// (mma_block<.., true>): lane l of block (ms, ns) holds row m0 + ms*16 + l%16
+// and columns n0 + ns*16 + 4*(l/16) .. +3; output voxel v of batch item b is
+// stored at out_voxel(v) (the nearest-2x remap, or b * s_out + v).  With
+// cout % 4 == 0 (not the planar tap-expanded output) each block is one
+// 16-byte store (and residual load); otherwise four masked scalar ones.
+// Residual values are all loaded before the first store: interleaved, each
+// load would wait for the stores before it (the compiler cannot prove the
+// output and its inputs apart).  Rows past the grid are clamped for the loads
+// and masked for the stores.
+template <int NSUB, int WM, int WN, typename OutVoxel>
+__device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB], const f4 (&bq)[NSUB], int b,
+                                           int m0, int n0, int S, int split_id, int wave, int lane, int col0,
+                                           int tile_id, OutVoxel out_voxel) {
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const bool partial = p.split > 1;
+  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
+  const bool add_res = !partial && p.has_res;
+  const bool wide = !p.planar && (p.cout & 3) == 0;
+  bool row_ok[4], col_ok[NSUB];
+  int64_t vox[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+    const int v = m0 + ms * 16 + lrow;
+    row_ok[ms] = v < S;
+    vox[ms] = out_voxel(min(v, S - 1));
+  }
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) col_ok[ns] = n0 + ns * 16 + 4 * lgrp < p.cout;  // whole quad when wide
+  if (!partial && p.has_bias) {  // bias first, then the residual (the reference's epilogue order)
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += bq[ns];
+  }
+  if (add_res) {
+    f4 rq[4][NSUB];
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) {
+        const int c0 = n0 + ns * 16 + 4 * lgrp;
+        if (wide) {
+          rq[ms][ns] = *reinterpret_cast<const f4*>(p.res + vox[ms] * p.cout + min(c0, p.cout - 4));
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rq[ms][ns][r] = p.res[vox[ms] * p.cout + min(c0 + r, p.cout - 1)];
+        }
+      }
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += rq[ms][ns];
+  }
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) {
+      const int c0 = n0 + ns * 16 + 4 * lgrp;
+      const f4 val = acc[ms][ns];
+      if (wide) {
+        if (row_ok[ms] && col_ok[ns]) *reinterpret_cast<f4*>(out + vox[ms] * p.cout + c0) = val;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (row_ok[ms] && c0 + r < p.cout)
+            out[p.planar ? (int64_t)(c0 + r) * p.zstride + vox[ms] : vox[ms] * p.cout + c0 + r] = val[r];
+      }
+    }
+  if (p.stats) {  // wave-uniform (a kernel argument): every thread reaches the barrier
     __shared__ double red[WM * WN][64][2];
-    write_gn_partials<NSUB, WM, WN>(s1, s2, red, wave, lane, col0, p.cout, p.gn_cpg, p.gn_groups,
-                                    p.stats + ((int64_t)b * p.stats_tiles + tile_id) * p.gn_groups * 2);
+    if (!wide) {
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) col_ok[ns] = true;  // per-column masks below
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n0 + ns * 16 + 4 * lgrp + r >= p.cout) acc[ms][ns][r] = 0.f;
+    }
+    column_sums<NSUB>(acc, row_ok, col_ok, red, wave, lane);
+    __syncthreads();
+    combine_gn_partials<NSUB, WM, WN>(red, col0, p.cout, p.gn_cpg, p.gn_groups,
+                                      p.stats + ((int64_t)b * p.stats_tiles + tile_id) * p.gn_groups * 2);
   }
 }
 
@@ -600,7 +637,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
       }
     }
   };
-  auto compute = [&](const u4 (&A)[4], const u4 (&B)[NSUB]) { mma_block<DT, NSUB>(acc, A, B); };
+  auto compute = [&](const u4 (&A)[4], const u4 (&B)[NSUB]) { mma_block<DT, NSUB, true>(acc, A, B); };
 
   // Register double buffer: the next K block is in flight while this one
   // multiplies.  The scheduling barriers keep the prefetch loads ahead of the
@@ -632,9 +669,9 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   }
 
   const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
-  float bv[NSUB];
-  load_bias<NSUB>(p, b, n0, lane, bv);
-  store_tile<NSUB, WM, WN>(p, acc, bv, b, m0, n0, S, split_id, wave, lane, n_tile * (WN * NSUB * 16), tile_id,
+  f4 bq[NSUB];
+  load_bias<NSUB>(p, b, n0, lane, bq);
+  store_tile<NSUB, WM, WN>(p, acc, bq, b, m0, n0, S, split_id, wave, lane, n_tile * (WN * NSUB * 16), tile_id,
                            [&](int v) -> int64_t {
                              int o = v;
                              if (UP) {
@@ -667,6 +704,64 @@ constexpr int kHD = kBD + 2, kHH = kBH + 2, kHW = kBW + 2;
 constexpr int kHaloVox = kHD * kHH * kHW;                 // 600
 constexpr int kLdsRow = 80;
 constexpr int kStageIters = (kHaloVox * 4 + 255) / 256;  // 16-byte pieces per thread
+
+// Epilogue of the brick GEMMs (conv_lds_kernel, conv_lds_bf16_kernel) from
+// transposed accumulators: lane l of block (ms, ns) holds voxel (z0 + wave,
+// y0 + ms + 4*((l/8)%2), x0 + l%8) of the 4x8x8 brick and output columns
+// n0 + ns*16 + 4*(l/16) .. +3 (cout % 64 == 0), stored -- bias first, then the
+// residual -- as 16 bytes.  Group-norm column sums go through `red` (4 KiB of
+// LDS, which may alias the kernel's staging buffers: a barrier precedes it).
+template <typename Args>
+__device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int b, int split_id, int z0, int y0,
+                                            int x0, int n0, int wave, int lane, int tile_id,
+                                            double (*red)[64][2]) {
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const bool partial = p.split > 1;
+  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
+  const int z = z0 + wave, x = x0 + (lrow & 7);
+  bool row_ok[4];
+  int64_t base[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+    const int y = y0 + ms + 4 * (lrow >> 3);
+    row_ok[ms] = z < p.d && y < p.h && x < p.w;
+    base[ms] = ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout +
+               n0 + 4 * lgrp;
+  }
+  if (!partial && p.has_bias) {
+    const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0) + n0 + 4 * lgrp;
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) {
+      const f4 bq = f4{bias_b[ns * 16], bias_b[ns * 16 + 1], bias_b[ns * 16 + 2], bias_b[ns * 16 + 3]};
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) acc[ms][ns] += bq;
+    }
+  }
+  if (!partial && p.has_res) {  // every residual load before the first store
+    f4 rq[4][4];
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) rq[ms][ns] = *reinterpret_cast<const f4*>(p.res + base[ms] + ns * 16);
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) acc[ms][ns] += rq[ms][ns];
+  }
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns)
+      if (row_ok[ms]) *reinterpret_cast<f4*>(out + base[ms] + ns * 16) = acc[ms][ns];
+  if (p.stats) {  // a kernel argument: every thread reaches the barriers
+    __syncthreads();
+    const bool col_ok[4] = {true, true, true, true};
+    column_sums<4>(acc, row_ok, col_ok, red, wave, lane);
+    __syncthreads();
+    combine_gn_partials<4, 4, 1>(red, n0, p.cout, p.gn_cpg, p.gn_groups,
+                                 p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
+  }
+}
 
 struct LdsArgs {
   const float* x;       // unpadded NDHWC input
@@ -801,8 +896,8 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
         for (int ns = 0; ns < 4; ++ns)
-          acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x4f32(A[ms][j], __builtin_bit_cast(f4, B[ns])[j],
-                                                             acc[ms][ns], 0, 0, 0);
+          acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(f4, B[ns])[j], A[ms][j],
+                                                             acc[ms][ns], 0, 0, 0);  // B^T A^T: see store_brick
   };
 
   fetch(c_begin);
@@ -837,64 +932,8 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
     }
   }
 
-  // Epilogue: D row 4*(lane/16)+r of block ms is brick row ms + 4*(lane/32),
-  // column 4*((lane/16)&1) + r.
-  // (Bias and residual values loaded before the first store, as in conv_kernel.)
-  const bool partial = p.split > 1;
-  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
-  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
-  const int z = z0 + wave;
-  auto out_base = [&](int y, int x) -> int64_t {
-    return ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout;
-  };
-  float bv[4];
-#pragma unroll
-  for (int ns = 0; ns < 4; ++ns) bv[ns] = (!partial && p.has_bias) ? bias_b[n0 + ns * 16 + lrow] : 0.f;
-  float rv[4][4][4];
-  const bool add_res = !partial && p.has_res;
-  if (add_res) {
-#pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t base = out_base(y0 + ms + 4 * (lgrp >> 1), x0 + 4 * (lgrp & 1) + r);
-#pragma unroll
-        for (int ns = 0; ns < 4; ++ns) rv[ms][r][ns] = p.res[base + n0 + ns * 16 + lrow];
-      }
-  }
-  double s1[4], s2[4];
-#pragma unroll
-  for (int ns = 0; ns < 4; ++ns) s1[ns] = s2[ns] = 0.0;
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms) {
-    const int y = y0 + ms + 4 * (lgrp >> 1);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int x = x0 + 4 * (lgrp & 1) + r;
-      if (z >= p.d || y >= p.h || x >= p.w) continue;
-      const int64_t base = out_base(y, x);
-#pragma unroll
-      for (int ns = 0; ns < 4; ++ns) {
-        const int col = n0 + ns * 16 + lrow;
-        float sum = acc[ms][ns][r];
-        if (!partial) {
-          if (p.has_bias) sum += bv[ns];
-          if (add_res) sum += rv[ms][r][ns];
-        }
-        out[base + col] = sum;
-        if (p.stats) {
-          s1[ns] += (double)sum;
-          s2[ns] = fma((double)sum, (double)sum, s2[ns]);
-        }
-      }
-    }
-  }
-  if (p.stats) {  // a kernel argument: every thread reaches the barrier inside
-    __shared__ double red[4][64][2];
-    const int tile_id = (bz * p.ty + by) * p.tx + bx;
-    write_gn_partials<4, 4, 1>(s1, s2, red, wave, lane, n0, p.cout, p.gn_cpg, p.gn_groups,
-                               p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
-  }
+  __shared__ double red[4][64][2];
+  store_brick(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, (bz * p.ty + by) * p.tx + bx, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -1141,85 +1180,8 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
 #undef CTMR_LDS16_ROW
   }
 
-  // Epilogue.  Lane l of accumulator block (ms, ns) holds voxel (z0 + wave,
-  // y0 + ms + 4 * ((l / 8) % 2), x0 + l % 8) and output columns n0 + ns * 16 +
-  // 4 * (l / 16) .. +3, stored (with bias and residual) as 16 bytes.
-  const bool partial = p.split > 1;
-  const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0);
-  float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
-  const int z = z0 + wave, x = x0 + (lrow & 7);
-  auto out_base = [&](int y) -> int64_t {
-    return ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout;
-  };
-  f4 bq[4];
-#pragma unroll
-  for (int ns = 0; ns < 4; ++ns)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) bq[ns][r] = (!partial && p.has_bias) ? bias_b[n0 + ns * 16 + 4 * lgrp + r] : 0.f;
-  f4 rq[4][4];
-  const bool add_res = !partial && p.has_res;
-  if (add_res) {
-#pragma unroll
-    for (int ms = 0; ms < 4; ++ms) {
-      const int64_t base = out_base(y0 + ms + 4 * (lrow >> 3)) + n0 + 4 * lgrp;
-#pragma unroll
-      for (int ns = 0; ns < 4; ++ns) rq[ms][ns] = *reinterpret_cast<const f4*>(p.res + base + ns * 16);
-    }
-  }
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms) {
-    const int y = y0 + ms + 4 * (lrow >> 3);
-    const bool ok = z < p.d && y < p.h && x < p.w;
-    const int64_t base = out_base(y) + n0 + 4 * lgrp;
-#pragma unroll
-    for (int ns = 0; ns < 4; ++ns) {
-      f4 v = acc[ms][ns];
-      if (!partial) {
-        if (p.has_bias) v += bq[ns];
-        if (add_res) v += rq[ms][ns];
-      }
-      acc[ms][ns] = v;
-      if (ok) *reinterpret_cast<f4*>(out + base + ns * 16) = v;
-    }
-  }
-  if (p.stats) {  // a kernel argument: every thread reaches the barriers
-    __syncthreads();  // the reduction buffer reuses the halo
-    double (*red)[64][2] = reinterpret_cast<double (*)[64][2]>(halo);
-#pragma unroll
-    for (int ns = 0; ns < 4; ++ns) {
-      // column sums over the wave's 64 voxels: its 4 row blocks, then xor butterflies over lane % 16
-      double q1[4] = {0.0, 0.0, 0.0, 0.0}, q2[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-      for (int ms = 0; ms < 4; ++ms) {
-        const int y = y0 + ms + 4 * (lrow >> 3);
-        const bool ok = z < p.d && y < p.h && x < p.w;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const double d = ok ? (double)acc[ms][ns][r] : 0.0;
-          q1[r] += d;
-          q2[r] = fma(d, d, q2[r]);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) {
-          q1[r] += __shfl_xor(q1[r], m);
-          q2[r] += __shfl_xor(q2[r], m);
-        }
-      if (lrow == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          red[wave][ns * 16 + 4 * lgrp + r][0] = q1[r];
-          red[wave][ns * 16 + 4 * lgrp + r][1] = q2[r];
-        }
-      }
-    }
-    __syncthreads();
-    const int tile_id = (bz * p.ty + by) * p.tx + bx;
-    combine_gn_partials<4, 4, 1>(red, n0, p.cout, p.gn_cpg, p.gn_groups,
-                                 p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
-  }
+  store_brick(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, (bz * p.ty + by) * p.tx + bx,
+              reinterpret_cast<double (*)[64][2]>(halo));  // the reduction buffer reuses the halo
 }
 
 // ---------------------------------------------------------------------------
@@ -1415,44 +1377,25 @@ __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
     float* out = p.y + (p.split > 1 ? (int64_t)it.split_id * p.plane : 0) + ((int64_t)it.b * p.s_out + m0) * p.cout;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, (short)0, valid_rows * p.cout * 4, 0x00020000);
-    const bool add_bias = p.split == 1 && p.has_bias;
+    if (p.split == 1 && p.has_bias) {
 #pragma unroll
-    for (int ns = 0; ns < NSUB; ++ns) {
-      double q1[4] = {0.0, 0.0, 0.0, 0.0}, q2[4] = {0.0, 0.0, 0.0, 0.0};
+      for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms) {
-        f4 v = acc[ms][ns];
-        if (add_bias) v += bq[ns];
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), orsrc, q_off[ns] + ms * 16 * p.cout * 4, 0,
-                                               0);
-        if (p.stats) {
-          const bool ok = ms * 16 + lrow < valid_rows && q_off[ns] < 0x40000000;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const double d = ok ? (double)v[r] : 0.0;
-            q1[r] += d;
-            q2[r] = fma(d, d, q2[r]);
-          }
-        }
-      }
-      if (p.stats) {  // column sums over the wave's rows: xor butterflies over lane%16
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int m = 1; m < 16; m <<= 1) {
-            q1[r] += __shfl_xor(q1[r], m);
-            q2[r] += __shfl_xor(q2[r], m);
-          }
-        if (lrow == 0) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            red[wave][ns * 16 + 4 * lgrp + r][0] = q1[r];
-            red[wave][ns * 16 + 4 * lgrp + r][1] = q2[r];
-          }
-        }
-      }
+        for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += bq[ns];
     }
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns)
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[ms][ns]), orsrc,
+                                               q_off[ns] + ms * 16 * p.cout * 4, 0, 0);
     if (p.stats) {  // a kernel argument: every thread reaches the barriers
+      bool row_ok[4], col_ok[NSUB];
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) row_ok[ms] = ms * 16 + lrow < valid_rows;
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) col_ok[ns] = q_off[ns] < 0x40000000;
+      column_sums<NSUB>(acc, row_ok, col_ok, red, wave, lane);
       __syncthreads();
       combine_gn_partials<NSUB, WM, WN>(red, n_tile * TN, p.cout, p.gn_cpg, p.gn_groups,
                                         p.stats + ((int64_t)it.b * p.stats_tiles + it.m_tile) * p.gn_groups * 2);
@@ -1845,9 +1788,17 @@ static void launch_split_reduce(const ctmr_conv_desc* d, const Geometry& g, cons
 
 typedef void (*ConvFn)(dim3, dim3, hipStream_t, const ConvArgs&);
 
+// The 64-column register-streaming GEMM is tuned for two resident workgroups
+// per CU (two waves per SIMD; its split policy and round sizes assume 512 per
+// launch).  Its ~160 VGPRs would let a third in, which measured slower
+// (config 0: 0.533 ms against 0.443 ms), so the launch reserves LDS it does
+// not use: 60 KiB + 4 KiB of partial buffers per workgroup, two per 160 KiB CU.
+constexpr size_t kConvTwoPerCuLds = 60 * 1024;
+
 template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
 static void launch_conv(dim3 grid, dim3 block, hipStream_t st, const ConvArgs& a) {
-  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP>), grid, block, 0, st, a);
+  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP>), grid, block, NSUB == 4 ? kConvTwoPerCuLds : 0,
+                     st, a);
 }
 
 // Compute units of the current device (cached per device).
