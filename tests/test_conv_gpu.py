@@ -427,6 +427,23 @@ def test_group_norm_affine_and_apply(ctmr, dev):
         _assert_rel(_h(y), rm.group_norm(x, gamma, beta, 32, 1e-6, apply_silu=silu), 1e-6, f"gn silu={silu}")
 
 
+def test_silu_elementwise_accuracy(ctmr, dev):
+    """SiLU on the hardware exp2 and reciprocal: per element within 1e-6 relative of float64 over the
+    whole fp32 range that matters (and the limits: -0 below -88, the identity above 88)."""
+    rng = np.random.default_rng(29)
+    x = np.concatenate([np.linspace(-100.0, 100.0, 200_001), 4 * rng.standard_normal(200_000),
+                        [0.0, -0.0, 1e-30, -1e-30, 88.0, -88.0, 89.0, -89.0, 1e30, -1e30]]).astype(np.float32)
+    y = _h(ctmr.fast_fp32.silu(_t(x, dev)))
+    xd = x.astype(np.float64)
+    ref = xd / (1.0 + np.exp(-np.clip(xd, -700, 700)))
+    big = np.abs(ref) > 1e-30
+    rel = np.abs(y[big] - ref[big]) / np.abs(ref[big])
+    print(f"silu max rel error {rel.max():.3e}", flush=True)
+    assert rel.max() <= 1e-6
+    assert np.all(np.abs(y[~big]) <= 1e-30)
+    assert np.isfinite(y).all()
+
+
 def test_group_norm_matches_recorded_golden(ctmr, dev):
     from golden_util import load_fixture
 
