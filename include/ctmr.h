@@ -225,7 +225,10 @@ int ctmr_resample(int32_t op, int32_t n, int32_t d, int32_t h, int32_t w, int32_
  * may be column slices of one fused (n, l, 3C) projection.  head_dim must be
  * 32 (the MAISI UNet's num_head_channels).  Any lq, lk >= 1.  query_tiles
  * picks 16 (1) or 32 (2) queries per wave, 0 = the library's policy; results
- * are bit-identical either way (keys are visited in the same fixed order). */
+ * are bit-identical either way (keys are visited in the same fixed order:
+ * ascending 64-key blocks, or -- for grids of under two waves per SIMD, decided
+ * from n, lq, lk and heads only -- two such runs over the key halves, combined
+ * first half first). */
 typedef struct ctmr_attn_desc {
   int32_t n, lq, lk, heads, head_dim, query_tiles;
   int64_t ldq, ldk, ldv, ldo;

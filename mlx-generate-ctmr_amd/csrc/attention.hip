@@ -44,20 +44,37 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// First key of the second part of a two-part key split: half the keys,
+// rounded up to a whole 64-key block (so only the second part is ragged).
+__device__ __forceinline__ int attention_key_split_point(int lk) {
+  return min(lk, (((lk + 1) / 2 + 63) / 64) * 64);
+}
+
 // Keys and values of one 64-key block in MFMA operand order.
 struct KeyBlock {
   f4 k[kKeyTiles][2];      // K row (tile*16 + l%16), dims 8g .. 8g+7
   float v[kKeyTiles][4][2];  // V row (tile*16 + 4g + r), dims (l%16) and (16 + l%16)
 };
 
-template <int QT>
+// KS = 2 splits the keys of each query group between two waves of the
+// workgroup (keys [0, split) and [split, lk), split a multiple of the 64-key
+// block): small grids then keep two waves per SIMD.  The second wave hands its
+// running max, sum and output to the first through LDS, which combines them
+// in that fixed order.
+template <int QT, int KS>
 __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
+  static_assert(KS == 1 || KS == 2, "one or two key parts");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, g = lane >> 4;
   const int b = blockIdx.y / a.heads, h = blockIdx.y % a.heads;
-  const int q0 = (blockIdx.x * kWaves + wave) * (QT * 16);
-  if (q0 >= a.lq) return;  // wave-uniform; the kernel has no barriers
+  const int q0 = (blockIdx.x * (kWaves / KS) + wave / KS) * (QT * 16);
+  const int part = wave % KS;
+  // Wave-uniform.  With KS = 2 every wave reaches the combine barrier: a query
+  // group past the end runs on clamped rows and stores nothing.
+  if (KS == 1 && q0 >= a.lq) return;
+  const int split = KS == 1 ? a.lk : attention_key_split_point(a.lk);
+  const int k_begin = part == 0 ? 0 : split, k_end = part == 0 ? split : a.lk;
 
   const float* Q = a.q + (int64_t)b * a.lq * a.ldq + h * kHeadDim;
   const float* K = a.k + (int64_t)b * a.lk * a.ldk + h * kHeadDim;
@@ -112,12 +129,12 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
           for (int e = 0; e < 4; ++e) acc = mfma4(kb.k[u][j][e], qa[t][j][e], acc);
         s[u][t] = acc;
       }
-    if (k0 + 16 * kKeyTiles > a.lk) {  // wave-uniform: only the last block is ragged
+    if (k0 + 16 * kKeyTiles > k_end) {  // wave-uniform: only the last block is ragged
 #pragma unroll
       for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (k0 + u * 16 + 4 * g + r >= a.lk)
+          if (k0 + u * 16 + 4 * g + r >= k_end)
 #pragma unroll
             for (int t = 0; t < QT; ++t) s[u][t][r] = -INFINITY;
     }
@@ -163,17 +180,49 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
   // current block's products run.
   constexpr int kBlock = 16 * kKeyTiles;
   KeyBlock b0, b1;
-  load(b0, 0);
-  for (int k0 = 0; k0 < a.lk; k0 += 2 * kBlock) {
-    if (k0 + kBlock < a.lk) load(b1, k0 + kBlock);
+  if (k_begin < k_end) load(b0, k_begin);
+  for (int k0 = k_begin; k0 < k_end; k0 += 2 * kBlock) {
+    if (k0 + kBlock < k_end) load(b1, k0 + kBlock);
     __builtin_amdgcn_sched_barrier(0);
     compute(b0, k0);
     __builtin_amdgcn_sched_barrier(0);
-    if (k0 + kBlock >= a.lk) break;
-    if (k0 + 2 * kBlock < a.lk) load(b0, k0 + 2 * kBlock);
+    if (k0 + kBlock >= k_end) break;
+    if (k0 + 2 * kBlock < k_end) load(b0, k0 + 2 * kBlock);
     __builtin_amdgcn_sched_barrier(0);
     compute(b1, k0 + kBlock);
     __builtin_amdgcn_sched_barrier(0);
+  }
+
+  if constexpr (KS == 2) {
+    // Lane-for-lane state of the second key part: max, partial sum, output.
+    __shared__ float xch[kWaves / 2][QT][10][64];
+    float(*mine)[10][64] = xch[wave / 2];
+    if (part == 1) {
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        mine[t][0][lane] = m[t];
+        mine[t][1][lane] = l[t];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          mine[t][2 + e][lane] = o[t][0][e];
+          mine[t][6 + e][lane] = o[t][1][e];
+        }
+      }
+    }
+    __syncthreads();
+    if (part == 1) return;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const float m1 = mine[t][0][lane];
+      const float mm = fmaxf(m[t], m1);  // the first part always holds keys: finite
+      const float a0 = exp2f(m[t] - mm), a1 = exp2f(m1 - mm);  // a1 = 0 for an empty second part
+      l[t] = l[t] * a0 + mine[t][1][lane] * a1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[t][0][e] = o[t][0][e] * a0 + mine[t][2 + e][lane] * a1;
+        o[t][1][e] = o[t][1][e] * a0 + mine[t][6 + e][lane] * a1;
+      }
+    }
   }
 
   float* O = a.out + (int64_t)b * a.lq * a.ldo + h * kHeadDim;
@@ -194,11 +243,11 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
   }
 }
 
-template <int QT>
+template <int QT, int KS>
 int launch_attention(const AttnArgs& a, int n, hipStream_t stream) {
-  const int64_t per_block = (int64_t)kWaves * QT * 16;
+  const int64_t per_block = (int64_t)(kWaves / KS) * QT * 16;
   dim3 grid((unsigned)ceil_div(a.lq, per_block), (unsigned)(n * a.heads));
-  hipLaunchKernelGGL(flash_attention_kernel<QT>, grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((flash_attention_kernel<QT, KS>), grid, dim3(256), 0, stream, a);
   return check_launch("flash_attention_kernel");
 }
 
@@ -211,6 +260,14 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 int attention_query_tiles(int n, int lq, int heads) {
   const int64_t waves2 = ceil_div(lq, 32) * (int64_t)n * heads;
   return waves2 >= 1024 ? 2 : 1;
+}
+
+// Key parts per query group, from the shape only (never from query_tiles, so
+// both tilings give the same bits): two when there are at least two 64-key
+// blocks and fewer than two waves per SIMD would run otherwise.
+int attention_key_parts(int n, int lq, int lk, int heads) {
+  const int64_t waves2 = ceil_div(lq, 32) * (int64_t)n * heads;
+  return (lk >= 128 && waves2 < 2048) ? 2 : 1;
 }
 
 }  // namespace ctmr
@@ -241,5 +298,7 @@ extern "C" int ctmr_flash_attention(const ctmr_attn_desc* d, const float* q, con
              (float)((double)d->scale * 1.4426950408889634)};
   hipStream_t st = (hipStream_t)stream;
   const int qt = d->query_tiles ? d->query_tiles : attention_query_tiles(d->n, d->lq, d->heads);
-  return qt == 2 ? launch_attention<2>(a, d->n, st) : launch_attention<1>(a, d->n, st);
+  if (attention_key_parts(d->n, d->lq, d->lk, d->heads) == 2)
+    return qt == 2 ? launch_attention<2, 2>(a, d->n, st) : launch_attention<1, 2>(a, d->n, st);
+  return qt == 2 ? launch_attention<2, 1>(a, d->n, st) : launch_attention<1, 1>(a, d->n, st);
 }
