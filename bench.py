@@ -188,8 +188,25 @@ def secondary(pkg, dev, steps):
     return out
 
 
-def unet_flops(constructor, batch, d, h, w):
-    """Conv FLOPs of one UNet pass (8-tap folded upsample convs) and attention FLOPs."""
+def controlnet_flops(constructor, batch, d, h, w):
+    """Conv and attention FLOPs of one ControlNetMaisi pass with a precomputed conditioning embedding:
+    the UNet's encoder (conv_in, down path, mid block) plus a 1x1 zero conv per residual."""
+    conv, attn_f = unet_flops(constructor, batch, d, h, w, encoder_only=True)
+    ch = list(constructor["num_channels"])
+    nl, nres = len(ch), constructor["num_res_blocks"]
+    vox = [batch * d * h * w // 8**i for i in range(nl)]
+    conv += 2.0 * vox[0] * ch[0] * ch[0]  # conv_in's residual
+    for i in range(nl):
+        conv += nres * 2.0 * vox[i] * ch[i] * ch[i]  # res-block outputs
+        if i != nl - 1:
+            conv += 2.0 * vox[i + 1] * ch[i] * ch[i]  # down-sampler outputs
+    conv += 2.0 * vox[-1] * ch[-1] * ch[-1]  # mid block
+    return conv, attn_f
+
+
+def unet_flops(constructor, batch, d, h, w, encoder_only=False):
+    """Conv FLOPs of one UNet pass (8-tap folded upsample convs) and attention FLOPs; with
+    ``encoder_only`` the conv_in + down path + mid block part."""
     ch = list(constructor["num_channels"])
     nl = len(ch)
     nres = [constructor["num_res_blocks"]] * nl
@@ -217,6 +234,8 @@ def unet_flops(constructor, batch, d, h, w):
             conv += res(vox[i + 1], ch[i], ch[i])  # down: convs at the pooled grid
     conv += 2 * res(vox[-1], ch[-1], ch[-1])
     attn_f += att(vox[-1], ch[-1])
+    if encoder_only:
+        return conv, attn_f
     rc = ch[::-1]
     out = rc[0]
     for i in range(nl):
@@ -299,6 +318,29 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         {"graph_ms": round(gms, 3), "graph_frac_roofline": round(floor_ms / gms, 4),
          "bf16_ms": round(ms16, 3), "bf16_graph_ms": round(gms16, 3), "bf16_roofline_ms": round(floor16, 3),
          "bf16_frac_roofline": round(floor16 / min(ms16, gms16), 4)})
+    # CT from mask: ControlNetMaisi (production constructor, conditioning embedding computed once per
+    # generation) + the UNet with its residuals, per denoising step
+    cc = m.PRODUCTION_CONTROLNET_CONSTRUCTOR
+    cw = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.controlnet_weight_shapes(cc), seed=13).items()}
+    cond_emb = torch.from_numpy(rng.standard_normal((2, 64, 64, 32, 64), dtype=np.float32)).to(dev)
+
+    def ct_step():
+        down, mid = m.controlnet_residuals(x, t, classes, None, cw, constructor=cc, conditioning_embedding=cond_emb)
+        return m.denoise_unet(x, t, classes, spacing, uw, constructor=uc, down_block_additional_residuals=down,
+                              mid_block_additional_residual=mid)
+
+    ctrl = lambda: m.controlnet_residuals(x, t, classes, None, cw, constructor=cc, conditioning_embedding=cond_emb)
+    for _ in range(2):
+        ct_step()
+    ct_ms = _wall_ms(ct_step, max(3, steps // 2))
+    ctrl_ms = _wall_ms(ctrl, max(3, steps // 2))
+    cconv, cattn = controlnet_flops(cc, 2, 64, 64, 32)
+    ct_flop = conv_f + attn_f + cconv + cattn
+    out["ct_controlnet_unet_step_batch2_64x64x32"] = {
+        "ms": round(ct_ms, 3), "controlnet_ms": round(ctrl_ms, 3),
+        "controlnet_tflop": round((cconv + cattn) / 1e12, 4), "tflops": round(ct_flop / ct_ms / 1e9, 2),
+        "roofline_ms": round(ct_flop / FP32_PEAK * 1e3, 3), "frac_roofline": round(ct_flop / FP32_PEAK * 1e3 / ct_ms, 4)}
+    del cw, cond_emb
     if cpu:
         from oracle import maisi_torch as mt
 
