@@ -312,6 +312,7 @@ struct ConvArgs {
   double* stats;           // group-norm partials of the output (ctmr_conv3d_gn) or null
   int gn_groups, gn_cpg, stats_tiles;
   int items;               // pointwise_kernel: row tiles x batch items x split ranges
+  int in_d, in_h, in_w;    // input extent (conv_kernel<.., DIRECT>: A read from x itself)
 };
 
 // Final step of the group-norm partials of a stored tile: red[wave][c] holds
@@ -532,9 +533,16 @@ __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB]
   }
 }
 
-template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
+// DIRECT: a plain fp32 3x3x3 conv with cin % 16 == 0 reads its A rows from the
+// unpadded input x itself instead of a zero-padded packed copy (no pack pass).
+// A lane's window may cross the volume border, so for each tap the lane's
+// offset is either the real row or one past the buffer's range, which the
+// hardware reads as zeros -- the padded copy's zeros, so the products and their
+// order, and the output bits, are those of the packed form.
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false>
 __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   static_assert(WM * WN == 4, "four waves per workgroup");
+  static_assert(!DIRECT || (KT == 3 && !UP && DT == CTMR_F32), "direct reads: plain fp32 3x3x3 convs");
   const int lane = threadIdx.x & 63;
   // Wave index made provably uniform so every address base below lives in SGPRs.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -571,14 +579,38 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   // A: one window-start row per 16-voxel block; rows past the grid reuse the
   // last voxel and are not stored.  Rows grow with the voxel index, so the
   // wave's first voxel has the smallest row and every lane offset is >= 0.
-  const int64_t row0 = window_row(min(m0, S - 1));
+  const int64_t row0 = DIRECT ? 0 : window_row(min(m0, S - 1));
   const int64_t abase_off = ((int64_t)b * p.rows_per_batch + row0) * p.row_bytes;
   const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.xp + abase_off), (short)0, (int)min(p.x_bytes - abase_off, (int64_t)0x7fffffff), 0x00020000);
   int aoff[4];
+  // DIRECT: per lane and row block, the byte offset of the window origin (the
+  // voxel at -1, -1, -1 from the window centre; negative at the low borders)
+  // and 9 validity bits: bit t / 3 + t / 6 + t set when origin + t lies inside
+  // the volume along d / h / w.
+  int lane_off[4];
+  unsigned vmask[4];
 #pragma unroll
-  for (int ms = 0; ms < 4; ++ms)
-    aoff[ms] = (int)((window_row(min(m0 + ms * 16 + lrow, S - 1)) - row0) * p.row_bytes) + lgrp * 16;
+  for (int ms = 0; ms < 4; ++ms) {
+    if constexpr (DIRECT) {
+      const int v = min(m0 + ms * 16 + lrow, S - 1);
+      const int d = v / ghw, r = v - d * ghw;
+      const int h = r / p.gw, w = r - h * p.gw;
+      const int zi = STRIDE * d - 1, yi = STRIDE * h - 1, xi = STRIDE * w - 1;
+      lane_off[ms] = ((zi * p.in_h + yi) * p.in_w + xi) * (int)p.row_bytes + lgrp * 16;
+      unsigned m = 0;
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        m |= (unsigned)(zi + t >= 0 && zi + t < p.in_d) << t;
+        m |= (unsigned)(yi + t >= 0 && yi + t < p.in_h) << (3 + t);
+        m |= (unsigned)(xi + t >= 0 && xi + t < p.in_w) << (6 + t);
+      }
+      vmask[ms] = m;
+      aoff[ms] = 0;
+    } else {
+      aoff[ms] = (int)((window_row(min(m0 + ms * 16 + lrow, S - 1)) - row0) * p.row_bytes) + lgrp * 16;
+    }
+  }
   // B: one output column per lane per 16-column block.
   const int n0 = n_tile * (WN * NSUB * 16) + wave_n * (NSUB * 16);
   const int64_t bbase_off = (int64_t)phase * p.taps * p.kb * p.np * 64;
@@ -604,20 +636,36 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   // Load cursor over the step sequence (tap-major, 64-byte channel block
   // minor), advanced incrementally so a step costs a few scalar adds.
   const int rb = (int)p.row_bytes;
-  int c_kb, c_tw, c_th, c_tapoff, c_bo;
+  int c_kb, c_tw, c_th, c_td, c_tapoff, c_bo;
   {
     const int tap = s_begin / p.kb;
     c_kb = s_begin - tap * p.kb;
     c_tw = tap % KT;
     c_th = (tap / KT) % KT;
-    const int td = tap / (KT * KT);
-    c_tapoff = (td * p.P + c_th * p.Q + c_tw) * rb;
+    c_td = tap / (KT * KT);
+    c_tapoff = (c_td * p.P + c_th * p.Q + c_tw) * rb;
     c_bo = s_begin * bstep;
   }
+  // DIRECT: the lane offsets of the cursor's tap (recomputed when the tap
+  // changes): the real row, or 0x80000000 -- past any buffer range -- where the
+  // tap leaves the volume.  A prefetch past the last step may test bits of a
+  // tap that does not exist; its offset is then a row inside the input or out
+  // of range, and the data is never used.
+  auto direct_offsets = [&]() {
+    if constexpr (DIRECT) {
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) {
+        const unsigned m = vmask[ms];
+        const bool in = ((m >> c_td) & (m >> (3 + c_th)) & (m >> (6 + c_tw)) & 1u) != 0;
+        aoff[ms] = in ? lane_off[ms] + c_tapoff : (int)0x80000000;
+      }
+    }
+  };
+  direct_offsets();
   auto load = [&](u4 (&A)[4], u4 (&B)[NSUB]) {
     // readfirstlane: the step offsets are wave-uniform; saying so keeps them in
     // SGPRs (buffer soffset) instead of a per-lane waterfall.
-    const int ao = __builtin_amdgcn_readfirstlane(c_tapoff + c_kb * 64);
+    const int ao = __builtin_amdgcn_readfirstlane(DIRECT ? c_kb * 64 : c_tapoff + c_kb * 64);
     const int bo = __builtin_amdgcn_readfirstlane(c_bo);
 #pragma unroll
     for (int ms = 0; ms < 4; ++ms) A[ms] = __builtin_amdgcn_raw_buffer_load_b128(arsrc, aoff[ms], ao, 0);
@@ -632,9 +680,11 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
         c_tapoff += (p.Q - KT) * rb;
         if (++c_th == KT) {
           c_th = 0;
+          ++c_td;
           c_tapoff += (p.P - KT * p.Q) * rb;
         }
       }
+      direct_offsets();
     }
   };
   auto compute = [&](const u4 (&A)[4], const u4 (&B)[NSUB]) { mma_block<DT, NSUB, true>(acc, A, B); };
@@ -1538,6 +1588,7 @@ struct Geometry {
   bool lds;              // LDS-staged GEMM (conv_lds_kernel)
   bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
   bool pointwise;        // one-tap GEMM on the persistent pointwise_kernel
+  bool direct;           // streaming GEMM reading the unpadded input (no pack)
   int tz, ty, tx;        // its bricks per axis
   int layout;            // WL_TAPS, WL_EXPAND (cout <= 4) or WL_IM2COL (small cin)
   int ncols;             // GEMM columns: cout, or 27 * cout for WL_EXPAND
@@ -1696,6 +1747,21 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
       g.tz = tz; g.ty = ty; g.tx = tx;
     }
   }
+  // Plain fp32 3x3x3 convs whose channels fill whole 16-channel K blocks
+  // need no packed copy: the streaming GEMM reads x itself, with out-of-range
+  // offsets for taps outside the volume (the padded copy's zeros).  Its lane
+  // offsets are 32-bit: one batch item must stay below 2 GiB.
+  g.direct = !g.lds16 && g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 &&
+             d->mode == CTMR_MODE_PLAIN && !(d->flags & (CTMR_F_AFFINE | CTMR_F_SILU)) && d->cin % 16 == 0 &&
+             (int64_t)d->d * d->h * d->w * d->cin * 4 < (1ll << 31) - (1ll << 20);
+  if (g.direct) {
+    g.pack = false;
+    g.cp = d->cin;
+    g.kblocks = d->cin / 16;
+    g.Q = d->w;
+    g.P = d->h * d->w;
+    g.rows_per_batch = (int64_t)d->d * g.P;
+  }
   // Tile shape by GEMM width.
   if (g.lds16) { g.nsub = 4; g.wm = 4; g.wn = 1; }
   else if (g.ncols <= 16) { g.nsub = 1; g.wm = 4; g.wn = 1; }
@@ -1795,10 +1861,10 @@ typedef void (*ConvFn)(dim3, dim3, hipStream_t, const ConvArgs&);
 // not use: 60 KiB + 4 KiB of partial buffers per workgroup, two per 160 KiB CU.
 constexpr size_t kConvTwoPerCuLds = 60 * 1024;
 
-template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP>
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false>
 static void launch_conv(dim3 grid, dim3 block, hipStream_t st, const ConvArgs& a) {
-  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP>), grid, block, NSUB == 4 ? kConvTwoPerCuLds : 0,
-                     st, a);
+  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP, DIRECT>), grid, block,
+                     NSUB == 4 ? kConvTwoPerCuLds : 0, st, a);
 }
 
 // Compute units of the current device (cached per device).
@@ -1844,6 +1910,10 @@ template <int DT, int NSUB, int WM, int WN>
 static ConvFn pick_kind(const Geometry& g, int stride, bool up) {
   if constexpr (NSUB == 4) {
     if (g.pointwise) return launch_pointwise<DT, WM, WN>;
+  }
+  if constexpr (DT == CTMR_F32) {
+    if (g.direct) return stride == 2 ? launch_conv<DT, NSUB, WM, WN, 3, 2, false, true>
+                                     : launch_conv<DT, NSUB, WM, WN, 3, 1, false, true>;
   }
   return pick_kind<DT, NSUB, WM, WN>(g.KT, stride, up);
 }
@@ -2164,6 +2234,9 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
   }
   const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
   a.items = g.pointwise ? (int)((int64_t)g.m_tiles * desc->n * g.split) : 0;  // launch_pointwise sizes its grid
+  a.in_d = desc->d;
+  a.in_h = desc->h;
+  a.in_w = desc->w;
   ConvFn fn = pick(desc, g);
   fn(dim3((unsigned)blocks), dim3(256), st, a);
   if ((rc = check_launch("conv"))) return rc;

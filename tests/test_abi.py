@@ -44,8 +44,11 @@ def test_output_dims(ctmr, dims, kw, expected):
 def test_workspace_and_packed_sizes(ctmr):
     L = ctmr._lib
     d = L.conv_desc(1, 64, 64, 64, 64, 64)
-    # streaming GEMM (cin < 128): padded copy, 66^3 rows x 64 fp32 channels, 256-byte aligned
-    assert L.workspace_bytes(d) == ((66**3 * 64 * 4 + 255) // 256) * 256
+    # streaming GEMM (cin < 128) of a plain conv with whole 16-channel blocks reads x directly: no
+    # workspace; with the GN affine it packs a padded copy, 66^3 rows x 64 fp32 channels, 256-byte aligned
+    assert L.workspace_bytes(d) == 0
+    assert L.workspace_bytes(L.conv_desc(1, 64, 64, 64, 64, 64, flags=L.F_AFFINE)) == \
+        ((66**3 * 64 * 4 + 255) // 256) * 256
     assert L.packed_weight_elems(d) == 27 * 64 * 64
     assert L.conv_split(d) == 1
     # the LDS-staged GEMM (cin >= 128) reads x directly: no workspace without affine or
@@ -55,6 +58,8 @@ def test_workspace_and_packed_sizes(ctmr):
     assert L.workspace_bytes(L.conv_desc(1, 64, 64, 64, 128, 128, flags=L.F_AFFINE)) == 1024
     assert L.packed_weight_elems(d128) == 27 * 128 * 128
     ds = L.conv_desc(1, 64, 64, 64, 128, 128, flags=L.F_STREAM)
+    assert L.workspace_bytes(ds) == 0
+    ds = L.conv_desc(1, 64, 64, 64, 128, 128, flags=L.F_STREAM | L.F_SILU)
     assert L.workspace_bytes(ds) == ((66**3 * 128 * 4 + 255) // 256) * 256
     # cin below one K block packs im2col rows: K = 27 * cin rounded to the block
     d4 = L.conv_desc(1, 8, 8, 8, 4, 64)

@@ -482,6 +482,53 @@ def test_validation_errors(ctmr, dev):
         f.implicit_gemm_conv3d(torch.zeros((1, 4, 4, 4, 32), device=dev), packed, None, cout=16)
 
 
+DIRECT_CASES = [
+    # (name, x shape NDHWC, cout, keyword arguments)
+    ("ragged, batch 2", (2, 9, 13, 11, 32), 48, {}),
+    ("stride 2", (1, 16, 16, 16, 64), 64, {"stride": 2}),
+    ("stride 2, odd extents", (1, 7, 9, 5, 16), 40, {"stride": 2}),
+    ("128 channels on the streaming GEMM", (2, 8, 8, 8, 128), 128, {"stream_gemm": True}),
+    ("batch bias + residual + statistics", (2, 12, 12, 12, 64), 64, {"bbias": True, "res": True, "gn": 32}),
+    ("forced K split", (1, 4, 8, 8, 256), 256, {"split": 7, "stream_gemm": True}),
+    ("one voxel", (1, 1, 1, 1, 16), 16, {}),
+]
+
+
+@pytest.mark.parametrize(("name", "shape", "cout", "kw"), DIRECT_CASES, ids=[c[0] for c in DIRECT_CASES])
+def test_direct_reads_equal_the_packed_copy(ctmr, dev, name, shape, cout, kw):
+    """Plain fp32 3x3x3 convs with cin % 16 == 0 read x itself (taps outside the volume read as zero
+    through out-of-range buffer offsets) instead of a zero-padded packed copy: bit-identical to the
+    packed form (forced here with an identity affine, which packs the same values), and within the
+    float64 bar."""
+    print(f"direct {name}: {shape} -> {cout} {kw}", flush=True)
+    f = ctmr.fast_fp32
+    kw = dict(kw)
+    rng = np.random.default_rng(sum(shape) + cout)
+    n, c = shape[0], shape[-1]
+    x = rng.standard_normal(shape, dtype=np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal((n, cout) if kw.pop("bbias", False) else (cout,)).astype(np.float32)
+    stride = kw.get("stride", 1)
+    out_sp = tuple((s - 1) // stride + 1 for s in shape[1:4])
+    res = rng.standard_normal((n, *out_sp, cout)).astype(np.float32) if kw.pop("res", False) else None
+    groups = kw.pop("gn", 0)
+    packed = f.pack_weight(_t(w, dev))
+    xt = _t(x, dev)
+    ident = torch.stack([torch.ones(n, c, device=dev), torch.zeros(n, c, device=dev)], dim=-1).contiguous()
+    call = dict(cout=cout, residual=None if res is None else _t(res, dev), gn_groups=groups, **kw)
+    y = f.implicit_gemm_conv3d(xt, packed, _t(bias, dev), **call)
+    y_packed = f.implicit_gemm_conv3d(xt, packed, _t(bias, dev), affine=ident, **call)
+    assert torch.equal(y, y_packed), f"{name}: direct reads differ from the packed copy"
+    assert torch.equal(f.implicit_gemm_conv3d(xt, packed, _t(bias, dev), **call), y)
+    if groups:
+        st, stp = f.conv_output_stats(y, groups), f.conv_output_stats(y_packed, groups)
+        assert st is not None and torch.equal(st, stp)
+    expected = rm.conv3d(x, w, stride=stride) + (bias[:, None, None, None, :] if bias.ndim == 2 else bias)
+    if res is not None:
+        expected = expected + res
+    _assert_rel(_h(y), expected, FP32_REL, f"direct {name}")
+
+
 def test_sixteen_byte_alignment_contract(ctmr, dev):
     """The pointwise and bf16 LDS GEMMs store 16 bytes at a time: the C ABI rejects a misaligned output
     (no launch), and the operator copies a misaligned residual view, giving the aligned result."""
