@@ -99,13 +99,16 @@ def test_split_policy_is_shape_only(ctmr):
     # an explicit split may be any count up to the K step count (27 taps x 32
     # blocks here); the LDS-staged GEMM takes a split only while each range keeps
     # at least 4 of its 16-channel chunks (5 here: no packed copy in the
-    # workspace), larger splits go to the streaming GEMM (packed copy)
+    # workspace), larger splits go to the streaming GEMM, which reads a plain
+    # conv straight from x (only the partial planes) and packs a GN-affine one
     d5 = L.conv_desc(2, 4, 8, 8, 512, 512, split=5)
     assert L.conv_split(d5) == 5
     assert L.workspace_bytes(d5) == 5 * 2 * 256 * 512 * 4
     d33 = L.conv_desc(2, 4, 8, 8, 512, 512, split=33)
     assert L.conv_split(d33) == 33
-    assert L.workspace_bytes(d33) > 33 * 2 * 256 * 512 * 4
+    assert L.workspace_bytes(d33) == 33 * 2 * 256 * 512 * 4
+    d33a = L.conv_desc(2, 4, 8, 8, 512, 512, split=33, flags=L.F_AFFINE)
+    assert L.workspace_bytes(d33a) > 33 * 2 * 256 * 512 * 4
     assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32, flags=L.F_STREAM)) == 27 * 32
     with pytest.raises(L.CtmrError, match="step count"):
         L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=27 * 32 + 1, flags=L.F_STREAM))
