@@ -2,13 +2,14 @@
 
 Headline workload (the north-star conv target):
 conv3d 3x3x3, stride 1, padding 1, +bias, NDHWC fp32, N=1, 64^3 voxels,
-Cin = Cout = 64; 57.98 GFLOP per step.  One step = the full operator
-(input pack + implicit-GEMM kernel) on inputs already resident in HBM.
+Cin = Cout = 64; 57.98 GFLOP per step.  One step = the full operator on
+inputs already resident in HBM: a plain fp32 conv with whole 16-channel blocks
+is one implicit-GEMM kernel reading x directly (no pack pass).
 
 ``roofline`` is the GEMM kernel, timed live with HIP events on the stream it
-is launched on around each GEMM of pack+GEMM rounds (so it reads a freshly
-packed input, as inside the operator), against the FP32 MFMA peak
-(157.3 TFLOP/s).
+is launched on around each GEMM of (pack, GEMM) rounds through the two-stage
+C ABI (the pack stage has nothing to do for this conv), against the FP32 MFMA
+peak (157.3 TFLOP/s).
 ``cpu_baseline`` is the same conv via PyTorch CPU (the op the reference's
 parity tests compare against), timed on this host's cores.
 ``secondary`` reports the other configs' GPU numbers (config 1 residual
@@ -551,10 +552,10 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (numpy default_rng(0) Gaussian input/weights, bias N(0,0.01))",
         "config": {"workload": "config0: conv3d 3x3x3 s1 p1 +bias, NDHWC fp32, N=1, 64^3, Cin=Cout=64",
-                   "flop_per_step": flops, "step": "input pack + implicit-GEMM conv"},
+                   "flop_per_step": flops, "step": "implicit-GEMM conv reading x directly"},
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": FP32_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK, 4), "traffic": None,
-                     "kernel": "conv_kernel<0,4,4,1,3,1,false> (fp32 streaming implicit GEMM)",
+                     "kernel": "conv_kernel<0,4,4,1,3,1,false,true> (fp32 streaming implicit GEMM, direct reads)",
                      "kernel_ms": round(gemm_ms, 4), "kernel_timing": "HIP events around each GEMM launch "
                      "of pack+GEMM rounds on the launch stream"},
     }
