@@ -138,7 +138,11 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  * bf16 GEMM, chosen for stride-1 bf16 convs (plain or trilinear-2x) with
  * cout % 64 == 0 and bricks at least 3/4 full (CTMR_F_STREAM not set), reads the
  * bf16 packed copy and visits 32-channel chunks ascending (outer), taps
- * ascending (inner).  One-tap GEMMs (1x1x1, im2col rows) with cout % 4 == 0 and
+ * ascending (inner).  Deep small grids split by the library's policy (split of
+ * at least 4 for the 128-wide tiles) run 64 x 64 tiles whose four waves sum
+ * four contiguous quarters of each split range, added in ascending order
+ * before the partial plane is stored; ctmr_conv3d_split reports the planes.
+ * One-tap GEMMs (1x1x1, im2col rows) with cout % 4 == 0 and
  * no per-batch bias or residual run on a persistent grid with the streaming
  * GEMM's per-output order, so their outputs equal the CTMR_F_STREAM ones bit
  * for bit.  With a split, each

@@ -539,14 +539,19 @@ __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB]
 // offset is either the real row or one past the buffer's range, which the
 // hardware reads as zeros -- the padded copy's zeros, so the products and their
 // order, and the output bits, are those of the packed form.
-template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false>
+// KWS = 4 (small K-split grids, a 64 x 64 tile per workgroup): the four waves
+// sum four contiguous quarters of the workgroup's K range for the same tile and
+// combine them through LDS in ascending order, so a launch needs a quarter of
+// the split partial planes (and their reduction traffic).
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false, int KWS = 1>
 __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
-  static_assert(WM * WN == 4, "four waves per workgroup");
+  static_assert(WM * WN * KWS == 4, "four waves per workgroup");
   static_assert(!DIRECT || (KT == 3 && !UP && DT == CTMR_F32), "direct reads: plain fp32 3x3x3 convs");
   const int lane = threadIdx.x & 63;
   // Wave index made provably uniform so every address base below lives in SGPRs.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wave_m = wave % WM, wave_n = wave / WM;
+  const int wave_mn = wave % (WM * WN), wave_k = wave / (WM * WN);
+  const int wave_m = wave_mn % WM, wave_n = wave_mn / WM;
 
   // XCD-aware tile order: hardware deals consecutive workgroups round-robin
   // to the 8 XCDs; give each XCD a contiguous range of tiles so neighbouring
@@ -629,8 +634,10 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   const int steps = p.taps * p.kb;
   // Wave-uniform (readfirstlane) so the loop counter and the load cursor
   // derived from them stay in SGPRs.
-  const int s_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)split_id * steps / p.split));
-  const int s_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(split_id + 1) * steps / p.split));
+  const int g_begin = (int)((int64_t)split_id * steps / p.split);
+  const int g_end = (int)((int64_t)(split_id + 1) * steps / p.split);
+  const int s_begin = __builtin_amdgcn_readfirstlane(g_begin + (g_end - g_begin) * wave_k / KWS);
+  const int s_end = __builtin_amdgcn_readfirstlane(g_begin + (g_end - g_begin) * (wave_k + 1) / KWS);
   const int bstep = p.np * 64;
 
   // Load cursor over the step sequence (tap-major, 64-byte channel block
@@ -718,6 +725,26 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  if constexpr (KWS > 1) {
+    // Quarters 1..3 hand their sums to wave 0, which adds them in ascending
+    // order; the result is a split partial plane (no bias, residual or
+    // statistics: the host uses KWS only with a split), stored by wave 0.
+    __shared__ f4 xk[KWS - 1][4][NSUB][64];
+    if (wave_k > 0) {
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns) xk[wave_k - 1][ms][ns][lane] = acc[ms][ns];
+    }
+    __syncthreads();
+    if (wave_k > 0) return;
+#pragma unroll
+    for (int w = 0; w < KWS - 1; ++w)
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += xk[w][ms][ns][lane];
+  }
   const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
   f4 bq[NSUB];
   load_bias<NSUB>(p, b, n0, lane, bq);
@@ -1589,6 +1616,7 @@ struct Geometry {
   bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
   bool pointwise;        // one-tap GEMM on the persistent pointwise_kernel
   bool direct;           // streaming GEMM reading the unpadded input (no pack)
+  bool kws;              // 64 x 64 tiles, the K range of each split over the four waves
   int tz, ty, tx;        // its bricks per axis
   int layout;            // WL_TAPS, WL_EXPAND (cout <= 4) or WL_IM2COL (small cin)
   int ncols;             // GEMM columns: cout, or 27 * cout for WL_EXPAND
@@ -1796,6 +1824,24 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
       g.split = (int)std::min<int64_t>(ceil_div(slots, base), std::max(1, steps / 8));
     }
   }
+  // Deep small grids (library policy, 3x3x3 or nearest-2x, a split of at least
+  // 4): 64 x 64 tiles with the four waves summing quarters of each split range
+  // need a quarter of the partial planes.  Chosen only while that leaves at
+  // least 2 planes (the waves' quarter sums go to a partial plane; the bias,
+  // residual and statistics come from the reduction) and 8 steps per wave.
+  g.kws = false;
+  if (d->split == 0 && g.layout == WL_TAPS && !g.lds16 && g.KT != 1 && g.split >= 4) {
+    const int64_t mt = ceil_div(S, 64), nt = ceil_div(g.np, 64);
+    const int64_t base1 = mt * nt * d->n * g.phases;
+    const int64_t split1 = std::min<int64_t>(ceil_div(512, base1), steps / 32);
+    if (split1 >= 2) {
+      g.kws = true;
+      g.nsub = 4; g.wm = 1; g.wn = 1;
+      g.m_tiles = (int)mt;
+      g.n_tiles = (int)nt;
+      g.split = (int)split1;
+    }
+  }
   const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases * g.split;
   if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
   // One-tap GEMMs (1x1x1, im2col) with 64-column wave tiles walk their tiles
@@ -1861,10 +1907,11 @@ typedef void (*ConvFn)(dim3, dim3, hipStream_t, const ConvArgs&);
 // not use: 60 KiB + 4 KiB of partial buffers per workgroup, two per 160 KiB CU.
 constexpr size_t kConvTwoPerCuLds = 60 * 1024;
 
-template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false>
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false, int KWS = 1>
 static void launch_conv(dim3 grid, dim3 block, hipStream_t st, const ConvArgs& a) {
-  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP, DIRECT>), grid, block,
-                     NSUB == 4 ? kConvTwoPerCuLds : 0, st, a);
+  // KWS = 4 holds 48 KiB of quarter sums in LDS: 8 KiB more keeps it at two per CU.
+  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP, DIRECT, KWS>), grid, block,
+                     KWS > 1 ? 8 * 1024 : NSUB == 4 ? kConvTwoPerCuLds : 0, st, a);
 }
 
 // Compute units of the current device (cached per device).
@@ -1908,20 +1955,31 @@ static ConvFn pick_kind(int KT, int stride, bool up) {
 
 template <int DT, int NSUB, int WM, int WN>
 static ConvFn pick_kind(const Geometry& g, int stride, bool up) {
-  if constexpr (NSUB == 4) {
-    if (g.pointwise) return launch_pointwise<DT, WM, WN>;
+  if constexpr (WM * WN == 1) {  // the K split over the four waves (g.kws)
+    if constexpr (DT == CTMR_F32) {
+      if (g.direct) return stride == 2 ? launch_conv<DT, NSUB, 1, 1, 3, 2, false, true, 4>
+                                       : launch_conv<DT, NSUB, 1, 1, 3, 1, false, true, 4>;
+    }
+    if (up) return launch_conv<DT, NSUB, 1, 1, 2, 1, true, false, 4>;
+    if (stride == 2) return launch_conv<DT, NSUB, 1, 1, 3, 2, false, false, 4>;
+    return launch_conv<DT, NSUB, 1, 1, 3, 1, false, false, 4>;
+  } else {
+    if constexpr (NSUB == 4) {
+      if (g.pointwise) return launch_pointwise<DT, WM, WN>;
+    }
+    if constexpr (DT == CTMR_F32) {
+      if (g.direct) return stride == 2 ? launch_conv<DT, NSUB, WM, WN, 3, 2, false, true>
+                                       : launch_conv<DT, NSUB, WM, WN, 3, 1, false, true>;
+    }
+    return pick_kind<DT, NSUB, WM, WN>(g.KT, stride, up);
   }
-  if constexpr (DT == CTMR_F32) {
-    if (g.direct) return stride == 2 ? launch_conv<DT, NSUB, WM, WN, 3, 2, false, true>
-                                     : launch_conv<DT, NSUB, WM, WN, 3, 1, false, true>;
-  }
-  return pick_kind<DT, NSUB, WM, WN>(g.KT, stride, up);
 }
 
 static ConvFn pick(const ctmr_conv_desc* d, const Geometry& g) {
   const bool up = d->mode == CTMR_MODE_NEAREST2X;
   const int st = d->stride;
 #define CTMR_PICK(DT)                                                            \
+  if (g.kws) return pick_kind<DT, 4, 1, 1>(g, st, up);                           \
   if (g.nsub == 1) return pick_kind<DT, 1, 4, 1>(g, st, up);                     \
   if (g.nsub == 2) return pick_kind<DT, 2, 4, 1>(g, st, up);                     \
   if (g.wn == 1) return pick_kind<DT, 4, 4, 1>(g, st, up);                       \

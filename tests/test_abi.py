@@ -84,9 +84,11 @@ def test_workspace_and_packed_sizes(ctmr):
 
 def test_split_policy_is_shape_only(ctmr):
     L = ctmr._lib
-    # UNet levels at a 64x64x32 latent, batch 2: the split fills 512 resident workgroups
-    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512)) == 32  # 16 tiles x 32
-    assert L.conv_split(L.conv_desc(2, 8, 16, 16, 256, 256)) == 8  # 64 tiles x 8
+    # UNet levels at a 64x64x32 latent, batch 2: the split fills 512 resident workgroups; the deep levels
+    # take 64 x 64 tiles whose four waves each sum a quarter of a split range, so a quarter of the planes
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512)) == 8  # 64 tiles x 8 (x 4 wave ranges)
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 512, 512, split=32)) == 32  # an explicit split stays
+    assert L.conv_split(L.conv_desc(2, 8, 16, 16, 256, 256)) == 2  # 256 tiles x 2 (x 4 wave ranges)
     assert L.conv_split(L.conv_desc(2, 16, 32, 32, 128, 128)) == 2  # 256 tiles x 2
     assert L.conv_split(L.conv_desc(2, 16, 32, 32, 64, 64)) == 4  # streaming: 128 tiles x 4
     # bf16 stride-1 convs with 64-wide column tiles use the LDS-staged bf16 GEMM: its split divides the

@@ -482,6 +482,71 @@ def test_validation_errors(ctmr, dev):
         f.implicit_gemm_conv3d(torch.zeros((1, 4, 4, 4, 32), device=dev), packed, None, cout=16)
 
 
+KWS_CASES = [
+    # (name, x shape NDHWC, cout, keyword arguments): deep small grids the library splits over K,
+    # where the four waves of a 64 x 64 tile sum quarters of each split range
+    ("8x8x4 level, 512 ch, GN affine + SiLU", (2, 4, 8, 8, 512), 512, {"fused": True}),
+    ("16x16x8 level, 256 ch, residual", (2, 8, 16, 16, 256), 256, {"res": True}),
+    ("nearest-2x from the 8x8x4 level", (2, 4, 8, 8, 512), 256, {"upsample": True}),
+    ("stride 2", (1, 8, 16, 16, 256), 512, {"stride": 2}),
+    ("bf16", (2, 4, 4, 4, 512), 512, {"bf16": True}),
+]
+
+
+@pytest.mark.parametrize(("name", "shape", "cout", "kw"), KWS_CASES, ids=[c[0] for c in KWS_CASES])
+def test_wave_k_split_matches_float64(ctmr, dev, name, shape, cout, kw):
+    """Library-policy splits of deep grids (64 x 64 tiles, four waves per K range, combined in LDS in
+    ascending order, then the partial planes): within the bar of float64, agreeing with a forced
+    one-wave-per-tile split to fp32 rounding, bit-identical run to run, and with epilogue-free group-norm
+    statistics from the reduction."""
+    print(f"wave K split {name}: {shape} -> {cout} {kw}", flush=True)
+    f, L, ops = ctmr.fast_fp32, ctmr._lib, ctmr.ops
+    kw = dict(kw)
+    fused, res_on, bf16 = kw.pop("fused", False), kw.pop("res", False), kw.pop("bf16", False)
+    rng = np.random.default_rng(sum(shape) + cout)
+    n, c = shape[0], shape[-1]
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal((n, cout)).astype(np.float32)
+    dtype = "bf16" if bf16 else "fp32"
+    wt = _t(w, dev)
+    packed = f.pack_upsample_weight(wt, dtype=dtype) if kw.get("upsample") else f.pack_weight(wt, dtype=dtype)
+    xin = x
+    affine = None
+    if fused:
+        gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+        affine = f.group_norm_affine(_t(x, dev), _t(gw, dev), _t(gb, dev), groups=32, eps=1e-6)
+        xin = rm.group_norm(x, gw, gb, 32, 1e-6, apply_silu=True)
+    if kw.get("upsample"):
+        xin = rm.upsample_nearest(xin)
+    stride = kw.get("stride", 1)
+    expected = rm.conv3d(xin, w, stride=stride) + bias[:, None, None, None, :]
+    res = rng.standard_normal(expected.shape).astype(np.float32) if res_on else None
+    if res is not None:
+        expected = expected + res
+    code = L.DT_BF16 if bf16 else L.DT_F32
+    mode = L.MODE_NEAREST2X if kw.get("upsample") else L.MODE_PLAIN
+    desc = ops.make_desc(tuple(x.shape), cout, 3, stride, mode, L.F_AFFINE if fused else 0, code, 0)
+    split = L.conv_split(desc)
+    assert split >= 2, "this shape should take the library's K split"
+    call = dict(cout=cout, affine=affine, silu=fused, residual=None if res is None else _t(res, dev), **kw)
+    y = f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), **call)
+    assert torch.equal(y, f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), **call))
+    _assert_rel(_h(y), expected, BF16_REL if bf16 else FP32_REL, f"wave K split {name}")
+    forced = f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), split=4 * split, **call)
+    err = rm.max_rel_error(_h(y), _h(forced))
+    print(f"{name}: policy split {split} (x4 wave ranges) vs forced split {4 * split}: {err:.3e}", flush=True)
+    assert err <= FP32_REL
+    y_gn = f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), gn_groups=32, **call)
+    assert torch.equal(y_gn, y)
+    stats = f.conv_output_stats(y_gn, 32)
+    assert stats is not None
+    yh = _h(y).reshape(n, -1, 32, cout // 32)
+    totals = stats.cpu().numpy().sum(axis=1)
+    assert rm.max_rel_error(totals[..., 0], yh.sum(axis=(1, 3))) <= 1e-12
+
+
 DIRECT_CASES = [
     # (name, x shape NDHWC, cout, keyword arguments)
     ("ragged, batch 2", (2, 9, 13, 11, 32), 48, {}),
