@@ -3,8 +3,8 @@
 Headline workload (the north-star conv target):
 conv3d 3x3x3, stride 1, padding 1, +bias, NDHWC fp32, N=1, 64^3 voxels,
 Cin = Cout = 64; 57.98 GFLOP per step.  One step = the full operator on
-inputs already resident in HBM: a plain fp32 conv with whole 16-channel blocks
-is one implicit-GEMM kernel reading x directly (no pack pass).
+inputs already resident in HBM: one implicit-GEMM kernel (the LDS-staged GEMM,
+which stages halo bricks of x itself; no pack pass).
 
 ``roofline`` is the GEMM kernel, timed live with HIP events on the stream it
 is launched on around each GEMM of (pack, GEMM) rounds through the two-stage
@@ -555,7 +555,7 @@ def main() -> int:
                    "flop_per_step": flops, "step": "implicit-GEMM conv reading x directly"},
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": FP32_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK, 4), "traffic": None,
-                     "kernel": "conv_kernel<0,4,4,1,3,1,false,true> (fp32 streaming implicit GEMM, direct reads)",
+                     "kernel": "conv_lds_kernel (fp32 LDS-staged implicit GEMM, reads x directly)",
                      "kernel_ms": round(gemm_ms, 4), "kernel_timing": "HIP events around each GEMM launch "
                      "of pack+GEMM rounds on the launch stream"},
     }

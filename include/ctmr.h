@@ -131,7 +131,7 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  * Accumulation order is fixed for a given desc.  The register-streaming GEMM
  * visits taps kd*9+kh*3+kw ascending (outer) and input channels in ascending
  * 16-wide (fp32) / 32-wide (bf16) blocks (inner).  The LDS-staged GEMM, chosen
- * by shape for large stride-1 fp32 volumes (cin >= 128 and a multiple of 16,
+ * by shape for large stride-1 fp32 volumes (cin >= 64 and a multiple of 16,
  * cout % 64 == 0, no resampling, CTMR_F_STREAM not set), stages 16-channel chunks of the input
  * with their halo (affine + SiLU and zero padding applied while staging) and
  * visits chunks ascending (outer), taps ascending (inner).  The LDS-staged

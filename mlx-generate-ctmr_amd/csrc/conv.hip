@@ -1717,14 +1717,15 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   if (S > (1ll << 30) || s_out * d->cout > (1ll << 40))
     return fail(CTMR_E_UNSUPPORTED, "volume too large for 32-bit voxel indexing");
   // LDS-staged GEMM: stride-1 fp32 volumes whose 4x8x8 bricks are at least
-  // 3/4 full, with at least 128 input channels (8 staged chunks; below that
-  // the per-chunk staging and barriers cost more than the pack pass they
-  // replace, measured on MI355X), 64-wide column tiles, at least 4 chunks per
-  // split, and 6 staged planes within 32-bit buffer offsets.
+  // 3/4 full, with at least 64 input channels (4 staged chunks; measured on
+  // MI355X: 64-channel UNet-level convs 3-6 % faster than the streaming GEMM
+  // with or without its pack pass; below that the per-chunk staging and
+  // barriers dominate), 64-wide column tiles, at least 4 chunks per split, and
+  // 6 staged planes within 32-bit buffer offsets.
   g.lds = false;
   g.lds16 = false;
   if (g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 && d->stride == 1 &&
-      d->mode == CTMR_MODE_PLAIN && d->cin % 16 == 0 && d->cin >= 128 && d->cout % 64 == 0 &&
+      d->mode == CTMR_MODE_PLAIN && d->cin % 16 == 0 && d->cin >= 64 && d->cout % 64 == 0 &&
       !(d->flags & CTMR_F_STREAM)) {
     g.tz = (int)ceil_div(d->d, kBD);
     g.ty = (int)ceil_div(d->h, kBH);

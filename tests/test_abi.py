@@ -44,14 +44,19 @@ def test_output_dims(ctmr, dims, kw, expected):
 def test_workspace_and_packed_sizes(ctmr):
     L = ctmr._lib
     d = L.conv_desc(1, 64, 64, 64, 64, 64)
-    # streaming GEMM (cin < 128) of a plain conv with whole 16-channel blocks reads x directly: no
-    # workspace; with the GN affine it packs a padded copy, 66^3 rows x 64 fp32 channels, 256-byte aligned
+    # the LDS-staged GEMM (cin >= 64) reads x directly: no workspace, the (n, cin, 2) affine table with a
+    # GN affine; the streaming GEMM (CTMR_F_STREAM, or cin < 64) reads a plain conv with whole 16-channel
+    # blocks directly too and packs a padded copy (66^3 rows x 64 fp32 channels, 256-byte aligned) for
+    # a GN-affine one
     assert L.workspace_bytes(d) == 0
-    assert L.workspace_bytes(L.conv_desc(1, 64, 64, 64, 64, 64, flags=L.F_AFFINE)) == \
+    assert L.workspace_bytes(L.conv_desc(1, 64, 64, 64, 64, 64, flags=L.F_AFFINE)) == 512
+    assert L.workspace_bytes(L.conv_desc(1, 64, 64, 64, 64, 64, flags=L.F_AFFINE | L.F_STREAM)) == \
         ((66**3 * 64 * 4 + 255) // 256) * 256
+    assert L.workspace_bytes(L.conv_desc(1, 64, 64, 64, 32, 64, flags=L.F_AFFINE)) == \
+        ((66**3 * 32 * 4 + 255) // 256) * 256
     assert L.packed_weight_elems(d) == 27 * 64 * 64
     assert L.conv_split(d) == 1
-    # the LDS-staged GEMM (cin >= 128) reads x directly: no workspace without affine or
+    # the LDS-staged GEMM (cin >= 64) reads x directly: no workspace without affine or
     # split, just the (n, cin, 2) affine table with one; same packed weight
     d128 = L.conv_desc(1, 64, 64, 64, 128, 128)
     assert L.workspace_bytes(d128) == 0

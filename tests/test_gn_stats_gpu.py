@@ -31,10 +31,10 @@ def _t(a, dev):
 
 CASES = [
     # (name, x shape NDHWC, cout, groups, keyword arguments)
-    ("streaming", (2, 8, 16, 16, 64), 64, 32, {"split": 1}),
-    ("streaming ragged", (1, 7, 9, 13, 64), 64, 8, {"split": 1}),
-    ("streaming 2x2 waves", (1, 16, 16, 32, 64), 256, 32, {"split": 1}),
-    ("streaming 128-wide groups", (1, 16, 16, 32, 64), 256, 2, {"split": 1}),
+    ("streaming", (2, 8, 16, 16, 64), 64, 32, {"split": 1, "stream_gemm": True}),
+    ("streaming ragged", (1, 7, 9, 13, 48), 64, 8, {"split": 1}),
+    ("streaming 2x2 waves", (1, 16, 16, 32, 64), 256, 32, {"split": 1, "stream_gemm": True}),
+    ("streaming 128-wide groups", (1, 16, 16, 32, 32), 256, 2, {"split": 1}),
     ("lds fused", (2, 8, 16, 16, 128), 128, 32, {"split": 1, "fused": True}),
     ("lds ragged", (1, 7, 16, 15, 128), 64, 16, {"split": 1}),
     ("lds split", (1, 4, 8, 8, 512), 512, 32, {"split": 8}),
