@@ -57,21 +57,24 @@ struct PackArgs {
   int c, cp;            // source / packed channels
   int id, ih, iw;       // source grid (trilinear)
   int affine_on, silu_on, trilinear, bf16;
+  int n;                // batch items
 };
 
+// Grid: blockIdx.y walks the (batch item, padded plane) pairs, blockIdx.x
+// and the thread the plane's (row, column, 4-channel group) items, so the
+// index arithmetic is 32-bit (the host checks a plane holds < 2^31 items).
 __global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total4;
-       idx += (int64_t)gridDim.x * blockDim.x) {
   const int c4n = a.cp >> 2;
-  const int c4 = (int)(idx % c4n);
-  int64_t pos = idx / c4n;
   const int PW = a.gw + 2 * a.halo, PH = a.gh + 2 * a.halo, PD = a.gd + 2 * a.halo;
-  const int px = (int)(pos % PW);
-  pos /= PW;
-  const int py = (int)(pos % PH);
-  pos /= PH;
-  const int pz = (int)(pos % PD);
-  const int b = (int)(pos / PD);
+  const unsigned plane4 = (unsigned)PH * (unsigned)PW * (unsigned)c4n;
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= plane4) return;
+  const int c4 = (int)(i % (unsigned)c4n);
+  const unsigned r = i / (unsigned)c4n;
+  const int px = (int)(r % (unsigned)PW), py = (int)(r / (unsigned)PW);
+  for (int bz = blockIdx.y; bz < a.n * PD; bz += gridDim.y) {
+  const int b = bz / PD, pz = bz - b * PD;
+  const int64_t idx = (int64_t)bz * plane4 + i;
   const int z = pz - a.halo, y = py - a.halo, x = px - a.halo;
   const int ch = c4 * 4;
   f4 v = {0.f, 0.f, 0.f, 0.f};
@@ -2135,8 +2138,12 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
   pa.trilinear = desc->mode == CTMR_MODE_TRILINEAR2X;
   pa.bf16 = desc->dtype == CTMR_BF16;
   pa.total4 = (int64_t)desc->n * g.rows_per_batch * (g.cp / 4);
-  hipLaunchKernelGGL(pack_input_kernel, dim3(elementwise_blocks(pa.total4)), dim3(256), 0,
-                     (hipStream_t)stream, pa);
+  pa.n = desc->n;
+  const int64_t plane4 = (int64_t)(g.th + 2 * g.halo) * (g.tw + 2 * g.halo) * (g.cp / 4);
+  const int64_t planes = (int64_t)desc->n * (g.td + 2 * g.halo);
+  if (plane4 >= (1ll << 31)) return fail(CTMR_E_UNSUPPORTED, "padded plane too large for the pack");
+  hipLaunchKernelGGL(pack_input_kernel, dim3((unsigned)ceil_div(plane4, 256), (unsigned)std::min<int64_t>(planes, 65535)),
+                     dim3(256), 0, (hipStream_t)stream, pa);
   return check_launch("pack_input");
 }
 
