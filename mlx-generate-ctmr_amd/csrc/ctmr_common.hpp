@@ -15,7 +15,6 @@ namespace ctmr {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef unsigned short us8 __attribute__((ext_vector_type(8)));
 
 // Message for the last failing call on this thread (ctmr_last_error).
 void set_error(const char* fmt, ...);
@@ -54,7 +53,6 @@ __device__ __forceinline__ unsigned short f32_to_bf16_bits(float v) {
   return (unsigned short)(u >> 16);
 }
 
-// SiLU through ROCm's device expf (ocml), y / (1 + exp(-y)).
 // SiLU y * sigmoid(y) = y / (1 + e^-y), with e^-y = 2^(-y log2 e) on the
 // hardware exponential (v_exp_f32) and the quotient as y times the hardware
 // reciprocal (v_rcp_f32): within 1e-6 relative of the exact value over the
