@@ -6,7 +6,7 @@
 // sum, exp2 of log2(e)-scaled scores (the scale is folded into Q once).
 //
 // MI355X layout.  One wave owns QT x 16 queries and walks all keys in blocks of
-// 64.  Both products run on v_mfma_f32_16x16x4_f32 in the transposed form:
+// 32.  Both products run on v_mfma_f32_16x16x4_f32 in the transposed form:
 //   S^T = K Q^T   (rows = keys, columns = queries; k runs over the 32 head dims)
 //   O^T += V^T P^T (rows = head dims, columns = queries; k runs over keys)
 // With the MFMA result layout (lane l, register r -> row 4*(l/16)+r, column
@@ -19,16 +19,21 @@
 // (step s, lane group g -> dim 8g+s) so each lane loads 8 contiguous floats.
 // Everything accumulates in FP32; keys are visited in ascending blocks, so the
 // result does not depend on the launch shape or on other work on the device.
+// Within a wave the loop is software-pipelined: the next block's K Q^T
+// products are issued between this block's softmax instructions, so the
+// exp2 / max / rescale work runs while the matrix core is busy.
 #include "ctmr_common.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace ctmr {
 namespace {
 
 constexpr int kHeadDim = 32;
 constexpr int kWaves = 4;     // waves per workgroup (independent; no LDS, no barriers)
-constexpr int kKeyTiles = 4;  // 16-key tiles per key block
+constexpr int kKeyTiles = 2;  // 16-key tiles per key block
+constexpr int kBlock = 16 * kKeyTiles;
 
 struct AttnArgs {
   const float* q;
@@ -45,20 +50,23 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
 }
 
 // First key of the second part of a two-part key split: half the keys,
-// rounded up to a whole 64-key block (so only the second part is ragged).
+// rounded up to a multiple of 64 keys (whole key blocks, so only the second
+// part is ragged).
 __device__ __forceinline__ int attention_key_split_point(int lk) {
   return min(lk, (((lk + 1) / 2 + 63) / 64) * 64);
 }
 
-// Keys and values of one 64-key block in MFMA operand order.
-struct KeyBlock {
-  f4 k[kKeyTiles][2];      // K row (tile*16 + l%16), dims 8g .. 8g+7
+// Keys and values of one key block in MFMA operand order.
+struct KeyTiles {
+  f4 k[kKeyTiles][2];  // K row (tile*16 + l%16), dims 8g .. 8g+7
+};
+struct ValueTiles {
   float v[kKeyTiles][4][2];  // V row (tile*16 + 4g + r), dims (l%16) and (16 + l%16)
 };
 
 // KS = 2 splits the keys of each query group between two waves of the
-// workgroup (keys [0, split) and [split, lk), split a multiple of the 64-key
-// block): small grids then keep two waves per SIMD.  The second wave hands its
+// workgroup (keys [0, split) and [split, lk), split a multiple of 64 keys):
+// small grids then keep two waves per SIMD.  The second wave hands its
 // running max, sum and output to the first through LDS, which combines them
 // in that fixed order.
 template <int QT, int KS>
@@ -100,24 +108,27 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
   }
 
   // Rows past the end are clamped to the last key (in bounds) and masked below.
-  auto load = [&](KeyBlock& kb, int k0) {
+  auto load_k = [&](KeyTiles& kt, int k0) {
 #pragma unroll
     for (int u = 0; u < kKeyTiles; ++u) {
       const int row = min(k0 + u * 16 + col, a.lk - 1);
       const f4* p = reinterpret_cast<const f4*>(K + (int64_t)row * a.ldk + 8 * g);
-      kb.k[u][0] = p[0];
-      kb.k[u][1] = p[1];
+      kt.k[u][0] = p[0];
+      kt.k[u][1] = p[1];
+    }
+  };
+  auto load_v = [&](ValueTiles& vt, int k0) {
+#pragma unroll
+    for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float* vr = V + (int64_t)min(k0 + u * 16 + 4 * g + r, a.lk - 1) * a.ldv;
-        kb.v[u][r][0] = vr[col];
-        kb.v[u][r][1] = vr[16 + col];
+        vt.v[u][r][0] = vr[col];
+        vt.v[u][r][1] = vr[16 + col];
       }
-    }
   };
-
-  auto compute = [&](const KeyBlock& kb, int k0) {
-    f4 s[kKeyTiles][QT];
+  // S^T tiles of one key block.
+  auto qk = [&](const KeyTiles& kt, f4 (&s)[kKeyTiles][QT]) {
 #pragma unroll
     for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
@@ -126,10 +137,14 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc = mfma4(kb.k[u][j][e], qa[t][j][e], acc);
+          for (int e = 0; e < 4; ++e) acc = mfma4(kt.k[u][j][e], qa[t][j][e], acc);
         s[u][t] = acc;
       }
-    if (k0 + 16 * kKeyTiles > k_end) {  // wave-uniform: only the last block is ragged
+  };
+  // Online softmax of one block: scores -> P^T in place, running max / sum,
+  // output rescale.  RAGGED masks keys at or past k_end (the last block only).
+  auto softmax = [&](f4 (&s)[kKeyTiles][QT], int k0, auto ragged) {
+    if constexpr (decltype(ragged)::value) {
 #pragma unroll
       for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
@@ -148,16 +163,18 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
       bm = fmaxf(bm, __shfl_xor(bm, 16));
       bm = fmaxf(bm, __shfl_xor(bm, 32));
       // Every block holds at least one real key, so mn is finite and the first
-      // block's alpha is exp2(-inf) = 0.
+      // block's alpha is 2^-inf = 0.  Arguments are <= 0: the hardware exp2
+      // (v_exp_f32) differs from exp2f only below 2^-126, far under the
+      // resolution of the running sum (>= 1).
       const float mn = fmaxf(m[t], bm);
-      const float alpha = exp2f(m[t] - mn);
+      const float alpha = __builtin_amdgcn_exp2f(m[t] - mn);
       m[t] = mn;
       float ps = 0.f;
 #pragma unroll
       for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = exp2f(s[u][t][r] - mn);
+          const float p = __builtin_amdgcn_exp2f(s[u][t][r] - mn);
           s[u][t][r] = p;
           ps += p;
         }
@@ -165,32 +182,69 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
       o[t][0] *= alpha;
       o[t][1] *= alpha;
     }
+  };
+  auto pv = [&](const ValueTiles& vt, const f4 (&s)[kKeyTiles][QT]) {
 #pragma unroll
     for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
-          o[t][0] = mfma4(kb.v[u][r][0], s[u][t][r], o[t][0]);
-          o[t][1] = mfma4(kb.v[u][r][1], s[u][t][r], o[t][1]);
+          o[t][0] = mfma4(vt.v[u][r][0], s[u][t][r], o[t][0]);
+          o[t][1] = mfma4(vt.v[u][r][1], s[u][t][r], o[t][1]);
         }
   };
+  // One pipeline step for a full block k0 that has a successor, scores in
+  // `sc`: the loads of the next block's V and of the K after next (rows past
+  // the end are clamped: in bounds, unused) go out first; then the next
+  // block's K Q^T products (into `sn`, from `kn`) are interleaved with this
+  // block's softmax -- one MFMA, then VALU work while the matrix core runs --
+  // and this block's P V products follow.  Branch-free, so the scheduler can
+  // interleave.
+  auto step = [&](f4 (&sc)[kKeyTiles][QT], f4 (&sn)[kKeyTiles][QT], const ValueTiles& vc, ValueTiles& vn,
+                  const KeyTiles& kn, KeyTiles& kf, int k0) {
+    load_v(vn, k0 + kBlock);
+    load_k(kf, k0 + 2 * kBlock);
+    __builtin_amdgcn_sched_barrier(0);
+    qk(kn, sn);
+    softmax(sc, k0, std::false_type{});
+#pragma unroll
+    for (int i = 0; i < kKeyTiles * QT * 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    pv(vc, sc);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // The last block (possibly ragged): softmax, then its products.
+  auto last = [&](f4 (&sc)[kKeyTiles][QT], const ValueTiles& vc, int k0) {
+    softmax(sc, k0, std::true_type{});
+    pv(vc, sc);
+  };
 
-  // Register double buffer: the next block's loads are in flight while the
-  // current block's products run.
-  constexpr int kBlock = 16 * kKeyTiles;
-  KeyBlock b0, b1;
-  if (k_begin < k_end) load(b0, k_begin);
-  for (int k0 = k_begin; k0 < k_end; k0 += 2 * kBlock) {
-    if (k0 + kBlock < k_end) load(b1, k0 + kBlock);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(b0, k0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (k0 + kBlock >= k_end) break;
-    if (k0 + 2 * kBlock < k_end) load(b0, k0 + 2 * kBlock);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(b1, k0 + kBlock);
-    __builtin_amdgcn_sched_barrier(0);
+  // Registers: K of the next two blocks, V of this and the next block, the
+  // scores of this and the next block (names alternate between steps).
+  KeyTiles ka, kb;
+  ValueTiles va, vb;
+  f4 sa[kKeyTiles][QT], sb[kKeyTiles][QT];
+  const int nb = k_begin < k_end ? (k_end - k_begin + kBlock - 1) / kBlock : 0;
+  if (nb > 0) {
+    load_k(ka, k_begin);
+    load_v(va, k_begin);
+    load_k(kb, k_begin + kBlock);
+    qk(ka, sa);
+    int i = 0;
+    for (; i + 2 < nb; i += 2) {
+      step(sa, sb, va, vb, kb, ka, k_begin + i * kBlock);
+      step(sb, sa, vb, va, ka, kb, k_begin + (i + 1) * kBlock);
+    }
+    if (nb - i == 2) {
+      step(sa, sb, va, vb, kb, ka, k_begin + i * kBlock);
+      last(sb, vb, k_begin + (i + 1) * kBlock);
+    } else {
+      last(sa, va, k_begin + i * kBlock);
+    }
   }
 
   if constexpr (KS == 2) {
@@ -263,8 +317,8 @@ int attention_query_tiles(int n, int lq, int heads) {
 }
 
 // Key parts per query group, from the shape only (never from query_tiles, so
-// both tilings give the same bits): two when there are at least two 64-key
-// blocks and fewer than two waves per SIMD would run otherwise.
+// both tilings give the same bits): two when there are at least 128 keys and
+// fewer than two waves per SIMD would run otherwise.
 int attention_key_parts(int n, int lq, int lk, int heads) {
   const int64_t waves2 = ceil_div(lq, 32) * (int64_t)n * heads;
   return (lk >= 128 && waves2 < 2048) ? 2 : 1;
