@@ -49,6 +49,17 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Maximum over lanes l, l^16, l^32, l^48 (the four lane groups holding one
+// query's scores): v_permlane16_swap / v_permlane32_swap of a value with
+// itself yield the pair {x[l], x[l^16]} / {x[l], x[l^32]} (VALU, no LDS round
+// trip as with ds_bpermute).
+__device__ __forceinline__ float lane_group_max(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 // First key of the second part of a two-part key split: half the keys,
 // rounded up to a multiple of 64 keys (whole key blocks, so only the second
 // part is ragged).
@@ -160,8 +171,7 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
       for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
         for (int r = 0; r < 4; ++r) bm = fmaxf(bm, s[u][t][r]);
-      bm = fmaxf(bm, __shfl_xor(bm, 16));
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      bm = lane_group_max(bm);
       // Every block holds at least one real key, so mn is finite and the first
       // block's alpha is 2^-inf = 0.  Arguments are <= 0: the hardware exp2
       // (v_exp_f32) differs from exp2f only below 2^-126, far under the
