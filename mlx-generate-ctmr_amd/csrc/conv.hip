@@ -60,23 +60,11 @@ struct PackArgs {
   int n;                // batch items
 };
 
-// Grid: blockIdx.y walks the (batch item, padded plane) pairs, blockIdx.x
-// and the thread the plane's (row, column, 4-channel group) items, so the
-// index arithmetic is 32-bit (the host checks a plane holds < 2^31 items).
-__global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
-  const int c4n = a.cp >> 2;
-  const int PW = a.gw + 2 * a.halo, PH = a.gh + 2 * a.halo, PD = a.gd + 2 * a.halo;
-  const unsigned plane4 = (unsigned)PH * (unsigned)PW * (unsigned)c4n;
-  const unsigned i = blockIdx.x * 256u + threadIdx.x;
-  if (i >= plane4) return;
-  const int c4 = (int)(i % (unsigned)c4n);
-  const unsigned r = i / (unsigned)c4n;
-  const int px = (int)(r % (unsigned)PW), py = (int)(r / (unsigned)PW);
-  for (int bz = blockIdx.y; bz < a.n * PD; bz += gridDim.y) {
-  const int b = bz / PD, pz = bz - b * PD;
-  const int64_t idx = (int64_t)bz * plane4 + i;
+// The packed value of channels ch..ch+3 at padded voxel (pz, py, px) of batch
+// item b: zero in the halo and past the source channels, else the source (or
+// its trilinear-2x sample) with the optional GN affine and SiLU.
+__device__ __forceinline__ f4 pack_value4(const PackArgs& a, int b, int pz, int py, int px, int ch) {
   const int z = pz - a.halo, y = py - a.halo, x = px - a.halo;
-  const int ch = c4 * 4;
   f4 v = {0.f, 0.f, 0.f, 0.f};
   if (z >= 0 && z < a.gd && y >= 0 && y < a.gh && x >= 0 && x < a.gw && ch < a.c) {
     if ((a.c & 3) == 0) {
@@ -113,16 +101,38 @@ __global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
       }
     }
   }
-  if (a.bf16) {
-    unsigned short h0 = f32_to_bf16_bits(v[0]), h1 = f32_to_bf16_bits(v[1]);
-    unsigned short h2 = f32_to_bf16_bits(v[2]), h3 = f32_to_bf16_bits(v[3]);
-    uint2 packed;
-    packed.x = (unsigned)h0 | ((unsigned)h1 << 16);
-    packed.y = (unsigned)h2 | ((unsigned)h3 << 16);
-    reinterpret_cast<uint2*>(a.out)[idx] = packed;
-  } else {
-    reinterpret_cast<f4*>(a.out)[idx] = v;
-  }
+  return v;
+}
+
+// Grid: blockIdx.y walks the (batch item, padded plane) pairs, blockIdx.x
+// and the thread the plane's (row, column, channel group) items, so the index
+// arithmetic is 32-bit (the host checks a plane holds < 2^31 items).  A
+// thread packs 4 channels (fp32: one 16-byte store) or 8 (bf16: one 16-byte
+// store of 8 rounded values; the bf16 copy's cp is a multiple of 32).
+__global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
+  const int G = a.bf16 ? 2 : 1;
+  const int cgn = (a.cp >> 2) / G;
+  const int PW = a.gw + 2 * a.halo, PH = a.gh + 2 * a.halo, PD = a.gd + 2 * a.halo;
+  const unsigned plane = (unsigned)PH * (unsigned)PW * (unsigned)cgn;
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= plane) return;
+  const int cg = (int)(i % (unsigned)cgn);
+  const unsigned r = i / (unsigned)cgn;
+  const int px = (int)(r % (unsigned)PW), py = (int)(r / (unsigned)PW);
+  for (int bz = blockIdx.y; bz < a.n * PD; bz += gridDim.y) {
+    const int b = bz / PD, pz = bz - b * PD;
+    const int64_t idx = (int64_t)bz * plane + i;
+    if (a.bf16) {
+      const f4 v0 = pack_value4(a, b, pz, py, px, cg * 8), v1 = pack_value4(a, b, pz, py, px, cg * 8 + 4);
+      u4 packed;
+      packed.x = (unsigned)f32_to_bf16_bits(v0[0]) | ((unsigned)f32_to_bf16_bits(v0[1]) << 16);
+      packed.y = (unsigned)f32_to_bf16_bits(v0[2]) | ((unsigned)f32_to_bf16_bits(v0[3]) << 16);
+      packed.z = (unsigned)f32_to_bf16_bits(v1[0]) | ((unsigned)f32_to_bf16_bits(v1[1]) << 16);
+      packed.w = (unsigned)f32_to_bf16_bits(v1[2]) | ((unsigned)f32_to_bf16_bits(v1[3]) << 16);
+      reinterpret_cast<u4*>(a.out)[idx] = packed;
+    } else {
+      reinterpret_cast<f4*>(a.out)[idx] = pack_value4(a, b, pz, py, px, cg * 4);
+    }
   }
 }
 
@@ -2139,10 +2149,11 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
   pa.bf16 = desc->dtype == CTMR_BF16;
   pa.total4 = (int64_t)desc->n * g.rows_per_batch * (g.cp / 4);
   pa.n = desc->n;
-  const int64_t plane4 = (int64_t)(g.th + 2 * g.halo) * (g.tw + 2 * g.halo) * (g.cp / 4);
+  const int64_t plane_items = (int64_t)(g.th + 2 * g.halo) * (g.tw + 2 * g.halo) * (g.cp / (pa.bf16 ? 8 : 4));
   const int64_t planes = (int64_t)desc->n * (g.td + 2 * g.halo);
-  if (plane4 >= (1ll << 31)) return fail(CTMR_E_UNSUPPORTED, "padded plane too large for the pack");
-  hipLaunchKernelGGL(pack_input_kernel, dim3((unsigned)ceil_div(plane4, 256), (unsigned)std::min<int64_t>(planes, 65535)),
+  if (plane_items >= (1ll << 31)) return fail(CTMR_E_UNSUPPORTED, "padded plane too large for the pack");
+  hipLaunchKernelGGL(pack_input_kernel,
+                     dim3((unsigned)ceil_div(plane_items, 256), (unsigned)std::min<int64_t>(planes, 65535)),
                      dim3(256), 0, (hipStream_t)stream, pa);
   return check_launch("pack_input");
 }
