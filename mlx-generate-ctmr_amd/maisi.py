@@ -148,17 +148,47 @@ def _time_projections(weights: Mapping[str, Tensor]) -> tuple[Tensor, Tensor, di
     return weight, bias, spans
 
 
+_block_index: dict[tuple, tuple[Tensor, dict[str, tuple[int, int]]]] = {}
+_block_index_lock = threading.Lock()
+
+
+def _block_major_index(spans: Mapping[str, tuple[int, int]], n: int, total: int, device) -> tuple:
+    """Gather index that reorders an (n, total) row-major matrix of per-block columns
+    [lo, hi) into block-major order (block, batch item, column), and each block's
+    (offset, width) in it; cached per (spans, n, total, device)."""
+    key = (tuple(sorted(spans.items())), n, total, str(device))
+    with _block_index_lock:
+        hit = _block_index.get(key)
+    if hit is not None:
+        return hit
+    parts, offsets, off = [], {}, 0
+    for prefix, (lo, hi) in sorted(spans.items(), key=lambda kv: kv[1][0]):
+        rows = torch.arange(n, dtype=torch.int64).unsqueeze(1) * total
+        parts.append((rows + torch.arange(lo, hi, dtype=torch.int64)).reshape(-1))
+        offsets[prefix] = (off, hi - lo)
+        off += n * (hi - lo)
+    hit = (torch.cat(parts).to(device), offsets)
+    with _block_index_lock:
+        _block_index[key] = hit
+    return hit
+
+
 def _blocks(weights: Mapping[str, Tensor], emb: Tensor, groups: int, eps: float, include_fc: bool):
     """Residual-block and attention callables bound to one embedding and weight dict.  The
     per-block conv1 biases (``conv1.bias + time_emb_proj(silu(emb))``) come from one GEMM."""
     proj_w, proj_b, spans = _time_projections(weights)
-    conv1_bias = F.linear(F.silu(emb), proj_w, proj_b)
+    conv1_bias = F.linear(F.silu(emb), proj_w, proj_b)  # (n, all blocks' channels)
+    # One gather into block-major order, so each block's (n, cout) bias is a
+    # contiguous view (instead of a copy kernel per block).
+    n = int(conv1_bias.shape[0])
+    index, offsets = _block_major_index(spans, n, int(conv1_bias.shape[1]), conv1_bias.device)
+    blocked = conv1_bias.reshape(-1).index_select(0, index)
 
     def resnet(h: Tensor, prefix: str, *, normed_next: bool = True, **kw) -> Tensor:
         """``normed_next``: a group norm reads the output next (its statistics come from conv2)."""
-        lo, hi = spans[prefix]
+        off, width = offsets[prefix]
         return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps,
-                                 conv1_bias=conv1_bias[:, lo:hi].contiguous(),
+                                 conv1_bias=blocked[off:off + n * width].view(n, width),
                                  out_gn_groups=groups if normed_next else 0, **kw)
 
     def attention(h: Tensor, prefix: str, n_heads: int) -> Tensor:
