@@ -73,6 +73,29 @@ def test_flash_attention_matches_float64(ctmr, dev, seed, n, lq, lk, heads, q_ga
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
+def _sweep_cases(count, seed):
+    """Random shapes around the kernel's block boundaries: key counts that leave the last 32-key block
+    full or ragged, an odd or even number of blocks per key part, one or two key parts (at least 128
+    keys and a small grid), both query tilings, cross lengths and large score ranges."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        lk = int(rng.choice([int(rng.integers(1, 97)), 32 * int(rng.integers(1, 12)) + int(rng.integers(-1, 2)),
+                             int(rng.integers(128, 700))]))
+        lk = max(lk, 1)
+        lq = int(rng.integers(1, 300))
+        cases.append((1000 + i, int(rng.integers(1, 3)), lq, lk, int(rng.integers(1, 6)),
+                      float(rng.choice([0.5, 1.0, 4.0]))))
+    return cases
+
+
+@pytest.mark.parametrize(("seed", "n", "lq", "lk", "heads", "q_gain"), _sweep_cases(40, 11),
+                         ids=[f"sweep{i:02d}" for i in range(40)])
+def test_flash_attention_random_shapes(ctmr, dev, seed, n, lq, lk, heads, q_gain):
+    """Seeded sweep: every shape within the FP32 bar of float64 and both query tilings bit-identical."""
+    test_flash_attention_matches_float64(ctmr, dev, seed, n, lq, lk, heads, q_gain)
+
+
 def test_flash_attention_on_fused_projection_views(ctmr, dev):
     """q/k/v as column slices of one (B, L, 3C) projection (row stride 3C), as the UNet calls it."""
     rng = np.random.default_rng(9)
