@@ -1639,6 +1639,21 @@ struct Geometry {
   int64_t pack_bytes, part_bytes, z_bytes;
 };
 
+// K-range (chunk) split of the LDS-staged GEMMs, from the shape only: small
+// grids are split until they fill a round of 512 resident workgroups (two per
+// CU on 256 CUs); grids of under 4 rounds whose last round would run at most
+// 90 % as full as with two ranges take two (e.g. 1280 workgroups: 2.5 rounds
+// -> 5 whole rounds).  `chunks` caps it.
+static int64_t lds_policy_split(int64_t base, int64_t chunks) {
+  if (base < 512) return std::min<int64_t>(ceil_div(512, base), chunks);
+  if (base < 2048 && chunks >= 8) {
+    const double e1 = (double)base / (512.0 * ceil_div(base, 512));
+    const double e2 = (double)(2 * base) / (512.0 * ceil_div(2 * base, 512));
+    if (e2 >= e1 + 0.1) return 2;
+  }
+  return 1;
+}
+
 static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   if (!d) return fail(CTMR_E_INVALID, "null descriptor");
   if (d->n <= 0 || d->d <= 0 || d->h <= 0 || d->w <= 0 || d->cin <= 0 || d->cout <= 0)
@@ -1752,7 +1767,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     // with fewer, the exposed first-chunk staging outweighs the saved pack
     // (measured on the UNet's 16x16x8 level: streaming 68 % vs LDS 63 %).
     const int64_t base = (int64_t)g.tz * g.ty * g.tx * (d->cout / 64) * d->n;
-    const int64_t policy_split = base < 512 ? std::min<int64_t>(ceil_div(512, base), d->cin / 16) : 1;
+    const int64_t policy_split = lds_policy_split(base, d->cin / 16);
     const int64_t split = d->split > 0 ? d->split : policy_split;
     if (4 * S >= 3 * slots && planes < (1ll << 31) && (d->cin / 16) / split >= 4) g.lds = true;
   }
@@ -1769,7 +1784,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
       g.split = d->split;
     } else {
       const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n;
-      g.split = base < 512 ? (int)std::min<int64_t>(ceil_div(512, base), chunks) : 1;
+      g.split = (int)lds_policy_split(base, chunks);
     }
     g.pack_bytes = (d->flags & CTMR_F_AFFINE) ? round_up((int64_t)d->n * d->cin * 2 * 4, 256) : 0;
     g.part_bytes = g.split > 1 ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;

@@ -103,6 +103,13 @@ def test_split_policy_is_shape_only(ctmr):
     # large grids never split
     assert L.conv_split(L.conv_desc(1, 128, 128, 128, 128, 128)) == 1
     assert L.conv_split(L.conv_desc(1, 64, 64, 64, 64, 64)) == 1
+    # an LDS grid of under 4 rounds whose last round is far from full takes two K ranges: the decoder's
+    # 256-channel level, 320 bricks x 4 column tiles = 1280 workgroups (2.5 rounds -> 5 whole rounds);
+    # whole rounds (1024) and grids of 4 rounds or more do not
+    assert L.conv_split(L.conv_desc(1, 20, 64, 64, 256, 256)) == 2
+    assert L.workspace_bytes(L.conv_desc(1, 20, 64, 64, 256, 256)) == 2 * 20 * 64 * 64 * 256 * 4
+    assert L.conv_split(L.conv_desc(2, 64, 64, 32, 64, 64)) == 1  # 1024
+    assert L.conv_split(L.conv_desc(1, 40, 128, 128, 128, 128)) == 1  # 5120
     # an explicit split may be any count up to the K step count (27 taps x 32
     # blocks here); the LDS-staged GEMM takes a split only while each range keeps
     # at least 4 of its 16-channel chunks (5 here: no packed copy in the
