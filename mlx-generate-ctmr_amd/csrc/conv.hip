@@ -1639,11 +1639,14 @@ struct Geometry {
   int64_t pack_bytes, part_bytes, z_bytes;
 };
 
-// K-range (chunk) split of the LDS-staged GEMMs, from the shape only: small
-// grids are split until they fill a round of 512 resident workgroups (two per
-// CU on 256 CUs); grids of under 4 rounds whose last round would run at most
-// 90 % as full as with two ranges take two (e.g. 1280 workgroups: 2.5 rounds
-// -> 5 whole rounds).  `chunks` caps it.
+// K-range (chunk) split of the fp32 LDS-staged GEMM, from the shape only:
+// small grids are split until they fill a round of 512 resident workgroups
+// (two per CU on 256 CUs); grids of under 4 rounds whose last round would run
+// at most 90 % as full as with two ranges take two (e.g. 1280 workgroups: 2.5
+// rounds -> 5 whole rounds).  `chunks` caps it.  (The bf16 LDS GEMM keeps
+// only the first rule: its products are 8x faster, so the partial planes and
+// their reduction cost more than the fuller rounds save -- measured on the
+// decoder's 256-channel level, 257 -> 314 us.)
 static int64_t lds_policy_split(int64_t base, int64_t chunks) {
   if (base < 512) return std::min<int64_t>(ceil_div(512, base), chunks);
   if (base < 2048 && chunks >= 8) {
