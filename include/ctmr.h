@@ -82,7 +82,9 @@ typedef struct ctmr_conv_desc {
   int32_t mode;         /* enum ctmr_conv_mode */
   int32_t flags;        /* enum ctmr_conv_flags, OR-ed */
   int32_t dtype;        /* enum ctmr_dtype */
-  int32_t split;        /* K split for small grids: 0 = library policy, else the number of
+  int32_t split;        /* K split: 0 = library policy (from the shape only: grids of under
+                           512 workgroups, and fp32 LDS-GEMM grids of under 4 rounds whose
+                           last round would be far from full), else the number of
                            contiguous ranges of the (tap, channel block) step sequence,
                            1 .. taps * ceil(cin / K block) */
 } ctmr_conv_desc;
