@@ -1578,7 +1578,16 @@ __global__ __launch_bounds__(256) void split_reduce_gn_kernel(const float* __res
     if (v >= s_out) break;
     const int64_t i = ((int64_t)b * s_out + v) * cout + c0;
     float4 a = bv;
-    for (int k = 0; k < split; ++k) {
+    // Four partial planes' loads in flight at a time, added in ascending order.
+    int k = 0;
+    for (; k + 4 <= split; k += 4) {
+      float4 q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = *(const float4*)(part + (int64_t)(k + u) * plane + i);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) { a.x += q[u].x; a.y += q[u].y; a.z += q[u].z; a.w += q[u].w; }
+    }
+    for (; k < split; ++k) {
       const float4 q = *(const float4*)(part + (int64_t)k * plane + i);
       a.x += q.x; a.y += q.y; a.z += q.z; a.w += q.w;
     }
