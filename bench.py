@@ -325,10 +325,9 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
     cw = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.controlnet_weight_shapes(cc), seed=13).items()}
     cond_emb = torch.from_numpy(rng.standard_normal((2, 64, 64, 32, 64), dtype=np.float32)).to(dev)
 
-    def ct_step():
-        down, mid = m.controlnet_residuals(x, t, classes, None, cw, constructor=cc, conditioning_embedding=cond_emb)
-        return m.denoise_unet(x, t, classes, spacing, uw, constructor=uc, down_block_additional_residuals=down,
-                              mid_block_additional_residual=mid)
+    def ct_step():  # the ControlNet on a second stream, overlapping the UNet encoder
+        return m.controlnet_unet_step(x, t, classes, spacing, uw, cw, unet_constructor=uc, controlnet_constructor=cc,
+                                      conditioning_embedding=cond_emb)
 
     ctrl = lambda: m.controlnet_residuals(x, t, classes, None, cw, constructor=cc, conditioning_embedding=cond_emb)
     for _ in range(2):

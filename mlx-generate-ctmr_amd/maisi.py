@@ -231,8 +231,13 @@ def denoise_unet(
     constructor: Mapping,
     down_block_additional_residuals: Optional[Sequence[Tensor]] = None,
     mid_block_additional_residual: Optional[Tensor] = None,
+    residuals_ready: Optional["torch.cuda.Event"] = None,
 ) -> tuple[Tensor, Tensor]:
-    """One DiffusionModelUNetMaisi pass on NDHWC ``x``; returns ``(t_emb, y)`` (NDHWC)."""
+    """One DiffusionModelUNetMaisi pass on NDHWC ``x``; returns ``(t_emb, y)`` (NDHWC).
+
+    ``residuals_ready``: an event the current stream waits for after the encoder and before the ControlNet
+    residuals are read (they may still be in flight on another stream until then; see
+    ``controlnet_unet_step``)."""
     if int(constructor.get("spatial_dims", 3)) != 3 or constructor.get("use_flash_attention"):
         raise ValueError("MAISI UNet destination is 3D without CUDA flash attention")
     if constructor.get("with_conditioning"):
@@ -255,6 +260,8 @@ def denoise_unet(
     hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1,
                        gn_groups=groups)
     hidden, skips = _down_path(hidden, resnet, attention, res_blocks, attn_levels, heads)
+    if residuals_ready is not None:
+        torch.cuda.current_stream(x.device).wait_event(residuals_ready)
     if down_block_additional_residuals is not None:
         extras = list(down_block_additional_residuals)
         if len(extras) != len(skips):
@@ -459,6 +466,48 @@ def controlnet_residuals(
         down = [d * conditioning_scale for d in down]
         mid = mid * conditioning_scale
     return down, mid
+
+
+_side_streams: dict[int, "torch.cuda.Stream"] = {}
+
+
+def controlnet_unet_step(
+    x: Tensor,
+    timesteps: Tensor,
+    class_labels: Optional[Tensor],
+    spacing: Optional[Tensor],
+    unet_weights: Mapping[str, Tensor],
+    controlnet_weights: Mapping[str, Tensor],
+    *,
+    unet_constructor: Mapping,
+    controlnet_constructor: Mapping,
+    cond: Optional[Tensor] = None,
+    conditioning_embedding: Optional[Tensor] = None,
+    conditioning_scale: float = 1.0,
+) -> tuple[Tensor, Tensor]:
+    """One CT-from-mask denoiser evaluation: the ControlNet's residuals fed to the UNet
+    (``controlnet_residuals`` then ``denoise_unet``), with the ControlNet issued on a second stream of
+    default priority so it runs while the UNet's encoder (which does not read the residuals) runs on the
+    current one; the current stream waits for the residuals after the encoder.  Same kernels, same inputs
+    per kernel: the result equals the serial composition bit for bit.  Returns ``(t_emb, y)``."""
+    if x.device.type != "cuda":
+        raise ValueError("controlnet_unet_step runs on the GPU; x must be a CUDA tensor")
+    main = torch.cuda.current_stream(x.device)
+    side = _side_streams.get(x.device.index)
+    if side is None:
+        side = _side_streams.setdefault(x.device.index, torch.cuda.Stream(device=x.device))
+    side.wait_stream(main)  # inputs written on the current stream
+    with torch.cuda.stream(side):
+        down, mid = controlnet_residuals(x, timesteps, class_labels, cond, controlnet_weights,
+                                         constructor=controlnet_constructor, conditioning_scale=conditioning_scale,
+                                         conditioning_embedding=conditioning_embedding)
+        ready = torch.cuda.Event()
+        ready.record(side)
+    for r in (*down, mid):  # read on the current stream: keep their memory until that use is done
+        r.record_stream(main)
+    return denoise_unet(x, timesteps, class_labels, spacing, unet_weights, constructor=unet_constructor,
+                        down_block_additional_residuals=down, mid_block_additional_residual=mid,
+                        residuals_ready=ready)
 
 
 def controlnet_residuals_ncdhw(x, timesteps, class_labels, cond, weights, *, constructor, mx=None,

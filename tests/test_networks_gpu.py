@@ -141,6 +141,28 @@ def test_unet_step_with_controlnet_matches_oracle(ctmr, dev):
     assert np.abs(ref.numpy() - plain.numpy()).max() > 1e-3
 
 
+def test_controlnet_unet_step_overlap_equals_serial(ctmr, dev):
+    """``controlnet_unet_step`` (ControlNet on a second stream while the UNet encoder runs) gives the serial
+    composition's bits, call after call, with other work on the current stream in between."""
+    f, cctor, cond = _controlnet_case()
+    u = load_fixture("unet.npz")
+    uctor = u["__metadata__"]["constructor"]
+    m, ff = ctmr.maisi, ctmr.fast_fp32
+    x = ff.to_ndhwc(_g(u["input.x"], dev))
+    t, cls = _g(u["input.timesteps"], dev), _g(u["input.class_labels"], dev, torch.int64)
+    spacing, c = _g(u["input.spacing"], dev), ff.to_ndhwc(_g(cond, dev))
+    uw, cw = _gw(u, dev), _gw(f, dev)
+    down, mid = m.controlnet_residuals(x, t, cls, c, cw, constructor=cctor)
+    _, serial = m.denoise_unet(x, t, cls, spacing, uw, constructor=uctor, down_block_additional_residuals=down,
+                               mid_block_additional_residual=mid)
+    for i in range(3):
+        _, y = m.controlnet_unet_step(x, t, cls, spacing, uw, cw, unet_constructor=uctor, controlnet_constructor=cctor,
+                                      cond=c)
+        assert torch.equal(y, serial), f"call {i}"
+        scratch = torch.randn(1 << 20, device=dev) * 2  # unrelated work reusing freed memory
+        del scratch
+
+
 def test_vae_goldens(ctmr, dev):
     f = load_fixture("vae.npz")
     ctor = f["__metadata__"]["constructor"]
