@@ -106,6 +106,21 @@ int64_t ctmr_conv3d_workspace_bytes(const ctmr_conv_desc* desc);
 /* The split ctmr_conv3d will use for `desc` (resolves desc->split == 0). */
 int ctmr_conv3d_split(const ctmr_conv_desc* desc);
 
+/* GEMM formulation ctmr_conv3d runs for `desc`.  No entry point of its own in
+ * the reference, whose route is the _use_nax gate plus the split choice
+ * (fast_fp32.py:93-99, _nax_conv.py:578-581); tests and tools use it to
+ * assert which kernel a shape takes (the choice depends on the desc only). */
+enum ctmr_conv_kernel {
+  CTMR_K_STREAM = 0,        /* register-streaming GEMM over the packed copy */
+  CTMR_K_STREAM_DIRECT = 1, /* register-streaming GEMM reading x itself */
+  CTMR_K_LDS = 2,           /* fp32 LDS-staged GEMM (halo bricks of x) */
+  CTMR_K_LDS_BF16 = 3,      /* bf16 LDS-staged GEMM over the packed copy */
+  CTMR_K_POINTWISE = 4,     /* persistent one-tap GEMM (1x1x1, im2col rows) */
+  CTMR_K_SPLIT_WAVES = 5,   /* 64 x 64 tiles, each split range over the four waves */
+  CTMR_K_TAP_EXPAND = 6     /* cout <= 4: 27*cout-column GEMM + tap sum */
+};
+int ctmr_conv3d_kernel(const ctmr_conv_desc* desc);
+
 /*
  * Reorder a Torch-layout weight (Cout, Cin, k, k, k) fp32 into the layout the
  * conv kernel reads.  desc->mode NEAREST2X is rejected here (use

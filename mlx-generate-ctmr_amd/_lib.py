@@ -20,6 +20,8 @@ E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_LAUNCH = -1, -2, -3, -4
 MODE_PLAIN, MODE_NEAREST2X, MODE_TRILINEAR2X = 0, 1, 2
 F_AFFINE, F_SILU, F_BATCH_BIAS, F_RESIDUAL, F_STREAM = 1, 2, 4, 8, 16
 DT_F32, DT_BF16 = 0, 1
+K_STREAM, K_STREAM_DIRECT, K_LDS, K_LDS_BF16, K_POINTWISE, K_SPLIT_WAVES, K_TAP_EXPAND = range(7)
+KERNEL_NAMES = ("stream", "stream_direct", "lds", "lds_bf16", "pointwise", "split_waves", "tap_expand")
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2
 ABI_VERSION = 1
 
@@ -52,6 +54,7 @@ _PROTOTYPES = {
     "ctmr_packed_weight_elems": (_c_i64, [_desc_p]),
     "ctmr_conv3d_workspace_bytes": (_c_i64, [_desc_p]),
     "ctmr_conv3d_split": (_c_int, [_desc_p]),
+    "ctmr_conv3d_kernel": (_c_int, [_desc_p]),
     "ctmr_pack_weight": (_c_int, [_desc_p, _vp, _vp, _vp]),
     "ctmr_pack_upsample_weight": (_c_int, [_desc_p, _vp, _vp, _vp]),
     "ctmr_conv3d": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
@@ -154,6 +157,11 @@ def workspace_bytes(desc: ConvDesc) -> int:
 
 def conv_split(desc: ConvDesc) -> int:
     return check(lib().ctmr_conv3d_split(ctypes.byref(desc)), "ctmr_conv3d_split")
+
+
+def conv_kernel(desc: ConvDesc) -> str:
+    """Name of the GEMM formulation ``ctmr_conv3d`` runs for ``desc`` (``ctmr_conv3d_kernel``)."""
+    return KERNEL_NAMES[check(lib().ctmr_conv3d_kernel(ctypes.byref(desc)), "ctmr_conv3d_kernel")]
 
 
 def gn_workspace_bytes(n: int, s: int, c: int) -> int:

@@ -2077,6 +2077,18 @@ int ctmr_conv3d_split(const ctmr_conv_desc* desc) {
   return g.split;
 }
 
+int ctmr_conv3d_kernel(const ctmr_conv_desc* desc) {
+  Geometry g;
+  int rc = geometry(desc, g);
+  if (rc) return rc;
+  if (g.lds) return CTMR_K_LDS;
+  if (g.lds16) return CTMR_K_LDS_BF16;
+  if (g.layout == WL_EXPAND) return CTMR_K_TAP_EXPAND;
+  if (g.kws) return CTMR_K_SPLIT_WAVES;
+  if (g.pointwise) return CTMR_K_POINTWISE;
+  return g.direct ? CTMR_K_STREAM_DIRECT : CTMR_K_STREAM;
+}
+
 static int pack_weight_impl(const ctmr_conv_desc* desc, const float* weight, void* packed,
                             void* stream, bool up) {
   Geometry g;

@@ -91,11 +91,61 @@ def _vec(t: Optional[Tensor], n: int, name: str, device: torch.device) -> Option
 
 
 # ---------------------------------------------------------------------------
-# packed-weight cache (fast_fp32.py:70-91): keyed by (id(weight), mode,
-# dtype); the weak reference validates the id and evicts on collection.
+# derived-weight caches (fast_fp32.py:70-91): keyed by the ids of every source
+# tensor (weights and biases) plus the mode/dtype; an entry is valid while weak
+# references to the same source objects are alive and each source's
+# ``_version`` is what it was when the entry was built (torch tensors, unlike
+# MLX arrays, can change in place: ``copy_`` or an in-place reload bumps it).
 # ---------------------------------------------------------------------------
-_packed: dict[tuple[int, int, int], tuple[weakref.ref, Tensor]] = {}
-_packed_lock = threading.Lock()
+_packed: dict[tuple, tuple[tuple[weakref.ref, ...], tuple[int, ...], Tensor]] = {}
+_packed_lock = threading.RLock()  # re-entrant: a weakref eviction may run inside a locked section
+_retained = threading.local()
+
+
+def _sources_match(refs: tuple[weakref.ref, ...], versions: tuple[int, ...], sources: tuple[Tensor, ...]) -> bool:
+    return all(r() is t and v == t._version for r, v, t in zip(refs, versions, sources))
+
+
+def _note_use(*derived: Optional[Tensor]) -> None:
+    """Record derived tensors handed to a kernel while ``retain_cached`` is active."""
+    sink = getattr(_retained, "sink", None)
+    if sink is not None:
+        sink.extend(t for t in derived if t is not None)
+
+
+@contextlib.contextmanager
+def retain_cached(sink: list) -> Iterator[list]:
+    """Collect into ``sink`` every cached derived tensor (packed conv weights, fused Q/K/V
+    projections, stacked time projections) used on this thread while the context is active.
+    A recorded HIP graph keeps such a list so its kernels' weight addresses stay valid even
+    after ``drop_packed_weights`` or a cache refresh releases the cache's own reference."""
+    previous = getattr(_retained, "sink", None)
+    _retained.sink = sink
+    try:
+        yield sink
+    finally:
+        _retained.sink = previous
+
+
+def cached_derived(cache: dict, lock: threading.Lock, key: tuple, sources: tuple[Tensor, ...], build):
+    """The cache entry for ``key`` built from ``sources`` by ``build()``, rebuilt when a source was
+    collected, replaced or modified in place since.  ``build`` returns a tensor or a tuple whose
+    tensors are the derived data (recorded for ``retain_cached``)."""
+    with lock:
+        hit = cache.get(key)
+        if hit is not None and _sources_match(hit[0], hit[1], sources):
+            _note_use(*(hit[2] if isinstance(hit[2], tuple) else (hit[2],)))
+            return hit[2]
+    value = build()
+
+    def _evict(_ref, key=key):
+        with lock:
+            cache.pop(key, None)
+
+    with lock:
+        cache[key] = (tuple(weakref.ref(t, _evict) for t in sources), tuple(t._version for t in sources), value)
+    _note_use(*(value if isinstance(value, tuple) else (value,)))
+    return value
 
 
 def pack_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tensor:
@@ -119,29 +169,35 @@ def _pack(weight: Tensor, mode: int) -> Tensor:
     if not isinstance(weight, Tensor) or weight.device.type != "cuda":
         raise ValueError("conv weight must be a torch.Tensor on the GPU (there is no CPU path)")
     code = _dtype_code()
-    key = (id(weight), mode, code)
-    with _packed_lock:
-        hit = _packed.get(key)
-        if hit is not None and hit[0]() is weight:
-            return hit[1]
     dtype = "bf16" if code == _lib.DT_BF16 else "fp32"
-    packed = (pack_upsample_weight if mode == _lib.MODE_NEAREST2X else pack_weight)(weight, dtype=dtype)
-
-    def _evict(_ref, key=key):
-        with _packed_lock:
-            _packed.pop(key, None)
-
-    with _packed_lock:
-        _packed[key] = (weakref.ref(weight, _evict), packed)
-    return packed
+    packer = pack_upsample_weight if mode == _lib.MODE_NEAREST2X else pack_weight
+    return cached_derived(_packed, _packed_lock, ("conv", mode, code, id(weight)), (weight,),
+                          lambda: packer(weight, dtype=dtype))
 
 
 def drop_packed_weights(weights: Iterable[Tensor]) -> None:
-    """Forget the packed copies of ``weights``; a later use packs them again."""
+    """Forget every cached tensor derived from ``weights`` (packed conv weights, fused Q/K/V
+    projections); a later use derives them again.  A recorded graph that used them keeps its
+    own references (``retain_cached``), so its replays stay valid."""
     ids = {id(w) for w in weights}
-    with _packed_lock:
-        for key in [k for k in _packed if k[0] in ids]:
-            del _packed[key]
+    for cache, lock in _caches:
+        with lock:
+            for key in [k for k, entry in cache.items() if any(id(r()) in ids for r in entry[0] if r() is not None)]:
+                del cache[key]
+
+
+def register_cache(cache: dict, lock) -> None:
+    """Add a ``cached_derived`` cache to those ``drop_packed_weights`` and ``cache_size`` cover."""
+    _caches.append((cache, lock))
+
+
+def cache_size() -> int:
+    """Number of live derived-weight cache entries (every registered cache)."""
+    total = 0
+    for cache, lock in _caches:
+        with lock:
+            total += len(cache)
+    return total
 
 
 # ---------------------------------------------------------------------------
@@ -399,27 +455,23 @@ def flash_attention(q: Tensor, k: Tensor, v: Tensor, *, heads: int, scale: float
     return ops.flash_attention(q, k, v, int(heads), float(scale), int(query_tiles))
 
 
-# Fused (3C, C) Q/K/V projection weights, keyed by the three weights' ids and
-# validated by weak references like the packed conv weights.
-_qkv: dict[tuple[int, int, int], tuple[tuple[weakref.ref, ...], Tensor, Optional[Tensor]]] = {}
+# Fused (3C, C) Q/K/V projection weights and biases, keyed by all six source
+# tensors and validated like the packed conv weights.
+_qkv: dict[tuple, tuple] = {}
+_caches: list[tuple[dict, object]] = [(_packed, _packed_lock), (_qkv, _packed_lock)]
 
 
 def _fused_qkv(wq: Tensor, wk: Tensor, wv: Tensor, biases) -> tuple[Tensor, Optional[Tensor]]:
-    key = (id(wq), id(wk), id(wv))
-    with _packed_lock:
-        hit = _qkv.get(key)
-        if hit is not None and all(r() is t for r, t in zip(hit[0], (wq, wk, wv))):
-            return hit[1], hit[2]
-    weight = torch.cat([wq, wk, wv], dim=0).to(torch.float32).contiguous()
-    bias = None if biases is None else torch.cat(list(biases), dim=0).to(torch.float32).contiguous()
+    sources = (wq, wk, wv) + (() if biases is None else tuple(biases))
 
-    def _evict(_ref, key=key):
-        with _packed_lock:
-            _qkv.pop(key, None)
+    def build():
+        weight = torch.cat([wq, wk, wv], dim=0).to(torch.float32).contiguous()
+        if biases is None:
+            return (weight,)
+        return weight, torch.cat(list(biases), dim=0).to(torch.float32).contiguous()
 
-    with _packed_lock:
-        _qkv[key] = (tuple(weakref.ref(t, _evict) for t in (wq, wk, wv)), weight, bias)
-    return weight, bias
+    fused = cached_derived(_qkv, _packed_lock, tuple(id(t) for t in sources), sources, build)
+    return fused[0], (fused[1] if len(fused) > 1 else None)
 
 
 def attention(query: Tensor, key: Tensor, value: Tensor, *, scale: float, mx=None) -> Tensor:

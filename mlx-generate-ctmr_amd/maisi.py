@@ -22,7 +22,6 @@ from __future__ import annotations
 
 import math
 import threading
-import weakref
 from collections.abc import Callable, Mapping, Sequence
 from itertools import product
 from typing import Optional
@@ -116,35 +115,31 @@ def spatial_attention(x: Tensor, weights: Mapping[str, Tensor], *, num_groups: i
 # UNet (unet.py:42-487)
 # ---------------------------------------------------------------------------
 # Every residual block's time-embedding projection stacked into one GEMM, with
-# conv1's bias folded into the GEMM bias: keyed by the projection weights' ids
-# and validated by weak references (evicted when a weight is collected).
+# conv1's bias folded into the GEMM bias: keyed by every source tensor (the
+# projection weights and biases and the conv1 biases), rebuilt when one is
+# collected or modified in place (fast_fp32.cached_derived).
 _TIME_SUFFIX = ".time_emb_proj.weight"
 _time_proj: dict[tuple[int, ...], tuple] = {}
-_time_proj_lock = threading.Lock()
+_time_proj_lock = threading.RLock()
+ff.register_cache(_time_proj, _time_proj_lock)
 
 
 def _time_projections(weights: Mapping[str, Tensor]) -> tuple[Tensor, Tensor, dict[str, tuple[int, int]]]:
     prefixes = sorted(k[: -len(_TIME_SUFFIX)] for k in weights if k.endswith(_TIME_SUFFIX))
     mats = [weights[p + _TIME_SUFFIX] for p in prefixes]
-    key = tuple(id(m) for m in mats)
-    with _time_proj_lock:
-        hit = _time_proj.get(key)
-        if hit is not None and all(r() is m for r, m in zip(hit[0], mats)):
-            return hit[1], hit[2], hit[3]
-    weight = torch.cat(mats, dim=0).to(torch.float32).contiguous()
-    bias = torch.cat([_need(weights, f"{p}.time_emb_proj.bias") + _need(weights, f"{p}.conv1.conv.bias")
-                      for p in prefixes]).to(torch.float32).contiguous()
+    biases = [(_need(weights, f"{p}.time_emb_proj.bias"), _need(weights, f"{p}.conv1.conv.bias")) for p in prefixes]
+    sources = tuple(mats) + tuple(t for pair in biases for t in pair)
+
+    def build():
+        weight = torch.cat(mats, dim=0).to(torch.float32).contiguous()
+        bias = torch.cat([tb + cb for tb, cb in biases]).to(torch.float32).contiguous()
+        return weight, bias
+
+    weight, bias = ff.cached_derived(_time_proj, _time_proj_lock, tuple(id(t) for t in sources), sources, build)
     spans, start = {}, 0
     for p, m in zip(prefixes, mats):
         spans[p] = (start, start + int(m.shape[0]))
         start += int(m.shape[0])
-
-    def _evict(_ref, key=key):
-        with _time_proj_lock:
-            _time_proj.pop(key, None)
-
-    with _time_proj_lock:
-        _time_proj[key] = (tuple(weakref.ref(m, _evict) for m in mats), weight, bias, spans)
     return weight, bias, spans
 
 
@@ -305,7 +300,9 @@ class UNetGraph:
     ``(t_emb, y)``, which the next call overwrites (clone them to keep them).  The weights, their packed
     copies and the precision mode (``fast_fp32.precision``) are those at construction; build a new graph
     after changing any of them.  Construction runs the step twice eagerly (filling the packed-weight and
-    projection caches) before recording.
+    projection caches) before recording.  The graph holds its own references to every cached derived
+    tensor the recording read (``fast_fp32.retain_cached``), so ``drop_packed_weights`` or a cache
+    refresh cannot free memory its kernels still address.
     """
 
     def __init__(self, x: Tensor, timesteps: Tensor, class_labels: Optional[Tensor], spacing: Optional[Tensor],
@@ -335,7 +332,8 @@ class UNetGraph:
                 run()
         torch.cuda.current_stream(dev).wait_stream(side)
         self._graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self._graph):
+        self._retained: list[Tensor] = []
+        with ff.retain_cached(self._retained), torch.cuda.graph(self._graph):
             self._out = run()
 
     @staticmethod
@@ -580,10 +578,47 @@ def decode_vae_ncdhw(latent: Tensor, weights, *, constructor, mx=None):
 # ---------------------------------------------------------------------------
 # sliding-window decode (decode.py:30-245)
 # ---------------------------------------------------------------------------
+DEFAULT_ROI_SIZE = (48, 48, 64)
+DEFAULT_OVERLAP = 0.6666
+DEFAULT_SIGMA_SCALE = 0.125
+DEFAULT_MODE = "gaussian"
+
+
+def _check_roi(roi: Sequence[int]) -> tuple[int, int, int]:
+    """Three positive window sizes (decode.py _check_roi)."""
+    if len(roi) != 3:
+        raise ValueError(f"roi must be three positive ints; got {tuple(roi)}")
+    windows = (int(roi[0]), int(roi[1]), int(roi[2]))
+    if any(v < 1 for v in windows):
+        raise ValueError(f"roi must be three positive ints; got {windows}")
+    return windows
+
+
+def _check_overlap(overlap: float) -> None:
+    """``0 <= overlap < 1`` (decode.py _check_overlap)."""
+    if not 0.0 <= float(overlap) < 1.0:
+        raise ValueError(f"overlap must be >= 0 and < 1; got {overlap}")
+
+
+def _spatial3(values: Sequence[int], name: str) -> tuple[int, int, int]:
+    if len(values) != 3:
+        raise ValueError(f"{name} must have 3 spatial axes; got {tuple(values)}")
+    out = (int(values[0]), int(values[1]), int(values[2]))
+    if any(v < 1 for v in out):
+        raise ValueError(f"{name} must be positive; got {out}")
+    return out
+
+
 def scan_interval(image_size: Sequence[int], roi: Sequence[int], overlap: float) -> tuple[int, int, int]:
-    """``int(roi * (1 - overlap))`` (at least 1), or ``roi`` where it equals the axis (decode.py:30-45)."""
+    """``int(roi * (1 - overlap))`` (at least 1), or ``roi`` where it equals the axis (decode.py:30-45).
+
+    Raises:
+        ValueError: on a roi that is not three positive sizes, an overlap outside [0, 1) or a
+            non-positive image size."""
+    roi = _check_roi(roi)
+    _check_overlap(overlap)
     out = []
-    for size, window in zip(image_size, roi):
+    for size, window in zip(_spatial3(image_size, "image_size"), roi):
         if window == size:
             out.append(int(window))
             continue
@@ -594,6 +629,8 @@ def scan_interval(image_size: Sequence[int], roi: Sequence[int], overlap: float)
 
 def dense_patch_slices(image_size: Sequence[int], patch: Sequence[int], interval: Sequence[int]):
     """Window slices; the last start of each axis is pulled back inside (decode.py:48-78)."""
+    image_size, patch, interval = _spatial3(image_size, "image_size"), _check_roi(patch), _spatial3(interval,
+                                                                                                   "interval")
     starts = []
     for size, window, step in zip(image_size, patch, interval):
         count = int(math.ceil(float(size) / float(step)))
@@ -611,6 +648,9 @@ def dense_patch_slices(image_size: Sequence[int], patch: Sequence[int], interval
 
 def gaussian_importance(roi: Sequence[int], sigma_scale: float = 0.125, device=None) -> Tensor:
     """Outer product of 1-D Gaussians, floored at 1e-3, ``(D, H, W)`` fp32 (decode.py:81-101)."""
+    roi = _check_roi(roi)
+    if float(sigma_scale) <= 0.0:
+        raise ValueError(f"sigma_scale must be > 0; got {sigma_scale}")
     axes = []
     for length in roi:
         half = (length - 1) / 2.0
@@ -621,13 +661,24 @@ def gaussian_importance(roi: Sequence[int], sigma_scale: float = 0.125, device=N
     return torch.clamp(imp, min=_GAUSSIAN_FLOOR)
 
 
-def sliding_window(latent: Tensor, predict: Callable[[Tensor], Tensor], *, roi: Sequence[int],
-                   overlap: float, sigma_scale: float = 0.125, z_scale: int = Z_SCALE) -> Tensor:
+def sliding_window(latent: Tensor, predict: Callable[[Tensor], Tensor], *, roi: Sequence[int] = DEFAULT_ROI_SIZE,
+                   overlap: float = DEFAULT_OVERLAP, sigma_scale: float = DEFAULT_SIGMA_SCALE,
+                   mode: str = DEFAULT_MODE, z_scale: int = Z_SCALE) -> Tensor:
     """Blend ``predict`` over overlapping NDHWC latent windows (decode.py:104-184).
 
     Each window's prediction is weighted by the nearest-x4-resized Gaussian and
     accumulated with the weights in window order; the result is the ratio.
+
+    Raises:
+        ValueError: if ``mode`` is not ``"gaussian"``, ``z_scale`` is not 4, the window or
+            overlap is invalid, or ``predict`` returns the wrong size (decode.py:132-146).
     """
+    if mode != DEFAULT_MODE:
+        raise ValueError(f"from-mask dest mode is {DEFAULT_MODE!r}; got {mode!r}")
+    if int(z_scale) != Z_SCALE:
+        raise ValueError(f"image VAE dest z_scale is {Z_SCALE}; got {z_scale}")
+    roi = _check_roi(roi)
+    _check_overlap(overlap)
     n, d, h, w, c = latent.shape
     pads = []
     for size, window in zip((d, h, w), roi):
@@ -664,10 +715,13 @@ def sliding_window(latent: Tensor, predict: Callable[[Tensor], Tensor], *, roi: 
 
 
 def sliding_window_decode(latent: Tensor, weights: Mapping[str, Tensor], *, constructor: Mapping,
-                          roi: Sequence[int] = (48, 48, 64), overlap: float = 0.6666, sigma_scale: float = 0.125,
+                          roi: Sequence[int] = DEFAULT_ROI_SIZE, overlap: float = DEFAULT_OVERLAP,
+                          sigma_scale: float = DEFAULT_SIGMA_SCALE, mode: str = DEFAULT_MODE,
                           scale_factor: Optional[float] = None) -> Tensor:
     """Decode an NDHWC latent, tiling with Gaussian-blended windows when larger than ``roi``
-    (decode.py:187-245)."""
+    (decode.py:187-245).  As in the reference, the one-pass branch validates ``roi`` only;
+    ``overlap``, ``sigma_scale`` and ``mode`` are validated when tiling."""
+    roi = _check_roi(roi)
     if scale_factor is not None:
         value = float(scale_factor)
         if not math.isfinite(value) or value == 0.0:
@@ -681,13 +735,15 @@ def sliding_window_decode(latent: Tensor, weights: Mapping[str, Tensor], *, cons
     if math.prod(spatial) <= math.prod(roi):
         return decode_window(latent)
     adjusted = tuple(min(r, s) for r, s in zip(roi, spatial))
-    return sliding_window(latent, decode_window, roi=adjusted, overlap=overlap, sigma_scale=sigma_scale)
+    return sliding_window(latent, decode_window, roi=adjusted, overlap=overlap, sigma_scale=sigma_scale, mode=mode)
 
 
-def sliding_window_decode_ncdhw(latent: Tensor, weights, *, constructor, mx=None, roi=(48, 48, 64),
-                                overlap=0.6666, sigma_scale=0.125, scale_factor=None) -> Tensor:
+def sliding_window_decode_ncdhw(latent: Tensor, weights, *, constructor, mx=None, roi=DEFAULT_ROI_SIZE,
+                                overlap=DEFAULT_OVERLAP, sigma_scale=DEFAULT_SIGMA_SCALE, mode=DEFAULT_MODE,
+                                scale_factor=None) -> Tensor:
     return ff.to_ncdhw(sliding_window_decode(ff.to_ndhwc(latent), weights, constructor=constructor, roi=roi,
-                                             overlap=overlap, sigma_scale=sigma_scale, scale_factor=scale_factor))
+                                             overlap=overlap, sigma_scale=sigma_scale, mode=mode,
+                                             scale_factor=scale_factor))
 
 
 # ---------------------------------------------------------------------------
@@ -953,8 +1009,19 @@ def random_weights(shapes: Sequence[tuple[str, tuple[int, ...]]], *, seed: int) 
     return out
 
 
-def output_intensities(decoded: np.ndarray, *, configuration: str = "mr") -> np.ndarray:
-    """int16 image: CT ``clip(x*2000-1000, -1000, 1000)``, MR ``max(x*1000, 0)``, truncated (image.py:68-87)."""
+CONFIGURATIONS = ("ct", "mr", "mr-brain")
+
+
+def output_intensities(decoded: np.ndarray, *, configuration: str = "ct") -> np.ndarray:
+    """int16 image: CT ``clip(x*2000-1000, -1000, 1000)``, MR and MR-Brain ``max(x*1000, 0)`` (no
+    upper clip), truncated (image.py:68-87).
+
+    Raises:
+        ValueError: for a configuration other than ``"ct"``, ``"mr"`` or ``"mr-brain"`` (the
+            reference's InvalidInputError, configurations.py:188-200), or a non-finite image.
+    """
+    if not isinstance(configuration, str) or configuration not in CONFIGURATIONS:
+        raise ValueError("configuration must be 'ct', 'mr', or 'mr-brain'")
     data = np.asarray(decoded, dtype=np.float32)
     if not np.isfinite(data).all():
         raise ValueError("decoded image must be finite")

@@ -42,26 +42,86 @@ def conv3d(x: np.ndarray, w: np.ndarray, b: np.ndarray | None = None, *, stride:
 
 
 def conv3d_points(x: np.ndarray, w: np.ndarray, b: np.ndarray | None, points: np.ndarray, *,
-                  stride: int = 1) -> np.ndarray:
-    """The same padding-1 3x3x3 (or 1x1x1) conv evaluated only at output voxels ``points``.
+                  stride: int = 1, upsample: bool = False, affine: np.ndarray | None = None,
+                  apply_silu: bool = False, chunk: int = 512) -> np.ndarray:
+    """The padding-``k // 2`` conv of ``conv3d`` evaluated only at output voxels ``points``.
 
     ``points`` is ``(P, 4)`` integer ``(n, d, h, w)`` output coordinates; the
-    result is ``(P, O)`` float64.  Used to spot-check full-size volumes whose
-    complete float64 convolution would take too long on the CPU.
+    result is ``(P, O)`` float64.  The conv input is ``x`` after the optional
+    prologue of the reference's pack kernel (_nax_conv.py:174-197):
+    ``silu?(x * scale + offset)`` with ``(N, C, 2)`` pairs ``affine``, then the
+    optional nearest-2x upsampling (output voxel ``u`` of an axis reads source
+    voxel ``u // 2``, test_fast_fp32.py:123-125); the zero padding lies outside
+    the transformed (and upsampled) volume.  Used to check full-size volumes
+    whose complete float64 convolution would take too long on the CPU.
     """
-    x = np.asarray(x, F64)
+    x = np.asarray(x)
     w = np.asarray(w, F64)
+    pts = np.asarray(points, np.int64)
     k = w.shape[2]
     p = k // 2
-    xp = np.pad(x, [(0, 0), (p, p), (p, p), (p, p), (0, 0)])
-    out = np.zeros((len(points), w.shape[0]), F64)
-    for i, (n, d, h, wi) in enumerate(np.asarray(points)):
-        patch = xp[n, stride * d : stride * d + k, stride * h : stride * h + k, stride * wi : stride * wi + k, :]
-        out[i] = np.einsum("dhwc,ocdhw->o", patch, w)
+    n_, d_, h_, w_, c = x.shape
+    extent = np.array([d_, h_, w_]) * (2 if upsample else 1)
+    offs = np.arange(k) - p
+    out = np.zeros((len(pts), w.shape[0]), F64)
+    wk = w.transpose(2, 3, 4, 1, 0).reshape(k * k * k * c, w.shape[0])  # (tap * C + c, O)
+    for lo in range(0, len(pts), chunk):
+        blk = pts[lo:lo + chunk]
+        # (P, k) coordinates per axis on the (upsampled) conv-input grid
+        coords = [stride * blk[:, 1 + a, None] + offs[None, :] for a in range(3)]
+        valid = [(cc >= 0) & (cc < extent[a]) for a, cc in enumerate(coords)]
+        src = [np.clip(cc, 0, extent[a] - 1) // (2 if upsample else 1) for a, cc in enumerate(coords)]
+        nn = blk[:, 0, None, None, None]
+        patch = np.asarray(x[nn, src[0][:, :, None, None], src[1][:, None, :, None], src[2][:, None, None, :]],
+                           F64)  # (P, k, k, k, C)
+        if affine is not None:
+            a = np.asarray(affine, F64)[blk[:, 0]]  # (P, C, 2)
+            patch = patch * a[:, None, None, None, :, 0] + a[:, None, None, None, :, 1]
+        if apply_silu:
+            patch = silu(patch)
+        mask = valid[0][:, :, None, None] & valid[1][:, None, :, None] & valid[2][:, None, None, :]
+        patch = patch * mask[..., None]
+        out[lo:lo + chunk] = patch.reshape(len(blk), -1) @ wk
     if b is not None:
         b = np.asarray(b, F64)
-        out += b[np.asarray(points)[:, 0]] if b.ndim == 2 else b
+        out += b[pts[:, 0]] if b.ndim == 2 else b
     return out
+
+
+def boundary_points(n: int, spatial: tuple[int, int, int], count: int, seed: int) -> np.ndarray:
+    """``(P, 4)`` output coordinates covering every corner, the 12 edges and 6 faces of each batch
+    item's output volume (three points per edge, eight per face) plus ``count`` random voxels."""
+    rng = np.random.default_rng(seed)
+    ext = [int(s) for s in spatial]
+    picks = []
+    for item in range(n):
+        for corner in np.ndindex(2, 2, 2):
+            picks.append((item, *[(ext[a] - 1) * corner[a] for a in range(3)]))
+        for free in range(3):  # edges: one free axis, the others at 0 or max
+            for fixed in np.ndindex(2, 2):
+                for v in (0, ext[free] // 2, ext[free] - 1):
+                    pt, j = [0, 0, 0], 0
+                    for a in range(3):
+                        if a == free:
+                            pt[a] = v
+                        else:
+                            pt[a] = (ext[a] - 1) * fixed[j]
+                            j += 1
+                    picks.append((item, *pt))
+        for axis in range(3):  # faces
+            for side in (0, ext[axis] - 1):
+                for _ in range(8):
+                    pt = [int(rng.integers(0, e)) for e in ext]
+                    pt[axis] = side
+                    picks.append((item, *pt))
+    rand = np.stack([rng.integers(0, n, count)] + [rng.integers(0, e, count) for e in ext], axis=1)
+    return np.concatenate([np.asarray(picks, np.int64), rand.astype(np.int64)])
+
+
+def gather_points(y: np.ndarray, points: np.ndarray) -> np.ndarray:
+    """``(P, C)`` rows of NDHWC ``y`` at ``points``."""
+    p = np.asarray(points, np.int64)
+    return np.asarray(y[p[:, 0], p[:, 1], p[:, 2], p[:, 3]])
 
 
 def upsample_nearest(x: np.ndarray) -> np.ndarray:

@@ -242,3 +242,23 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     assert rc == L.E_INVALID and "divisible" in L.last_error()
     rc = native_loaded.ctmr_gn_affine_from_stats(1, 0, 12, 4, 64, 1e-6, fake, fake, fake, fake, None)
     assert rc == L.E_INVALID
+
+
+@pytest.mark.parametrize(("shape", "cout", "kw", "expected"), [
+    ((1, 64, 64, 64, 64), 64, {}, "lds"),                                 # config 0
+    ((1, 128, 128, 128, 128), 128, {"flags": 3}, "lds"),                  # config 1 (GN affine + SiLU)
+    ((1, 128, 128, 128, 64), 128, {"stride": 2}, "stream_direct"),       # config 2a
+    ((1, 64, 64, 64, 256), 128, {"mode": 1}, "stream"),                   # config 2b
+    ((1, 64, 64, 64, 128), 256, {"ksize": 1}, "pointwise"),               # config 2c
+    ((1, 64, 64, 64, 64), 64, {"flags": 16}, "stream_direct"),            # CTMR_F_STREAM
+    ((1, 64, 64, 64, 64), 64, {"dtype": 1}, "lds_bf16"),
+    ((2, 4, 8, 8, 512), 512, {}, "split_waves"),                          # deep UNet level
+    ((1, 20, 64, 64, 64), 1, {}, "tap_expand"),                           # decoder output conv
+    ((2, 64, 64, 32, 4), 64, {}, "pointwise"),                            # conv_in: im2col rows
+])
+def test_conv_kernel_route(ctmr, shape, cout, kw, expected):
+    """``ctmr_conv3d_kernel`` names the formulation the library picks (a function of the desc only)."""
+    L = ctmr._lib
+    n, d, h, w, cin = shape
+    desc = L.conv_desc(n, d, h, w, cin, cout, **kw)
+    assert L.conv_kernel(desc) == expected

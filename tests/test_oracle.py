@@ -129,6 +129,49 @@ def test_conv_points_match_full_conv():
     np.testing.assert_allclose(rm.conv3d_points(x, w, b, pts2, stride=2), full2[tuple(pts2.T)], rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize(("stride", "upsample", "prologue", "ksize"), [
+    (1, False, False, 3), (2, False, False, 3), (1, True, False, 3), (1, False, True, 3), (1, True, True, 3),
+    (1, False, True, 1), (2, False, True, 3)])
+def test_conv_points_with_prologue_match_full_conv(stride, upsample, prologue, ksize):
+    """The point evaluator used at full config sizes equals the whole-volume oracle on every output
+    voxel of small volumes (odd extents, ragged last stride-2 window): the GN affine + SiLU prologue
+    is applied before the zero padding, the nearest-2x upsampling reads voxel ``u // 2``."""
+    x = 2 * _rand((2, 5, 4, 7, 6), 40) + 0.5
+    w = _rand((3, 6, ksize, ksize, ksize), 41)
+    b = _rand((2, 3), 42)
+    affine = np.stack([1 + 0.3 * _rand((2, 6), 43), 0.5 * _rand((2, 6), 44)], axis=-1) if prologue else None
+    src = rm.apply_affine(x, affine, True) if prologue else x
+    if upsample:
+        src = rm.upsample_nearest(src)
+    full = rm.conv3d(src, w, b, stride=stride)
+    pts = np.stack(np.meshgrid(*[np.arange(s) for s in full.shape[:4]], indexing="ij"), -1).reshape(-1, 4)
+    got = rm.conv3d_points(x, w, b, pts, stride=stride, upsample=upsample, affine=affine, apply_silu=prologue,
+                           chunk=7)
+    np.testing.assert_allclose(got, rm.gather_points(full, pts), rtol=1e-12, atol=1e-12)
+
+
+def test_conv_points_planted_padding_before_prologue_fails():
+    """Zero padding applied before the affine + SiLU (instead of after) changes every border voxel:
+    the point evaluator's border handling is what the full-volume oracle checks."""
+    x = _rand((1, 4, 4, 4, 2), 45)
+    w = _rand((2, 2, 3, 3, 3), 46)
+    affine = np.stack([np.full((1, 2), 1.5), np.full((1, 2), 0.7)], axis=-1)
+    wrong = rm.conv3d(rm.apply_affine(np.pad(x, [(0, 0), (1, 1), (1, 1), (1, 1), (0, 0)]), affine, True), w,
+                      padding=0)
+    pts = np.array([[0, 0, 0, 0], [0, 3, 3, 3]])
+    got = rm.conv3d_points(x, w, None, pts, affine=affine, apply_silu=True)
+    assert np.abs(got - rm.gather_points(wrong, pts)).max() > 1e-3
+
+
+def test_boundary_points_cover_corners_edges_faces():
+    pts = rm.boundary_points(2, (5, 6, 7), 10, seed=0)
+    assert pts.shape[1] == 4 and len(pts) == 2 * (8 + 36 + 48) + 10
+    assert (pts >= 0).all() and (pts[:, 1] < 5).all() and (pts[:, 2] < 6).all() and (pts[:, 3] < 7).all()
+    corners = {tuple(p) for p in pts[:, 1:]}
+    assert all((a, b, c) in corners for a in (0, 4) for b in (0, 5) for c in (0, 6))
+    assert set(pts[:, 0]) == {0, 1}
+
+
 def test_upsample_fold_is_exact_identity():
     x = _rand((2, 3, 4, 5, 3), 15)
     w = _rand((2, 3, 3, 3, 3), 16)

@@ -61,3 +61,56 @@ def test_unet_graph_rejects_cpu_inputs(ctmr):
 
     with pytest.raises(ValueError, match="CUDA"):
         ctmr.maisi.UNetGraph(torch.zeros(1, 4, 4, 4, 4), torch.zeros(1), None, None, {}, constructor={})
+
+
+def test_output_intensities_default_and_configurations(ctmr):
+    """image.py:68-87: the default configuration is CT; MR and MR-Brain share ``max(1000 x, 0)``
+    with no upper clip; any other name raises (the reference's InvalidInputError)."""
+    import numpy as np
+
+    m = ctmr.maisi
+    x = np.array([-0.2, 0.0, 0.25, 0.5004, 1.7], np.float32)
+    np.testing.assert_array_equal(m.output_intensities(x), [-1000, -1000, -500, 0, 1000])
+    np.testing.assert_array_equal(m.output_intensities(x, configuration="ct"), m.output_intensities(x))
+    for name in ("mr", "mr-brain"):
+        np.testing.assert_array_equal(m.output_intensities(x, configuration=name), [0, 0, 250, 500, 1700])
+    for bad in ("CT", "mri", "", None):
+        with pytest.raises(ValueError, match="configuration must be"):
+            m.output_intensities(x, configuration=bad)
+    with pytest.raises(ValueError, match="finite"):
+        m.output_intensities(np.array([np.nan], np.float32))
+
+
+@pytest.mark.parametrize(("kw", "message"), [
+    ({"roi": (4, 4)}, "roi must be three"),
+    ({"roi": (4, 0, 4)}, "roi must be three"),
+    ({"overlap": 1.0}, "overlap must be"),
+    ({"overlap": -0.1}, "overlap must be"),
+    ({"mode": "constant"}, "mode"),
+    ({"z_scale": 2}, "z_scale"),
+])
+def test_sliding_window_argument_validation(ctmr, kw, message):
+    """decode.py:132-146, 336-351: window arguments are checked before any window is decoded."""
+    import torch
+
+    args = {"roi": (4, 4, 4), "overlap": 0.25}
+    args.update(kw)
+    called = []
+    with pytest.raises(ValueError, match=message):
+        ctmr.maisi.sliding_window(torch.zeros(1, 8, 8, 8, 4), lambda t: called.append(t), **args)
+    assert not called
+
+
+def test_window_helpers_validate(ctmr):
+    m = ctmr.maisi
+    with pytest.raises(ValueError, match="overlap"):
+        m.scan_interval((8, 8, 8), (4, 4, 4), 1.5)
+    with pytest.raises(ValueError, match="image_size"):
+        m.scan_interval((8, 8), (4, 4, 4), 0.5)
+    with pytest.raises(ValueError, match="interval"):
+        m.dense_patch_slices((8, 8, 8), (4, 4, 4), (0, 1, 1))
+    with pytest.raises(ValueError, match="sigma_scale"):
+        m.gaussian_importance((4, 4, 4), 0.0)
+    with pytest.raises(ValueError, match="roi"):
+        m.sliding_window_decode(None, {}, constructor={}, roi=(1, 2))
+    assert m.scan_interval((64, 64, 64), (20, 64, 64), 0.25) == (15, 64, 64)
