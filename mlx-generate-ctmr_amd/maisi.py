@@ -439,6 +439,13 @@ def controlnet_residuals(
         if tuple(int(s) for s in cond.shape[1:4]) != expected:
             raise ValueError(f"controlnet cond spatial {tuple(cond.shape[1:4])} must be {scale}x latent")
     channels = tuple(int(c) for c in constructor["num_channels"])
+    if conditioning_embedding is not None:  # controlnet.py:96-104
+        expected = (int(x.shape[0]), *(int(s) for s in x.shape[1:4]), channels[0])
+        if tuple(int(s) for s in conditioning_embedding.shape) != expected:
+            raise ValueError(f"controlnet conditioning embedding shape {tuple(conditioning_embedding.shape)} "
+                             f"must be {expected}")
+        if conditioning_embedding.dtype != torch.float32:
+            raise ValueError("controlnet conditioning embedding must be float32")
     n_levels = len(channels)
     res_blocks = _per_level(constructor["num_res_blocks"], n_levels)
     attn_levels = tuple(bool(a) for a in constructor["attention_levels"])
@@ -1036,3 +1043,229 @@ def spacing_tensor(spacing_mm: Sequence[float], device=None) -> Tensor:
     """``spacing_mm * 100`` rounded through float16, ``(1, 3)`` fp32 (image.py:90-115)."""
     scaled = np.asarray([spacing_mm], dtype=np.float64) * 100.0
     return torch.from_numpy(scaled.astype(np.float16).astype(np.float32)).to(device)
+
+
+# ---------------------------------------------------------------------------
+# CT from a label mask: ControlNet-conditioned rflow sampling + windowed decode
+# + label-masked Hounsfield units (from_mask.py:121-338, condition.py:20-62,
+# decode.py:248-259)
+# ---------------------------------------------------------------------------
+CT_MODALITY = 1  # modality index "ct" of the reference's configurations table (default for CT)
+LABEL_BITS = 8
+BODY_LABEL = 200
+VALID_LABELS = frozenset(range(133)) | {BODY_LABEL}  # MAISI ids 0..132 plus the body envelope
+SUPPORTED_PRODUCTION_SHAPES = ((256, 256, 128), (256, 256, 256))
+SEAM_NOT_APPLICABLE = "not_applicable_below_roi"
+DEFAULT_STEPS = 30
+
+
+def require_ct_label(label: np.ndarray) -> np.ndarray:
+    """Host ``(N, 1, D, H, W)`` integer MAISI label map, validated (from_mask.py:355-378): ids in
+    0..132 plus body 200, body present, spatial sizes multiples of 4."""
+    host = np.asarray(label)
+    if host.ndim != 5 or int(host.shape[1]) != 1:
+        raise ValueError(f"label must be NCDHW with 1 channel; got {host.shape}")
+    if not np.issubdtype(host.dtype, np.integer):
+        raise ValueError(f"label must be integer; got {host.dtype}")
+    unique = {int(v) for v in np.unique(host)}
+    unknown = sorted(v for v in unique if v not in VALID_LABELS)
+    if unknown:
+        raise ValueError("MAISI mask contains labels outside 0..132 plus body label 200: "
+                         + ", ".join(str(v) for v in unknown[:10]))
+    if BODY_LABEL not in unique:
+        raise ValueError("MAISI mask is missing body-envelope label 200; add it before generation")
+    spatial = tuple(int(s) for s in host.shape[2:])
+    if any(s % Z_SCALE for s in spatial):
+        raise ValueError(f"label spatial {spatial} must be multiples of {Z_SCALE}")
+    return host
+
+
+def require_supported_production_shape(shape: Sequence[int]) -> tuple[int, int, int]:
+    """The label grids the reference's from-mask sampler accepts (from_mask.py:101-118)."""
+    spatial = tuple(int(v) for v in shape)
+    if len(spatial) != 3:
+        raise ValueError(f"MLX NV-Generate-CT mask shape must be 3D; got {spatial}")
+    if spatial not in SUPPORTED_PRODUCTION_SHAPES:
+        raise ValueError(f"from_mask shape {spatial} is not production-proven; supported shapes: "
+                         "(256, 256, 128) and (256, 256, 256)")
+    return spatial[0], spatial[1], spatial[2]
+
+
+def require_scale_factor(scale_factor: float) -> float:
+    """A finite non-zero latent scale from the UNet checkpoint; no default (from_mask.py:341-352)."""
+    value = float(scale_factor)
+    if not math.isfinite(value) or value == 0.0:
+        raise ValueError(f"scale_factor must be a finite non-zero caller value; got {scale_factor!r}")
+    return value
+
+
+def binarize_labels(label: Tensor) -> Tensor:
+    """The 8-channel ControlNet condition of an integer label map, NDHWC: channel ``k`` of the
+    ``(N, D, H, W, 8)`` float32 result is bit ``k`` of the id, least significant first
+    (condition.py:20-43).  ``label`` is ``(N, D, H, W)`` or ``(N, D, H, W, 1)`` integers."""
+    if label.dim() == 5:
+        if int(label.shape[-1]) != 1:
+            raise ValueError(f"maisi label must have 1 channel; got {int(label.shape[-1])}")
+        label = label[..., 0]
+    if label.dim() != 4:
+        raise ValueError(f"maisi label must be (N, D, H, W[, 1]); got {tuple(label.shape)}")
+    ids = label.to(torch.int32).unsqueeze(-1)
+    powers = torch.bitwise_left_shift(torch.ones(LABEL_BITS, dtype=torch.int32, device=label.device),
+                                      torch.arange(LABEL_BITS, dtype=torch.int32, device=label.device))
+    return (torch.bitwise_and(ids, powers) != 0).to(torch.float32).contiguous()
+
+
+def ct_spacing_tensor(spacing_mm: Sequence[float], device=None) -> Tensor:
+    """``spacing_mm * 100`` as a ``(1, 3)`` float32 tensor, no float16 rounding (the from-mask
+    path, condition.py:46-62; the image-only path rounds, ``spacing_tensor``)."""
+    if len(spacing_mm) != 3:
+        raise ValueError(f"spacing_mm must have 3 values; got {tuple(spacing_mm)}")
+    values = [float(v) * 100.0 for v in spacing_mm]
+    if any(not math.isfinite(v) or v <= 0.0 for v in values):
+        raise ValueError(f"spacing_mm * 100.0 must be finite and > 0; got {values}")
+    return torch.tensor([values], dtype=torch.float32, device=device)
+
+
+def to_hu(image: Tensor, label: Tensor) -> Tensor:
+    """Decoded intensities to float32 Hounsfield units: ``clip(x, 0, 1) * 2000 - 1000``, and -1000
+    where the label is background (0) (decode.py:248-259).  NDHWC ``image`` ``(N, D, H, W, 1)``;
+    ``label`` of the same spatial shape, with or without the channel axis."""
+    if label.dim() == image.dim() - 1:
+        label = label.unsqueeze(-1)
+    if tuple(label.shape) != tuple(image.shape):
+        raise ValueError(f"label shape {tuple(label.shape)} does not match the image {tuple(image.shape)}")
+    hu = torch.clamp(image, 0.0, 1.0) * 2000.0 - 1000.0
+    return torch.where(label == 0, torch.full_like(hu, -1000.0), hu)
+
+
+class FromMaskResult:
+    """Outputs of ``sample_ct_from_mask`` (the reference's FromMaskArrays, from_mask.py:67-86), NDHWC on
+    the GPU: ``latent`` the sampled latent before the scale division, ``decoded`` the VAE output,
+    ``hu`` float32 Hounsfield units (label 0 forced to -1000), ``seam_audit`` ``"tiled"`` when the decode
+    used more than one window, ``stage_timings_s`` synchronized wall-clock seconds per stage."""
+
+    def __init__(self, latent, decoded, hu, scale_factor, num_inference_steps, seam_audit, stage_timings_s):
+        self.latent, self.decoded, self.hu = latent, decoded, hu
+        self.scale_factor, self.num_inference_steps = scale_factor, num_inference_steps
+        self.seam_audit, self.stage_timings_s = seam_audit, dict(stage_timings_s)
+
+
+def ct_velocity(cond_embedding: Tensor, class_labels: Tensor, spacing: Tensor, *, unet_weights, controlnet_weights,
+                unet_constructor, controlnet_constructor, overlap_streams: bool = True) -> Callable[[Tensor, float], Tensor]:
+    """The ControlNet-conditioned UNet velocity of one generation (from_mask.py:298-338): per step the
+    ControlNet's residuals (from the conditioning embedding computed once) feed the UNet.  With
+    ``overlap_streams`` the ControlNet runs on a second stream beside the UNet encoder
+    (``controlnet_unet_step``; the same bits as the serial composition)."""
+
+    def velocity(state: Tensor, timestep: float) -> Tensor:
+        t = torch.full((state.shape[0],), float(timestep), dtype=torch.float32, device=state.device)
+        if overlap_streams:
+            return controlnet_unet_step(state, t, class_labels, spacing, unet_weights, controlnet_weights,
+                                        unet_constructor=unet_constructor, controlnet_constructor=controlnet_constructor,
+                                        conditioning_embedding=cond_embedding)[1]
+        down, mid = controlnet_residuals(state, t, class_labels, None, controlnet_weights,
+                                         constructor=controlnet_constructor, conditioning_embedding=cond_embedding)
+        return denoise_unet(state, t, class_labels, spacing, unet_weights, constructor=unet_constructor,
+                            down_block_additional_residuals=down, mid_block_additional_residual=mid)[1]
+
+    return velocity
+
+
+def _synced_time(device) -> float:
+    import time
+
+    torch.cuda.synchronize(device)
+    return time.perf_counter()
+
+
+def sample_ct_latent(label: np.ndarray, spacing_mm: Sequence[float], *, unet_weights: Mapping[str, Tensor],
+                     controlnet_weights: Mapping[str, Tensor], unet_constructor: Mapping,
+                     controlnet_constructor: Mapping, scale_factor: float, latent: Optional[Tensor] = None,
+                     seed: Optional[int] = None, num_inference_steps: int = DEFAULT_STEPS,
+                     guidance_scale: float = 0.0, device=None, overlap_streams: bool = True,
+                     drop_weights: bool = True) -> tuple[Tensor, float]:
+    """ControlNet-conditioned rflow sampling of a CT latent (from_mask.py:177-248); returns the NDHWC
+    latent ``(N, D/4, H/4, W/4, 4)`` and the sampling seconds.
+
+    The condition is encoded once; each of the ``num_inference_steps`` steps runs the ControlNet and
+    the UNet at the label's batch (no guidance: ``guidance_scale`` must be 0).  ``latent`` (NDHWC) or
+    ``seed`` gives the start: the reference draws it from MLX's generator, here ``seed`` seeds a torch
+    generator on the device, so seeded latents differ from the reference's (pass ``latent`` for the
+    same start).  With ``drop_weights`` the packed copies of both networks' weights are released after
+    sampling, as the reference does before decoding (from_mask.py:240).
+    """
+    if float(guidance_scale) != 0.0:
+        raise ValueError("CFG>0 majority vote is not an MLX destination")
+    require_scale_factor(scale_factor)
+    host = require_ct_label(label)
+    device = torch.device(device) if device is not None else next(iter(unet_weights.values())).device
+    n = int(host.shape[0])
+    latent_shape = (n, *(int(s) // Z_SCALE for s in host.shape[2:]), 4)
+    if latent is None:
+        if seed is None:
+            raise ValueError("seed is required when latent is omitted")
+        gen = torch.Generator(device=device).manual_seed(int(seed))
+        latent = torch.randn(latent_shape, generator=gen, device=device, dtype=torch.float32)
+    elif tuple(int(s) for s in latent.shape) != latent_shape:
+        raise ValueError(f"latent shape {tuple(int(s) for s in latent.shape)} != {latent_shape}")
+    label_dev = torch.from_numpy(np.ascontiguousarray(host[:, 0])).to(device)
+    cond = binarize_labels(label_dev)
+    spacing = ct_spacing_tensor(spacing_mm, device=device).repeat(n, 1)
+    class_labels = torch.full((n,), CT_MODALITY, dtype=torch.int64, device=device)
+    timesteps, _ = set_timesteps_rflow(num_inference_steps=int(num_inference_steps),
+                                       input_img_size_numel=int(np.prod(latent_shape[1:4])))
+    start = _synced_time(device)
+    embedding = encode_controlnet_condition(cond, controlnet_weights, constructor=controlnet_constructor)
+    del cond
+    velocity = ct_velocity(embedding, class_labels, spacing, unet_weights=unet_weights,
+                           controlnet_weights=controlnet_weights, unet_constructor=unet_constructor,
+                           controlnet_constructor=controlnet_constructor, overlap_streams=overlap_streams)
+    final = sample_rflow(latent, velocity, timesteps)
+    seconds = _synced_time(device) - start
+    del embedding, velocity
+    if drop_weights:
+        ff.drop_packed_weights([*unet_weights.values(), *controlnet_weights.values()])
+    return final, seconds
+
+
+def decode_ct_latent(latent: Tensor, label: np.ndarray, *, vae_weights: Mapping[str, Tensor], vae_constructor: Mapping,
+                     scale_factor: float, roi: Sequence[int] = DEFAULT_ROI_SIZE,
+                     overlap: float = DEFAULT_OVERLAP) -> tuple[Tensor, Tensor, str, dict[str, float]]:
+    """Windowed decode of a sampled CT latent and its label-masked HU image (from_mask.py:251-295):
+    returns ``(decoded, hu, seam_audit, timings)``, NDHWC."""
+    host = require_ct_label(label)
+    factor = require_scale_factor(scale_factor)
+    device = latent.device
+    start = _synced_time(device)
+    decoded = sliding_window_decode(latent, vae_weights, constructor=vae_constructor, roi=roi, overlap=overlap,
+                                    scale_factor=factor)
+    mid = _synced_time(device)
+    hu = to_hu(decoded, torch.from_numpy(np.ascontiguousarray(host[:, 0])).to(device))
+    end = _synced_time(device)
+    spatial = tuple(int(s) for s in decoded.shape[1:4])
+    seam = SEAM_NOT_APPLICABLE if math.prod(spatial) <= math.prod(int(r) * Z_SCALE for r in roi) else "tiled"
+    return decoded, hu, seam, {"vae_decode": mid - start, "hu_postprocess": end - mid}
+
+
+def sample_ct_from_mask(label: np.ndarray, spacing_mm: Sequence[float], *, unet_weights: Mapping[str, Tensor],
+                        controlnet_weights: Mapping[str, Tensor], vae_weights: Mapping[str, Tensor],
+                        unet_constructor: Mapping, controlnet_constructor: Mapping, vae_constructor: Mapping,
+                        scale_factor: float, seed: Optional[int] = None, latent: Optional[Tensor] = None,
+                        num_inference_steps: int = DEFAULT_STEPS, guidance_scale: float = 0.0,
+                        roi: Sequence[int] = DEFAULT_ROI_SIZE, overlap: float = DEFAULT_OVERLAP,
+                        overlap_streams: bool = True, drop_weights: bool = True) -> FromMaskResult:
+    """A CT volume from a MAISI label map (from_mask.py:121-174): ControlNet-conditioned rflow sampling,
+    then the windowed VAE decode of ``latent / scale_factor`` and the HU conversion.  ``label`` is a host
+    ``(N, 1, D, H, W)`` integer array; results are NDHWC GPU tensors."""
+    final, rflow_s = sample_ct_latent(label, spacing_mm, unet_weights=unet_weights,
+                                      controlnet_weights=controlnet_weights, unet_constructor=unet_constructor,
+                                      controlnet_constructor=controlnet_constructor, scale_factor=scale_factor,
+                                      latent=latent, seed=seed, num_inference_steps=num_inference_steps,
+                                      guidance_scale=guidance_scale, overlap_streams=overlap_streams,
+                                      drop_weights=drop_weights)
+    decoded, hu, seam, timings = decode_ct_latent(final, label, vae_weights=vae_weights,
+                                                  vae_constructor=vae_constructor, scale_factor=scale_factor,
+                                                  roi=roi, overlap=overlap)
+    stages = {"rflow_controlnet_unet": rflow_s, **timings}
+    stages["total_synchronized_inference"] = rflow_s + timings["vae_decode"] + timings["hu_postprocess"]
+    return FromMaskResult(final, decoded, hu, float(scale_factor), int(num_inference_steps), seam, stages)

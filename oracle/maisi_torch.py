@@ -9,6 +9,8 @@ HIP composition it checks:
   VAE decoder      vae.py:29-62, 103-200, 273-379 (materialized trilinear upsampling)
   sliding window   decode.py:30-245
   ControlNet       controlnet.py:31-274
+  CT from mask     from_mask.py:177-338 (sampling loop), condition.py:20-43 (label bits),
+                   decode.py:248-259 (HU)
 Pinned by the reference goldens in tests/golden (tests/test_oracle_networks.py).  The ControlNet
 has no recorded outputs in the reference fixtures (its boundary arrays live outside the repository);
 its shared down path is pinned through the UNet goldens and an identity invariant, its conditioning
@@ -265,6 +267,36 @@ def sliding_window_decode(z, w, ctor, roi, overlap, scale_factor=None, sigma_sca
     return out / wsum
 
 
+def binarize_labels(label):
+    """``(N, 1, D, H, W)`` integer ids -> ``(N, 8, D, H, W)`` float condition, channel k = bit k
+    (condition.py:20-43), written as repeated halving instead of masks."""
+    ids = label[:, 0].long()
+    bits = []
+    for _ in range(8):
+        bits.append((ids % 2).to(torch.float32))
+        ids = torch.div(ids, 2, rounding_mode="floor")
+    return torch.stack(bits, dim=1)
+
+
+def to_hu(image, label):
+    """Label-masked Hounsfield units (decode.py:248-259), NCDHW."""
+    hu = image.clamp(0.0, 1.0) * 2000.0 - 1000.0
+    return torch.where(label == 0, torch.full_like(hu, -1000.0), hu)
+
+
+def ct_sample(latent, cond, spacing, class_labels, unet_w, ctrl_w, unet_ctor, ctrl_ctor, timesteps):
+    """ControlNet-conditioned rflow Euler sampling (from_mask.py:177-248, 298-338; rflow.py:100-177),
+    NCDHW, with the ControlNet's residuals recomputed from ``cond`` every step."""
+    nxt = list(timesteps[1:]) + [0.0]
+    z = latent
+    for t, tn in zip(timesteps, nxt):
+        tt = torch.full((z.shape[0],), float(t), dtype=z.dtype)
+        down, mid = controlnet(z, tt, class_labels, cond, ctrl_w, ctrl_ctor)
+        _, v = unet(z, tt, class_labels, spacing, unet_w, unet_ctor, down_residuals=down, mid_residual=mid)
+        z = z + v * ((float(t) - int(float(tn))) / 1000.0)
+    return z
+
+
 def rflow_timesteps(steps: int, numel: int) -> np.ndarray:
     """The float16-rounded rflow schedule (rflow.py:19-97)."""
     out = []
@@ -281,4 +313,5 @@ def to_torch(weights: Mapping[str, np.ndarray], dtype=torch.float64, strip: str 
 
 
 __all__ = ["residual_block", "attention", "unet", "down_path", "mid_block", "controlnet", "controlnet_condition",
-           "vae_decode", "sliding_window_decode", "rflow_timesteps", "to_torch", "rm"]
+           "vae_decode", "sliding_window_decode", "rflow_timesteps", "to_torch", "binarize_labels", "to_hu",
+           "ct_sample", "rm"]

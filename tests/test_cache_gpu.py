@@ -49,7 +49,7 @@ def test_inplace_weight_update_repacks(ctmr, dev):
 
 
 def test_inplace_qkv_bias_update_refuses_stale_fusion(ctmr, dev):
-    """The fused Q/K/V projection includes the biases: a q bias changed in place is fused again."""
+    """The fused Q/K/V projection includes the biases: q and v biases changed in place are fused again."""
     manifest, a = load_boundary("attention")
     c = manifest["constructor"]
     weights = {k[len("weight."):]: _g(v, dev) for k, v in a.items() if k.startswith("weight.")}
@@ -59,11 +59,11 @@ def test_inplace_qkv_bias_update_refuses_stale_fusion(ctmr, dev):
                                                         eps=c["norm_eps"], num_head_channels=c["num_head_channels"],
                                                         include_fc=c.get("include_fc", True))))
     np.testing.assert_allclose(run(), a["y"], rtol=1e-4, atol=1e-5)
-    key = "attn.to_q.bias"
-    weights[key].add_(0.5)
     host = {k: torch.from_numpy(np.asarray(v, np.float64)) for k, v in
             ((k[len("weight."):], v) for k, v in a.items() if k.startswith("weight."))}
-    host[key] = host[key] + 0.5
+    for key, delta in (("attn.to_q.bias", 2.0), ("attn.to_v.bias", 0.5)):
+        weights[key].add_(delta)
+        host[key] = host[key] + delta
     with torch.no_grad():
         ref = mt.attention(torch.from_numpy(np.asarray(a["x"], np.float64)), host, c["norm_num_groups"], c["norm_eps"],
                            c["num_head_channels"], c.get("include_fc", True)).numpy()
@@ -84,10 +84,12 @@ def test_inplace_time_projection_bias_update(ctmr, dev):
             if k.startswith("weight.")}
     args = (_g(a["x"], dev), _g(a["timesteps"], dev), _g(a["class_labels"], dev, torch.int64), _g(a["spacing"], dev))
     y0 = _h(m.denoise_unet_ncdhw(*args, w, constructor=ctor)[1])
-    for name, delta in (("down_blocks.0.resnets.0.time_emb_proj.bias", 0.25),
-                        ("down_blocks.0.resnets.0.conv1.conv.bias", -0.5)):
-        w[name].add_(delta)
-        host[name] = host[name] + delta
+    # per-channel deltas (a uniform shift of every channel of a group is removed by norm2)
+    for name, lo, hi in (("down_blocks.0.resnets.0.time_emb_proj.bias", -0.5, 0.75),
+                         ("down_blocks.0.resnets.0.conv1.conv.bias", 0.6, -0.4)):
+        delta = np.linspace(lo, hi, int(w[name].numel()))
+        w[name].add_(torch.from_numpy(delta.astype(np.float32)).to(dev))
+        host[name] = host[name] + torch.from_numpy(delta)
     y1 = _h(m.denoise_unet_ncdhw(*args, w, constructor=ctor)[1])
     with torch.no_grad():
         _, ref = mt.unet(torch.from_numpy(np.asarray(a["x"], np.float64)),

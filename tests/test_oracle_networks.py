@@ -223,3 +223,168 @@ def test_planted_unscaled_scores_fail_attention_golden():
     y = x + out.transpose(1, 2).reshape(x.shape)
     with pytest.raises(AssertionError):
         np.testing.assert_allclose(y.numpy(), a["y"], rtol=RES_RTOL, atol=RES_ATOL)
+
+
+# --- ControlNet: closed-form pins of the conditioning encoder and the conditioning scale -------------
+def _encoder_brute_force(cond_ndhwc, w, ctor, *, strides=(1, 2), silu_mask=None):
+    """Conditioning encoder (controlnet.py:194-249) composed layer by layer from the float64 NumPy
+    oracle (oracle/reference_math, pinned on the recorded conv/SiLU goldens): conv_in + SiLU, per
+    level a conv of stride ``strides[0]`` + SiLU and one of ``strides[1]`` + SiLU, conv_out.
+    ``silu_mask`` (one flag per SiLU) plants a dropped SiLU."""
+    from oracle import reference_math as rm
+
+    p = "controlnet_cond_embedding"
+    get = lambda k: w[k].numpy()
+    flags = iter(silu_mask or [True] * 99)
+    act = lambda v: rm.silu(v) if next(flags) else v
+    h = act(rm.conv3d(cond_ndhwc, get(f"{p}.conv_in.conv.weight"), get(f"{p}.conv_in.conv.bias")))
+    block = 0
+    for _ in range(len(ctor["conditioning_embedding_num_channels"]) - 1):
+        for stride in strides:
+            h = act(rm.conv3d(h, get(f"{p}.blocks.{block}.conv.weight"), get(f"{p}.blocks.{block}.conv.bias"),
+                              stride=stride))
+            block += 1
+    return rm.conv3d(h, get(f"{p}.conv_out.conv.weight"), get(f"{p}.conv_out.conv.bias"))
+
+
+def _controlnet_fixture():
+    f = load_fixture("controlnet.npz")
+    ctor = f["__metadata__"]["constructor"]
+    cond = np.random.default_rng(21).integers(0, 2, (1, 16, 16, 16, 8)).astype(np.float64)
+    return f, ctor, mt.to_torch(f), cond
+
+
+def test_controlnet_encoder_matches_brute_force_and_planted_mistakes_fail():
+    """The oracle's encoder (torch F.conv3d) equals the NumPy layer-by-layer composition on the recorded
+    recipe network with a non-zero conv_out; swapping each level's stride order, or dropping the SiLU
+    after a stride-2 conv, changes the embedding beyond the comparison tolerance."""
+    _, ctor, w, cond = _controlnet_fixture()
+    got = mt.controlnet_condition(torch.from_numpy(np.moveaxis(cond, -1, 1).copy()), w, ctor)
+    got = np.moveaxis(got.numpy(), 1, -1)
+    assert np.abs(got).max() > 1e-3  # conv_out is live
+    np.testing.assert_allclose(got, _encoder_brute_force(cond, w, ctor), rtol=1e-10, atol=1e-12)
+    scale = np.abs(got).max()
+    with pytest.raises(AssertionError):  # stride-2 first, then stride-1
+        np.testing.assert_allclose(got, _encoder_brute_force(cond, w, ctor, strides=(2, 1)), rtol=0,
+                                   atol=1e-6 * scale)
+    with pytest.raises(AssertionError):  # SiLU dropped after the first stride-2 conv
+        np.testing.assert_allclose(got, _encoder_brute_force(cond, w, ctor, silu_mask=[True, True, False, True, True]),
+                                   rtol=0, atol=1e-6 * scale)
+
+
+def test_controlnet_first_residual_is_conv_in_plus_embedding():
+    """With identity zero convs, the first down residual is the skip taken before any block:
+    conv_in(x) + encoder(cond) (controlnet.py:119-131) -- so the embedding joins right after conv_in.
+    Closed form from the NumPy oracle."""
+    from oracle import reference_math as rm
+
+    f, ctor, w, cond = _controlnet_fixture()
+    for k in list(w):
+        if k.startswith("controlnet_down_blocks.") or k.startswith("controlnet_mid_block."):
+            if k.endswith("weight"):
+                c = w[k].shape[0]
+                w[k] = torch.eye(c, dtype=D).reshape(c, c, 1, 1, 1)
+            else:
+                w[k] = torch.zeros_like(w[k])
+    x = np.asarray(f["input.x"], np.float64)
+    down, _ = mt.controlnet(torch.from_numpy(x), _t(f["input.timesteps"]), torch.from_numpy(f["input.class_labels"]),
+                            torch.from_numpy(np.moveaxis(cond, -1, 1).copy()), w, ctor)
+    x_nd = np.moveaxis(x, 1, -1)
+    expected = rm.conv3d(x_nd, w["conv_in.conv.weight"].numpy(), w["conv_in.conv.bias"].numpy()) + \
+        _encoder_brute_force(cond, w, ctor)
+    np.testing.assert_allclose(np.moveaxis(down[0].numpy(), 1, -1), expected, rtol=1e-10, atol=1e-12)
+
+
+def test_controlnet_conditioning_scale_multiplies_zero_conv_outputs():
+    """``conditioning_scale`` multiplies every zero-conv output, bias included, down and mid alike
+    (controlnet.py:160-163): with zero 1x1 weights each residual is exactly ``scale * bias``; with the
+    recipe weights the residuals are exactly linear in the scale."""
+    f, ctor, w, cond = _controlnet_fixture()
+    args = (_t(f["input.x"]), _t(f["input.timesteps"]), torch.from_numpy(f["input.class_labels"]),
+            torch.from_numpy(np.moveaxis(cond, -1, 1).copy()))
+    base_down, base_mid = mt.controlnet(*args, w, ctor)
+    down, mid = mt.controlnet(*args, w, ctor, scale=-0.375)
+    for a, b in zip(down + [mid], base_down + [base_mid]):
+        np.testing.assert_allclose(a.numpy(), -0.375 * b.numpy(), rtol=1e-12, atol=1e-15)
+    zw = dict(w)
+    biases = {}
+    for k in list(zw):
+        if (k.startswith("controlnet_down_blocks.") or k.startswith("controlnet_mid_block.")) and k.endswith("weight"):
+            zw[k] = torch.zeros_like(zw[k])
+        elif k.startswith("controlnet_down_blocks.") or k.startswith("controlnet_mid_block."):
+            biases[k] = zw[k]
+    down, mid = mt.controlnet(*args, zw, ctor, scale=2.5)
+    keys = [k for k in sorted(biases, key=lambda s: (s.startswith("controlnet_mid"),
+                                                     int(s.split(".")[1]) if s.startswith("controlnet_down") else 0))]
+    for res, key in zip(down + [mid], keys):
+        expected = 2.5 * biases[key].numpy().reshape(1, -1, 1, 1, 1) * np.ones(res.shape)
+        np.testing.assert_allclose(res.numpy(), expected, rtol=1e-15, atol=0)
+
+
+# --- CT from mask: label bits, HU, sampling loop ------------------------------------------------------
+def test_binarize_labels_recomposes_every_id(ctmr):
+    """Both restatements of condition.py:20-43 (the product's bit masks, the oracle's halving) give
+    channels whose weighted sum sum_k 2^k c_k is the label id, for every valid MAISI id."""
+    ids = np.array(sorted(ctmr.maisi.VALID_LABELS), np.int64)
+    lab = ids.reshape(1, 1, 1, 1, -1)
+    ora = mt.binarize_labels(torch.from_numpy(lab)).numpy()  # (1, 8, 1, 1, L)
+    prod = ctmr.maisi.binarize_labels(torch.from_numpy(lab[:, 0])).numpy()  # (1, 1, 1, L, 8)
+    weights = 2.0 ** np.arange(8)
+    np.testing.assert_array_equal((ora[0, :, 0, 0, :] * weights[:, None]).sum(0), ids)
+    np.testing.assert_array_equal(np.moveaxis(ora, 1, -1)[0, 0], prod[0, 0])
+    assert set(np.unique(prod)) <= {0.0, 1.0} and prod.dtype == np.float32
+
+
+def test_to_hu_closed_form(ctmr):
+    img = torch.tensor([-0.5, 0.0, 0.25, 0.5, 1.0, 1.5]).reshape(1, 1, 1, 6, 1)  # NDHWC
+    lab = torch.tensor([1, 1, 200, 0, 5, 1]).reshape(1, 1, 1, 6)
+    expected = [-1000.0, -1000.0, -500.0, -1000.0, 1000.0, 1000.0]
+    np.testing.assert_array_equal(ctmr.maisi.to_hu(img, lab).reshape(-1).numpy(), expected)
+    np.testing.assert_array_equal(mt.to_hu(img.reshape(1, 1, 1, 1, 6), lab.reshape(1, 1, 1, 1, 6)).reshape(-1).numpy(),
+                                  expected)
+
+
+def test_ct_label_validation(ctmr):
+    m = ctmr.maisi
+    ok = np.full((1, 1, 8, 8, 8), 200, np.int16)
+    m.require_ct_label(ok)
+    with pytest.raises(ValueError, match="1 channel"):
+        m.require_ct_label(ok[:, 0])
+    with pytest.raises(ValueError, match="integer"):
+        m.require_ct_label(ok.astype(np.float32))
+    bad = ok.copy()
+    bad[0, 0, 0, 0, 0] = 150
+    with pytest.raises(ValueError, match="outside 0..132"):
+        m.require_ct_label(bad)
+    with pytest.raises(ValueError, match="body-envelope"):
+        m.require_ct_label(np.zeros((1, 1, 8, 8, 8), np.int32))
+    with pytest.raises(ValueError, match="multiples of 4"):
+        m.require_ct_label(np.full((1, 1, 8, 8, 6), 200, np.int32))
+    with pytest.raises(ValueError, match="scale_factor"):
+        m.require_scale_factor(float("nan"))
+    with pytest.raises(ValueError, match="not production-proven"):
+        m.require_supported_production_shape((128, 128, 128))
+    assert m.require_supported_production_shape([256, 256, 128]) == (256, 256, 128)
+    with pytest.raises(ValueError, match="finite and > 0"):
+        m.ct_spacing_tensor([1.0, 0.0, 1.0])
+    np.testing.assert_array_equal(m.ct_spacing_tensor([0.703125, 0.703125, 1.25]).numpy(), [[70.3125, 70.3125, 125.0]])
+
+
+def test_ct_sampling_oracle_euler_identity():
+    """With every zero conv and the UNet's output conv set to zero except the output bias ``b``,
+    the velocity is the constant ``b``; the sampler then moves the latent by ``b * sum(dt)`` with
+    ``dt = (t - int(t_next)) / 1000`` (rflow.py:100-119)."""
+    f, ctor, w, _ = _controlnet_fixture()
+    uf = load_fixture("unet.npz")
+    uctor = uf["__metadata__"]["constructor"]
+    uw = mt.to_torch(uf)
+    uw["out.2.conv.weight"] = torch.zeros_like(uw["out.2.conv.weight"])
+    b = uw["out.2.conv.bias"]
+    z0 = torch.from_numpy(np.random.default_rng(3).standard_normal((1, 4, 4, 4, 4)))
+    cond = mt.binarize_labels(torch.full((1, 1, 16, 16, 16), 200, dtype=torch.int64)).to(D)
+    times = mt.rflow_timesteps(3, 64)
+    ctor_u = dict(uctor)
+    z = mt.ct_sample(z0, cond, _t(uf["input.spacing"]), torch.tensor([1]), uw, w, ctor_u, ctor, times)
+    total = sum((float(t) - int(float(tn))) / 1000.0 for t, tn in zip(times, list(times[1:]) + [0.0]))
+    np.testing.assert_allclose(z.numpy(), z0.numpy() + total * b.numpy().reshape(1, -1, 1, 1, 1), rtol=1e-12,
+                               atol=1e-12)
