@@ -172,6 +172,24 @@ int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ctmr_conv3d without a caller workspace and without any allocation: the
+ * workspace is a library-owned device array of CTMR_NOALLOC_SCRATCH_BYTES per
+ * GPU (allocated when the library's code is loaded on that GPU, held until
+ * the process ends).  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same kernels and bits as
+ * ctmr_conv3d.  A convolution whose ctmr_conv3d_workspace_bytes exceeds the
+ * limit returns CTMR_E_WORKSPACE (256 MiB covers every conv of the MAISI UNet
+ * and ControlNet steps at a 64x64x32 latent, batch 2; not the decoder's
+ * full-resolution levels).  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race.  Call
+ * with the stream's device current.
+ */
+#define CTMR_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+int ctmr_conv3d_noalloc(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                        const float* affine, const float* residual, float* y, void* stream);
+
+/*
  * The two stages of ctmr_conv3d, callable separately with the same arguments
  * (ctmr_conv3d == ctmr_conv3d_pack then ctmr_conv3d_gemm on one stream).
  * _pack writes the zero-padded, transformed input copy (the reference's pack

@@ -17,7 +17,7 @@ CSRC = PACKAGE_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libctmr_hip.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
-SOURCES = ("conv.hip", "norm.hip", "attention.hip")
+SOURCES = ("conv.hip", "norm.hip", "attention.hip", "noalloc.hip")
 ARCH = "gfx950"
 
 # Packed FP32 VALU ops are disabled for every device pass; hipcc's host pass

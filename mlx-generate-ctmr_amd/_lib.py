@@ -24,6 +24,7 @@ K_STREAM, K_STREAM_DIRECT, K_LDS, K_LDS_BF16, K_POINTWISE, K_SPLIT_WAVES, K_TAP_
 KERNEL_NAMES = ("stream", "stream_direct", "lds", "lds_bf16", "pointwise", "split_waves", "tap_expand")
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2
 ABI_VERSION = 1
+NOALLOC_SCRATCH_BYTES = 256 << 20  # CTMR_NOALLOC_SCRATCH_BYTES
 
 
 class ConvDesc(ctypes.Structure):
@@ -58,6 +59,7 @@ _PROTOTYPES = {
     "ctmr_pack_weight": (_c_int, [_desc_p, _vp, _vp, _vp]),
     "ctmr_pack_upsample_weight": (_c_int, [_desc_p, _vp, _vp, _vp]),
     "ctmr_conv3d": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ctmr_conv3d_noalloc": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ctmr_conv3d_pack": (_c_int, [_desc_p, _vp, _vp, _vp, _sz, _vp]),
     "ctmr_conv3d_gemm": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ctmr_conv3d_stats_tiles": (_c_i32, [_desc_p, _c_i32]),

@@ -1,0 +1,86 @@
+"""``ctmr_conv3d_noalloc`` (the allocation-free variant of ``ctmr_conv3d``) through the C ABI.
+
+Its workspace is the library's own per-GPU scratch array; the output must equal ``ctmr_conv3d``'s
+(caller workspace, same kernels) bit for bit, on consecutive calls whose second input is smaller
+(the scratch keeps the previous call's contents), and a convolution whose workspace exceeds the
+scratch limit must be refused before anything is launched.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _g(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _case(ctmr, dev, seed, shape, cout, *, mode=0, affine=True, batch_bias=True, residual=True):
+    """Inputs of one conv, its output through ctmr_conv3d (ops.conv3d) and the noalloc call's arguments."""
+    L, ops = ctmr._lib, ctmr.ops
+    rng = np.random.default_rng(seed)
+    n, d, h, w, cin = shape
+    x = _g(rng.standard_normal(shape).astype(np.float32), dev)
+    wt = _g((rng.standard_normal((cout, cin, 3, 3, 3)) / np.sqrt(27 * cin)).astype(np.float32), dev)
+    packed = (ctmr.fast_fp32.pack_upsample_weight if mode == L.MODE_NEAREST2X else ctmr.fast_fp32.pack_weight)(
+        wt, dtype="fp32")
+    bias = _g(rng.standard_normal((n, cout) if batch_bias else (cout,)).astype(np.float32), dev)
+    aff = _g(np.stack([1 + 0.2 * rng.standard_normal((n, cin)), 0.3 * rng.standard_normal((n, cin))],
+                      axis=-1).astype(np.float32), dev) if affine else None
+    desc = ops.make_desc(shape, cout, 3, 1, mode, 0, L.DT_F32, 0)
+    od, oh, ow = L.output_dims(desc)
+    res = _g(rng.standard_normal((n, od, oh, ow, cout)).astype(np.float32), dev) if residual else None
+    ref = ops.conv3d(x, packed, bias, aff, res, cout, 3, 1, mode, affine, L.DT_F32, 0)
+    flags = ops._flags(affine, affine, batch_bias, residual)
+    desc = ops.make_desc(shape, cout, 3, 1, mode, flags, L.DT_F32, 0)
+    return desc, (x, packed, bias, aff, res), ref
+
+
+def _noalloc(ctmr, desc, inputs, out):
+    x, packed, bias, aff, res = inputs
+    ptr = lambda t: None if t is None else t.data_ptr()
+    return ctmr._lib.lib().ctmr_conv3d_noalloc(ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), ptr(bias),
+                                                ptr(aff), ptr(res), out.data_ptr(),
+                                                torch.cuda.current_stream().cuda_stream)
+
+
+def test_noalloc_equals_conv3d_on_consecutive_calls(ctmr, dev):
+    L = ctmr._lib
+    cases = [
+        # deep level: K split, partial planes in the scratch, GN affine + SiLU, batch bias, residual
+        ("split", (2, 8, 8, 4, 512), 512, {}),
+        # smaller, nearest-2x parity GEMM over a padded packed copy in the scratch
+        ("nearest", (1, 6, 8, 10, 64), 48, {"mode": L.MODE_NEAREST2X}),
+        # smaller still: cout <= 4 tap-expanded GEMM (packed copy + tap columns in the scratch)
+        ("tap_expand", (1, 5, 6, 7, 32), 4, {"batch_bias": False}),
+    ]
+    for name, shape, cout, kw in cases:
+        desc, inputs, ref = _case(ctmr, dev, len(name), shape, cout, **kw)
+        need = L.workspace_bytes(desc)
+        print(f"noalloc case {name}: {shape}->{cout} kernel {L.conv_kernel(desc)} workspace {need} B", flush=True)
+        assert 0 < need <= L.NOALLOC_SCRATCH_BYTES
+        out = torch.full_like(ref, float("nan"))
+        assert _noalloc(ctmr, desc, inputs, out) == L.OK, L.last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), name
+        out2 = torch.full_like(ref, float("nan"))  # the same call again: same bits
+        assert _noalloc(ctmr, desc, inputs, out2) == L.OK
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref), name
+
+
+def test_noalloc_refuses_workspace_above_the_limit(ctmr, dev):
+    """Config 2b's packed copy (281 MiB) exceeds the 256 MiB scratch: refused before any launch,
+    with a message naming both sizes; null pointers are never touched."""
+    L = ctmr._lib
+    desc = ctmr.ops.make_desc((1, 64, 64, 64, 256), 128, 3, 1, L.MODE_NEAREST2X, 0, L.DT_F32, 0)
+    assert L.workspace_bytes(desc) > L.NOALLOC_SCRATCH_BYTES
+    rc = L.lib().ctmr_conv3d_noalloc(ctypes.byref(desc), None, None, None, None, None, None, None)
+    assert rc == L.E_WORKSPACE
+    assert "scratch limit" in L.last_error() and str(L.NOALLOC_SCRATCH_BYTES) in L.last_error()
