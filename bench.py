@@ -41,6 +41,11 @@ BF16_PEAK = 2516.6e12
 HBM_PEAK = 8.0e12
 
 
+def progress(msg):
+    """One line per finished stage on stderr (stdout carries only the JSON result)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def conv_flops(n, d, h, w, cin, cout, taps=27):
     return 2.0 * n * d * h * w * cin * cout * taps
 
@@ -126,8 +131,9 @@ def cpu_baseline(budget_s=20.0):
     return cb.time_config0_conv(budget_s=budget_s)
 
 
-def secondary(pkg, dev, steps):
-    """Config 1 (VAE residual block at 128^3 x 128) and config 2 GPU numbers."""
+def secondary(pkg, dev, steps, cpu=False):
+    """Config 1 (VAE residual block at 128^3 x 128) and config 2 GPU numbers; with ``cpu`` the same
+    operations via PyTorch fp32 on the host cores beside each (the reference's CPU path)."""
     import numpy as np
     import torch
 
@@ -151,6 +157,7 @@ def secondary(pkg, dev, steps):
         block()
     ms = _wall_ms(block, max(2, steps // 4))
     flops = 2 * conv_flops(1, s, s, s, c, c)
+    progress(f"config 1 {ms:.3f} ms")
     out["config1_vae_resblock_128c_128^3"] = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 2),
                                               "frac_fp32_peak": round(flops / ms / 1e-3 / FP32_PEAK, 4)}
     del x
@@ -186,6 +193,16 @@ def secondary(pkg, dev, steps):
                                           "frac_fp32_peak": round(flops / ms / 1e-3 / FP32_PEAK, 4),
                                           "hbm_GBps": round(nbytes / ms / 1e6, 1),
                                           "frac_hbm": round(nbytes / ms / 1e-3 / HBM_PEAK, 4)}
+    del xc
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        legs = cb.config_legs()
+        progress("CPU legs of configs 1-2c done")
+        for key, leg in (("config1_vae_resblock_128c_128^3", "config1"), ("config2a_down_s2_64to128", "config2a"),
+                         ("config2b_nearest_up_256to128", "config2b"), ("config2c_pointwise_128to256", "config2c")):
+            out[key].update({"cpu_ms": round(legs[leg], 2), "cpu_cores": cb.cores(),
+                             "gpu_speedup": round(legs[leg] / out[key]["ms"], 1)})
     return out
 
 
@@ -255,6 +272,19 @@ def unet_flops(constructor, batch, d, h, w, encoder_only=False):
     return conv, attn_f
 
 
+def controlnet_cond_flops(constructor, n, d, h, w):
+    """Conv FLOPs of the ControlNet conditioning encoder on an (n, d, h, w) label grid (once per
+    generation): conv_in, per level a stride-1 and a stride-2 conv, conv_out at the latent grid."""
+    cc = list(constructor["conditioning_embedding_num_channels"])
+    vox = n * d * h * w
+    f = 2.0 * vox * constructor["conditioning_embedding_in_channels"] * cc[0] * 27
+    for i in range(len(cc) - 1):
+        f += 2.0 * vox * cc[i] * cc[i] * 27
+        vox //= 8
+        f += 2.0 * vox * cc[i] * cc[i + 1] * 27
+    return f + 2.0 * vox * cc[-1] * constructor["num_channels"][0] * 27
+
+
 def vae_decoder_flops(constructor, d, h, w):
     """Conv FLOPs of one decoder pass on a (d, h, w) latent (trilinear convs on the 2x grid)."""
     ch = list(constructor["num_channels"])[::-1]
@@ -294,6 +324,7 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
     for _ in range(2):
         step()
     ms = _wall_ms(step, max(3, steps // 2))
+    progress(f"config 3 UNet step {ms:.3f} ms")
     conv_f, attn_f = unet_flops(uc, 2, 64, 64, 32)
     floor_ms = (conv_f + attn_f) / FP32_PEAK * 1e3
     out["config3_unet_step_batch2_64x64x32"] = {
@@ -342,15 +373,18 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         "roofline_ms": round(ct_flop / FP32_PEAK * 1e3, 3), "frac_roofline": round(ct_flop / FP32_PEAK * 1e3 / ct_ms, 4)}
     del cw, cond_emb
     if cpu:
+        from oracle import cpu_baseline as cb
         from oracle import maisi_torch as mt
 
         host_w = {k: v.cpu() for k, v in uw.items()}
         xc = x.cpu().permute(0, 4, 1, 2, 3).contiguous()
+        torch.set_num_threads(cb.cores())
         with torch.no_grad():
-            t0 = time.perf_counter()
-            mt.unet(xc, t.cpu(), classes.cpu(), spacing.cpu(), host_w, uc)
-            out["config3_unet_step_batch2_64x64x32"]["cpu_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
-            out["config3_unet_step_batch2_64x64x32"]["cpu_cores"] = torch.get_num_threads()
+            cpu_s = cb.median_seconds(lambda: mt.unet(xc, t.cpu(), classes.cpu(), spacing.cpu(), host_w, uc), reps=3)
+        progress(f"config 3 CPU {cpu_s:.2f} s")
+        out["config3_unet_step_batch2_64x64x32"].update({"cpu_ms": round(cpu_s * 1e3, 1), "cpu_cores": cb.cores(),
+                                                         "cpu_timing": "median of 3 after 1 warm-up"})
+        del host_w, xc
     del x
     # config 4: 64^3 latent -> 256^3, 4 windows along D (roi 20x64x64, overlap 0.25), int16
     z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 64, 64, 64, 4), dtype=np.float32)).to(dev)
@@ -360,29 +394,44 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         img = torch.clamp(y * 1000.0, min=0.0).to(torch.int16)
         return img
 
-    decode()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    img = decode()
-    torch.cuda.synchronize()
-    sec = time.perf_counter() - t0
+    def timed(fn, reps=3):
+        """Median synchronized seconds of ``reps`` runs after one warm-up, and the peak device memory
+        allocated during them."""
+        fn()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            r = fn()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            del r
+        return float(np.median(times)), torch.cuda.max_memory_allocated(dev)
+
+    sec, peak = timed(decode)
+    progress(f"config 4 decode {sec:.3f} s")
     dec_f = 4 * vae_decoder_flops(vc, 20, 64, 64)
     out["config4_vae_decode_256^3_4windows"] = {
         "s": round(sec, 4), "tflop": round(dec_f / 1e12, 3), "tflops": round(dec_f / sec / 1e12, 2),
         "roofline_s": round(dec_f / FP32_PEAK, 4), "frac_roofline": round(dec_f / FP32_PEAK / sec, 4),
-        "output": list(img.shape)}
-    del img
+        "timing": "median of 3 after 1 warm-up", "peak_device_GiB": round(peak / 2**30, 2),
+        "output": [1, 256, 256, 256, 1]}
     with pkg.fast_fp32.precision("bf16"):
-        decode()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        img = decode()
-        torch.cuda.synchronize()
-        sec16 = time.perf_counter() - t0
+        sec16, _ = timed(decode)
     out["config4_vae_decode_256^3_4windows"].update(
         {"bf16_s": round(sec16, 4), "bf16_roofline_s": round(dec_f / BF16_PEAK, 4),
          "bf16_frac_roofline": round(dec_f / BF16_PEAK / sec16, 4)})
-    del img
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        host_v = {k: v.cpu().numpy() for k, v in vw.items()}
+        win = cb.vae_window_seconds(host_v, vc, np.ascontiguousarray(z[:, :20].cpu().numpy()))
+        out["config4_vae_decode_256^3_4windows"].update(
+            {"cpu_window_s": round(win, 2), "cpu_decode_s_est": round(4 * win, 2), "cpu_cores": cb.cores(),
+             "cpu_sample": "one 20x64x64 window (PyTorch fp32 decoder), one run after a small warm-up; x4 "
+                           "windows for the estimate (the blend is negligible)"})
+    del z
     if generation:
         # full 256^3 generation: 30 rflow steps with batched CFG at a 64^3 latent, then decode
         lat = torch.from_numpy(np.random.default_rng(5).standard_normal((1, 64, 64, 64, 4), dtype=np.float32)).to(dev)
@@ -391,20 +440,65 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         times, _ = m.set_timesteps_rflow(num_inference_steps=30, input_img_size_numel=64**3)
         vel = lambda s, tt: m.guided_velocity(s, tt, class_labels=cls, spacing=sp, weights=uw, constructor=uc,
                                               guidance_scale=5.0)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        final = m.sample_rflow(lat, vel, times)
-        torch.cuda.synchronize()
-        t_sample = time.perf_counter() - t0
-        y = m.sliding_window_decode(final, vw, constructor=vc, roi=(20, 64, 64), overlap=0.25, scale_factor=1.0)
-        img = torch.clamp(y * 1000.0, min=0.0).to(torch.int16).cpu()
-        total = time.perf_counter() - t0
+        phases = []
+
+        def generate():
+            t0 = time.perf_counter()
+            final = m.sample_rflow(lat, vel, times)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            y = m.sliding_window_decode(final, vw, constructor=vc, roi=(20, 64, 64), overlap=0.25, scale_factor=1.0)
+            img = torch.clamp(y * 1000.0, min=0.0).to(torch.int16).cpu()
+            phases.append(t1 - t0)
+            return img
+
+        total, peak = timed(generate)
+        progress(f"256^3 MR generation {total:.3f} s")
         gen_f = 30 * sum(unet_flops(uc, 2, 64, 64, 64)) + dec_f
         out["generation_256^3_30steps_cfg"] = {
-            "s": round(total, 3), "sampling_s": round(t_sample, 3), "tflop": round(gen_f / 1e12, 2),
+            "s": round(total, 3), "sampling_s": round(float(np.median(phases[1:])), 3), "tflop": round(gen_f / 1e12, 2),
             "roofline_s": round(gen_f / FP32_PEAK, 3), "frac_roofline": round(gen_f / FP32_PEAK / total, 4),
-            "target_s": 60, "image_dtype": str(img.dtype)}
+            "target_s": 60, "timing": "median of 3 after 1 warm-up", "peak_device_GiB": round(peak / 2**30, 2),
+            "image_dtype": "torch.int16"}
+        del lat
+        out["ct_from_mask_256^3_30steps"] = ct_generation(pkg, dev, uw, vw, timed)
     return out
+
+
+def ct_generation(pkg, dev, uw, vw, timed):
+    """CT from a 256^3 label map (from_mask.py:121-295): condition encoded once, 30 ControlNet + UNet
+    steps at batch 1 (64^3 latent), windowed decode (roi 48x48x64, overlap 0.6666: 4 windows), HU."""
+    import numpy as np
+    import torch
+
+    m = pkg.maisi
+    uc, cc, vc = m.PRODUCTION_UNET_CONSTRUCTOR, m.PRODUCTION_CONTROLNET_CONSTRUCTOR, m.PRODUCTION_VAE_CONSTRUCTOR
+    cw = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.controlnet_weight_shapes(cc), seed=13).items()}
+    rng = np.random.default_rng(8)
+    label = rng.choice(np.array(sorted(m.VALID_LABELS)), size=(1, 1, 256, 256, 256)).astype(np.int16)
+    lat = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 4), dtype=np.float32)).to(dev)
+    results = []
+
+    def run():
+        r = m.sample_ct_from_mask(label, (0.75, 0.75, 0.75), unet_weights=uw, controlnet_weights=cw,
+                                  vae_weights=vw, unet_constructor=uc, controlnet_constructor=cc, vae_constructor=vc,
+                                  scale_factor=1.0, latent=lat, drop_weights=False)
+        hu = r.hu.cpu()
+        results.append(r.stage_timings_s)
+        return hu
+
+    sec, peak = timed(run)
+    progress(f"CT from mask generation {sec:.3f} s")
+    windows = len(m.dense_patch_slices((64, 64, 64), (48, 48, 64), m.scan_interval((64, 64, 64), (48, 48, 64), 0.6666)))
+    unet_f = sum(unet_flops(uc, 1, 64, 64, 64))
+    ctrl_f = sum(controlnet_flops(cc, 1, 64, 64, 64))
+    flop = controlnet_cond_flops(cc, 1, 256, 256, 256) + 30 * (unet_f + ctrl_f) + windows * vae_decoder_flops(
+        vc, 48, 48, 64)
+    stages = {k: round(float(np.median([r[k] for r in results[1:]])), 3) for k in results[0]}
+    return {"s": round(sec, 3), "stages_s": stages, "tflop": round(flop / 1e12, 2), "decode_windows": windows,
+            "roofline_s": round(flop / FP32_PEAK, 3), "frac_roofline": round(flop / FP32_PEAK / sec, 4),
+            "timing": "median of 3 after 1 warm-up, label upload to HU download", "peak_device_GiB":
+            round(peak / 2**30, 2)}
 
 
 def profile_only(pkg, dev, what, steps, warmup):
@@ -448,6 +542,17 @@ def profile_only(pkg, dev, what, steps, warmup):
         w = torch.from_numpy((rng.standard_normal((256, 128, 1, 1, 1)) / np.sqrt(128)).astype(np.float32)).to(dev)
         b = torch.zeros(256, device=dev)
         fn = lambda: f.pointwise_conv(x, w, b)
+    elif what in ("config2a", "config2b"):
+        # config 2a: stride-2 conv 64->128, 128^3 -> 64^3; config 2b: nearest-2x + conv 256->128, 64^3 -> 128^3
+        rng = np.random.default_rng(1)
+        cin, cout, s = (64, 128, 128) if what == "config2a" else (256, 128, 64)
+        x = torch.from_numpy(rng.standard_normal((1, s, s, s, cin), dtype=np.float32)).to(dev)
+        w = torch.from_numpy((rng.standard_normal((cout, cin, 3, 3, 3)) / np.sqrt(27 * cin)).astype(np.float32)).to(dev)
+        b = torch.zeros(cout, device=dev)
+        if what == "config2a":
+            fn = lambda: f.conv3d(x, w, b, padding=1, stride=2)
+        else:
+            fn = lambda: f.norm_conv3d(x, w, b, norm=None, num_groups=1, eps=1e-6, apply_silu=False, upsample=True)
     elif what == "attention":
         # production UNet level-2 attention: 16x16x8 latent = 2048 tokens, 256 channels = 8 heads, batch 2
         g = torch.Generator(device=dev).manual_seed(0)
@@ -478,7 +583,7 @@ def main() -> int:
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
     ap.add_argument("--only", choices=["unet", "unet_bf16", "decode", "resblock", "attention", "pointwise",
-                                       "gemms", "gemms_stream"],
+                                       "gemms", "gemms_stream", "config2a", "config2b"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
@@ -567,12 +672,13 @@ def main() -> int:
     sec = {"config0_bf16_gemm": {"ms": round(bf16_ms, 4), "tflops": round(flops / bf16_ms / 1e9, 2),
                                  "frac_bf16_peak": round(flops / (bf16_ms * 1e-3) / BF16_PEAK, 4)}}
     if not args.no_secondary:
-        sec.update(secondary(pkg, dev, args.steps))
+        sec.update(secondary(pkg, dev, args.steps, cpu=not args.no_cpu))
     if not args.no_networks:
         sec.update(networks(pkg, dev, args.steps, generation=not args.no_generation, cpu=not args.no_cpu))
     result["secondary"] = sec
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
+        progress("config 0 CPU baseline done")
     print(json.dumps(result), flush=True)
     return 0
 

@@ -64,3 +64,84 @@ def time_config0_conv(budget_s: float = 20.0) -> dict:
                    f"{layout} layout (faster of channels_last_3d/contiguous), median of >=3 runs, "
                    f"{sec * 1e3:.1f} ms/conv; torch {torch.__version__}; {_cpu_model()}"),
     }
+
+
+def cores() -> int:
+    return len(os.sched_getaffinity(0))
+
+
+def median_seconds(fn, reps: int = 3, warmup: int = 1) -> float:
+    """Median wall-clock seconds of ``fn()`` over ``reps`` runs after ``warmup`` untimed ones."""
+    import numpy as np
+
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def _cl(t):
+    import torch
+
+    return t.contiguous(memory_format=torch.channels_last_3d)
+
+
+def config_legs(reps: int = 3) -> dict:
+    """PyTorch CPU fp32 timings of configs 1, 2a, 2b and 2c (the reference's CPU-path ops, all host
+    cores, channels-last), median of ``reps`` after one warm-up: milliseconds per operation."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    torch.set_num_threads(cores())
+    rng = np.random.default_rng(1)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    w = lambda o, i, k=3: _cl(t(rng.standard_normal((o, i, k, k, k)) / np.sqrt(k ** 3 * i)))
+    out = {}
+    with torch.no_grad():
+        x1 = _cl(t(rng.standard_normal((1, 128, 128, 128, 128))).permute(0, 4, 1, 2, 3))
+        w1, w2, b = w(128, 128), w(128, 128), torch.zeros(128)
+        g, z = torch.ones(128), torch.zeros(128)
+
+        def block():
+            h = F.conv3d(_cl(F.silu(F.group_norm(x1, 32, g, z, 1e-6))), w1, b, padding=1)
+            h = F.conv3d(_cl(F.silu(F.group_norm(h, 32, g, z, 1e-6))), w2, b, padding=1)
+            return x1 + h
+
+        out["config1"] = median_seconds(block, reps) * 1e3
+        del x1
+        xa = _cl(t(rng.standard_normal((1, 128, 128, 128, 64))).permute(0, 4, 1, 2, 3))
+        wa = w(128, 64)
+        out["config2a"] = median_seconds(lambda: F.conv3d(xa, wa, torch.zeros(128), padding=1, stride=2), reps) * 1e3
+        del xa
+        xb = _cl(t(rng.standard_normal((1, 64, 64, 64, 256))).permute(0, 4, 1, 2, 3))
+        wb = w(128, 256)
+        out["config2b"] = median_seconds(
+            lambda: F.conv3d(_cl(F.interpolate(xb, scale_factor=2, mode="nearest")), wb, torch.zeros(128), padding=1),
+            reps) * 1e3
+        del xb
+        xc = _cl(t(rng.standard_normal((1, 64, 64, 64, 128))).permute(0, 4, 1, 2, 3))
+        wc = w(256, 128, 1)
+        out["config2c"] = median_seconds(lambda: F.conv3d(xc, wc, torch.zeros(256)), reps) * 1e3
+    return out
+
+
+def vae_window_seconds(weights_host: dict, constructor: dict, z_window) -> float:
+    """One decoder window on the CPU (PyTorch fp32, the restated MAISI decoder): seconds, one run
+    after a warm-up on a 1/8-size window (the full window takes several seconds)."""
+    import torch
+
+    from . import maisi_torch as mt
+
+    torch.set_num_threads(cores())
+    w = mt.to_torch(weights_host, dtype=torch.float32, strip="")
+    z = torch.from_numpy(z_window).permute(0, 4, 1, 2, 3).contiguous()
+    with torch.no_grad():
+        mt.vae_decode(z[:, :, :10, :32, :32].contiguous(), w, constructor)
+        t0 = time.perf_counter()
+        mt.vae_decode(z, w, constructor)
+        return time.perf_counter() - t0
