@@ -44,6 +44,12 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the ctmr HIP library cannot be built")
 
 
+# Per-source device flags.  The attention kernel's MFMA accumulators are
+# read and rescaled by VALU code; the VGPR form of the MFMAs keeps them out of
+# the AGPRs (no v_accvgpr copies in its loop).
+EXTRA_FLAGS = {"attention.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form")}
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every source and link ``libctmr_hip.so``; always rebuilds."""
     compiler = hipcc()
@@ -52,7 +58,8 @@ def build(verbose: bool = False) -> Path:
     objects = []
     for name in SOURCES:
         obj = build_dir / (Path(name).stem + ".o")
-        cmd = [compiler, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)]
+        cmd = [compiler, *HIP_FLAGS, *EXTRA_FLAGS.get(name, ()), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / name),
+               "-o", str(obj)]
         _run(cmd, verbose)
         objects.append(str(obj))
     tmp = LIB_PATH.with_suffix(".so.tmp")

@@ -24,6 +24,7 @@
 // exp2 / max / rescale work runs while the matrix core is busy.
 #include "ctmr_common.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -34,6 +35,7 @@ constexpr int kHeadDim = 32;
 constexpr int kWaves = 4;     // waves per workgroup (independent; no LDS, no barriers)
 constexpr int kKeyTiles = 2;  // 16-key tiles per key block
 constexpr int kBlock = 16 * kKeyTiles;
+constexpr float kLazyMax = 8.0f;  // log2 headroom before the softmax reference max moves
 
 struct AttnArgs {
   const float* q;
@@ -98,6 +100,23 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
   const float* Q = a.q + (int64_t)b * a.lq * a.ldq + h * kHeadDim;
   const float* K = a.k + (int64_t)b * a.lk * a.ldk + h * kHeadDim;
   const float* V = a.v + (int64_t)b * a.lk * a.ldv + h * kHeadDim;
+  // K and V rows of a key block through a buffer descriptor built per block
+  // from wave-uniform values (scalar instructions): base = row k0, range =
+  // the rows left before lk.  Per-lane offsets inside a block are fixed for the
+  // whole loop and rows at or past lk read as zero (masked below) -- no
+  // per-lane address arithmetic or clamping inside the loop.  The host keeps
+  // lk * ld * 4 within 31 bits.
+  auto rows_rsrc = [&](const float* base, int64_t ld, int k0) {
+    const int64_t left = (int64_t)max(a.lk - k0, 0) * ld * 4;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)k0 * ld), (short)0, (int)left, 0x00020000);
+  };
+  int koff[kKeyTiles], voff[kKeyTiles][4];
+#pragma unroll
+  for (int u = 0; u < kKeyTiles; ++u) {
+    koff[u] = (int)(((int64_t)(u * 16 + col) * a.ldk + 8 * g) * 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) voff[u][r] = (int)(((int64_t)(u * 16 + 4 * g + r) * a.ldv + col) * 4);
+  }
 
   f4 qa[QT][2];
 #pragma unroll
@@ -118,24 +137,23 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
     l[t] = 0.f;
   }
 
-  // Rows past the end are clamped to the last key (in bounds) and masked below.
+  // Rows past the end read as zero (outside the descriptors' range) and are masked below.
   auto load_k = [&](KeyTiles& kt, int k0) {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(K, a.ldk, k0);
 #pragma unroll
     for (int u = 0; u < kKeyTiles; ++u) {
-      const int row = min(k0 + u * 16 + col, a.lk - 1);
-      const f4* p = reinterpret_cast<const f4*>(K + (int64_t)row * a.ldk + 8 * g);
-      kt.k[u][0] = p[0];
-      kt.k[u][1] = p[1];
+      kt.k[u][0] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, koff[u], 0, 0));
+      kt.k[u][1] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, koff[u] + 16, 0, 0));
     }
   };
   auto load_v = [&](ValueTiles& vt, int k0) {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(V, a.ldv, k0);
 #pragma unroll
     for (int u = 0; u < kKeyTiles; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float* vr = V + (int64_t)min(k0 + u * 16 + 4 * g + r, a.lk - 1) * a.ldv;
-        vt.v[u][r][0] = vr[col];
-        vt.v[u][r][1] = vr[16 + col];
+        vt.v[u][r][0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, voff[u][r], 0, 0));
+        vt.v[u][r][1] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, voff[u][r] + 64, 0, 0));
       }
   };
   // S^T tiles of one key block.
@@ -152,8 +170,16 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
         s[u][t] = acc;
       }
   };
-  // Online softmax of one block: scores -> P^T in place, running max / sum,
-  // output rescale.  RAGGED masks keys at or past k_end (the last block only).
+  // Online softmax of one block: scores -> P^T in place, running reference
+  // max and sum, and the factor alpha[t] the output must be scaled by before
+  // this block's P V products.  The reference m[t] of a query moves only when
+  // the block's max exceeds it by more than kLazyMax (in log2 units; always on
+  // the first block, where m = -inf): P = 2^(s - m) then stays below 2^8, and
+  // in most blocks alpha is exactly 1, so the output rescale is skipped
+  // (output / sum is the same quotient for any reference).  The decision is
+  // per query, so every tiling computes the same bits.  RAGGED masks keys at or
+  // past k_end (the last block only).
+  float alpha[QT];
   auto softmax = [&](f4 (&s)[kKeyTiles][QT], int k0, auto ragged) {
     if constexpr (decltype(ragged)::value) {
 #pragma unroll
@@ -172,12 +198,13 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) bm = fmaxf(bm, s[u][t][r]);
       bm = lane_group_max(bm);
-      // Every block holds at least one real key, so mn is finite and the first
-      // block's alpha is 2^-inf = 0.  Arguments are <= 0: the hardware exp2
-      // (v_exp_f32) differs from exp2f only below 2^-126, far under the
-      // resolution of the running sum (>= 1).
-      const float mn = fmaxf(m[t], bm);
-      const float alpha = __builtin_amdgcn_exp2f(m[t] - mn);
+      // Every block holds at least one real key, so bm is finite and the first
+      // block moves the reference (alpha = 2^-inf = 0).  Arguments are <= 8:
+      // the hardware exp2 (v_exp_f32) differs from exp2f only below 2^-126,
+      // far under the resolution of the running sum (>= 1).
+      const bool move = bm > m[t] + kLazyMax;
+      const float mn = move ? bm : m[t];
+      alpha[t] = move ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
       m[t] = mn;
       float ps = 0.f;
 #pragma unroll
@@ -188,10 +215,18 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
           s[u][t][r] = p;
           ps += p;
         }
-      l[t] = l[t] * alpha + ps;
-      o[t][0] *= alpha;
-      o[t][1] *= alpha;
+      l[t] = l[t] * alpha[t] + ps;
     }
+  };
+  // o *= alpha, skipped (same bits: every factor is exactly 1) unless a lane of
+  // the wave moved its reference.
+  auto rescale = [&]() {
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+      if (__builtin_amdgcn_ballot_w64(alpha[t] != 1.0f)) {
+        o[t][0] *= alpha[t];
+        o[t][1] *= alpha[t];
+      }
   };
   auto pv = [&](const ValueTiles& vt, const f4 (&s)[kKeyTiles][QT]) {
 #pragma unroll
@@ -224,12 +259,14 @@ __global__ __launch_bounds__(256) void flash_attention_kernel(AttnArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
     }
     __builtin_amdgcn_sched_barrier(0);
+    rescale();
     pv(vc, sc);
     __builtin_amdgcn_sched_barrier(0);
   };
   // The last block (possibly ragged): softmax, then its products.
   auto last = [&](f4 (&sc)[kKeyTiles][QT], const ValueTiles& vc, int k0) {
     softmax(sc, k0, std::true_type{});
+    rescale();
     pv(vc, sc);
   };
 
@@ -357,6 +394,8 @@ extern "C" int ctmr_flash_attention(const ctmr_attn_desc* d, const float* q, con
     return fail(CTMR_E_INVALID, "ctmr_flash_attention: row strides must be multiples of 4 floats");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(CTMR_E_INVALID, "ctmr_flash_attention: q, k, v and out must be 16-byte aligned");
+  if ((int64_t)d->lk * std::max(d->ldk, d->ldv) * 4 > 0x7fffffffll)
+    return fail(CTMR_E_UNSUPPORTED, "ctmr_flash_attention: lk * row stride exceeds 2^31 bytes");
   if (!std::isfinite(d->scale)) return fail(CTMR_E_INVALID, "ctmr_flash_attention: scale must be finite");
   AttnArgs a{q, k, v, out, d->ldq, d->ldk, d->ldv, d->ldo, d->lq, d->lk, d->heads,
              (float)((double)d->scale * 1.4426950408889634)};
