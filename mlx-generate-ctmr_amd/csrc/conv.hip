@@ -1027,6 +1027,188 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// 3b'. LDS-staged im2col GEMM for small channel counts (fp32, stride 1, cin 4
+// or 8: the 4-channel latent input convs, the 8-channel label-condition convs)
+// ---------------------------------------------------------------------------
+// The im2col formulation (K = tap * cin + c, blocks of 16, the packed weight of
+// WL_IM2COL) without its HBM rows: a workgroup stages the brick's 6x10x10 halo
+// with all cin channels (plus a zero slot) in LDS once, then each K block's A
+// fragment is read straight from the halo -- lane group g of block b takes
+// K 16b + 4g .. +3, four consecutive channels of one tap of one voxel, or the
+// zero slot past tap 26.  Same operands, same K blocks in the same order and
+// the same MFMA sequence as the im2col GEMMs (B^T A^T, fixed order), so the
+// outputs are bit-identical to them.  Bricks and the wave / row mapping are
+// those of conv_lds_kernel; B (the weight) comes from L2 one block ahead.
+struct LdsSmallArgs {
+  const float* x;       // unpadded NDHWC input, cin channels
+  const float* affine;  // (n, cin, 2) or null
+  const char* wp;       // packed im2col weight [kblock][np][64 bytes]
+  const float* bias;
+  const float* res;
+  float* y;
+  int64_t x_bytes, w_bytes, plane;
+  int n, d, h, w, cin, cout, np, kb;
+  int tz, ty, tx, n_tiles, split;
+  int affine_on, silu_on, batch_bias, has_res, has_bias;
+  double* stats;
+  int gn_groups, gn_cpg;
+};
+
+template <int CIN, int NSUB>
+__global__ __launch_bounds__(256, 2) void conv_lds_small_kernel(LdsSmallArgs p) {
+  static_assert(CIN == 4 || CIN == 8, "4 or 8 input channels");
+  constexpr int kVox = CIN * 4;                      // bytes per halo voxel
+  constexpr int kQuads = kHaloVox * (CIN / 4);       // 16-byte halo pieces
+  constexpr int kIters = (kQuads + 255) / 256;
+  constexpr int kZero = kHaloVox * kVox;             // a 16-byte zero slot after the halo
+  constexpr int KB = (27 * CIN + 15) / 16;           // K blocks
+  __shared__ __attribute__((aligned(16))) char halo[kZero + 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int xcd = bid & 7, slot = bid >> 3, per = nb >> 3, rem = nb & 7;
+  const int tile = (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int n_tile = tile % p.n_tiles;
+  int rest = tile / p.n_tiles;
+  const int bx = rest % p.tx;
+  rest /= p.tx;
+  const int by = rest % p.ty;
+  rest /= p.ty;
+  const int bz = rest % p.tz;
+  const int b = rest / p.tz;
+  const int z0 = bz * kBD, y0 = by * kBH, x0 = bx * kBW;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+
+  // B: one output column per lane per 16-column block, from the block's rows
+  // of the packed weight; the first block's loads go out before the staging.
+  const int n0 = n_tile * NSUB * 16;
+  const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wp, (short)0, (int)min(p.w_bytes, (int64_t)0x7fffffff), 0x00020000);
+  int boff[NSUB];
+#pragma unroll
+  for (int ns = 0; ns < NSUB; ++ns) boff[ns] = min(n0 + ns * 16 + lrow, p.np - 1) * 64 + lgrp * 16;
+  const int bblock = p.np * 64;
+  auto load_b = [&](u4 (&B)[NSUB], int kblock) {
+    const int so = __builtin_amdgcn_readfirstlane(kblock * bblock);
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) B[ns] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, boff[ns], so, 0);
+  };
+  u4 B[2][NSUB];
+  load_b(B[0], 0);
+
+  // Halo: piece q is channels 4 (q % (CIN/4)) .. +3 of halo voxel q / (CIN/4);
+  // outside the volume it is zero (after the affine and SiLU, as the padding of
+  // the reference's pack kernel).  Offsets are relative to the first staged
+  // plane (the host checks 6 planes fit 31 bits).
+  const int zb = max(z0 - 1, 0);
+  const int64_t xbase = ((int64_t)b * p.d + zb) * p.h * p.w * CIN * 4;
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const char*)p.x + xbase), (short)0, (int)min(p.x_bytes - xbase, (int64_t)0x7fffffff),
+      0x00020000);
+  u4 stage[kIters];
+#pragma unroll
+  for (int i = 0; i < kIters; ++i) {
+    const int q = tid + 256 * i;
+    stage[i] = u4{0u, 0u, 0u, 0u};
+    if (q < kQuads) {
+      const int hv = q / (CIN / 4), part = q % (CIN / 4);
+      const int hz = hv / (kHH * kHW), hr = hv - hz * (kHH * kHW);
+      const int hy = hr / kHW, hx = hr - hy * kHW;
+      const int gz = z0 - 1 + hz, gy = y0 - 1 + hy, gx = x0 - 1 + hx;
+      if (gz >= 0 && gz < p.d && gy >= 0 && gy < p.h && gx >= 0 && gx < p.w) {
+        const int off = (int)((((int64_t)(gz - zb) * p.h + gy) * p.w + gx) * CIN * 4) + part * 16;
+        f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0));
+        if (p.affine_on) {
+          const f4* a = reinterpret_cast<const f4*>(p.affine + ((int64_t)b * CIN + part * 4) * 2);
+          const f4 a0 = a[0], a1 = a[1];
+          v = f4{fmaf(v[0], a0[0], a0[1]), fmaf(v[1], a0[2], a0[3]), fmaf(v[2], a1[0], a1[1]),
+                 fmaf(v[3], a1[2], a1[3])};
+        }
+        if (p.silu_on) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = silu_f(v[j]);
+        }
+        stage[i] = __builtin_bit_cast(u4, v);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kIters; ++i) {
+    const int q = tid + 256 * i;
+    if (q < kQuads) *reinterpret_cast<u4*>(halo + (q / (CIN / 4)) * kVox + (q % (CIN / 4)) * 16) = stage[i];
+  }
+  if (tid == 0) *reinterpret_cast<u4*>(halo + kZero) = u4{0u, 0u, 0u, 0u};
+  __syncthreads();
+
+  // A: this lane's voxel at tap (0,0,0) per row block (rows as conv_lds_kernel).
+  int abase[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) abase[ms] = ((wave * kHH + ms + 4 * (lrow >> 3)) * kHW + (lrow & 7)) * kVox;
+  auto load_a = [&](f4 (&A)[4], int kblock) {
+    const int k0 = kblock * 16 + lgrp * 4;
+    const int tap = k0 / CIN, c0 = k0 - tap * CIN;
+    const int off = (((tap / 9) * kHH + (tap / 3) % 3) * kHW + tap % 3) * kVox + c0 * 4;
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+      A[ms] = *reinterpret_cast<const f4*>(halo + (tap < 27 ? abase[ms] + off : kZero));
+  };
+
+  f4 acc[4][NSUB];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
+  f4 A[2][4];
+  load_a(A[0], 0);
+#pragma unroll
+  for (int kbk = 0; kbk < KB; ++kbk) {
+    if (kbk + 1 < KB) {
+      load_b(B[(kbk + 1) & 1], kbk + 1);
+      load_a(A[(kbk + 1) & 1], kbk + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns)
+          acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(f4, B[kbk & 1][ns])[j],
+                                                             A[kbk & 1][ms][j], acc[ms][ns], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  if constexpr (NSUB == 4) {
+    __shared__ double red[4][64][2];
+    store_brick(p, acc, b, 0, z0, y0, x0, n0, wave, lane, (bz * p.ty + by) * p.tx + bx, red);
+  } else {
+    // Narrow outputs (cout <= 32): lane holds columns n0 + 16 ns + 4 lgrp .. +3
+    // (all valid or all past cout: cout is a multiple of 4); no statistics.
+    const int z = z0 + wave, x = x0 + (lrow & 7);
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) {
+      const int y = y0 + ms + 4 * (lrow >> 3);
+      if (!(z < p.d && y < p.h && x < p.w)) continue;
+      const int64_t base = ((((int64_t)b * p.d + z) * p.h + y) * p.w + x) * p.cout;
+#pragma unroll
+      for (int ns = 0; ns < NSUB; ++ns) {
+        const int col = n0 + ns * 16 + 4 * lgrp;
+        if (col >= p.cout) continue;
+        f4 v = acc[ms][ns];
+        if (p.has_bias) {
+          const float* bq = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0) + col;
+          v += f4{bq[0], bq[1], bq[2], bq[3]};
+        }
+        if (p.has_res) v += *reinterpret_cast<const f4*>(p.res + base + col);
+        *reinterpret_cast<f4*>(p.y + base + col) = v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 3c. LDS-staged bf16 implicit GEMM (stride-1 bf16 volumes)
 // ---------------------------------------------------------------------------
 // The bf16 MFMA (16x16x32, 16 cycles) consumes operands 8x faster per cycle
@@ -1639,6 +1821,7 @@ struct Geometry {
   int nsub, wm, wn, m_tiles, n_tiles;
   bool lds;              // LDS-staged GEMM (conv_lds_kernel)
   bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
+  bool lds_small;        // LDS-staged im2col GEMM for cin 4 / 8 (conv_lds_small_kernel)
   bool pointwise;        // one-tap GEMM on the persistent pointwise_kernel
   bool direct;           // streaming GEMM reading the unpadded input (no pack)
   bool kws;              // 64 x 64 tiles, the K range of each split over the four waves
@@ -1759,6 +1942,40 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
   if (S > (1ll << 30) || s_out * d->cout > (1ll << 40))
     return fail(CTMR_E_UNSUPPORTED, "volume too large for 32-bit voxel indexing");
+  // LDS-staged im2col GEMM: the im2col formulation of stride-1 fp32 convs with
+  // 4 or 8 input channels, its rows read from a halo brick in LDS instead of
+  // HBM (same K blocks and products: bit-identical outputs); 64-column tiles
+  // for cout a multiple of 64, one 16- or 32-column tile for cout <= 32;
+  // bricks at least 3/4 full; 6 staged planes within 32-bit buffer offsets.
+  g.lds_small = false;
+  g.lds = false;
+  g.lds16 = false;
+  if (g.layout == WL_IM2COL && d->dtype == CTMR_F32 && d->stride == 1 && d->mode == CTMR_MODE_PLAIN &&
+      (d->cin == 4 || d->cin == 8) && d->cout % 4 == 0 && (d->cout % 64 == 0 || d->cout <= 32) &&
+      !(d->flags & CTMR_F_STREAM)) {
+    const int tz = (int)ceil_div(d->d, kBD), ty = (int)ceil_div(d->h, kBH), tx = (int)ceil_div(d->w, kBW);
+    const int64_t slots = (int64_t)tz * ty * tx * kBD * kBH * kBW;
+    const int64_t planes = (int64_t)kHD * d->h * d->w * d->cin * 4;
+    if (4 * S >= 3 * slots && planes < (1ll << 31)) {
+      g.lds_small = true;
+      g.pack = false;
+      g.tz = tz; g.ty = ty; g.tx = tx;
+      g.nsub = d->cout % 64 == 0 ? 4 : (d->cout <= 16 ? 1 : 2);
+      g.wm = 4; g.wn = 1;
+      g.m_tiles = tz * ty * tx;
+      g.n_tiles = (int)ceil_div(d->cout, g.nsub * 16);
+      g.split = 1;
+      if (d->split > 1) return fail(CTMR_E_INVALID, "split must be 1 for the small-channel LDS GEMM");
+      g.direct = false;
+      g.kws = false;
+      g.pointwise = false;
+      g.pack_bytes = (d->flags & CTMR_F_AFFINE) ? round_up((int64_t)d->n * d->cin * 2 * 4, 256) : 0;
+      g.part_bytes = 0;
+      const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n;
+      if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
+      return CTMR_OK;
+    }
+  }
   // LDS-staged GEMM: stride-1 fp32 volumes whose 4x8x8 bricks are at least
   // 3/4 full, with at least 64 input channels (4 staged chunks; measured on
   // MI355X: 64-channel UNet-level convs 3-6 % faster than the streaming GEMM
@@ -1914,6 +2131,10 @@ static int split_gn_rows(const ctmr_conv_desc* d, const Geometry& g) {
 static int gn_stats_tiles(const ctmr_conv_desc* d, const Geometry& g, int groups) {
   if (groups <= 0 || d->cout % groups != 0) return 0;
   if (g.layout == WL_EXPAND) return 0;
+  if (g.lds_small) {  // 64-column bricks only (the narrow epilogue writes no statistics)
+    const int cpg = d->cout / groups;
+    return (g.nsub == 4 && cpg <= 64 && 64 % cpg == 0) ? g.tz * g.ty * g.tx : 0;
+  }
   const int cpg = d->cout / groups;
   if (g.split > 1) {
     if (d->cout % 64 != 0 || 64 % cpg != 0) return 0;
@@ -2082,6 +2303,7 @@ int ctmr_conv3d_kernel(const ctmr_conv_desc* desc) {
   int rc = geometry(desc, g);
   if (rc) return rc;
   if (g.lds) return CTMR_K_LDS;
+  if (g.lds_small) return CTMR_K_LDS_SMALL;
   if (g.lds16) return CTMR_K_LDS_BF16;
   if (g.layout == WL_EXPAND) return CTMR_K_TAP_EXPAND;
   if (g.kws) return CTMR_K_SPLIT_WAVES;
@@ -2143,7 +2365,7 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
   if (!x) return fail(CTMR_E_INVALID, "null input");
   if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
   if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
-  if (g.lds) {
+  if (g.lds || g.lds_small) {
     if (!(desc->flags & CTMR_F_AFFINE)) return CTMR_OK;
     if (hipMemcpyAsync(workspace, affine, (size_t)desc->n * desc->cin * 2 * 4, hipMemcpyDeviceToDevice,
                        (hipStream_t)stream) != hipSuccess)
@@ -2268,6 +2490,44 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
     }
     return CTMR_OK;
   }
+  if (g.lds_small) {
+    LdsSmallArgs a;
+    a.x = x;
+    a.affine = (desc->flags & CTMR_F_AFFINE) ? (affine_direct ? affine_direct : (const float*)workspace) : nullptr;
+    a.wp = (const char*)packed;
+    a.bias = bias;
+    a.res = residual;
+    a.y = y;
+    a.x_bytes = (int64_t)desc->n * desc->d * desc->h * desc->w * desc->cin * 4;
+    a.w_bytes = (int64_t)g.kblocks * g.np * 64;
+    a.plane = 0;
+    a.n = desc->n; a.d = desc->d; a.h = desc->h; a.w = desc->w;
+    a.cin = desc->cin; a.cout = desc->cout; a.np = g.np; a.kb = g.kblocks;
+    a.tz = g.tz; a.ty = g.ty; a.tx = g.tx;
+    a.n_tiles = g.n_tiles;
+    a.split = 1;
+    a.affine_on = (desc->flags & CTMR_F_AFFINE) != 0;
+    a.silu_on = (desc->flags & CTMR_F_SILU) != 0;
+    a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
+    a.has_bias = bias != nullptr;
+    a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
+    a.stats = stats;
+    a.gn_groups = stats ? groups : 0;
+    a.gn_cpg = stats ? desc->cout / groups : 1;
+    if (a.affine_on && !a.affine) return fail(CTMR_E_INVALID, "affine flag without affine");
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n;
+    const dim3 grid((unsigned)blocks), block(256);
+    if (desc->cin == 4) {
+      if (g.nsub == 4) hipLaunchKernelGGL((conv_lds_small_kernel<4, 4>), grid, block, 0, st, a);
+      else if (g.nsub == 2) hipLaunchKernelGGL((conv_lds_small_kernel<4, 2>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((conv_lds_small_kernel<4, 1>), grid, block, 0, st, a);
+    } else {
+      if (g.nsub == 4) hipLaunchKernelGGL((conv_lds_small_kernel<8, 4>), grid, block, 0, st, a);
+      else if (g.nsub == 2) hipLaunchKernelGGL((conv_lds_small_kernel<8, 2>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((conv_lds_small_kernel<8, 1>), grid, block, 0, st, a);
+    }
+    return check_launch("conv_lds_small");
+  }
   if (g.lds16) {
     Lds16Args a;
     a.xp = xp;
@@ -2381,7 +2641,7 @@ int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed, 
   int rc = geometry(desc, g);
   if (rc) return rc;
   if (!x || !packed || !y) return fail(CTMR_E_INVALID, "null input, weight or output");
-  if (g.lds) {  // no pack stage: the LDS GEMM reads x and the caller's affine table directly
+  if (g.lds || g.lds_small) {  // no pack stage: the LDS GEMMs read x and the caller's affine table directly
     if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
     return conv3d_gemm_impl(desc, x, packed, bias, affine, residual, y, workspace, workspace_bytes, 0, nullptr,
                             stream);
@@ -2406,12 +2666,13 @@ int ctmr_conv3d_gn(const ctmr_conv_desc* desc, const float* x, const void* packe
   if (!x || !packed || !y || !stats) return fail(CTMR_E_INVALID, "null input, weight, output or stats");
   if (gn_stats_tiles(desc, g, groups) == 0)
     return fail(CTMR_E_UNSUPPORTED, "this convolution cannot produce group-norm partials");
-  if (g.lds) {
+  const bool direct_affine = g.lds || g.lds_small;
+  if (direct_affine) {
     if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
   } else if ((rc = ctmr_conv3d_pack(desc, x, affine, workspace, workspace_bytes, stream))) {
     return rc;
   }
-  return conv3d_gemm_impl(desc, x, packed, bias, g.lds ? affine : nullptr, residual, y, workspace,
+  return conv3d_gemm_impl(desc, x, packed, bias, direct_affine ? affine : nullptr, residual, y, workspace,
                           workspace_bytes, groups, stats, stream);
 }
 

@@ -66,10 +66,14 @@ def test_workspace_and_packed_sizes(ctmr):
     assert L.workspace_bytes(ds) == 0
     ds = L.conv_desc(1, 64, 64, 64, 128, 128, flags=L.F_STREAM | L.F_SILU)
     assert L.workspace_bytes(ds) == ((66**3 * 128 * 4 + 255) // 256) * 256
-    # cin below one K block packs im2col rows: K = 27 * cin rounded to the block
+    # cin below one K block packs im2col rows: K = 27 * cin rounded to the block; the stride-1
+    # fp32 cin 4 / 8 convs read those rows from an LDS halo (no workspace, the affine table with one)
     d4 = L.conv_desc(1, 8, 8, 8, 4, 64)
     assert L.packed_weight_elems(d4) == 112 * 64
-    assert L.workspace_bytes(d4) == 8**3 * 112 * 4
+    assert L.workspace_bytes(d4) == 0
+    assert L.workspace_bytes(L.conv_desc(1, 8, 8, 8, 4, 64, flags=L.F_AFFINE)) == 256
+    assert L.workspace_bytes(L.conv_desc(1, 8, 8, 8, 4, 64, flags=L.F_STREAM)) == 8**3 * 112 * 4
+    assert L.workspace_bytes(L.conv_desc(1, 8, 8, 8, 4, 64, stride=2)) == 4**3 * 112 * 4
     d16 = L.conv_desc(1, 8, 8, 8, 4, 4, dtype=L.DT_BF16)
     assert L.packed_weight_elems(d16) == 128 * 16
     # cout <= 4: one GEMM with 27 * cout columns (padded to 16) over every
@@ -254,7 +258,10 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     ((1, 64, 64, 64, 64), 64, {"dtype": 1}, "lds_bf16"),
     ((2, 4, 8, 8, 512), 512, {}, "split_waves"),                          # deep UNet level
     ((1, 20, 64, 64, 64), 1, {}, "tap_expand"),                           # decoder output conv
-    ((2, 64, 64, 32, 4), 64, {}, "pointwise"),                            # conv_in: im2col rows
+    ((2, 64, 64, 32, 4), 64, {}, "lds_small"),                            # conv_in: im2col rows from LDS
+    ((1, 256, 256, 256, 8), 8, {}, "lds_small"),                          # condition encoder 8 -> 8
+    ((1, 256, 256, 256, 8), 32, {"stride": 2}, "stream"),                 # stride 2: im2col rows in HBM
+    ((2, 64, 64, 32, 4), 64, {"flags": 16}, "stream"),                    # CTMR_F_STREAM: the im2col GEMM
 ])
 def test_conv_kernel_route(ctmr, shape, cout, kw, expected):
     """``ctmr_conv3d_kernel`` names the formulation the library picks (a function of the desc only)."""

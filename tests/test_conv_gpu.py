@@ -252,7 +252,8 @@ PERSISTENT_CASES = [
     ("K split", (1, 8, 8, 8, 512), 256, 1, {"split": 3, "gn": 32}),
     ("affine + SiLU pack", (1, 32, 32, 32, 64), 128, 1, {"fused": True, "gn": 32}),
     ("bf16", (1, 48, 48, 48, 128), 256, 1, {"bf16": True}),
-    ("im2col 3x3", (2, 32, 64, 64, 4), 64, 3, {"gn": 32}),
+    # 3 input channels: im2col rows in HBM (4 and 8 read them from an LDS halo, tested below)
+    ("im2col 3x3", (2, 32, 64, 64, 3), 64, 3, {"gn": 32, "route": "pointwise"}),
     ("tap-expanded 3x3 -> 1", (1, 40, 64, 64, 64), 1, 3, {}),
 ]
 
@@ -283,6 +284,9 @@ def test_persistent_pointwise_gemm_equals_one_tile_gemm(ctmr, dev, name, shape, 
     out_shape = (*shape[:-1], cout)
     res = _t(rng.standard_normal(out_shape, dtype=np.float32), dev) if opts.get("residual") else None
     groups = opts.get("gn", 0)
+    if "route" in opts:
+        L = ctmr._lib
+        assert L.conv_kernel(ctmr.ops.make_desc(shape, cout, ksize, 1, L.MODE_PLAIN, 0, L.DT_F32, 0)) == opts["route"]
     run = lambda stream: f.implicit_gemm_conv3d(xt, packed, _t(bias, dev), cout=cout, ksize=ksize, affine=affine,
                                                 silu=affine is not None, residual=res, split=opts.get("split", 0),
                                                 stream_gemm=stream, gn_groups=groups)
@@ -669,3 +673,62 @@ def test_two_stage_abi_equals_combined_call(ctmr, dev, shape, cout, flags_extra)
     expected = (rm.conv3d(rm.group_norm(xn, np.ones(c), np.zeros(c), 8, 1e-6, apply_silu=True), _h(w))
                 + _h(bias)[:, None, None, None, :] + _h(res))
     _assert_rel(_h(outs[0]), expected, FP32_REL, f"two-stage {shape}->{cout} flags {flags}")
+
+
+SMALL_CIN_CASES = [
+    # (name, x shape NDHWC, cout, options) -- routes to the LDS-staged im2col GEMM
+    ("conv_in class", (2, 8, 16, 16, 4), 64, {}),
+    ("ragged bricks, batch bias, residual", (1, 7, 16, 14, 4), 64, {"batch_bias": True, "residual": True}),
+    ("condition conv 8->8, GN affine + SiLU", (2, 8, 16, 16, 8), 8, {"fused": True}),
+    ("8->32, residual", (1, 8, 16, 12, 8), 32, {"fused": True, "residual": True}),
+    ("decoder blocks.0 class, 4 column tiles, statistics", (1, 4, 8, 16, 4), 256, {"gn": 32}),
+    ("8->128, affine, batch bias, statistics", (1, 4, 8, 8, 8), 128, {"fused": True, "gn": 16, "batch_bias": True}),
+]
+
+
+@pytest.mark.parametrize(("name", "shape", "cout", "opts"), SMALL_CIN_CASES, ids=[c[0] for c in SMALL_CIN_CASES])
+def test_small_cin_lds_gemm_equals_im2col_gemm(ctmr, dev, name, shape, cout, opts):
+    """cin 4 / 8 stride-1 convs read their im2col rows from an LDS halo brick: the same K blocks and
+    products as the im2col GEMM over HBM rows (CTMR_F_STREAM), so bit-identical outputs; within the
+    float64 bar; epilogue group-norm partials (64-column tiles) match the other tiling's to fp64
+    rounding and the float64 group statistics."""
+    print(f"small-cin LDS GEMM {name}: {shape} -> {cout} {opts}", flush=True)
+    f, L = ctmr.fast_fp32, ctmr._lib
+    rng = np.random.default_rng(sum(shape) + cout)
+    n, c = shape[0], shape[-1]
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal((n, cout) if opts.get("batch_bias") else (cout,)).astype(np.float32)
+    res = rng.standard_normal((*shape[:-1], cout)).astype(np.float32) if opts.get("residual") else None
+    affine = None
+    if opts.get("fused"):
+        affine = np.stack([1 + 0.3 * rng.standard_normal((n, c)), 0.4 * rng.standard_normal((n, c))],
+                          axis=-1).astype(np.float32)
+    flags = (L.F_AFFINE | L.F_SILU if affine is not None else 0) | (L.F_BATCH_BIAS if opts.get("batch_bias") else 0) | (
+        L.F_RESIDUAL if res is not None else 0)
+    assert L.conv_kernel(ctmr.ops.make_desc(shape, cout, 3, 1, L.MODE_PLAIN, flags, L.DT_F32, 0)) == "lds_small"
+    assert L.conv_kernel(ctmr.ops.make_desc(shape, cout, 3, 1, L.MODE_PLAIN, flags | L.F_STREAM, L.DT_F32, 0)) != \
+        "lds_small"
+    packed = f.pack_weight(_t(w, dev))
+    groups = opts.get("gn", 0)
+    run = lambda stream: f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), cout=cout,
+                                                affine=None if affine is None else _t(affine, dev),
+                                                silu=affine is not None, residual=None if res is None else _t(res, dev),
+                                                stream_gemm=stream, gn_groups=groups)
+    y, y1 = run(False), run(True)
+    assert torch.equal(y, y1), f"{name}: LDS-staged and HBM im2col GEMMs differ"
+    assert torch.equal(run(False), y)
+    src = rm.apply_affine(x, affine, True) if affine is not None else x
+    expected = rm.conv3d(src, w) + (bias[:, None, None, None, :] if bias.ndim == 2 else bias)
+    if res is not None:
+        expected = expected + res
+    _assert_rel(_h(y), expected, FP32_REL, f"small-cin {name}")
+    if groups:
+        st, st1 = f.conv_output_stats(y, groups), f.conv_output_stats(y1, groups)
+        assert st is not None and st1 is not None
+        hs = _h(st).sum(axis=1)  # (n, groups, 2) over all tiles
+        hs1 = _h(st1).sum(axis=1)
+        assert rm.max_rel_error(hs, hs1) <= 1e-12, f"{name}: epilogue partials differ"
+        yy = _h(y).reshape(n, -1, groups, cout // groups)
+        ref = np.stack([yy.sum(axis=(1, 3)), (yy * yy).sum(axis=(1, 3))], axis=-1)
+        assert rm.max_rel_error(hs, ref) <= 1e-10
