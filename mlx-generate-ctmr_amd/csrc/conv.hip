@@ -2078,8 +2078,15 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     if (d->split > steps) return fail(CTMR_E_INVALID, "split must not exceed the K step count");
     g.split = d->split;
   } else {
+    // The persistent one-tap GEMM (below) keeps every resident workgroup busy
+    // once a launch has 256 tiles: splitting it further only adds the partial
+    // planes and their reduction (measured on MI355X: the 32x32x16-level
+    // 384 -> 128 skip projection 49.5 us with a split of 2, 35.5 us without;
+    // the 16x16x8- and 8x8x4-level ones fastest at 256 / base ranges).
+    const bool one_tap = g.KT == 1 && g.nsub == 4 && g.layout != WL_EXPAND && d->cout % 4 == 0 &&
+                         !(d->flags & (CTMR_F_STREAM | CTMR_F_BATCH_BIAS | CTMR_F_RESIDUAL));
     const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases;
-    const int64_t slots = 512;
+    const int64_t slots = one_tap ? 256 : 512;
     g.split = 1;
     if (base < slots && steps >= 16) {
       g.split = (int)std::min<int64_t>(ceil_div(slots, base), std::max(1, steps / 8));

@@ -104,6 +104,11 @@ def test_split_policy_is_shape_only(ctmr):
     # 32-channel chunks (2 here) over 4x8x8 bricks; the streaming bf16 GEMM splits the 54 K steps
     assert L.conv_split(L.conv_desc(2, 8, 16, 16, 64, 64, dtype=L.DT_BF16)) == 2  # 16 bricks x 2 chunks
     assert L.conv_split(L.conv_desc(2, 8, 16, 16, 64, 64, dtype=L.DT_BF16, flags=L.F_STREAM)) == 6
+    # the persistent one-tap GEMM (1x1x1) splits only launches of under 256 tiles, up to 256 work items
+    assert L.conv_split(L.conv_desc(2, 16, 32, 32, 384, 128, ksize=1)) == 1  # 256 tiles of 128 x 128
+    assert L.conv_split(L.conv_desc(2, 8, 16, 16, 768, 256, ksize=1)) == 4  # 64 tiles x 4
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 1024, 512, ksize=1)) == 8  # 32 tiles x 8
+    assert L.conv_split(L.conv_desc(2, 4, 8, 8, 128, 512, ksize=1)) == 1  # 8 K steps: below 16, no split
     # large grids never split
     assert L.conv_split(L.conv_desc(1, 128, 128, 128, 128, 128)) == 1
     assert L.conv_split(L.conv_desc(1, 64, 64, 64, 64, 64)) == 1
