@@ -501,6 +501,80 @@ def ct_generation(pkg, dev, uw, vw, timed):
             round(peak / 2**30, 2)}
 
 
+def _sclk_under(fn, seconds=4.0):
+    """Shader clock read by ``rocm-smi --showclocks`` (a child process) while ``fn`` runs back to back."""
+    import subprocess
+
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    probe = subprocess.Popen(["rocm-smi", "--showclocks"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                             text=True)
+    t0 = time.perf_counter()
+    while probe.poll() is None and time.perf_counter() - t0 < 30:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+    while time.perf_counter() - t0 < seconds:  # keep the load on for the whole sample window
+        fn()
+    torch.cuda.synchronize()
+    text = probe.communicate()[0]
+    for line in text.splitlines():
+        if "sclk" in line.lower():
+            return line.split(":")[-1].strip()
+    return None
+
+
+def reference_gemms(pkg, dev):
+    """hipBLASLt GEMM rates (torch.matmul) at square and conv-shaped sizes, and the shader clock under each
+    sustained MFMA load, beside this library's config-0 fp32 and bf16 implicit GEMMs."""
+    import numpy as np
+    import torch
+
+    def med_us(fn, n=10):
+        warm_up(fn, 3)
+        times = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3)
+        return float(np.median(times))
+
+    out = {"gemms": {}, "sclk_under_load": {}}
+    cases = [("bf16", 16384, 16384, 16384), ("bf16", 8192, 8192, 8192), ("bf16", 262144, 1728, 64),
+             ("fp32", 8192, 8192, 8192), ("fp32", 262144, 1728, 64)]
+    for dt, m, k, n in cases:
+        dtype = torch.bfloat16 if dt == "bf16" else torch.float32
+        a = torch.randn(m, k, device=dev, dtype=dtype)
+        bt = torch.randn(n, k, device=dev, dtype=dtype)
+        fn = lambda: a @ bt.t()
+        us = med_us(fn)
+        key = f"{dt}_{m}x{k}x{n}"
+        peak = BF16_PEAK if dt == "bf16" else FP32_PEAK
+        tf = 2.0 * m * k * n / us / 1e6
+        out["gemms"][key] = {"us": round(us, 1), "tflops": round(tf, 1), "frac_nominal_peak": round(tf * 1e12 / peak, 4)}
+        if (m, k, n) in ((16384, 16384, 16384), (8192, 8192, 8192)) and not (dt == "bf16" and m == 8192):
+            out["sclk_under_load"][f"hipblaslt_{key}"] = _sclk_under(fn)
+        del a, bt
+    rng = np.random.default_rng(0)
+    x = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 64), dtype=np.float32)).to(dev)
+    w = torch.from_numpy((rng.standard_normal((64, 64, 3, 3, 3)) / np.sqrt(27 * 64)).astype(np.float32)).to(dev)
+    b = torch.zeros(64, device=dev)
+    for code, name in ((pkg._lib.DT_F32, "fp32"), (pkg._lib.DT_BF16, "bf16")):
+        pack, gemm, _keep = staged_op(pkg, x, w, b, code)
+        pack()
+        us = med_us(gemm, 20)
+        tf = conv_flops(1, 64, 64, 64, 64, 64) / us / 1e6
+        out["gemms"][f"ctmr_config0_{name}_gemm"] = {"us": round(us, 1), "tflops": round(tf, 1)}
+        out["sclk_under_load"][f"ctmr_config0_{name}_gemm"] = _sclk_under(gemm)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def profile_only(pkg, dev, what, steps, warmup):
     """Run one workload alone (for rocprofv3 traces) and print its mean time."""
     import numpy as np
@@ -587,6 +661,9 @@ def main() -> int:
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
+    ap.add_argument("--reference-gemms", action="store_true",
+                    help="only time the platform's own GEMMs (torch.matmul -> hipBLASLt) and sample the shader "
+                         "clock under sustained fp32 / bf16 MFMA load, this library's config-0 GEMMs included")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (N=1); multi-GPU runs are not part of it",
@@ -609,6 +686,8 @@ def main() -> int:
     pkg = importlib.import_module("mlx-generate-ctmr_amd")
     f = pkg.fast_fp32
     dev = torch.device("cuda:0")
+    if args.reference_gemms:
+        return reference_gemms(pkg, dev)
     if args.only:
         return profile_only(pkg, dev, args.only, args.steps, args.warmup)
     rng = np.random.default_rng(0)
