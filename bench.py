@@ -589,6 +589,16 @@ def profile_only(pkg, dev, what, steps, warmup):
         cls = torch.tensor([9, 0], device=dev)
         sp = m.spacing_tensor([0.94, 0.94, 1.36], device=dev).repeat(2, 1)
         fn = lambda: m.denoise_unet(x, t, cls, sp, w, constructor=uc)
+    elif what == "controlnet":
+        # the CT step's ControlNet (production constructor, batch 2, conditioning embedding precomputed)
+        cc = m.PRODUCTION_CONTROLNET_CONSTRUCTOR
+        w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.controlnet_weight_shapes(cc), seed=13).items()}
+        rng = np.random.default_rng(3)
+        x = torch.from_numpy(rng.standard_normal((2, 64, 64, 32, 4), dtype=np.float32)).to(dev)
+        emb = torch.from_numpy(rng.standard_normal((2, 64, 64, 32, 64), dtype=np.float32)).to(dev)
+        t = torch.full((2,), 500.0, device=dev)
+        cls = torch.tensor([9, 0], device=dev)
+        fn = lambda: m.controlnet_residuals(x, t, cls, None, w, constructor=cc, conditioning_embedding=emb)
     elif what == "decode":
         vc = m.PRODUCTION_VAE_CONSTRUCTOR
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
@@ -656,8 +666,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "unet_bf16", "decode", "resblock", "attention", "pointwise",
-                                       "gemms", "gemms_stream", "config2a", "config2b"],
+    ap.add_argument("--only", choices=["unet", "unet_bf16", "controlnet", "decode", "resblock", "attention",
+                                       "pointwise", "gemms", "gemms_stream", "config2a", "config2b"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")

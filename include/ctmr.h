@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define CTMR_ABI_VERSION 1
+#define CTMR_ABI_VERSION 2
 
 enum ctmr_status {
   CTMR_OK = 0,
@@ -87,6 +87,10 @@ typedef struct ctmr_conv_desc {
                            last round would be far from full), else the number of
                            contiguous ranges of the (tap, channel block) step sequence,
                            1 .. taps * ceil(cin / K block) */
+  int32_t cin1;         /* 0: the input is one tensor of cin channels.  Else the input is the
+                           channel concatenation of two tensors (ctmr_conv3d_cat), x1 with
+                           channels [0, cin1) and x2 with [cin1, cin); cin1 and cin multiples
+                           of 16, CTMR_MODE_PLAIN */
 } ctmr_conv_desc;
 
 /* Library identity; returns CTMR_ABI_VERSION. */
@@ -173,6 +177,24 @@ int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ctmr_conv3d of the channel concatenation of two NDHWC tensors without
+ * materialising it: x1 holds channels [0, desc->cin1), x2 channels
+ * [desc->cin1, desc->cin) (cin1 and cin multiples of 16, CTMR_MODE_PLAIN),
+ * both on the same voxel grid.  Replaces the concatenation ahead of the
+ * UNet's up-path residual blocks (unet.py:444, mx.concatenate of the hidden
+ * state and the skip, then fast_fp32.residual_block_ncdhw); no separate
+ * entry point exists in the reference.  The LDS-staged GEMM stages each
+ * 16-channel chunk from its tensor and the persistent 1x1x1 GEMM reads each
+ * K block from its tensor; other routes pack both into the usual padded copy.
+ * Same products in the same order as ctmr_conv3d on the concatenated tensor,
+ * so bit-identical outputs.  Workspace: ctmr_conv3d_workspace_bytes(desc).
+ * ctmr_conv3d_cat_gn is the ctmr_conv3d_gn counterpart.
+ */
+int ctmr_conv3d_cat(const ctmr_conv_desc* desc, const float* x1, const float* x2, const void* packed,
+                    const float* bias, const float* affine, const float* residual, float* y, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
  * ctmr_conv3d without a caller workspace and without any allocation: the
  * workspace is a library-owned device array of CTMR_NOALLOC_SCRATCH_BYTES per
  * GPU (allocated when the library's code is loaded on that GPU, held until
@@ -233,14 +255,25 @@ int ctmr_conv3d_gn(const ctmr_conv_desc* desc, const float* x, const void* packe
 int ctmr_gn_affine_from_stats(int32_t n, int32_t tiles, int32_t c, int32_t groups, int64_t count, float eps,
                               const double* stats, const float* gamma, const float* beta, float* affine,
                               void* stream);
+int ctmr_conv3d_cat_gn(const ctmr_conv_desc* desc, const float* x1, const float* x2, const void* packed,
+                       const float* bias, const float* affine, const float* residual, float* y, void* workspace,
+                       size_t workspace_bytes, int32_t groups, double* stats, void* stream);
 
 /* Group-norm statistics: affine (n, c, 2) = (gamma*rstd, beta - mean*gamma*rstd)
- * over (c/groups channels) x s voxels, biased variance, fp64 accumulation in a
- * fixed-order tree.  Needs ctmr_gn_workspace_bytes(n, s, c) of scratch. */
+ * over (c/groups channels) x s voxels, biased variance, fp64 accumulation combined
+ * in a fixed order.  Needs ctmr_gn_workspace_bytes(n, s, c) of scratch. */
 int64_t ctmr_gn_workspace_bytes(int32_t n, int64_t s, int32_t c);
 int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, const float* x,
                    const float* gamma, const float* beta, float* affine, void* workspace,
                    size_t workspace_bytes, void* stream);
+/* ctmr_gn_affine of the channel concatenation of x1 (c1 channels) and x2 (c2
+ * channels) on the same voxels, without materialising it (the norm1 of an
+ * up-path residual block, whose input is that concatenation, unet.py:444);
+ * c1 and c2 multiples of 4; workspace ctmr_gn_workspace_bytes(n, s, c1 + c2).
+ * Bit-identical to ctmr_gn_affine on the concatenated tensor. */
+int ctmr_gn_affine_cat(int32_t n, int64_t s, int32_t c1, int32_t c2, int32_t groups, float eps, const float* x1,
+                       const float* x2, const float* gamma, const float* beta, float* affine, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* y = silu?(x*scale + offset) with affine from ctmr_gn_affine; y may equal x. */
 int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,

@@ -23,7 +23,7 @@ DT_F32, DT_BF16 = 0, 1
 K_STREAM, K_STREAM_DIRECT, K_LDS, K_LDS_BF16, K_POINTWISE, K_SPLIT_WAVES, K_TAP_EXPAND, K_LDS_SMALL = range(8)
 KERNEL_NAMES = ("stream", "stream_direct", "lds", "lds_bf16", "pointwise", "split_waves", "tap_expand", "lds_small")
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 NOALLOC_SCRATCH_BYTES = 256 << 20  # CTMR_NOALLOC_SCRATCH_BYTES
 
 
@@ -32,7 +32,8 @@ class ConvDesc(ctypes.Structure):
 
     _fields_ = [
         (name, ctypes.c_int32)
-        for name in ("n", "d", "h", "w", "cin", "cout", "ksize", "stride", "mode", "flags", "dtype", "split")
+        for name in ("n", "d", "h", "w", "cin", "cout", "ksize", "stride", "mode", "flags", "dtype", "split",
+                     "cin1")
     ]
 
 
@@ -64,8 +65,12 @@ _PROTOTYPES = {
     "ctmr_conv3d_gemm": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ctmr_conv3d_stats_tiles": (_c_i32, [_desc_p, _c_i32]),
     "ctmr_conv3d_gn": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _c_i32, _vp, _vp]),
+    "ctmr_conv3d_cat": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ctmr_conv3d_cat_gn": (_c_int, [_desc_p, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _c_i32, _vp, _vp]),
     "ctmr_gn_workspace_bytes": (_c_i64, [_c_i32, _c_i64, _c_i32]),
     "ctmr_gn_affine": (_c_int, [_c_i32, _c_i64, _c_i32, _c_i32, _f, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ctmr_gn_affine_cat": (_c_int, [_c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _f, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                    _vp]),
     "ctmr_gn_affine_from_stats": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _f, _vp, _vp, _vp, _vp, _vp]),
     "ctmr_gn_apply": (_c_int, [_c_i32, _c_i64, _c_i32, _vp, _vp, _c_i32, _vp, _vp]),
     "ctmr_silu": (_c_int, [_c_i64, _vp, _vp, _vp]),
@@ -137,9 +142,10 @@ def conv_desc(
     flags: int = 0,
     dtype: int = DT_F32,
     split: int = 0,
+    cin1: int = 0,
 ) -> ConvDesc:
-    """Build a ``ctmr_conv_desc``."""
-    return ConvDesc(n, d, h, w, cin, cout, ksize, stride, mode, flags, dtype, split)
+    """Build a ``ctmr_conv_desc`` (``cin1``: channels of the first of two input tensors, 0 for one)."""
+    return ConvDesc(n, d, h, w, cin, cout, ksize, stride, mode, flags, dtype, split, cin1)
 
 
 def output_dims(desc: ConvDesc) -> tuple[int, int, int]:

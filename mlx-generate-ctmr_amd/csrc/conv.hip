@@ -48,7 +48,9 @@ typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 // 1. Input packing
 // ---------------------------------------------------------------------------
 struct PackArgs {
-  const float* x;
+  const float* x;       // source (channels [0, c1) of a two-source input)
+  const float* x2;      // channels [c1, c) of a two-source input, or null
+  int c1;               // channels of x (c for one source; a multiple of 4)
   void* out;
   const float* affine;
   int64_t total4;       // 4-channel groups to write
@@ -72,8 +74,9 @@ __device__ __forceinline__ f4 pack_value4(const PackArgs& a, int b, int pz, int 
         const float* src = a.x + (int64_t)b * a.id * a.ih * a.iw * a.c;
         v = trilinear_sample4(src, a.id, a.ih, a.iw, a.c, ch, z, y, x);
       } else {
-        v = *reinterpret_cast<const f4*>(
-            a.x + ((((int64_t)b * a.gd + z) * a.gh + y) * a.gw + x) * a.c + ch);
+        const int64_t vox = (((int64_t)b * a.gd + z) * a.gh + y) * a.gw + x;
+        v = ch < a.c1 ? *reinterpret_cast<const f4*>(a.x + vox * a.c1 + ch)
+                      : *reinterpret_cast<const f4*>(a.x2 + vox * (a.c - a.c1) + (ch - a.c1));
       }
     } else {
 #pragma unroll
@@ -326,6 +329,11 @@ struct ConvArgs {
   int gn_groups, gn_cpg, stats_tiles;
   int items;               // pointwise_kernel: row tiles x batch items x split ranges
   int in_d, in_h, in_w;    // input extent (conv_kernel<.., DIRECT>: A read from x itself)
+  // Two-source input (pointwise_kernel reading x directly): K blocks from kb1
+  // on come from xp2, rows of row_bytes2 bytes; kb1 = kb for one source.
+  const char* xp2;
+  int64_t row_bytes2;
+  int kb1;
 };
 
 // Final step of the group-norm partials of a stored tile: red[wave][c] holds
@@ -854,7 +862,9 @@ __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int 
 }
 
 struct LdsArgs {
-  const float* x;       // unpadded NDHWC input
+  const float* x;       // unpadded NDHWC input (channels [0, c1) of a two-source input)
+  const float* x2;      // channels [c1, cin) of a two-source input, or null
+  int c1;               // channels of x (cin for one source; a multiple of 16)
   const float* affine;  // (n, cin, 2) or null
   const char* wp;       // packed weight [tap][kblock][np][64 bytes]
   const float* bias;
@@ -892,29 +902,51 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 
   // Staging: piece i of thread t is channels 4*(t&3)..+3 of the chunk at halo
   // voxel (t>>2) + 64i.  Offsets are relative to the first staged plane, so
-  // they stay within 32 bits (the host checks 6 planes fit).
+  // they stay within 32 bits (the host checks 6 planes fit).  A chunk comes
+  // from x (chunks below c1 / 16) or from x2, whose rows have the remaining
+  // channels; gvox[i] is the piece's voxel index, the byte offset follows from
+  // the chunk's source.
   const int part = tid & 3;
   const int zb = max(z0 - 1, 0);
-  const int64_t xbase = ((int64_t)b * p.d + zb) * p.h * p.w * p.cin * 4;
-  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const char*)p.x + xbase), (short)0, (int)min(p.x_bytes - xbase, (int64_t)0x7fffffff),
+  const int c2 = p.cin - p.c1;
+  const int kb1 = p.c1 >> 4;
+  const int64_t vbase = ((int64_t)b * p.d + zb) * p.h * p.w;     // first staged voxel
+  const int64_t vtotal = (int64_t)p.n * p.d * p.h * p.w;
+  const __amdgpu_buffer_rsrc_t xrsrc1 = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + vbase * p.c1), (short)0, (int)min((vtotal - vbase) * p.c1 * 4, (int64_t)0x7fffffff),
       0x00020000);
-  int goff[kStageIters];
+  const __amdgpu_buffer_rsrc_t xrsrc2 = p.x2 ? __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x2 + vbase * c2), (short)0, (int)min((vtotal - vbase) * c2 * 4, (int64_t)0x7fffffff),
+      0x00020000) : xrsrc1;
+  int gvox[kStageIters];
   unsigned valid = 0;
 #pragma unroll
   for (int i = 0; i < kStageIters; ++i) {
     const int hv = (tid >> 2) + 64 * i;
-    goff[i] = 0;
+    gvox[i] = 0;
     if (hv < kHaloVox) {
       const int hz = hv / (kHH * kHW), hr = hv - hz * (kHH * kHW);
       const int hy = hr / kHW, hx = hr - hy * kHW;
       const int gz = z0 - 1 + hz, gy = y0 - 1 + hy, gx = x0 - 1 + hx;
       if (gz >= 0 && gz < p.d && gy >= 0 && gy < p.h && gx >= 0 && gx < p.w) {
         valid |= 1u << i;
-        goff[i] = (int)((((int64_t)(gz - zb) * p.h + gy) * p.w + gx) * p.cin * 4) + part * 16;
+        gvox[i] = ((gz - zb) * p.h + gy) * p.w + gx;
       }
     }
   }
+  // Source of a chunk: descriptor, row bytes and the chunk's byte offset in a row.
+  struct ChunkSrc {
+    __amdgpu_buffer_rsrc_t rs;
+    int row, so;
+  };
+  auto chunk_src = [&](int chunk) {
+    ChunkSrc c;
+    const bool second = chunk >= kb1;
+    c.rs = second ? xrsrc2 : xrsrc1;
+    c.row = (second ? c2 : p.c1) * 4;
+    c.so = __builtin_amdgcn_readfirstlane((second ? chunk - kb1 : chunk) * 64);
+    return c;
+  };
 
   // A: LDS byte address of this lane's voxel at tap (0,0,0) per row block.
   int abase[4];
@@ -941,9 +973,10 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 
   u4 stage[kStageIters];
   auto fetch = [&](int chunk) {
-    const int so = __builtin_amdgcn_readfirstlane(chunk * 64);
+    const ChunkSrc c = chunk_src(chunk);
 #pragma unroll
-    for (int i = 0; i < kStageIters; ++i) stage[i] = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, goff[i], so, 0);
+    for (int i = 0; i < kStageIters; ++i)
+      stage[i] = __builtin_amdgcn_raw_buffer_load_b128(c.rs, gvox[i] * c.row + part * 16, c.so, 0);
   };
   auto commit = [&](int chunk) {
     f4 sc = {1.f, 1.f, 1.f, 1.f}, of = {0.f, 0.f, 0.f, 0.f};
@@ -1000,7 +1033,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
     load_b(B[0], 0, chunk);
     load_a(A[0], 0);
     // Unconditional (see conv_kernel): the last chunk re-reads itself.
-    const int next_so = __builtin_amdgcn_readfirstlane(min(chunk + 1, c_end - 1) * 64);
+    const ChunkSrc nx = chunk_src(min(chunk + 1, c_end - 1));
 #pragma unroll
     for (int t = 0; t < 27; ++t) {
       if (t + 1 < 27) {
@@ -1011,7 +1044,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
       // retire in order, so each piece has two taps of products to arrive
       // before a later weight load has to wait for it.
       if ((t & 1) && (t >> 1) < kStageIters)
-        stage[t >> 1] = __builtin_amdgcn_raw_buffer_load_b128(xrsrc, goff[t >> 1], next_so, 0);
+        stage[t >> 1] = __builtin_amdgcn_raw_buffer_load_b128(nx.rs, gvox[t >> 1] * nx.row + part * 16, nx.so, 0);
       __builtin_amdgcn_sched_barrier(0);
       // Raised priority while this wave's MFMAs issue, so a wave whose
       // operands are ready wins issue slots over waves in their staging code.
@@ -1504,6 +1537,16 @@ __device__ __forceinline__ u32x4 raw_rsrc(const void* base, int64_t bytes) {
   return r;
 }
 
+// A descriptor chosen by a wave-uniform condition, kept in scalar registers.
+__device__ __forceinline__ u32x4 uniform4(u32x4 v) {
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(v.x);
+  r.y = __builtin_amdgcn_readfirstlane(v.y);
+  r.z = __builtin_amdgcn_readfirstlane(v.z);
+  r.w = __builtin_amdgcn_readfirstlane(v.w);
+  return r;
+}
+
 // Direct-to-LDS 16-byte buffer load of lane i (offset voff + soff, zero out
 // of range) into LDS byte lds_addr + 16 i.  Inline assembly for the reason
 // given at lds_dma16; callers wait with wait_vmcnt.
@@ -1566,35 +1609,42 @@ __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
   // Load t of this wave fills stage rows 16 * (wave * kDma + t) + lane / 4,
   // slot lane % 4 -- piece (lane % 4) ^ swizzle of that row: an A row (voxel)
   // or a B column.  The lane offsets are fixed; items move the A base only.
-  int voff[R::kDma];
+  // A rows of a two-source input: K blocks below kb1 from xp (rows of rb
+  // bytes), the rest from xp2 (rows of rb2 bytes); kb1 = kb for one source.
+  const int rb2 = (int)p.row_bytes2;
+  int voff[R::kDma], voff2[R::kDma];
 #pragma unroll
   for (int t = 0; t < R::kDma; ++t) {
     const int row = 16 * (wave * R::kDma + t) + (lane >> 2);
     const int piece = (lane & 3) ^ row64_swizzle(row);
     voff[t] = row < TM ? row * rb + piece * 16 : (n_tile * TN + row - TM) * 64 + piece * 16;
+    voff2[t] = row < TM ? row * rb2 + piece * 16 : voff[t];
   }
   const u32x4 brsrc = raw_rsrc(p.wp, p.w_bytes);
   const unsigned ring_lds = (unsigned)(uintptr_t)(lds_ptr_t)ring;
 
   // Load cursor: item d_r, K block d_s of [.., d_end), the item's A rows.
   int d_r = first, d_s, d_end;
-  u32x4 arsrc;
+  u32x4 arsrc, arsrc2;
   auto start_item = [&](int r) {
     const Item it = item(r);
     d_s = it.s_begin;
     d_end = it.s_end;
     const int64_t row = (int64_t)it.b * p.rows_per_batch + (int64_t)it.m_tile * TM;
     arsrc = raw_rsrc(p.xp + row * rb, (int64_t)(S - it.m_tile * TM) * rb);
+    arsrc2 = p.xp2 ? raw_rsrc(p.xp2 + row * rb2, (int64_t)(S - it.m_tile * TM) * rb2) : arsrc;
   };
   start_item(d_r);
   auto fill = [&](int st) {
     const unsigned lds = ring_lds + st * R::kStageBytes + wave * R::kDma * 1024;
-    const int sa = __builtin_amdgcn_readfirstlane(d_s * 64);
+    const bool second = __builtin_amdgcn_readfirstlane(d_s) >= p.kb1;  // wave-uniform
+    const int sa = __builtin_amdgcn_readfirstlane((second ? d_s - p.kb1 : d_s) * 64);
     const int sb = __builtin_amdgcn_readfirstlane(d_s * bstep);
+    const u32x4 asrc = uniform4(second ? arsrc2 : arsrc);
 #pragma unroll
     for (int t = 0; t < R::kDma; ++t) {
       const bool a_rows = 16 * (wave * R::kDma + t) < TM;  // wave-uniform: a scalar select, no branch
-      lds_dma_buf16(a_rows ? arsrc : brsrc, voff[t], a_rows ? sa : sb, lds + t * 1024);
+      lds_dma_buf16(a_rows ? asrc : brsrc, second ? voff2[t] : voff[t], a_rows ? sa : sb, lds + t * 1024);
     }
     if (++d_s == d_end) {
       if (d_r + lanes < p.items) {
@@ -1822,6 +1872,8 @@ struct Geometry {
   bool lds;              // LDS-staged GEMM (conv_lds_kernel)
   bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
   bool lds_small;        // LDS-staged im2col GEMM for cin 4 / 8 (conv_lds_small_kernel)
+  bool cat;              // input given as two tensors, channels [0, c1) and [c1, cin)
+  int c1;
   bool pointwise;        // one-tap GEMM on the persistent pointwise_kernel
   bool direct;           // streaming GEMM reading the unpadded input (no pack)
   bool kws;              // 64 x 64 tiles, the K range of each split over the four waves
@@ -1864,6 +1916,12 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     return fail(CTMR_E_UNSUPPORTED, "trilinear packing supports only a plain convolution");
   if (d->ksize == 1 && (d->mode != CTMR_MODE_PLAIN || d->stride != 1))
     return fail(CTMR_E_UNSUPPORTED, "1x1x1 conv supports only stride 1, no resampling");
+  g.cat = d->cin1 != 0;
+  g.c1 = g.cat ? d->cin1 : d->cin;
+  if (g.cat && (d->cin1 < 0 || d->cin1 >= d->cin || d->cin1 % 16 != 0 || d->cin % 16 != 0))
+    return fail(CTMR_E_INVALID, "two-source input needs 0 < cin1 < cin, both multiples of 16");
+  if (g.cat && d->mode != CTMR_MODE_PLAIN)
+    return fail(CTMR_E_UNSUPPORTED, "a two-source input supports only CTMR_MODE_PLAIN");
   g.ks = d->ksize;
   g.kstep = d->dtype == CTMR_F32 ? 16 : 32;
   g.esize = d->dtype == CTMR_F32 ? 4 : 2;
@@ -1897,6 +1955,11 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     g.tw = g.gw = g.ow = d->w;
     g.pack = (d->flags & (CTMR_F_AFFINE | CTMR_F_SILU)) || d->dtype != CTMR_F32 ||
              (d->cin % g.kstep) != 0;
+    // A two-source input is read directly only by the persistent pointwise
+    // GEMM (its conditions below); every other one-tap route packs it.
+    if (g.cat && !(d->cout > 32 && d->cout % 4 == 0 &&
+                   !(d->flags & (CTMR_F_STREAM | CTMR_F_BATCH_BIAS | CTMR_F_RESIDUAL))))
+      g.pack = true;
   }
   g.cp = g.pack ? (int)round_up(d->cin, g.kstep) : d->cin;
   g.kblocks = g.cp / g.kstep;
@@ -1950,7 +2013,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   g.lds_small = false;
   g.lds = false;
   g.lds16 = false;
-  if (g.layout == WL_IM2COL && d->dtype == CTMR_F32 && d->stride == 1 && d->mode == CTMR_MODE_PLAIN &&
+  if (g.layout == WL_IM2COL && !g.cat && d->dtype == CTMR_F32 && d->stride == 1 && d->mode == CTMR_MODE_PLAIN &&
       (d->cin == 4 || d->cin == 8) && d->cout % 4 == 0 && (d->cout % 64 == 0 || d->cout <= 32) &&
       !(d->flags & CTMR_F_STREAM)) {
     const int tz = (int)ceil_div(d->d, kBD), ty = (int)ceil_div(d->h, kBH), tx = (int)ceil_div(d->w, kBW);
@@ -2040,7 +2103,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // need no packed copy: the streaming GEMM reads x itself, with out-of-range
   // offsets for taps outside the volume (the padded copy's zeros).  Its lane
   // offsets are 32-bit: one batch item must stay below 2 GiB.
-  g.direct = !g.lds16 && g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 &&
+  g.direct = !g.lds16 && !g.cat && g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 &&
              d->mode == CTMR_MODE_PLAIN && !(d->flags & (CTMR_F_AFFINE | CTMR_F_SILU)) && d->cin % 16 == 0 &&
              (int64_t)d->d * d->h * d->w * d->cin * 4 < (1ll << 31) - (1ll << 20);
   if (g.direct) {
@@ -2364,12 +2427,22 @@ static int check_workspace(const Geometry& g, const void* workspace, size_t work
   return CTMR_OK;
 }
 
+static int pack_impl(const ctmr_conv_desc* desc, const float* x, const float* x2, const float* affine,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* affine,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (desc && desc->cin1 != 0) return fail(CTMR_E_INVALID, "two-source input: use ctmr_conv3d_cat");
+  return pack_impl(desc, x, nullptr, affine, workspace, workspace_bytes, stream);
+}
+
+// x2: channels [cin1, cin) of a two-source input (desc->cin1 != 0), else null.
+static int pack_impl(const ctmr_conv_desc* desc, const float* x, const float* x2, const float* affine,
                      void* workspace, size_t workspace_bytes, void* stream) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
-  if (!x) return fail(CTMR_E_INVALID, "null input");
+  if (!x || (g.cat && !x2)) return fail(CTMR_E_INVALID, "null input");
   if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
   if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
   if (g.lds || g.lds_small) {
@@ -2400,10 +2473,12 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
                        (hipStream_t)stream, ia);
     return check_launch("im2col");
   }
-  if ((desc->cin & 3) == 0 && ((uintptr_t)x & 15) != 0)
+  if ((desc->cin & 3) == 0 && (((uintptr_t)x | (g.cat ? (uintptr_t)x2 : 0)) & 15) != 0)
     return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
   PackArgs pa;
   pa.x = x;
+  pa.x2 = g.cat ? x2 : nullptr;
+  pa.c1 = g.c1;
   pa.out = workspace;
   pa.affine = affine;
   pa.gd = g.td; pa.gh = g.th; pa.gw = g.tw;
@@ -2426,26 +2501,31 @@ int ctmr_conv3d_pack(const ctmr_conv_desc* desc, const float* x, const float* af
   return check_launch("pack_input");
 }
 
-static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
-                            const float* affine_direct, const float* residual, float* y, void* workspace,
-                            size_t workspace_bytes, int groups, double* stats, void* stream);
+static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const float* x2, const void* packed,
+                            const float* bias, const float* affine_direct, const float* residual, float* y,
+                            void* workspace, size_t workspace_bytes, int groups, double* stats, void* stream);
 
 int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* packed,
                      const float* bias, const float* residual, float* y, void* workspace,
                      size_t workspace_bytes, void* stream) {
-  return conv3d_gemm_impl(desc, x, packed, bias, nullptr, residual, y, workspace, workspace_bytes, 0, nullptr,
-                          stream);
+  if (desc && desc->cin1 != 0) return fail(CTMR_E_INVALID, "two-source input: use ctmr_conv3d_cat");
+  return conv3d_gemm_impl(desc, x, nullptr, packed, bias, nullptr, residual, y, workspace, workspace_bytes, 0,
+                          nullptr, stream);
 }
 
 // affine_direct: the caller's (n, cin, 2) table when the pack stage was skipped
 // (ctmr_conv3d on the LDS path); null means "read it from the workspace".
 // stats: group-norm partials for `groups` (validated by the caller) or null.
-static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
-                            const float* affine_direct, const float* residual, float* y, void* workspace,
-                            size_t workspace_bytes, int groups, double* stats, void* stream) {
+static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const float* x2, const void* packed,
+                            const float* bias, const float* affine_direct, const float* residual, float* y,
+                            void* workspace, size_t workspace_bytes, int groups, double* stats, void* stream) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
+  if (g.cat && !g.pack && !g.lds && !g.pointwise)
+    return fail(CTMR_E_UNSUPPORTED, "internal: unpacked two-source input on a route that reads one tensor");
+  if (g.cat && !g.pack && (!x2 || ((uintptr_t)x2 & 15) != 0))
+    return fail(CTMR_E_INVALID, "x2 must be non-null and 16-byte aligned");
   const int tiles = stats ? gn_stats_tiles(desc, g, groups) : 0;
   if (stats && tiles == 0) return fail(CTMR_E_UNSUPPORTED, "this convolution cannot produce group-norm partials");
   if (!packed || !y || (!g.pack && !x)) return fail(CTMR_E_INVALID, "null input, weight or output");
@@ -2465,6 +2545,8 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
   if (g.lds) {
     LdsArgs a;
     a.x = x;
+    a.x2 = g.cat ? x2 : nullptr;
+    a.c1 = g.c1;
     a.affine = (desc->flags & CTMR_F_AFFINE) ? (affine_direct ? affine_direct : (const float*)workspace) : nullptr;
     a.wp = (const char*)packed;
     a.bias = bias;
@@ -2572,6 +2654,11 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
   }
   ConvArgs a;
   a.xp = xp;
+  // A two-source input reaches the GEMM unpacked only on the pointwise route.
+  const bool two = g.cat && !g.pack;
+  a.xp2 = two ? (const char*)x2 : nullptr;
+  a.kb1 = two ? g.c1 / 16 : g.kblocks;
+  a.row_bytes2 = two ? (int64_t)(desc->cin - g.c1) * 4 : 0;
   a.wp = (const char*)packed;
   a.bias = bias;
   a.res = residual;
@@ -2579,7 +2666,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
   a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
   a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
   a.rows_per_batch = g.rows_per_batch;
-  a.row_bytes = (int64_t)g.cp * g.esize;
+  a.row_bytes = two ? (int64_t)g.c1 * 4 : (int64_t)g.cp * g.esize;
   a.x_bytes = (int64_t)desc->n * g.rows_per_batch * a.row_bytes;
   a.w_bytes = (int64_t)g.phases * g.taps * g.kblocks * g.np * 64;
   a.plane = (int64_t)desc->n * s_out * desc->cout;
@@ -2641,20 +2728,36 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const vo
   return CTMR_OK;
 }
 
-int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
-                const float* affine, const float* residual, float* y, void* workspace,
-                size_t workspace_bytes, void* stream) {
+// ctmr_conv3d and ctmr_conv3d_cat: x2 null for one source.
+static int conv3d_run(const ctmr_conv_desc* desc, const float* x, const float* x2, const void* packed,
+                      const float* bias, const float* affine, const float* residual, float* y, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
-  if (!x || !packed || !y) return fail(CTMR_E_INVALID, "null input, weight or output");
+  if (!x || !packed || !y || (g.cat && !x2)) return fail(CTMR_E_INVALID, "null input, weight or output");
   if (g.lds || g.lds_small) {  // no pack stage: the LDS GEMMs read x and the caller's affine table directly
     if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
-    return conv3d_gemm_impl(desc, x, packed, bias, affine, residual, y, workspace, workspace_bytes, 0, nullptr,
-                            stream);
+    return conv3d_gemm_impl(desc, x, x2, packed, bias, affine, residual, y, workspace, workspace_bytes, 0,
+                            nullptr, stream);
   }
-  if ((rc = ctmr_conv3d_pack(desc, x, affine, workspace, workspace_bytes, stream))) return rc;
-  return ctmr_conv3d_gemm(desc, x, packed, bias, residual, y, workspace, workspace_bytes, stream);
+  if ((rc = pack_impl(desc, x, x2, affine, workspace, workspace_bytes, stream))) return rc;
+  return conv3d_gemm_impl(desc, x, x2, packed, bias, nullptr, residual, y, workspace, workspace_bytes, 0,
+                          nullptr, stream);
+}
+
+int ctmr_conv3d(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                const float* affine, const float* residual, float* y, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  if (desc && desc->cin1 != 0) return fail(CTMR_E_INVALID, "two-source input: use ctmr_conv3d_cat");
+  return conv3d_run(desc, x, nullptr, packed, bias, affine, residual, y, workspace, workspace_bytes, stream);
+}
+
+int ctmr_conv3d_cat(const ctmr_conv_desc* desc, const float* x1, const float* x2, const void* packed,
+                    const float* bias, const float* affine, const float* residual, float* y, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (!desc || desc->cin1 == 0) return fail(CTMR_E_INVALID, "ctmr_conv3d_cat needs desc->cin1 > 0");
+  return conv3d_run(desc, x1, x2, packed, bias, affine, residual, y, workspace, workspace_bytes, stream);
 }
 
 int32_t ctmr_conv3d_stats_tiles(const ctmr_conv_desc* desc, int32_t groups) {
@@ -2664,23 +2767,40 @@ int32_t ctmr_conv3d_stats_tiles(const ctmr_conv_desc* desc, int32_t groups) {
   return gn_stats_tiles(desc, g, groups);
 }
 
-int ctmr_conv3d_gn(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
-                   const float* affine, const float* residual, float* y, void* workspace,
-                   size_t workspace_bytes, int32_t groups, double* stats, void* stream) {
+static int conv3d_gn_run(const ctmr_conv_desc* desc, const float* x, const float* x2, const void* packed,
+                         const float* bias, const float* affine, const float* residual, float* y, void* workspace,
+                         size_t workspace_bytes, int32_t groups, double* stats, void* stream) {
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
-  if (!x || !packed || !y || !stats) return fail(CTMR_E_INVALID, "null input, weight, output or stats");
+  if (!x || !packed || !y || !stats || (g.cat && !x2))
+    return fail(CTMR_E_INVALID, "null input, weight, output or stats");
   if (gn_stats_tiles(desc, g, groups) == 0)
     return fail(CTMR_E_UNSUPPORTED, "this convolution cannot produce group-norm partials");
   const bool direct_affine = g.lds || g.lds_small;
   if (direct_affine) {
     if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
-  } else if ((rc = ctmr_conv3d_pack(desc, x, affine, workspace, workspace_bytes, stream))) {
+  } else if ((rc = pack_impl(desc, x, x2, affine, workspace, workspace_bytes, stream))) {
     return rc;
   }
-  return conv3d_gemm_impl(desc, x, packed, bias, direct_affine ? affine : nullptr, residual, y, workspace,
+  return conv3d_gemm_impl(desc, x, x2, packed, bias, direct_affine ? affine : nullptr, residual, y, workspace,
                           workspace_bytes, groups, stats, stream);
+}
+
+int ctmr_conv3d_gn(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
+                   const float* affine, const float* residual, float* y, void* workspace,
+                   size_t workspace_bytes, int32_t groups, double* stats, void* stream) {
+  if (desc && desc->cin1 != 0) return fail(CTMR_E_INVALID, "two-source input: use ctmr_conv3d_cat_gn");
+  return conv3d_gn_run(desc, x, nullptr, packed, bias, affine, residual, y, workspace, workspace_bytes, groups,
+                       stats, stream);
+}
+
+int ctmr_conv3d_cat_gn(const ctmr_conv_desc* desc, const float* x1, const float* x2, const void* packed,
+                       const float* bias, const float* affine, const float* residual, float* y, void* workspace,
+                       size_t workspace_bytes, int32_t groups, double* stats, void* stream) {
+  if (!desc || desc->cin1 == 0) return fail(CTMR_E_INVALID, "ctmr_conv3d_cat_gn needs desc->cin1 > 0");
+  return conv3d_gn_run(desc, x1, x2, packed, bias, affine, residual, y, workspace, workspace_bytes, groups, stats,
+                       stream);
 }
 
 }  // extern "C"

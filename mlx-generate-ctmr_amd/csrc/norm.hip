@@ -56,9 +56,13 @@ __device__ __forceinline__ double wave_butterfly_sum(double v) {
 // are summed by a butterfly across the wave (lanes l ^ 32, l ^ 16, ..), then
 // the four waves' sums in wave order; otherwise (one voxel lane per wave or
 // cgn not a power of two) the voxel lanes in ascending order through LDS.
+// A two-source input (x2 non-null) is the channel concatenation of x
+// (channels [0, c1)) and x2 (channels [c1, c)); a thread's channels lie in one
+// of them (c1 % VEC == 0) and it reads the same values in the same order as
+// from the concatenated tensor.
 template <int VEC>
-__global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict__ x, int64_t s,
-                                                         int c, int64_t chunk_vox, int chunks,
+__global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict__ x, const float* __restrict__ x2,
+                                                         int c1, int64_t s, int c, int64_t chunk_vox, int chunks,
                                                          double* __restrict__ part) {
   const int chunk = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int cgn = c / VEC;
@@ -86,11 +90,13 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict
     }
   };
   if (vl < vl_count) {
-    const float* xb = x + (int64_t)b * s * c + cg * VEC;
+    const bool second = x2 != nullptr && cg * VEC >= c1;
+    const int stride = x2 == nullptr ? c : (second ? c - c1 : c1);
+    const float* xb = second ? x2 + (int64_t)b * s * stride + (cg * VEC - c1) : x + (int64_t)b * s * stride + cg * VEC;
     const int64_t step = vl_count;
     for (int64_t v = v0 + vl; v < v1; v += step) {
       float q[VEC];
-      load(xb + v * c, q);
+      load(xb + v * stride, q);
       add(q);
     }
   }
@@ -330,16 +336,20 @@ int64_t ctmr_gn_workspace_bytes(int32_t n, int64_t s, int32_t c) {
   return (int64_t)n * gn_chunks(n, s, c).count * c * 2 * (int64_t)sizeof(double);
 }
 
-int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, const float* x,
-                   const float* gamma, const float* beta, float* affine, void* workspace,
-                   size_t workspace_bytes, void* stream) {
+// ctmr_gn_affine and ctmr_gn_affine_cat: x2 null for one source.
+static int gn_affine_run(int32_t n, int64_t s, int32_t c, int32_t c1, int32_t groups, float eps, const float* x,
+                         const float* x2, const float* gamma, const float* beta, float* affine, void* workspace,
+                         size_t workspace_bytes, void* stream) {
   if (n <= 0 || s <= 0 || c <= 0 || groups <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
   if (c % groups != 0) return fail(CTMR_E_INVALID, "channels must be divisible by groups");
   const bool vec = (c % 4 == 0);
   if ((vec && c > 1024) || (!vec && c > 256))
     return fail(CTMR_E_UNSUPPORTED, "group norm needs c <= 1024 (c % 4 == 0) or c <= 256");
-  if (!x || !gamma || !beta || !affine) return fail(CTMR_E_INVALID, "null pointer");
-  if (vec && ((uintptr_t)x & 15) != 0) return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
+  if (!x || !gamma || !beta || !affine || (c1 != c && !x2)) return fail(CTMR_E_INVALID, "null pointer");
+  if (c1 != c && (!vec || c1 <= 0 || c1 >= c || c1 % 4 != 0))
+    return fail(CTMR_E_INVALID, "two-source group norm needs 0 < c1 < c, both multiples of 4");
+  if (vec && (((uintptr_t)x | (c1 != c ? (uintptr_t)x2 : 0)) & 15) != 0)
+    return fail(CTMR_E_INVALID, "x must be 16-byte aligned");
   const GnChunks ch = gn_chunks(n, s, c);
   const int64_t chunk_vox = ch.vox, chunks = ch.count;
   const int64_t need = (int64_t)n * chunks * c * 2 * (int64_t)sizeof(double);
@@ -350,17 +360,33 @@ int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, c
   if (chunks >= (1 << 30) || n > 65535) return fail(CTMR_E_UNSUPPORTED, "volume too large");
   hipStream_t st = (hipStream_t)stream;
   double* part = (double*)workspace;
+  const float* second = c1 != c ? x2 : nullptr;
   if (vec)
-    hipLaunchKernelGGL(gn_partial_kernel<4>, dim3((unsigned)chunks, n), dim3(256), 0, st, x, s, c,
+    hipLaunchKernelGGL(gn_partial_kernel<4>, dim3((unsigned)chunks, n), dim3(256), 0, st, x, second, c1, s, c,
                        chunk_vox, (int)chunks, part);
   else
-    hipLaunchKernelGGL(gn_partial_kernel<1>, dim3((unsigned)chunks, n), dim3(256), 0, st, x, s, c,
+    hipLaunchKernelGGL(gn_partial_kernel<1>, dim3((unsigned)chunks, n), dim3(256), 0, st, x, second, c1, s, c,
                        chunk_vox, (int)chunks, part);
   int rc = check_launch("gn_partial");
   if (rc) return rc;
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups, n), dim3(256), 0, st, part, (int)chunks, c,
                      groups, s * (c / groups), gamma, beta, eps, affine);
   return check_launch("gn_finalize");
+}
+
+int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, const float* x,
+                   const float* gamma, const float* beta, float* affine, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  return gn_affine_run(n, s, c, c, groups, eps, x, nullptr, gamma, beta, affine, workspace, workspace_bytes,
+                       stream);
+}
+
+int ctmr_gn_affine_cat(int32_t n, int64_t s, int32_t c1, int32_t c2, int32_t groups, float eps, const float* x1,
+                       const float* x2, const float* gamma, const float* beta, float* affine, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (c1 <= 0 || c2 <= 0) return fail(CTMR_E_INVALID, "two-source group norm needs c1 > 0 and c2 > 0");
+  return gn_affine_run(n, s, c1 + c2, c1, groups, eps, x1, x2, gamma, beta, affine, workspace, workspace_bytes,
+                       stream);
 }
 
 int ctmr_gn_affine_from_stats(int32_t n, int32_t tiles, int32_t c, int32_t groups, int64_t count, float eps,

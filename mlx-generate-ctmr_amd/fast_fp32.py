@@ -81,6 +81,57 @@ def _require(x: Tensor, name: str, ndim: int = 5) -> Tensor:
     return x.contiguous()
 
 
+class ChannelCat:
+    """The channel concatenation of two NDHWC fp32 tensors on the same voxels, never materialised.
+
+    The up path of the diffusion UNet concatenates its hidden state with a skip before every residual
+    block (``unet.py:444``); the block's group norm, 3x3x3 conv and 1x1x1 skip projection read each
+    channel block from its own tensor instead (``ctmr_gn_affine_cat``, ``ctmr_conv3d_cat``), with the
+    same values in the same order, so the results equal those on ``torch.cat`` bit for bit.  Both
+    channel counts must be multiples of 16; ``materialize()`` returns the concatenated tensor for
+    consumers that need one.
+    """
+
+    __slots__ = ("first", "second")
+
+    def __init__(self, first: Tensor, second: Tensor):
+        first, second = _require(first, "first"), _require(second, "second")
+        if tuple(first.shape[:-1]) != tuple(second.shape[:-1]):
+            raise ValueError(f"concatenated tensors differ in voxels: {tuple(first.shape)} vs {tuple(second.shape)}")
+        if first.device != second.device:
+            raise ValueError("concatenated tensors are on different devices")
+        if int(first.shape[-1]) % 16 or int(second.shape[-1]) % 16:
+            raise ValueError("concatenated channel counts must be multiples of 16; got "
+                             f"{int(first.shape[-1])} and {int(second.shape[-1])}")
+        self.first, self.second = first, second
+
+    @property
+    def shape(self) -> torch.Size:
+        return torch.Size((*self.first.shape[:-1], int(self.first.shape[-1]) + int(self.second.shape[-1])))
+
+    @property
+    def device(self) -> torch.device:
+        return self.first.device
+
+    def materialize(self) -> Tensor:
+        return torch.cat([self.first, self.second], dim=-1)
+
+
+def concat_channels(first: Tensor, second: Tensor):
+    """``ChannelCat(first, second)`` when both channel counts are multiples of 16 (the two-source
+    kernels' channel blocks), else the materialised ``torch.cat``."""
+    if int(first.shape[-1]) % 16 == 0 and int(second.shape[-1]) % 16 == 0:
+        return ChannelCat(first, second)
+    return torch.cat([first, second], dim=-1)
+
+
+def _split_input(x, name: str = "x") -> tuple[Tensor, Optional[Tensor]]:
+    """``(x, None)`` for a tensor, ``(first, second)`` for a ``ChannelCat``."""
+    if isinstance(x, ChannelCat):
+        return x.first, x.second
+    return _require(x, name), None
+
+
 def _vec(t: Optional[Tensor], n: int, name: str, device: torch.device) -> Optional[Tensor]:
     if t is None:
         return None
@@ -240,8 +291,12 @@ def implicit_gemm_conv3d(
         ValueError: on a packed weight that does not fit, unsupported option
             combinations, or a residual of the wrong shape.
     """
-    x = _require(x, "x")
+    x, x2 = _split_input(x)
+    cin2 = 0 if x2 is None else int(x2.shape[-1])
     n, d, h, w, cin = (int(v) for v in x.shape)
+    cin += cin2
+    if x2 is not None and (upsample or trilinear):
+        raise ValueError("a concatenated input supports only a plain convolution")
     if trilinear and (upsample or stride != 1 or affine is not None or silu):
         raise ValueError("trilinear packing supports only a plain stride-1 convolution")
     if upsample and stride != 1:
@@ -251,7 +306,7 @@ def implicit_gemm_conv3d(
     mode = _lib.MODE_NEAREST2X if upsample else (_lib.MODE_TRILINEAR2X if trilinear else _lib.MODE_PLAIN)
     code = _lib.DT_BF16 if packed.dtype == torch.bfloat16 else _lib.DT_F32
     desc = ops.make_desc(tuple(x.shape), cout, ksize, stride, mode, _lib.F_STREAM if stream_gemm else 0, code,
-                         split)
+                         split, cin2)
     if packed.numel() != _lib.packed_weight_elems(desc):
         raise ValueError(
             f"packed weight of {packed.numel()} elements does not fit {cin} input / {cout} output "
@@ -270,13 +325,13 @@ def implicit_gemm_conv3d(
         if tuple(residual.shape) != out_shape:
             raise ValueError(f"residual shape {tuple(residual.shape)} != output {out_shape}")
     if gn_groups > 0 and ops.conv_stats_tiles(tuple(x.shape), cout, ksize, stride, mode, code, split,
-                                              stream_gemm, int(gn_groups)) > 0:
+                                              stream_gemm, int(gn_groups), cin2) > 0:
         y, stats = ops.conv3d_gn(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split,
-                                 stream_gemm, int(gn_groups))
+                                 stream_gemm, int(gn_groups), x2)
         y._ctmr_gn_stats = (int(gn_groups), stats, y._version)
         return y
     return ops.conv3d(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split,
-                      stream_gemm)
+                      stream_gemm, x2)
 
 
 def conv_output_stats(x: Tensor, groups: int) -> Optional[Tensor]:
@@ -315,13 +370,16 @@ def pointwise_conv(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
 
 def group_norm_affine(x: Tensor, weight: Tensor, bias: Tensor, *, groups: int, eps: float) -> Tensor:
     """``(N, C, 2)`` scale/offset pairs of a group norm of NDHWC ``x`` (``medmlx_core.group_norm_affine``).
-    Uses the statistics a convolution epilogue wrote for ``x`` when there are any."""
-    x = _require(x, "x")
-    c = int(x.shape[-1])
+    Uses the statistics a convolution epilogue wrote for ``x`` when there are any; ``x`` may be a
+    ``ChannelCat``."""
+    x, x2 = _split_input(x)
+    c = int(x.shape[-1]) + (0 if x2 is None else int(x2.shape[-1]))
     if c % groups != 0:
         raise ValueError(f"{c} channels are not divisible by {groups} groups")
     gamma = _vec(weight, c, "norm weight", x.device)
     beta = _vec(bias, c, "norm bias", x.device)
+    if x2 is not None:
+        return ops.gn_affine(x, gamma, beta, int(groups), float(eps), x2)
     stats = conv_output_stats(x, int(groups))
     if stats is not None:
         count = (x.numel() // (int(x.shape[0]) * c)) * (c // int(groups))
@@ -369,8 +427,10 @@ def norm_conv3d(
     out_gn_groups: int = 0,
 ) -> Tensor:
     """``conv(upsample?(silu?(norm?(x)))) + bias (+ residual)`` for 3x3x3 kernels (:162-211);
-    ``out_gn_groups`` asks for the output's group-norm statistics (``implicit_gemm_conv3d``)."""
-    x = _require(x, "x")
+    ``out_gn_groups`` asks for the output's group-norm statistics (``implicit_gemm_conv3d``).  ``x``
+    may be a ``ChannelCat`` (no upsampling then)."""
+    if not isinstance(x, ChannelCat):
+        x = _require(x, "x")
     affine = None if norm is None else group_norm_affine(x, norm[0], norm[1], groups=num_groups, eps=eps)
     mode = _lib.MODE_NEAREST2X if upsample else _lib.MODE_PLAIN
     return implicit_gemm_conv3d(x, _pack(weight, mode), bias, cout=int(weight.shape[0]), affine=affine,
@@ -533,7 +593,8 @@ def residual_block(
     conv1_bias: Optional[Tensor] = None,
     out_gn_groups: int = 0,
 ) -> Tensor:
-    """Fused ``DiffusionUNetResnetBlock`` on NDHWC ``x`` (``fast_fp32.residual_block_ncdhw``, :214-291).
+    """Fused ``DiffusionUNetResnetBlock`` on NDHWC ``x`` (``fast_fp32.residual_block_ncdhw``, :214-291);
+    ``x`` may be a ``ChannelCat`` (the up path's hidden state and skip).
 
     The time-embedding projection joins conv1's bias per batch item, the skip
     path (after its optional 1x1x1 projection) joins conv2's accumulator.
@@ -546,6 +607,9 @@ def residual_block(
     them for the block's output when ``out_gn_groups`` is set (the next
     consumer is a group norm with that many groups).
     """
+    if isinstance(x, ChannelCat) and (up or down or
+                                      int(x.shape[-1]) == int(weights["conv1.conv.weight"].shape[0])):
+        x = x.materialize()  # resampled or unprojected inputs need the concatenated tensor itself
     if conv1_bias is None:
         temb = linear(F.silu(emb), weights["time_emb_proj.weight"], weights["time_emb_proj.bias"])
         bias1 = weights["conv1.conv.bias"].reshape(1, -1) + temb

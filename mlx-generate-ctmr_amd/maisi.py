@@ -179,7 +179,7 @@ def _blocks(weights: Mapping[str, Tensor], emb: Tensor, groups: int, eps: float,
     index, offsets = _block_major_index(spans, n, int(conv1_bias.shape[1]), conv1_bias.device)
     blocked = conv1_bias.reshape(-1).index_select(0, index)
 
-    def resnet(h: Tensor, prefix: str, *, normed_next: bool = True, **kw) -> Tensor:
+    def resnet(h, prefix: str, *, normed_next: bool = True, **kw) -> Tensor:
         """``normed_next``: a group norm reads the output next (its statistics come from conv2)."""
         off, width = offsets[prefix]
         return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps,
@@ -272,8 +272,9 @@ def denoise_unet(
         samples, skips = skips[-n_res:], skips[:-n_res]
         for r in range(n_res):
             skip = samples.pop()
-            hidden = torch.cat([hidden, skip], dim=-1)
-            hidden = resnet(hidden, f"up_blocks.{index}.resnets.{r}", normed_next=rev_attn[index] or r == n_res - 1)
+            # cat([hidden, skip]) (unet.py:444) read in place by the block's norm and convolutions
+            hidden = resnet(ff.concat_channels(hidden, skip), f"up_blocks.{index}.resnets.{r}",
+                            normed_next=rev_attn[index] or r == n_res - 1)
             if rev_attn[index]:
                 hidden = attention(hidden, f"up_blocks.{index}.attentions.{r}", rev_heads[index])
         if index != n_levels - 1:

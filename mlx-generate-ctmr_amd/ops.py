@@ -58,10 +58,17 @@ def make_desc(
     flags: int,
     dtype: int,
     split: int,
+    cin2: int = 0,
 ) -> _lib.ConvDesc:
+    """Descriptor of a conv of ``x_shape`` (NDHWC); ``cin2`` > 0: the input is the channel concatenation
+    of that tensor and a second one of ``cin2`` channels (``ctmr_conv3d_cat``)."""
     n, d, h, w, cin = (int(v) for v in x_shape)
-    return _lib.conv_desc(n, d, h, w, cin, cout, ksize=ksize, stride=stride, mode=mode,
-                          flags=flags, dtype=dtype, split=split)
+    return _lib.conv_desc(n, d, h, w, cin + cin2, cout, ksize=ksize, stride=stride, mode=mode,
+                          flags=flags, dtype=dtype, split=split, cin1=cin if cin2 else 0)
+
+
+def _cin2(x2: Optional[Tensor]) -> int:
+    return 0 if x2 is None else int(x2.shape[-1])
 
 
 # ---------------------------------------------------------------------------
@@ -106,42 +113,54 @@ def conv3d(
     dtype: int,
     split: int,
     stream_gemm: bool = False,
+    x2: Optional[Tensor] = None,
 ) -> Tensor:
     """``ctmr_conv3d`` on an NDHWC fp32 tensor; returns the NDHWC output.  ``stream_gemm``
-    forces the register-streaming GEMM where the LDS-staged one would be chosen."""
-    _require_device(x, packed, bias, affine, residual)
-    x, residual = _aligned16(x), _aligned16(residual)
+    forces the register-streaming GEMM where the LDS-staged one would be chosen.  With ``x2`` the
+    input is the channel concatenation of ``x`` and ``x2`` (``ctmr_conv3d_cat``)."""
+    _require_device(x, packed, bias, affine, residual, x2)
+    x, residual, x2 = _aligned16(x), _aligned16(residual), _aligned16(x2)
     batch_bias = bias is not None and bias.dim() == 2
     flags = _flags(affine is not None, silu, batch_bias, residual is not None)
     if stream_gemm:
         flags |= _lib.F_STREAM
-    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split)
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split, _cin2(x2))
     od, oh, ow = _lib.output_dims(desc)
     y = torch.empty((x.shape[0], od, oh, ow, cout), device=x.device, dtype=torch.float32)
     ws_bytes = _lib.workspace_bytes(desc)
     ws = torch.empty(max(ws_bytes, 1), device=x.device, dtype=torch.uint8)
-    _lib.check(
-        _lib.lib().ctmr_conv3d(
-            ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
-            _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, _stream(x.device),
-        ),
-        "ctmr_conv3d",
-    )
+    if x2 is None:
+        _lib.check(
+            _lib.lib().ctmr_conv3d(
+                ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
+                _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, _stream(x.device),
+            ),
+            "ctmr_conv3d",
+        )
+    else:
+        _lib.check(
+            _lib.lib().ctmr_conv3d_cat(
+                ctypes.byref(desc), x.data_ptr(), x2.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
+                _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, _stream(x.device),
+            ),
+            "ctmr_conv3d_cat",
+        )
     return y
 
 
 @conv3d.register_fake
-def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split, stream_gemm=False):
-    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, 0, dtype, split)
+def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split, stream_gemm=False,
+      x2=None):
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, 0, dtype, split, _cin2(x2))
     od, oh, ow = _lib.output_dims(desc)
     return x.new_empty((x.shape[0], od, oh, ow, cout))
 
 
 def conv_stats_tiles(x_shape: tuple[int, ...], cout: int, ksize: int, stride: int, mode: int, dtype: int,
-                     split: int, stream_gemm: bool, groups: int) -> int:
+                     split: int, stream_gemm: bool, groups: int, cin2: int = 0) -> int:
     """Group-norm partials per batch item that ``conv3d_gn`` writes for this shape, 0 if it cannot."""
     flags = _lib.F_STREAM if stream_gemm else 0
-    desc = make_desc(tuple(x_shape), cout, ksize, stride, mode, flags, dtype, split)
+    desc = make_desc(tuple(x_shape), cout, ksize, stride, mode, flags, dtype, split, cin2)
     return max(int(_lib.lib().ctmr_conv3d_stats_tiles(ctypes.byref(desc), groups)), 0)
 
 
@@ -161,16 +180,18 @@ def conv3d_gn(
     split: int,
     stream_gemm: bool,
     groups: int,
+    x2: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor]:
     """``ctmr_conv3d_gn``: the ``conv3d`` output plus float64 group-norm partials of it, shape
-    ``(N, tiles, groups, 2)`` holding (sum, sum of squares) per output tile and group."""
-    _require_device(x, packed, bias, affine, residual)
-    x, residual = _aligned16(x), _aligned16(residual)
+    ``(N, tiles, groups, 2)`` holding (sum, sum of squares) per output tile and group.  ``x2`` as in
+    ``conv3d`` (``ctmr_conv3d_cat_gn``)."""
+    _require_device(x, packed, bias, affine, residual, x2)
+    x, residual, x2 = _aligned16(x), _aligned16(residual), _aligned16(x2)
     batch_bias = bias is not None and bias.dim() == 2
     flags = _flags(affine is not None, silu, batch_bias, residual is not None)
     if stream_gemm:
         flags |= _lib.F_STREAM
-    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split)
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split, _cin2(x2))
     tiles = _lib.check(_lib.lib().ctmr_conv3d_stats_tiles(ctypes.byref(desc), groups), "ctmr_conv3d_stats_tiles")
     if tiles == 0:
         raise ValueError("this convolution cannot produce group-norm partials")
@@ -179,20 +200,32 @@ def conv3d_gn(
     stats = torch.empty((x.shape[0], tiles, groups, 2), device=x.device, dtype=torch.float64)
     ws_bytes = _lib.workspace_bytes(desc)
     ws = torch.empty(max(ws_bytes, 1), device=x.device, dtype=torch.uint8)
-    _lib.check(
-        _lib.lib().ctmr_conv3d_gn(
-            ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
-            _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, groups, stats.data_ptr(),
-            _stream(x.device),
-        ),
-        "ctmr_conv3d_gn",
-    )
+    if x2 is None:
+        _lib.check(
+            _lib.lib().ctmr_conv3d_gn(
+                ctypes.byref(desc), x.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
+                _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, groups, stats.data_ptr(),
+                _stream(x.device),
+            ),
+            "ctmr_conv3d_gn",
+        )
+    else:
+        _lib.check(
+            _lib.lib().ctmr_conv3d_cat_gn(
+                ctypes.byref(desc), x.data_ptr(), x2.data_ptr(), packed.data_ptr(), _ptr(bias), _ptr(affine),
+                _ptr(residual), y.data_ptr(), ws.data_ptr(), ws_bytes, groups, stats.data_ptr(),
+                _stream(x.device),
+            ),
+            "ctmr_conv3d_cat_gn",
+        )
     return y, stats
 
 
 @conv3d_gn.register_fake
-def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split, stream_gemm, groups):
-    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, _lib.F_STREAM if stream_gemm else 0, dtype, split)
+def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split, stream_gemm, groups,
+      x2=None):
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, _lib.F_STREAM if stream_gemm else 0, dtype, split,
+                     _cin2(x2))
     od, oh, ow = _lib.output_dims(desc)
     tiles = max(int(_lib.lib().ctmr_conv3d_stats_tiles(ctypes.byref(desc), groups)), 1)
     return (x.new_empty((x.shape[0], od, oh, ow, cout)),
@@ -225,26 +258,39 @@ def _(stats, gamma, beta, count, eps):
 
 
 @torch.library.custom_op("ctmr::gn_affine", mutates_args=())
-def gn_affine(x: Tensor, gamma: Tensor, beta: Tensor, groups: int, eps: float) -> Tensor:
-    """Per-(batch, channel) (scale, offset) pairs, shape ``(N, C, 2)``."""
-    _require_device(x, gamma, beta)
-    n, c = int(x.shape[0]), int(x.shape[-1])
-    s = x.numel() // (n * c)
+def gn_affine(x: Tensor, gamma: Tensor, beta: Tensor, groups: int, eps: float,
+              x2: Optional[Tensor] = None) -> Tensor:
+    """Per-(batch, channel) (scale, offset) pairs, shape ``(N, C, 2)``; with ``x2`` of the channel
+    concatenation of ``x`` and ``x2`` (``ctmr_gn_affine_cat``)."""
+    _require_device(x, gamma, beta, x2)
+    x, x2 = _aligned16(x), _aligned16(x2)
+    n, c1 = int(x.shape[0]), int(x.shape[-1])
+    c2 = _cin2(x2)
+    c = c1 + c2
+    s = x.numel() // (n * c1)
     out = torch.empty((n, c, 2), device=x.device, dtype=torch.float32)
     ws_bytes = _lib.gn_workspace_bytes(n, s, c)
     ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
-    _lib.check(
-        _lib.lib().ctmr_gn_affine(n, s, c, groups, float(eps), x.data_ptr(), gamma.data_ptr(),
-                                  beta.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
-                                  _stream(x.device)),
-        "ctmr_gn_affine",
-    )
+    if x2 is None:
+        _lib.check(
+            _lib.lib().ctmr_gn_affine(n, s, c, groups, float(eps), x.data_ptr(), gamma.data_ptr(),
+                                      beta.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                      _stream(x.device)),
+            "ctmr_gn_affine",
+        )
+    else:
+        _lib.check(
+            _lib.lib().ctmr_gn_affine_cat(n, s, c1, c2, groups, float(eps), x.data_ptr(), x2.data_ptr(),
+                                          gamma.data_ptr(), beta.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                          ws_bytes, _stream(x.device)),
+            "ctmr_gn_affine_cat",
+        )
     return out
 
 
 @gn_affine.register_fake
-def _(x, gamma, beta, groups, eps):
-    return x.new_empty((x.shape[0], x.shape[-1], 2))
+def _(x, gamma, beta, groups, eps, x2=None):
+    return x.new_empty((x.shape[0], x.shape[-1] + _cin2(x2), 2))
 
 
 @torch.library.custom_op("ctmr::gn_apply", mutates_args=())

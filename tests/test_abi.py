@@ -274,3 +274,55 @@ def test_conv_kernel_route(ctmr, shape, cout, kw, expected):
     n, d, h, w, cin = shape
     desc = L.conv_desc(n, d, h, w, cin, cout, **kw)
     assert L.conv_kernel(desc) == expected
+
+
+@pytest.mark.parametrize(("shape", "cin1", "cout", "kw", "expected"), [
+    ((2, 64, 64, 32, 192), 128, 64, {}, "lds"),                      # up-block conv1: hidden 128 + skip 64
+    ((2, 64, 64, 32, 192), 128, 64, {"flags": 3}, "lds"),            # with the GN affine + SiLU staging
+    ((2, 64, 64, 32, 192), 128, 64, {"ksize": 1}, "pointwise"),      # skip projection: read in place
+    ((2, 64, 64, 32, 192), 128, 64, {"ksize": 1, "flags": 4}, "stream"),  # per-batch bias: packed first
+    ((2, 4, 8, 8, 1024), 512, 512, {}, "split_waves"),               # deep level: packed first
+    ((2, 64, 64, 32, 192), 128, 64, {"flags": 16}, "stream"),        # CTMR_F_STREAM: packed, never direct
+    ((2, 32, 32, 16, 384), 256, 128, {"dtype": 1}, "lds_bf16"),      # bf16: the packed copy
+])
+def test_two_source_routes(ctmr, shape, cin1, cout, kw, expected):
+    """A two-source input (cin1 > 0) is read in place by the LDS-staged and the persistent 1x1 GEMMs
+    and packed (both tensors into the usual padded copy) for every other route."""
+    L = ctmr._lib
+    n, d, h, w, cin = shape
+    desc = L.conv_desc(n, d, h, w, cin, cout, cin1=cin1, **kw)
+    assert L.conv_kernel(desc) == expected
+    one = L.conv_desc(n, d, h, w, cin, cout, **kw)
+    assert L.packed_weight_elems(desc) == L.packed_weight_elems(one)  # the weight does not change
+    if expected in ("lds", "pointwise"):
+        assert L.workspace_bytes(desc) == L.workspace_bytes(one)
+    else:
+        assert L.workspace_bytes(desc) > 0  # the packed copy of both tensors
+
+
+def test_two_source_validation(ctmr, native_loaded):
+    L = ctmr._lib
+    fake = 0x1000  # never dereferenced: the checks fail first
+    for cin1 in (-16, 8, 192, 200):  # negative, not a multiple of 16, not below cin
+        d = L.conv_desc(1, 8, 8, 8, 192, 64, cin1=cin1)
+        with pytest.raises(RuntimeError):
+            L.conv_kernel(d)
+    d = L.conv_desc(1, 8, 8, 8, 192, 64, cin1=128, mode=L.MODE_NEAREST2X)
+    with pytest.raises(RuntimeError, match="PLAIN"):
+        L.conv_kernel(d)
+    d = L.conv_desc(1, 8, 8, 8, 192, 64, cin1=128)
+    rc = native_loaded.ctmr_conv3d(ctypes.byref(d), fake, fake, None, None, None, fake, fake, 1 << 20, None)
+    assert rc == L.E_INVALID and "ctmr_conv3d_cat" in L.last_error()
+    one = L.conv_desc(1, 8, 8, 8, 192, 64)
+    rc = native_loaded.ctmr_conv3d_cat(ctypes.byref(one), fake, fake, fake, None, None, None, fake, fake, 1 << 20,
+                                       None)
+    assert rc == L.E_INVALID and "cin1" in L.last_error()
+    rc = native_loaded.ctmr_conv3d_cat(ctypes.byref(d), fake, None, fake, None, None, None, fake, fake, 1 << 20,
+                                       None)
+    assert rc == L.E_INVALID
+    rc = native_loaded.ctmr_gn_affine_cat(1, 512, 128, 0, 32, 1e-6, fake, fake, fake, fake, fake, fake, 1 << 20,
+                                          None)
+    assert rc == L.E_INVALID
+    rc = native_loaded.ctmr_gn_affine_cat(1, 512, 126, 66, 32, 1e-6, fake, fake, fake, fake, fake, fake, 1 << 20,
+                                          None)
+    assert rc == L.E_INVALID and "multiples of 4" in L.last_error()

@@ -732,3 +732,103 @@ def test_small_cin_lds_gemm_equals_im2col_gemm(ctmr, dev, name, shape, cout, opt
         yy = _h(y).reshape(n, -1, groups, cout // groups)
         ref = np.stack([yy.sum(axis=(1, 3)), (yy * yy).sum(axis=(1, 3))], axis=-1)
         assert rm.max_rel_error(hs, ref) <= 1e-10
+
+
+CAT_CASES = [
+    # (name, voxels (n, d, h, w), c1, c2, cout, ksize, options, route of the two-source desc)
+    ("LDS GEMM, up-block conv1 class", (2, 64, 64, 32), 128, 64, 64, 3,
+     {"fused": True, "batch_bias": True, "gn": 32}, "lds"),
+    ("LDS GEMM, residual, two K ranges", (1, 32, 64, 48), 64, 64, 128, 3, {"residual": True}, "lds"),
+    ("LDS GEMM, ragged bricks", (1, 30, 60, 44), 96, 32, 64, 3, {"fused": True}, "lds"),
+    ("persistent 1x1 skip projection", (2, 16, 32, 32), 256, 128, 128, 1, {}, "pointwise"),
+    ("persistent 1x1, K split", (2, 8, 16, 16), 512, 256, 256, 1, {}, "pointwise"),
+    ("1x1 with per-batch bias (packed)", (2, 8, 16, 16), 64, 32, 64, 1, {"batch_bias": True}, "stream"),
+    ("deep level (packed, wave K split)", (2, 4, 8, 8), 512, 512, 512, 3, {"fused": True, "gn": 32},
+     "split_waves"),
+    ("streaming GEMM (CTMR_F_STREAM)", (1, 32, 32, 32), 64, 64, 64, 3, {"stream": True}, "stream"),
+    ("bf16 LDS GEMM", (2, 8, 16, 16), 128, 64, 64, 3, {"bf16": True, "fused": True}, "lds_bf16"),
+    ("bf16 1x1", (2, 8, 16, 16), 128, 64, 128, 1, {"bf16": True}, "pointwise"),
+]
+
+
+@pytest.mark.parametrize(("name", "vox", "c1", "c2", "cout", "ksize", "opts", "route"), CAT_CASES,
+                         ids=[c[0] for c in CAT_CASES])
+def test_channel_cat_conv_equals_conv_of_concatenation(ctmr, dev, name, vox, c1, c2, cout, ksize, opts, route):
+    """A conv of ChannelCat(a, b) (``ctmr_conv3d_cat``: each channel block read from its own tensor, or both
+    packed into the padded copy) equals the same conv of torch.cat([a, b]) bit for bit -- output and
+    epilogue group-norm partials -- on every route, and stays within the float64 bar."""
+    print(f"channel-cat conv {name}: {vox} {c1}+{c2} -> {cout} k{ksize} {opts}", flush=True)
+    f, L = ctmr.fast_fp32, ctmr._lib
+    rng = np.random.default_rng(sum(vox) + c1 + c2 + cout + ksize)
+    n = vox[0]
+    a = rng.standard_normal((*vox, c1)).astype(np.float32)
+    bb = (1.5 * rng.standard_normal((*vox, c2)) + 0.3).astype(np.float32)
+    cin = c1 + c2
+    w = (rng.standard_normal((cout, cin, ksize, ksize, ksize)) / np.sqrt(cin * ksize ** 3)).astype(np.float32)
+    bias = rng.standard_normal((n, cout) if opts.get("batch_bias") else (cout,)).astype(np.float32)
+    at, bt = _t(a, dev), _t(bb, dev)
+    cat_t = torch.cat([at, bt], dim=-1)
+    cc = f.ChannelCat(at, bt)
+    affine = None
+    if opts.get("fused"):
+        gw = (1 + 0.2 * rng.standard_normal(cin)).astype(np.float32)
+        gb = (0.2 * rng.standard_normal(cin)).astype(np.float32)
+        affine = f.group_norm_affine(cat_t, _t(gw, dev), _t(gb, dev), groups=32, eps=1e-6)
+        assert torch.equal(f.group_norm_affine(cc, _t(gw, dev), _t(gb, dev), groups=32, eps=1e-6), affine)
+    out_vox = vox
+    res = _t(rng.standard_normal((*out_vox, cout)).astype(np.float32), dev) if opts.get("residual") else None
+    dtype = "bf16" if opts.get("bf16") else "fp32"
+    flags = (L.F_AFFINE | L.F_SILU if affine is not None else 0) | (L.F_BATCH_BIAS if opts.get("batch_bias") else 0) \
+        | (L.F_RESIDUAL if res is not None else 0) | (L.F_STREAM if opts.get("stream") else 0)
+    desc = ctmr.ops.make_desc((*vox, c1), cout, ksize, 1, L.MODE_PLAIN, flags, L.DT_BF16 if opts.get("bf16")
+                              else L.DT_F32, 0, c2)
+    assert L.conv_kernel(desc) == route
+    packed = f.pack_weight(_t(w, dev), dtype=dtype)
+    groups = opts.get("gn", 0)
+    run = lambda x: f.implicit_gemm_conv3d(x, packed, _t(bias, dev), cout=cout, ksize=ksize, affine=affine,
+                                           silu=affine is not None, residual=res, stream_gemm=bool(opts.get("stream")),
+                                           gn_groups=groups)
+    y_cat, y_ref = run(cc), run(cat_t)
+    assert torch.equal(y_cat, y_ref), f"{name}: two-source conv differs from the conv of the concatenation"
+    if groups:
+        st, st_ref = f.conv_output_stats(y_cat, groups), f.conv_output_stats(y_ref, groups)
+        assert st is not None and st_ref is not None and torch.equal(st, st_ref)
+    # float64 bar on the concatenated input, at every corner, edge and face of the volume and 256 voxels
+    src = np.concatenate([a, bb], axis=-1)
+    pts = rm.boundary_points(n, vox[1:], 256, seed=11)
+    expected = rm.conv3d_points(src, w, None, pts, affine=None if affine is None else _h(affine),
+                                apply_silu=affine is not None)
+    expected = expected + (bias[pts[:, 0]] if bias.ndim == 2 else bias)
+    if res is not None:
+        expected = expected + rm.gather_points(_h(res), pts)
+    _assert_rel(rm.gather_points(_h(y_cat), pts), expected, BF16_REL if dtype == "bf16" else FP32_REL,
+                f"channel-cat {name}")
+
+
+def test_channel_cat_group_norm_straddling_groups(ctmr, dev):
+    """Group-norm statistics of ChannelCat(a, b) equal those of torch.cat([a, b]) bit for bit, with
+    groups that straddle the boundary (192 channels in 32 groups of 6: group 21 holds channels 126-131)
+    and at the UNet's 64^3-level size; the residual block on a ChannelCat equals the block on the
+    concatenation."""
+    f = ctmr.fast_fp32
+    g = torch.Generator(device=dev).manual_seed(5)
+    for vox, c1, c2 in (((2, 64, 64, 32), 128, 64), ((1, 5, 7, 9), 16, 48), ((2, 8, 8, 4), 512, 512)):
+        a = torch.randn(*vox, c1, device=dev, generator=g)
+        b = 2 * torch.randn(*vox, c2, device=dev, generator=g) + 1
+        c = c1 + c2
+        gamma = 1 + 0.1 * torch.randn(c, device=dev, generator=g)
+        beta = 0.1 * torch.randn(c, device=dev, generator=g)
+        ref = f.group_norm_affine(torch.cat([a, b], -1), gamma, beta, groups=32, eps=1e-6)
+        got = f.group_norm_affine(f.ChannelCat(a, b), gamma, beta, groups=32, eps=1e-6)
+        assert torch.equal(got, ref), f"{vox} {c1}+{c2}"
+    # a UNet up-path residual block (hidden 128 + skip 64 -> 64, time-embedding bias)
+    m = ctmr.maisi
+    wts = {k: torch.from_numpy(v).to(dev) for k, v in
+           m.random_weights(m._resnet_shapes("blk", 192, 64, 512), seed=3).items()}
+    wts = {k[len("blk."):]: v for k, v in wts.items()}
+    h = torch.randn(2, 16, 16, 8, 128, device=dev, generator=g)
+    s = torch.randn(2, 16, 16, 8, 64, device=dev, generator=g)
+    emb = torch.randn(2, 512, device=dev, generator=g)
+    y_cat = f.residual_block(f.ChannelCat(h, s), emb, wts, num_groups=32, eps=1e-6)
+    y_ref = f.residual_block(torch.cat([h, s], -1), emb, wts, num_groups=32, eps=1e-6)
+    assert torch.equal(y_cat, y_ref)
