@@ -25,7 +25,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-seco
 from __future__ import annotations
 
 import argparse
+import contextlib
 import ctypes
+import gc
 import importlib
 import json
 import os
@@ -70,15 +72,32 @@ def warm_up(fn, steps, settle_s=SETTLE_S):
     return done
 
 
+@contextlib.contextmanager
+def gc_quiet():
+    """A timed region without Python's cyclic garbage collector (as ``timeit`` runs).  A full
+    collection walks every tracked object of this process (~270k with torch imported; 60-105 ms
+    measured on the MI355X host), which would otherwise land in whichever step happens to trigger
+    it.  No collection is forced on entry: the GPU would idle for its duration right before the
+    timed steps and its clock drop (measured: the config-2c 1x1 conv 0.166 -> 0.199 ms)."""
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was_enabled:
+            gc.enable()
+
+
 def _wall_ms(fn, steps):
     import torch
 
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    with gc_quiet():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def staged_op(pkg, x, w, b, dtype_code, stream_gemm=False):
@@ -402,10 +421,11 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         torch.cuda.reset_peak_memory_stats(dev)
         times = []
         for _ in range(reps):
-            t0 = time.perf_counter()
-            r = fn()
-            torch.cuda.synchronize()
-            times.append(time.perf_counter() - t0)
+            with gc_quiet():
+                t0 = time.perf_counter()
+                r = fn()
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
             del r
         return float(np.median(times)), torch.cuda.max_memory_allocated(dev)
 
@@ -709,11 +729,12 @@ def main() -> int:
 
     step = lambda: f.conv3d(x, w, b, padding=1)
     warm_up(step, args.warmup)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    with gc_quiet():
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
     value = flops / (ms * 1e-3) / 1e12
 
     # dominant kernel (implicit GEMM), HIP events on its stream around each GEMM

@@ -879,6 +879,9 @@ struct LdsArgs {
   int gn_groups, gn_cpg;
 };
 
+// TWO: the input is two tensors (ctmr_conv3d_cat); the one-tensor kernel keeps
+// precomputed byte offsets and a single descriptor.
+template <bool TWO>
 __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
   __shared__ __attribute__((aligned(16))) char lds[kHaloVox * kLdsRow];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -902,10 +905,10 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 
   // Staging: piece i of thread t is channels 4*(t&3)..+3 of the chunk at halo
   // voxel (t>>2) + 64i.  Offsets are relative to the first staged plane, so
-  // they stay within 32 bits (the host checks 6 planes fit).  A chunk comes
-  // from x (chunks below c1 / 16) or from x2, whose rows have the remaining
-  // channels; gvox[i] is the piece's voxel index, the byte offset follows from
-  // the chunk's source.
+  // they stay within 32 bits (the host checks 6 planes fit).  goff[i] is the
+  // piece's byte offset; with TWO it is the piece's voxel index instead: a
+  // chunk comes from x (chunks below c1 / 16) or from x2, whose rows hold the
+  // remaining channels, and the byte offset follows from the chunk's source.
   const int part = tid & 3;
   const int zb = max(z0 - 1, 0);
   const int c2 = p.cin - p.c1;
@@ -915,38 +918,40 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
   const __amdgpu_buffer_rsrc_t xrsrc1 = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.x + vbase * p.c1), (short)0, (int)min((vtotal - vbase) * p.c1 * 4, (int64_t)0x7fffffff),
       0x00020000);
-  const __amdgpu_buffer_rsrc_t xrsrc2 = p.x2 ? __builtin_amdgcn_make_buffer_rsrc(
+  const __amdgpu_buffer_rsrc_t xrsrc2 = TWO ? __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.x2 + vbase * c2), (short)0, (int)min((vtotal - vbase) * c2 * 4, (int64_t)0x7fffffff),
       0x00020000) : xrsrc1;
-  int gvox[kStageIters];
+  int goff[kStageIters];
   unsigned valid = 0;
 #pragma unroll
   for (int i = 0; i < kStageIters; ++i) {
     const int hv = (tid >> 2) + 64 * i;
-    gvox[i] = 0;
+    goff[i] = 0;
     if (hv < kHaloVox) {
       const int hz = hv / (kHH * kHW), hr = hv - hz * (kHH * kHW);
       const int hy = hr / kHW, hx = hr - hy * kHW;
       const int gz = z0 - 1 + hz, gy = y0 - 1 + hy, gx = x0 - 1 + hx;
       if (gz >= 0 && gz < p.d && gy >= 0 && gy < p.h && gx >= 0 && gx < p.w) {
         valid |= 1u << i;
-        gvox[i] = ((gz - zb) * p.h + gy) * p.w + gx;
+        const int vox = ((gz - zb) * p.h + gy) * p.w + gx;
+        goff[i] = TWO ? vox : vox * p.cin * 4 + part * 16;
       }
     }
   }
-  // Source of a chunk: descriptor, row bytes and the chunk's byte offset in a row.
+  // Source of a chunk: descriptor, row bytes (TWO) and the chunk's byte offset in a row.
   struct ChunkSrc {
     __amdgpu_buffer_rsrc_t rs;
     int row, so;
   };
   auto chunk_src = [&](int chunk) {
     ChunkSrc c;
-    const bool second = chunk >= kb1;
+    const bool second = TWO && chunk >= kb1;
     c.rs = second ? xrsrc2 : xrsrc1;
     c.row = (second ? c2 : p.c1) * 4;
     c.so = __builtin_amdgcn_readfirstlane((second ? chunk - kb1 : chunk) * 64);
     return c;
   };
+  auto piece_off = [&](int i, const ChunkSrc& c) { return TWO ? goff[i] * c.row + part * 16 : goff[i]; };
 
   // A: LDS byte address of this lane's voxel at tap (0,0,0) per row block.
   int abase[4];
@@ -976,7 +981,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
     const ChunkSrc c = chunk_src(chunk);
 #pragma unroll
     for (int i = 0; i < kStageIters; ++i)
-      stage[i] = __builtin_amdgcn_raw_buffer_load_b128(c.rs, gvox[i] * c.row + part * 16, c.so, 0);
+      stage[i] = __builtin_amdgcn_raw_buffer_load_b128(c.rs, piece_off(i, c), c.so, 0);
   };
   auto commit = [&](int chunk) {
     f4 sc = {1.f, 1.f, 1.f, 1.f}, of = {0.f, 0.f, 0.f, 0.f};
@@ -1044,7 +1049,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
       // retire in order, so each piece has two taps of products to arrive
       // before a later weight load has to wait for it.
       if ((t & 1) && (t >> 1) < kStageIters)
-        stage[t >> 1] = __builtin_amdgcn_raw_buffer_load_b128(nx.rs, gvox[t >> 1] * nx.row + part * 16, nx.so, 0);
+        stage[t >> 1] = __builtin_amdgcn_raw_buffer_load_b128(nx.rs, piece_off(t >> 1, nx), nx.so, 0);
       __builtin_amdgcn_sched_barrier(0);
       // Raised priority while this wave's MFMAs issue, so a wave whose
       // operands are ready wins issue slots over waves in their staging code.
@@ -1566,7 +1571,8 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int DT, int WM, int WN>
+// TWO: A rows of a two-source input read in place (ctmr_conv3d_cat, fp32).
+template <int DT, int WM, int WN, bool TWO>
 __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
   static_assert(WM * WN == 4, "four waves per workgroup");
   using R = PwRing<WM, WN>;
@@ -1609,16 +1615,16 @@ __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
   // Load t of this wave fills stage rows 16 * (wave * kDma + t) + lane / 4,
   // slot lane % 4 -- piece (lane % 4) ^ swizzle of that row: an A row (voxel)
   // or a B column.  The lane offsets are fixed; items move the A base only.
-  // A rows of a two-source input: K blocks below kb1 from xp (rows of rb
-  // bytes), the rest from xp2 (rows of rb2 bytes); kb1 = kb for one source.
-  const int rb2 = (int)p.row_bytes2;
-  int voff[R::kDma], voff2[R::kDma];
+  // A rows of a two-source input (TWO): K blocks below kb1 from xp (rows of
+  // rb bytes), the rest from xp2 (rows of rb2 bytes).
+  const int rb2 = TWO ? (int)p.row_bytes2 : 0;
+  int voff[R::kDma], voff2[TWO ? R::kDma : 1];
 #pragma unroll
   for (int t = 0; t < R::kDma; ++t) {
     const int row = 16 * (wave * R::kDma + t) + (lane >> 2);
     const int piece = (lane & 3) ^ row64_swizzle(row);
     voff[t] = row < TM ? row * rb + piece * 16 : (n_tile * TN + row - TM) * 64 + piece * 16;
-    voff2[t] = row < TM ? row * rb2 + piece * 16 : voff[t];
+    if constexpr (TWO) voff2[t] = row < TM ? row * rb2 + piece * 16 : voff[t];
   }
   const u32x4 brsrc = raw_rsrc(p.wp, p.w_bytes);
   const unsigned ring_lds = (unsigned)(uintptr_t)(lds_ptr_t)ring;
@@ -1632,19 +1638,29 @@ __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
     d_end = it.s_end;
     const int64_t row = (int64_t)it.b * p.rows_per_batch + (int64_t)it.m_tile * TM;
     arsrc = raw_rsrc(p.xp + row * rb, (int64_t)(S - it.m_tile * TM) * rb);
-    arsrc2 = p.xp2 ? raw_rsrc(p.xp2 + row * rb2, (int64_t)(S - it.m_tile * TM) * rb2) : arsrc;
+    if constexpr (TWO) arsrc2 = raw_rsrc(p.xp2 + row * rb2, (int64_t)(S - it.m_tile * TM) * rb2);
   };
   start_item(d_r);
   auto fill = [&](int st) {
     const unsigned lds = ring_lds + st * R::kStageBytes + wave * R::kDma * 1024;
-    const bool second = __builtin_amdgcn_readfirstlane(d_s) >= p.kb1;  // wave-uniform
-    const int sa = __builtin_amdgcn_readfirstlane((second ? d_s - p.kb1 : d_s) * 64);
-    const int sb = __builtin_amdgcn_readfirstlane(d_s * bstep);
-    const u32x4 asrc = uniform4(second ? arsrc2 : arsrc);
+    if constexpr (TWO) {
+      const bool second = __builtin_amdgcn_readfirstlane(d_s) >= p.kb1;  // wave-uniform
+      const int sa = __builtin_amdgcn_readfirstlane((second ? d_s - p.kb1 : d_s) * 64);
+      const int sb = __builtin_amdgcn_readfirstlane(d_s * bstep);
+      const u32x4 asrc = uniform4(second ? arsrc2 : arsrc);
 #pragma unroll
-    for (int t = 0; t < R::kDma; ++t) {
-      const bool a_rows = 16 * (wave * R::kDma + t) < TM;  // wave-uniform: a scalar select, no branch
-      lds_dma_buf16(a_rows ? asrc : brsrc, second ? voff2[t] : voff[t], a_rows ? sa : sb, lds + t * 1024);
+      for (int t = 0; t < R::kDma; ++t) {
+        const bool a_rows = 16 * (wave * R::kDma + t) < TM;  // wave-uniform: a scalar select, no branch
+        lds_dma_buf16(a_rows ? asrc : brsrc, second ? voff2[t] : voff[t], a_rows ? sa : sb, lds + t * 1024);
+      }
+    } else {
+      const int sa = __builtin_amdgcn_readfirstlane(d_s * 64);
+      const int sb = __builtin_amdgcn_readfirstlane(d_s * bstep);
+#pragma unroll
+      for (int t = 0; t < R::kDma; ++t) {
+        const bool a_rows = 16 * (wave * R::kDma + t) < TM;  // wave-uniform: a scalar select, no branch
+        lds_dma_buf16(a_rows ? arsrc : brsrc, voff[t], a_rows ? sa : sb, lds + t * 1024);
+      }
     }
     if (++d_s == d_end) {
       if (d_r + lanes < p.items) {
@@ -2266,18 +2282,18 @@ static int device_cus() {
 // as the device holds at once (capped by the item count).  Each tile is summed
 // by one wave in a fixed order whatever the grid, so the grid may follow the
 // device without changing a bit of the output.
-template <int DT, int WM, int WN>
+template <int DT, int WM, int WN, bool TWO>
 static void launch_pointwise(dim3, dim3 block, hipStream_t st, const ConvArgs& a) {
   static const int per_cu = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pointwise_kernel<DT, WM, WN>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, pointwise_kernel<DT, WM, WN, TWO>, 256, 0) !=
             hipSuccess ||
         n <= 0)
       n = 2;
     return n;
   }();
   const int64_t lanes = std::min<int64_t>(a.items, std::max(1, per_cu * device_cus() / a.n_tiles));
-  hipLaunchKernelGGL((pointwise_kernel<DT, WM, WN>), dim3((unsigned)(lanes * a.n_tiles)), block, 0, st, a);
+  hipLaunchKernelGGL((pointwise_kernel<DT, WM, WN, TWO>), dim3((unsigned)(lanes * a.n_tiles)), block, 0, st, a);
 }
 
 template <int DT, int NSUB, int WM, int WN>
@@ -2300,7 +2316,10 @@ static ConvFn pick_kind(const Geometry& g, int stride, bool up) {
     return launch_conv<DT, NSUB, 1, 1, 3, 1, false, false, 4>;
   } else {
     if constexpr (NSUB == 4) {
-      if (g.pointwise) return launch_pointwise<DT, WM, WN>;
+      if constexpr (DT == CTMR_F32) {
+        if (g.pointwise && g.cat && !g.pack) return launch_pointwise<DT, WM, WN, true>;
+      }
+      if (g.pointwise) return launch_pointwise<DT, WM, WN, false>;
     }
     if constexpr (DT == CTMR_F32) {
       if (g.direct) return stride == 2 ? launch_conv<DT, NSUB, WM, WN, 3, 2, false, true>
@@ -2571,7 +2590,8 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.y = g.split > 1 ? part : y;
     if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
     const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.split;
-    hipLaunchKernelGGL(conv_lds_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    if (a.x2) hipLaunchKernelGGL(conv_lds_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(conv_lds_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, a);
     if ((rc = check_launch("conv_lds"))) return rc;
     if (g.split > 1) {
       launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);

@@ -217,9 +217,12 @@ def pack_upsample_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tens
 
 
 def _pack(weight: Tensor, mode: int) -> Tensor:
+    """Packed weight for the active precision.  1x1x1 convs stay fp32 under ``precision("bf16")``: their
+    bf16 form needs a conversion pass over the input that costs more than the fp32 GEMM it would save
+    (the UNet's skip projections read the input once, at 2 MFLOP per byte moved)."""
     if not isinstance(weight, Tensor) or weight.device.type != "cuda":
         raise ValueError("conv weight must be a torch.Tensor on the GPU (there is no CPU path)")
-    code = _dtype_code()
+    code = _lib.DT_F32 if weight.dim() == 5 and int(weight.shape[2]) == 1 else _dtype_code()
     dtype = "bf16" if code == _lib.DT_BF16 else "fp32"
     packer = pack_upsample_weight if mode == _lib.MODE_NEAREST2X else pack_weight
     return cached_derived(_packed, _packed_lock, ("conv", mode, code, id(weight)), (weight,),
