@@ -748,6 +748,8 @@ CAT_CASES = [
     ("streaming GEMM (CTMR_F_STREAM)", (1, 32, 32, 32), 64, 64, 64, 3, {"stream": True}, "stream"),
     ("bf16 LDS GEMM", (2, 8, 16, 16), 128, 64, 64, 3, {"bf16": True, "fused": True}, "lds_bf16"),
     ("bf16 1x1", (2, 8, 16, 16), 128, 64, 128, 1, {"bf16": True}, "pointwise"),
+    ("tap-expanded output conv (cout 4)", (1, 8, 16, 16), 64, 32, 4, 3, {"fused": True}, "tap_expand"),
+    ("stride 2 (packed)", (1, 16, 16, 16), 64, 64, 128, 3, {"stride": 2}, "split_waves"),
 ]
 
 
@@ -775,19 +777,20 @@ def test_channel_cat_conv_equals_conv_of_concatenation(ctmr, dev, name, vox, c1,
         gb = (0.2 * rng.standard_normal(cin)).astype(np.float32)
         affine = f.group_norm_affine(cat_t, _t(gw, dev), _t(gb, dev), groups=32, eps=1e-6)
         assert torch.equal(f.group_norm_affine(cc, _t(gw, dev), _t(gb, dev), groups=32, eps=1e-6), affine)
-    out_vox = vox
+    stride = opts.get("stride", 1)
+    out_vox = (n, *[(v - 1) // stride + 1 for v in vox[1:]])
     res = _t(rng.standard_normal((*out_vox, cout)).astype(np.float32), dev) if opts.get("residual") else None
     dtype = "bf16" if opts.get("bf16") else "fp32"
     flags = (L.F_AFFINE | L.F_SILU if affine is not None else 0) | (L.F_BATCH_BIAS if opts.get("batch_bias") else 0) \
         | (L.F_RESIDUAL if res is not None else 0) | (L.F_STREAM if opts.get("stream") else 0)
-    desc = ctmr.ops.make_desc((*vox, c1), cout, ksize, 1, L.MODE_PLAIN, flags, L.DT_BF16 if opts.get("bf16")
+    desc = ctmr.ops.make_desc((*vox, c1), cout, ksize, stride, L.MODE_PLAIN, flags, L.DT_BF16 if opts.get("bf16")
                               else L.DT_F32, 0, c2)
     assert L.conv_kernel(desc) == route
     packed = f.pack_weight(_t(w, dev), dtype=dtype)
     groups = opts.get("gn", 0)
     run = lambda x: f.implicit_gemm_conv3d(x, packed, _t(bias, dev), cout=cout, ksize=ksize, affine=affine,
-                                           silu=affine is not None, residual=res, stream_gemm=bool(opts.get("stream")),
-                                           gn_groups=groups)
+                                           silu=affine is not None, residual=res, stride=stride,
+                                           stream_gemm=bool(opts.get("stream")), gn_groups=groups)
     y_cat, y_ref = run(cc), run(cat_t)
     assert torch.equal(y_cat, y_ref), f"{name}: two-source conv differs from the conv of the concatenation"
     if groups:
@@ -795,8 +798,8 @@ def test_channel_cat_conv_equals_conv_of_concatenation(ctmr, dev, name, vox, c1,
         assert st is not None and st_ref is not None and torch.equal(st, st_ref)
     # float64 bar on the concatenated input, at every corner, edge and face of the volume and 256 voxels
     src = np.concatenate([a, bb], axis=-1)
-    pts = rm.boundary_points(n, vox[1:], 256, seed=11)
-    expected = rm.conv3d_points(src, w, None, pts, affine=None if affine is None else _h(affine),
+    pts = rm.boundary_points(n, out_vox[1:], 256, seed=11)
+    expected = rm.conv3d_points(src, w, None, pts, stride=stride, affine=None if affine is None else _h(affine),
                                 apply_silu=affine is not None)
     expected = expected + (bias[pts[:, 0]] if bias.ndim == 2 else bias)
     if res is not None:
