@@ -392,8 +392,11 @@ def group_norm_affine(x: Tensor, weight: Tensor, bias: Tensor, *, groups: int, e
 
 def group_norm(x: Tensor, weight: Tensor, bias: Tensor, *, num_groups: int, eps: float,
                apply_silu: bool = False) -> Tensor:
-    """Group norm with fp64-accumulated statistics and optional fused SiLU (:102-118)."""
+    """Group norm with fp64-accumulated statistics and optional fused SiLU (:102-118); a ``ChannelCat``
+    input is normalised into one tensor."""
     affine = group_norm_affine(x, weight, bias, groups=num_groups, eps=eps)
+    if isinstance(x, ChannelCat):
+        x = x.materialize()
     return ops.gn_apply(x.contiguous(), affine, bool(apply_silu))
 
 

@@ -824,6 +824,9 @@ def test_channel_cat_group_norm_straddling_groups(ctmr, dev):
         ref = f.group_norm_affine(torch.cat([a, b], -1), gamma, beta, groups=32, eps=1e-6)
         got = f.group_norm_affine(f.ChannelCat(a, b), gamma, beta, groups=32, eps=1e-6)
         assert torch.equal(got, ref), f"{vox} {c1}+{c2}"
+        assert torch.equal(f.group_norm(f.ChannelCat(a, b), gamma, beta, num_groups=32, eps=1e-6, apply_silu=True),
+                           f.group_norm(torch.cat([a, b], -1), gamma, beta, num_groups=32, eps=1e-6,
+                                        apply_silu=True))
     # a UNet up-path residual block (hidden 128 + skip 64 -> 64, time-embedding bias)
     m = ctmr.maisi
     wts = {k: torch.from_numpy(v).to(dev) for k, v in

@@ -7,6 +7,7 @@ from __future__ import annotations
 import inspect
 
 import pytest
+import torch
 
 # protocol method -> keyword parameters the reference's callers pass by name
 PROTOCOLS = {
@@ -114,3 +115,16 @@ def test_window_helpers_validate(ctmr):
     with pytest.raises(ValueError, match="roi"):
         m.sliding_window_decode(None, {}, constructor={}, roi=(1, 2))
     assert m.scan_interval((64, 64, 64), (20, 64, 64), 0.25) == (15, 64, 64)
+
+
+def test_channel_cat_validation(ctmr):
+    """ChannelCat takes two fp32 GPU NDHWC tensors on the same voxels with channel counts that are
+    multiples of 16; concat_channels falls back to torch.cat otherwise (CPU-side checks only)."""
+    f = ctmr.fast_fp32
+    a = torch.zeros(1, 2, 2, 2, 16)
+    with pytest.raises(ValueError, match="GPU"):
+        f.ChannelCat(a, a)
+    with pytest.raises(ValueError, match="torch.Tensor"):
+        f.ChannelCat(a.numpy(), a)
+    out = f.concat_channels(torch.zeros(1, 2, 2, 2, 8), torch.ones(1, 2, 2, 2, 8))
+    assert isinstance(out, torch.Tensor) and tuple(out.shape) == (1, 2, 2, 2, 16)
