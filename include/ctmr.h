@@ -122,7 +122,8 @@ enum ctmr_conv_kernel {
   CTMR_K_POINTWISE = 4,     /* persistent one-tap GEMM (1x1x1, im2col rows) */
   CTMR_K_SPLIT_WAVES = 5,   /* 64 x 64 tiles, each split range over the four waves */
   CTMR_K_TAP_EXPAND = 6,    /* cout <= 4: 27*cout-column GEMM + tap sum */
-  CTMR_K_LDS_SMALL = 7      /* cin 4 / 8: im2col rows read from an LDS halo brick */
+  CTMR_K_LDS_SMALL = 7,     /* cin 4 / 8: im2col rows read from an LDS halo brick */
+  CTMR_K_SMALL_COUT = 8     /* cout <= 4: direct FMA conv from an LDS halo brick */
 };
 int ctmr_conv3d_kernel(const ctmr_conv_desc* desc);
 

@@ -1065,6 +1065,170 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// 3b''. Direct conv for cout <= 4 (fp32, stride 1, cin a multiple of 16: the
+// 64 -> 4 UNet and 64 -> 1 VAE output convs)
+// ---------------------------------------------------------------------------
+// A 16-column MFMA tile would idle 12-15 of its columns here, and the
+// tap-expanded GEMM pays a padded copy, 27 * cout columns of scratch and a tap
+// sum.  Instead each thread owns one output voxel of a 4x8x8 brick and
+// accumulates its cout outputs with FMAs: per 16-channel chunk the brick's
+// 6x10x10 halo is staged in LDS with the group-norm affine and SiLU applied
+// (as conv_lds_kernel; the next chunk's halo is loaded during this chunk's
+// products), and the thread reads its 27 neighbours' 16 channels as four
+// 16-byte pieces.  Weights come from the tap-expanded packing (column
+// tap * cout + o, 16 channels per K block) with workgroup-uniform addresses.
+// Summation order per output: chunks ascending, taps ascending, channels
+// ascending, then the bias -- fixed for a given shape.
+// Halo voxel v stores piece g at slot g ^ small_halo_swizzle(v): the reads of
+// a wave (8 x 8 voxels of one plane, one piece) then fall on twice fewer
+// conflicted bank groups than unswizzled (exhaustive check over taps under
+// the gfx950 ds_read_b128 service order), and the staging writes stay
+// conflict-free.
+struct SmallOutArgs {
+  const float* x;       // unpadded NDHWC input (channels [0, c1) of a two-source input)
+  const float* x2;      // channels [c1, cin) of a two-source input, or null
+  int c1;               // channels of x (cin for one source; a multiple of 16)
+  const float* affine;  // (n, cin, 2) or null
+  const float* wp;      // tap-expanded packed weight [kblock][np][16 floats]
+  const float* bias;    // (cout) or null
+  float* y;
+  int n, d, h, w, cin, np, kb;
+  int tz, ty, tx;
+};
+
+__host__ __device__ constexpr int small_halo_swizzle(int v) { return (v ^ (v >> 3)) & 3; }
+
+template <int COUT, bool AFF, bool SILU>
+__global__ __launch_bounds__(256, 2) void conv_small_cout_kernel(SmallOutArgs p) {
+  __shared__ __attribute__((aligned(16))) char lds[kHaloVox * 64];
+  const int tid = threadIdx.x;
+  // XCD-aware brick order (as conv_lds_kernel).
+  const int nb = gridDim.x, bid = blockIdx.x;
+  const int xcd = bid & 7, slot = bid >> 3, per = nb >> 3, rem = nb & 7;
+  int rest = (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int bx = rest % p.tx;
+  rest /= p.tx;
+  const int by = rest % p.ty;
+  rest /= p.ty;
+  const int bz = rest % p.tz;
+  const int b = rest / p.tz;
+  const int z0 = bz * kBD, y0 = by * kBH, x0 = bx * kBW;
+
+  // Staging: piece i of thread t is channels 4*(t&3)..+3 of the chunk at halo
+  // voxel (t>>2) + 64i; goff[i] is that voxel's index relative to the first
+  // staged plane.  A chunk comes from x (chunks below c1 / 16) or from x2,
+  // whose rows hold the remaining channels.
+  const int part = tid & 3;
+  const int zb = max(z0 - 1, 0);
+  const int c2 = p.cin - p.c1, kb1 = p.c1 >> 4;
+  const int64_t vbase = ((int64_t)b * p.d + zb) * p.h * p.w;
+  const int64_t vtotal = (int64_t)p.n * p.d * p.h * p.w;
+  const __amdgpu_buffer_rsrc_t xrsrc1 = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + vbase * p.c1), (short)0, (int)min((vtotal - vbase) * p.c1 * 4, (int64_t)0x7fffffff),
+      0x00020000);
+  const __amdgpu_buffer_rsrc_t xrsrc2 = p.x2 ? __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x2 + vbase * c2), (short)0, (int)min((vtotal - vbase) * c2 * 4, (int64_t)0x7fffffff),
+      0x00020000) : xrsrc1;
+  int goff[kStageIters];
+  unsigned valid = 0;
+#pragma unroll
+  for (int i = 0; i < kStageIters; ++i) {
+    const int hv = (tid >> 2) + 64 * i;
+    goff[i] = 0;
+    if (hv < kHaloVox) {
+      const int hz = hv / (kHH * kHW), hr = hv - hz * (kHH * kHW);
+      const int hy = hr / kHW, hx = hr - hy * kHW;
+      const int gz = z0 - 1 + hz, gy = y0 - 1 + hy, gx = x0 - 1 + hx;
+      if (gz >= 0 && gz < p.d && gy >= 0 && gy < p.h && gx >= 0 && gx < p.w) {
+        valid |= 1u << i;
+        goff[i] = ((gz - zb) * p.h + gy) * p.w + gx;
+      }
+    }
+  }
+  u4 stage[kStageIters];
+  auto fetch = [&](int chunk) {
+    const bool second = p.x2 != nullptr && chunk >= kb1;  // uniform
+    const __amdgpu_buffer_rsrc_t rs = second ? xrsrc2 : xrsrc1;
+    const int row = (second ? c2 : p.c1) * 4;
+    const int so = __builtin_amdgcn_readfirstlane((second ? chunk - kb1 : chunk) * 64);
+#pragma unroll
+    for (int i = 0; i < kStageIters; ++i)
+      stage[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, goff[i] * row + part * 16, so, 0);
+  };
+  auto commit = [&](int chunk) {
+    f4 sc = {1.f, 1.f, 1.f, 1.f}, of = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (AFF) {
+      const f4* q = reinterpret_cast<const f4*>(p.affine + ((int64_t)b * p.cin + chunk * 16 + part * 4) * 2);
+      const f4 a0 = q[0], a1 = q[1];
+      sc = f4{a0[0], a0[2], a1[0], a1[2]};
+      of = f4{a0[1], a0[3], a1[1], a1[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < kStageIters; ++i) {
+      const int hv = (tid >> 2) + 64 * i;
+      if (hv >= kHaloVox) continue;
+      f4 v = __builtin_bit_cast(f4, stage[i]);
+      const bool in = (valid >> i) & 1u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float t = v[j];
+        if constexpr (AFF) t = fmaf(t, sc[j], of[j]);
+        if constexpr (SILU) t = silu_f(t);
+        v[j] = in ? t : 0.f;
+      }
+      *reinterpret_cast<f4*>(lds + hv * 64 + ((part ^ small_halo_swizzle(hv)) << 4)) = v;
+    }
+  };
+
+  // This thread's output voxel and its halo voxel at tap (0,0,0); the swizzle
+  // depends on a voxel's bits 0, 1, 3 and 4 only, so the slot base of the
+  // voxel at tap offset `off` is entry off % 32 of a two-word table.
+  const int oz = tid >> 6, oy = (tid >> 3) & 7, ox = tid & 7;
+  const int hv0 = (oz * kHH + oy) * kHW + ox;
+  unsigned tab[2] = {0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 32; ++k) tab[k >> 4] |= (unsigned)small_halo_swizzle(hv0 + k) << (2 * (k & 15));
+
+  float acc[COUT];
+#pragma unroll
+  for (int o = 0; o < COUT; ++o) acc[o] = 0.f;
+  fetch(0);
+  for (int chunk = 0; chunk < p.kb; ++chunk) {
+    __syncthreads();  // every thread has finished reading the previous chunk
+    commit(chunk);
+    __syncthreads();
+    if (chunk + 1 < p.kb) fetch(chunk + 1);  // uniform; lands during this chunk's products
+    int base = hv0 * 64;
+    unsigned t0 = tab[0], t1 = tab[1];
+    // Keeps the per-tap address arithmetic inside the chunk loop.
+    asm volatile("" : "+v"(base), "+v"(t0), "+v"(t1));
+    // The constant address space: uniform weight reads become scalar loads.
+    const __attribute__((address_space(4))) float* wc =
+        (const __attribute__((address_space(4))) float*)(p.wp + (int64_t)chunk * p.np * 16);
+#pragma unroll
+    for (int tap = 0; tap < 27; ++tap) {
+      const int off = ((tap / 9) * kHH + (tap / 3) % 3) * kHW + tap % 3;
+      const int k = off & 31;
+      const unsigned sw = ((k < 16 ? t0 : t1) >> (2 * (k & 15))) & 3u;
+#pragma unroll
+      for (int pc = 0; pc < 4; ++pc) {
+        const f4 a = *reinterpret_cast<const f4*>(lds + base + off * 64 + (int)((pc ^ sw) << 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int o = 0; o < COUT; ++o) acc[o] = fmaf(a[j], wc[(tap * COUT + o) * 16 + pc * 4 + j], acc[o]);
+      }
+    }
+  }
+  const int z = z0 + oz, y = y0 + oy, x = x0 + ox;
+  if (z < p.d && y < p.h && x < p.w) {
+    float* out = p.y + ((((int64_t)b * p.d + z) * p.h + y) * p.w + x) * COUT;
+#pragma unroll
+    for (int o = 0; o < COUT; ++o) out[o] = acc[o] + (p.bias ? p.bias[o] : 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 3b'. LDS-staged im2col GEMM for small channel counts (fp32, stride 1, cin 4
 // or 8: the 4-channel latent input convs, the 8-channel label-condition convs)
 // ---------------------------------------------------------------------------
@@ -1887,6 +2051,7 @@ struct Geometry {
   int nsub, wm, wn, m_tiles, n_tiles;
   bool lds;              // LDS-staged GEMM (conv_lds_kernel)
   bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
+  bool small_out;        // direct cout <= 4 conv from an LDS halo (conv_small_cout_kernel)
   bool lds_small;        // LDS-staged im2col GEMM for cin 4 / 8 (conv_lds_small_kernel)
   bool cat;              // input given as two tensors, channels [0, c1) and [c1, cin)
   int c1;
@@ -2029,6 +2194,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   g.lds_small = false;
   g.lds = false;
   g.lds16 = false;
+  g.small_out = false;
   if (g.layout == WL_IM2COL && !g.cat && d->dtype == CTMR_F32 && d->stride == 1 && d->mode == CTMR_MODE_PLAIN &&
       (d->cin == 4 || d->cin == 8) && d->cout % 4 == 0 && (d->cout % 64 == 0 || d->cout <= 32) &&
       !(d->flags & CTMR_F_STREAM)) {
@@ -2055,6 +2221,33 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
       return CTMR_OK;
     }
   }
+  // Direct conv for cout <= 4 (the tap-expanded layout's shapes, fp32, stride
+  // 1, channels in whole 16-channel chunks, no residual or per-batch bias, no
+  // K split): reads x through an LDS halo, no padded copy, no tap-expanded
+  // scratch, no tap sum.
+  g.small_out = false;
+  if (g.layout == WL_EXPAND && d->dtype == CTMR_F32 && d->stride == 1 && d->mode == CTMR_MODE_PLAIN &&
+      d->cin % 16 == 0 && !(d->flags & (CTMR_F_STREAM | CTMR_F_RESIDUAL | CTMR_F_BATCH_BIAS))) {
+    const int tz = (int)ceil_div(d->d, kBD), ty = (int)ceil_div(d->h, kBH), tx = (int)ceil_div(d->w, kBW);
+    const int64_t planes = (int64_t)kHD * d->h * d->w * d->cin * 4;
+    if (planes < (1ll << 31)) {
+      if (d->split > 1) return fail(CTMR_E_INVALID, "split must be 1 for the cout <= 4 direct conv");
+      g.small_out = true;
+      g.pack = false;
+      g.tz = tz; g.ty = ty; g.tx = tx;
+      g.m_tiles = tz * ty * tx;
+      g.n_tiles = 1;
+      g.split = 1;
+      g.direct = false;
+      g.kws = false;
+      g.pointwise = false;
+      g.pack_bytes = (d->flags & CTMR_F_AFFINE) ? round_up((int64_t)d->n * d->cin * 2 * 4, 256) : 0;
+      g.part_bytes = 0;
+      g.z_bytes = 0;
+      if ((int64_t)g.m_tiles * d->n * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
+      return CTMR_OK;
+    }
+  }
   // LDS-staged GEMM: stride-1 fp32 volumes whose 4x8x8 bricks are at least
   // 3/4 full, with at least 64 input channels (4 staged chunks; measured on
   // MI355X: 64-channel UNet-level convs 3-6 % faster than the streaming GEMM
@@ -2063,6 +2256,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // 6 staged planes within 32-bit buffer offsets.
   g.lds = false;
   g.lds16 = false;
+  g.small_out = false;
   if (g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 && d->stride == 1 &&
       d->mode == CTMR_MODE_PLAIN && d->cin % 16 == 0 && d->cin >= 64 && d->cout % 64 == 0 &&
       !(d->flags & CTMR_F_STREAM)) {
@@ -2104,6 +2298,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // sampled by the pack) with 64-wide column tiles whose 4x8x8 bricks are at
   // least 3/4 full; the halo fill's 32-bit offsets span 6 packed planes.
   g.lds16 = false;
+  g.small_out = false;
   if (g.layout == WL_TAPS && d->dtype == CTMR_BF16 && d->ksize == 3 && d->stride == 1 && plain_weights &&
       d->cout % 64 == 0 && !(d->flags & CTMR_F_STREAM)) {
     const int tz = (int)ceil_div(g.gd, kBD), ty = (int)ceil_div(g.gh, kBH), tx = (int)ceil_div(g.gw, kBW);
@@ -2394,6 +2589,7 @@ int ctmr_conv3d_kernel(const ctmr_conv_desc* desc) {
   if (g.lds) return CTMR_K_LDS;
   if (g.lds_small) return CTMR_K_LDS_SMALL;
   if (g.lds16) return CTMR_K_LDS_BF16;
+  if (g.small_out) return CTMR_K_SMALL_COUT;
   if (g.layout == WL_EXPAND) return CTMR_K_TAP_EXPAND;
   if (g.kws) return CTMR_K_SPLIT_WAVES;
   if (g.pointwise) return CTMR_K_POINTWISE;
@@ -2464,7 +2660,7 @@ static int pack_impl(const ctmr_conv_desc* desc, const float* x, const float* x2
   if (!x || (g.cat && !x2)) return fail(CTMR_E_INVALID, "null input");
   if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
   if ((rc = check_workspace(g, workspace, workspace_bytes))) return rc;
-  if (g.lds || g.lds_small) {
+  if (g.lds || g.lds_small || g.small_out) {
     if (!(desc->flags & CTMR_F_AFFINE)) return CTMR_OK;
     if (hipMemcpyAsync(workspace, affine, (size_t)desc->n * desc->cin * 2 * 4, hipMemcpyDeviceToDevice,
                        (hipStream_t)stream) != hipSuccess)
@@ -2541,7 +2737,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
-  if (g.cat && !g.pack && !g.lds && !g.pointwise)
+  if (g.cat && !g.pack && !g.lds && !g.pointwise && !g.small_out)
     return fail(CTMR_E_UNSUPPORTED, "internal: unpacked two-source input on a route that reads one tensor");
   if (g.cat && !g.pack && (!x2 || ((uintptr_t)x2 & 15) != 0))
     return fail(CTMR_E_INVALID, "x2 must be non-null and 16-byte aligned");
@@ -2636,6 +2832,32 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
       else hipLaunchKernelGGL((conv_lds_small_kernel<8, 1>), grid, block, 0, st, a);
     }
     return check_launch("conv_lds_small");
+  }
+  if (g.small_out) {
+    SmallOutArgs a;
+    a.x = x;
+    a.x2 = g.cat ? x2 : nullptr;
+    a.c1 = g.c1;
+    a.affine = (desc->flags & CTMR_F_AFFINE) ? (affine_direct ? affine_direct : (const float*)workspace) : nullptr;
+    a.wp = (const float*)packed;
+    a.bias = bias;
+    a.y = y;
+    a.n = desc->n; a.d = desc->d; a.h = desc->h; a.w = desc->w;
+    a.cin = desc->cin; a.np = g.np; a.kb = desc->cin / 16;
+    a.tz = g.tz; a.ty = g.ty; a.tx = g.tx;
+    const int form = (desc->cout - 1) * 4 + ((desc->flags & CTMR_F_AFFINE) ? 2 : 0) + ((desc->flags & CTMR_F_SILU) ? 1 : 0);
+    static void (*const kernels[16])(SmallOutArgs) = {
+        conv_small_cout_kernel<1, false, false>, conv_small_cout_kernel<1, false, true>,
+        conv_small_cout_kernel<1, true, false>,  conv_small_cout_kernel<1, true, true>,
+        conv_small_cout_kernel<2, false, false>, conv_small_cout_kernel<2, false, true>,
+        conv_small_cout_kernel<2, true, false>,  conv_small_cout_kernel<2, true, true>,
+        conv_small_cout_kernel<3, false, false>, conv_small_cout_kernel<3, false, true>,
+        conv_small_cout_kernel<3, true, false>,  conv_small_cout_kernel<3, true, true>,
+        conv_small_cout_kernel<4, false, false>, conv_small_cout_kernel<4, false, true>,
+        conv_small_cout_kernel<4, true, false>,  conv_small_cout_kernel<4, true, true>};
+    const int64_t blocks = (int64_t)g.m_tiles * desc->n;
+    hipLaunchKernelGGL(kernels[form], dim3((unsigned)blocks), dim3(256), 0, st, a);
+    return check_launch("conv_small_cout");
   }
   if (g.lds16) {
     Lds16Args a;

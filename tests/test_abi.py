@@ -76,11 +76,17 @@ def test_workspace_and_packed_sizes(ctmr):
     assert L.workspace_bytes(L.conv_desc(1, 8, 8, 8, 4, 64, stride=2)) == 4**3 * 112 * 4
     d16 = L.conv_desc(1, 8, 8, 8, 4, 4, dtype=L.DT_BF16)
     assert L.packed_weight_elems(d16) == 128 * 16
-    # cout <= 4: one GEMM with 27 * cout columns (padded to 16) over every
-    # padded row, plus the planar tap columns it writes
+    # cout <= 4: weights packed for one GEMM with 27 * cout columns (padded to
+    # 16); fp32 stride-1 convs with whole 16-channel chunks and no residual run
+    # the direct conv over an LDS halo (no workspace, the affine table with
+    # one), the others the GEMM over every padded row plus the planar tap
+    # columns it writes
     d1 = L.conv_desc(1, 8, 8, 8, 64, 1)
     assert L.packed_weight_elems(d1) == 4 * 32 * 16
-    assert L.workspace_bytes(d1) == ((10**3 * 64 * 4 + 255) // 256) * 256 + 27 * 10**3 * 4
+    assert L.workspace_bytes(d1) == 0
+    assert L.workspace_bytes(L.conv_desc(1, 8, 8, 8, 64, 1, flags=L.F_AFFINE)) == 512
+    assert L.workspace_bytes(L.conv_desc(1, 8, 8, 8, 64, 1, flags=L.F_STREAM)) == \
+        ((10**3 * 64 * 4 + 255) // 256) * 256 + 27 * 10**3 * 4
     assert L.conv_split(d1) == 1
     assert L.packed_weight_elems(L.conv_desc(1, 8, 8, 8, 64, 4, stride=2)) == 4 * 112 * 16
     # nearest-2x parity weights: 8 phases x 8 taps
@@ -262,7 +268,10 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     ((1, 64, 64, 64, 64), 64, {"flags": 16}, "stream_direct"),            # CTMR_F_STREAM
     ((1, 64, 64, 64, 64), 64, {"dtype": 1}, "lds_bf16"),
     ((2, 4, 8, 8, 512), 512, {}, "split_waves"),                          # deep UNet level
-    ((1, 20, 64, 64, 64), 1, {}, "tap_expand"),                           # decoder output conv
+    ((1, 20, 64, 64, 64), 1, {"flags": 3}, "small_cout"),                 # decoder output conv (GN + SiLU)
+    ((2, 64, 64, 32, 64), 4, {"flags": 3}, "small_cout"),                 # UNet output conv
+    ((2, 64, 64, 32, 64), 4, {"flags": 3 | 8}, "tap_expand"),             # with a residual
+    ((1, 20, 64, 64, 64), 1, {"flags": 16}, "tap_expand"),                # CTMR_F_STREAM
     ((2, 64, 64, 32, 4), 64, {}, "lds_small"),                            # conv_in: im2col rows from LDS
     ((1, 256, 256, 256, 8), 8, {}, "lds_small"),                          # condition encoder 8 -> 8
     ((1, 256, 256, 256, 8), 32, {"stride": 2}, "stream"),                 # stride 2: im2col rows in HBM
@@ -284,17 +293,19 @@ def test_conv_kernel_route(ctmr, shape, cout, kw, expected):
     ((2, 4, 8, 8, 1024), 512, 512, {}, "split_waves"),               # deep level: packed first
     ((2, 64, 64, 32, 192), 128, 64, {"flags": 16}, "stream"),        # CTMR_F_STREAM: packed, never direct
     ((2, 32, 32, 16, 384), 256, 128, {"dtype": 1}, "lds_bf16"),      # bf16: the packed copy
+    ((2, 64, 64, 32, 96), 64, 4, {"flags": 3}, "small_cout"),        # cout <= 4 direct conv: read in place
 ])
 def test_two_source_routes(ctmr, shape, cin1, cout, kw, expected):
-    """A two-source input (cin1 > 0) is read in place by the LDS-staged and the persistent 1x1 GEMMs
-    and packed (both tensors into the usual padded copy) for every other route."""
+    """A two-source input (cin1 > 0) is read in place by the LDS-staged GEMM, the persistent 1x1 GEMM
+    and the cout <= 4 direct conv, and packed (both tensors into the usual padded copy) for every other
+    route."""
     L = ctmr._lib
     n, d, h, w, cin = shape
     desc = L.conv_desc(n, d, h, w, cin, cout, cin1=cin1, **kw)
     assert L.conv_kernel(desc) == expected
     one = L.conv_desc(n, d, h, w, cin, cout, **kw)
     assert L.packed_weight_elems(desc) == L.packed_weight_elems(one)  # the weight does not change
-    if expected in ("lds", "pointwise"):
+    if expected in ("lds", "pointwise", "small_cout"):
         assert L.workspace_bytes(desc) == L.workspace_bytes(one)
     else:
         assert L.workspace_bytes(desc) > 0  # the packed copy of both tensors

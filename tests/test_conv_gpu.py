@@ -87,14 +87,23 @@ def test_fused_norm_conv_matches_float64(ctmr, dev, upsample):
 @pytest.mark.parametrize(("cin", "cout"), [(3, 8), (32, 2)])
 def test_trilinear_small_channel_layouts_match_materialized(ctmr, dev, cin, cout):
     """The im2col (small cin) and tap-expanded (small cout) packings sample trilinear-2x with the
-    same helper as the padded packing: bitwise equal to convolving the materialized upsampling."""
+    same helper as the padded packing: bitwise equal to convolving the materialized upsampling with
+    the same GEMM formulation (for cout <= 4 a plain conv of the materialized input would take the
+    direct conv, another fixed order, so that comparison forces the tap-expanded GEMM)."""
     rng = np.random.default_rng(37)
     x = _t(rng.standard_normal((2, cin, 3, 4, 5)).astype(np.float32), dev)
     w = _t((rng.standard_normal((cout, cin, 3, 3, 3)) / np.sqrt(27 * cin)).astype(np.float32), dev)
     b = _t(rng.standard_normal(cout).astype(np.float32), dev)
     f = ctmr.fast_fp32
     fused = f.trilinear_conv3d_ncdhw(x, w, b)
-    assert torch.equal(fused, f.conv3d_ncdhw(f.upsample_trilinear_ncdhw(x), w, b, padding=1))
+    up = f.upsample_trilinear_ncdhw(x)
+    if cout <= 4:
+        y = f.implicit_gemm_conv3d(up.permute(0, 2, 3, 4, 1).contiguous(), f.pack_weight(w), b, cout=cout,
+                                   stream_gemm=True)
+        materialized = y.permute(0, 4, 1, 2, 3)
+    else:
+        materialized = f.conv3d_ncdhw(up, w, b, padding=1)
+    assert torch.equal(fused, materialized)
     expected = rm.conv3d(rm.upsample_trilinear(rm.ncdhw_to_ndhwc(_h(x))), _h(w), _h(b))
     _assert_rel(_h(fused), rm.ndhwc_to_ncdhw(expected), FP32_REL, f"trilinear {cin}->{cout}")
 
@@ -254,7 +263,9 @@ PERSISTENT_CASES = [
     ("bf16", (1, 48, 48, 48, 128), 256, 1, {"bf16": True}),
     # 3 input channels: im2col rows in HBM (4 and 8 read them from an LDS halo, tested below)
     ("im2col 3x3", (2, 32, 64, 64, 3), 64, 3, {"gn": 32, "route": "pointwise"}),
-    ("tap-expanded 3x3 -> 1", (1, 40, 64, 64, 64), 1, 3, {}),
+    # cout <= 4: the direct conv over an LDS halo (another fixed order than the tap-expanded GEMM
+    # that CTMR_F_STREAM keeps: equal to fp32 rounding)
+    ("tap-expanded 3x3 -> 1", (1, 40, 64, 64, 64), 1, 3, {"route": "small_cout", "bitwise": False}),
 ]
 
 
@@ -264,8 +275,8 @@ def test_persistent_pointwise_gemm_equals_one_tile_gemm(ctmr, dev, name, shape, 
     """One-tap GEMMs (1x1x1, im2col) run on a persistent grid whose workgroups walk the row tiles
     over an LDS ring; each output keeps the one-tile-per-workgroup GEMM's summation order, so outputs
     are bit-identical to it (CTMR_F_STREAM), epilogue group-norm partials agree to fp64 rounding, and
-    a sample of output voxels meets the float64 bar.  (Per-batch bias, residual and the tap-expanded
-    GEMM stay on the one-tile kernel: those cases check the routing.)"""
+    a sample of output voxels meets the float64 bar.  (Per-batch bias and residual stay on the one-tile
+    kernel and cout <= 4 takes the direct conv: those cases check the routing.)"""
     print(f"persistent pointwise {name}: {shape} -> {cout} k{ksize} {opts}", flush=True)
     f = ctmr.fast_fp32
     rng = np.random.default_rng(sum(shape) + cout + ksize)
@@ -292,7 +303,10 @@ def test_persistent_pointwise_gemm_equals_one_tile_gemm(ctmr, dev, name, shape, 
                                                 stream_gemm=stream, gn_groups=groups)
     y = run(False)
     y1 = run(True)
-    assert torch.equal(y, y1), f"{name}: persistent and one-tile GEMMs differ"
+    if opts.get("bitwise", True):
+        assert torch.equal(y, y1), f"{name}: persistent and one-tile GEMMs differ"
+    else:
+        assert rm.max_rel_error(_h(y), _h(y1)) <= 2 * FP32_REL, f"{name}: routes differ beyond fp32 rounding"
     assert torch.equal(run(False), y)
     if groups:
         # same per-(tile, group) partials; the persistent epilogue adds a tile's rows in another fixed
@@ -360,6 +374,48 @@ def test_small_cout_tap_expanded_conv(ctmr, dev, shape, cout, stride, fused):
     y = run()
     assert torch.equal(y, run())
     _assert_rel(_h(y), expected, FP32_REL, f"tap-expanded {shape}->{cout} s{stride}")
+
+
+@pytest.mark.parametrize(("shape", "cout", "fused"), [
+    ((1, 64, 8, 16, 16), 4, True),     # UNet output conv class: GN affine + SiLU staged, 64 -> 4
+    ((2, 64, 6, 7, 9), 1, True),       # VAE output conv class, ragged bricks (masked voxels)
+    ((1, 32, 9, 8, 10), 2, False),     # two 16-channel chunks, no affine
+    ((2, 16, 5, 6, 7), 3, True),       # one chunk, cout 3
+])
+def test_small_cout_direct_conv(ctmr, dev, shape, cout, fused):
+    """cout <= 4, fp32, stride 1, cin a multiple of 16, no residual: the direct FMA conv over an LDS
+    halo (``small_cout``) meets the float64 bar and agrees with the tap-expanded GEMM + tap sum (the
+    CTMR_F_STREAM route) to fp32 rounding; repeat runs bit-identical."""
+    print(f"small cout direct {shape}->{cout} fused={fused}", flush=True)
+    f, L = ctmr.fast_fp32, ctmr._lib
+    rng = np.random.default_rng(sum(shape) + cout)
+    n, c = shape[0], shape[1]
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal(cout).astype(np.float32)
+    xn = rm.ncdhw_to_ndhwc(x)
+    packed = f.pack_weight(_t(w, dev))
+    affine = None
+    xin = xn
+    if fused:
+        gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+        affine = f.group_norm_affine(_t(xn, dev), _t(gw, dev), _t(gb, dev), groups=8, eps=1e-6)
+        xin = rm.group_norm(xn, gw, gb, 8, 1e-6, apply_silu=True)
+    flags = (L.F_AFFINE | L.F_SILU) if fused else 0
+    desc = ctmr.ops.make_desc(xn.shape, cout, 3, 1, L.MODE_PLAIN, flags, L.DT_F32, 0)
+    assert L.conv_kernel(desc) == "small_cout"
+    assert L.workspace_bytes(desc) == (((n * c * 8 + 255) // 256) * 256 if fused else 0)
+    expected = rm.conv3d(xin, w) + bias
+    outs = []
+    for stream_gemm in (False, True):
+        run = lambda: f.implicit_gemm_conv3d(_t(xn, dev), packed, _t(bias, dev), cout=cout, affine=affine,
+                                             silu=fused, stream_gemm=stream_gemm)
+        y = run()
+        assert torch.equal(y, run())
+        _assert_rel(_h(y), expected, FP32_REL, f"{'tap-expanded' if stream_gemm else 'direct'} {shape}->{cout}")
+        outs.append(_h(y))
+    assert rm.max_rel_error(outs[0], outs[1]) <= 2 * FP32_REL
 
 
 @pytest.mark.parametrize(("cin", "cout", "stride", "fused"), [
@@ -748,7 +804,9 @@ CAT_CASES = [
     ("streaming GEMM (CTMR_F_STREAM)", (1, 32, 32, 32), 64, 64, 64, 3, {"stream": True}, "stream"),
     ("bf16 LDS GEMM", (2, 8, 16, 16), 128, 64, 64, 3, {"bf16": True, "fused": True}, "lds_bf16"),
     ("bf16 1x1", (2, 8, 16, 16), 128, 64, 128, 1, {"bf16": True}, "pointwise"),
-    ("tap-expanded output conv (cout 4)", (1, 8, 16, 16), 64, 32, 4, 3, {"fused": True}, "tap_expand"),
+    ("direct output conv (cout 4)", (1, 8, 16, 16), 64, 32, 4, 3, {"fused": True}, "small_cout"),
+    ("tap-expanded output conv (cout 4, residual)", (1, 8, 16, 16), 64, 32, 4, 3, {"fused": True, "residual": True},
+     "tap_expand"),
     ("stride 2 (packed)", (1, 16, 16, 16), 64, 64, 128, 3, {"stride": 2}, "split_waves"),
 ]
 
