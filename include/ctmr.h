@@ -24,6 +24,8 @@
  *   ctmr_gn_apply             <- fast_fp32.group_norm_ncdhw (fast_fp32.py:102-118)
  *   ctmr_conv3d (ksize 1)     <- fast_fp32.pointwise_conv_ncdhw (fast_fp32.py:121-130)
  *   ctmr_resample             <- medmlx_core.ops.avg_pool3d_ncdhw / upsample_nearest_ncdhw
+ *   ctmr_gn_avgpool           <- the down branch of fast_fp32.residual_block_ncdhw
+ *                                (fast_fp32.py:250-255: group norm + SiLU, then pooling)
  *                                (fast_fp32.py:48-59) and source_vae.upsample_trilinear_ncdhw
  *                                (fast_fp32.py:66-68; formula at _nax_conv.py:115-142)
  *   ctmr_flash_attention      <- _flash_attention.flash_attention (_flash_attention.py:320-360),
@@ -279,6 +281,15 @@ int ctmr_gn_affine_cat(int32_t n, int64_t s, int32_t c1, int32_t c2, int32_t gro
 /* y = silu?(x*scale + offset) with affine from ctmr_gn_affine; y may equal x. */
 int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,
                   int32_t silu, float* y, void* stream);
+
+/* Down-sampling residual-block input (fast_fp32.residual_block_ncdhw's down
+ * branch, fast_fp32.py:250-255: avg_pool3d of group_norm_ncdhw(x, silu) and
+ * avg_pool3d of x) from one read of x: y = 2x2x2 average pool of
+ * silu?(x*scale + offset) (affine from ctmr_gn_affine), y_skip (optional) =
+ * the pool of x.  NDHWC, output (n, d/2, h/2, w/2, c); bit-identical to
+ * ctmr_gn_apply followed by ctmr_resample(CTMR_AVGPOOL2), and to the pool of x. */
+int ctmr_gn_avgpool(int32_t n, int32_t d, int32_t h, int32_t w, int32_t c, const float* x, const float* affine,
+                    int32_t silu, float* y, float* y_skip, void* stream);
 
 /* Elementwise SiLU, y may equal x. */
 int ctmr_silu(int64_t count, const float* x, float* y, void* stream);

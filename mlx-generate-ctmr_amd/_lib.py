@@ -76,6 +76,7 @@ _PROTOTYPES = {
     "ctmr_gn_apply": (_c_int, [_c_i32, _c_i64, _c_i32, _vp, _vp, _c_i32, _vp, _vp]),
     "ctmr_silu": (_c_int, [_c_i64, _vp, _vp, _vp]),
     "ctmr_resample": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp]),
+    "ctmr_gn_avgpool": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _vp, _c_i32, _vp, _vp, _vp]),
     "ctmr_flash_attention": (_c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp, _vp]),
 }
 

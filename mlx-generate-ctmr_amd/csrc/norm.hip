@@ -261,6 +261,70 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(const float* __restrict__
   }
 }
 
+// Down-sampling residual block input (fast_fp32.py:250-255): the 2x2x2 average
+// pool of silu?(x * scale + offset) and, optionally, of x itself, from one
+// read of x.  Per output the same operations in the same order as gn_apply
+// followed by the average pool (and the pool of x alone): bit-identical to
+// them.
+template <int VEC>
+__global__ __launch_bounds__(256) void gn_avgpool_kernel(int n, int d, int h, int w, int c,
+                                                         const float* __restrict__ x,
+                                                         const float* __restrict__ affine, int silu,
+                                                         float* __restrict__ y, float* __restrict__ y_skip) {
+#pragma clang fp contract(off)
+  const int od = d / 2, oh = h / 2, ow = w / 2;
+  const int cg = c / VEC;
+  const int64_t total = (int64_t)n * od * oh * ow * cg;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t t = i;
+    const int cc = (int)(t % cg);
+    t /= cg;
+    const int xo = (int)(t % ow);
+    t /= ow;
+    const int yo = (int)(t % oh);
+    t /= oh;
+    const int zo = (int)(t % od);
+    const int b = (int)(t / od);
+    const float* src = x + (int64_t)b * d * h * w * c + cc * VEC;
+    const float* a = affine + ((int64_t)b * c + cc * VEC) * 2;
+    float sc[VEC], of[VEC], sg[VEC], sx[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      sc[k] = a[2 * k];
+      of[k] = a[2 * k + 1];
+      sg[k] = 0.f;
+      sx[k] = 0.f;
+    }
+    for (int p = 0; p < 2; ++p)
+      for (int q = 0; q < 2; ++q)
+        for (int e = 0; e < 2; ++e) {
+          const float* v = src + (((int64_t)(2 * zo + p) * h + (2 * yo + q)) * w + (2 * xo + e)) * c;
+          float u[VEC];
+          if constexpr (VEC == 4) {
+            const f4 w4 = *reinterpret_cast<const f4*>(v);
+            u[0] = w4[0]; u[1] = w4[1]; u[2] = w4[2]; u[3] = w4[3];
+          } else {
+            u[0] = v[0];
+          }
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) {
+            const float g = fmaf(u[k], sc[k], of[k]);
+            sg[k] += silu ? silu_f(g) : g;
+            sx[k] += u[k];
+          }
+        }
+    const int64_t obase = ((((int64_t)b * od + zo) * oh + yo) * ow + xo) * c + cc * VEC;
+    if constexpr (VEC == 4) {
+      *reinterpret_cast<f4*>(y + obase) = f4{sg[0], sg[1], sg[2], sg[3]} * 0.125f;
+      if (y_skip) *reinterpret_cast<f4*>(y_skip + obase) = f4{sx[0], sx[1], sx[2], sx[3]} * 0.125f;
+    } else {
+      y[obase] = sg[0] * 0.125f;
+      if (y_skip) y_skip[obase] = sx[0] * 0.125f;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ x, int64_t count,
                                                    float* __restrict__ y) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
@@ -423,6 +487,23 @@ int ctmr_silu(int64_t count, const float* x, float* y, void* stream) {
   hipLaunchKernelGGL(silu_kernel, dim3(elementwise_blocks(count)), dim3(256), 0,
                      (hipStream_t)stream, x, count, y);
   return check_launch("silu");
+}
+
+int ctmr_gn_avgpool(int32_t n, int32_t d, int32_t h, int32_t w, int32_t c, const float* x, const float* affine,
+                    int32_t silu, float* y, float* y_skip, void* stream) {
+  if (n <= 0 || d <= 0 || h <= 0 || w <= 0 || c <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (d < 2 || h < 2 || w < 2) return fail(CTMR_E_INVALID, "average pooling needs every axis >= 2");
+  if (!x || !affine || !y) return fail(CTMR_E_INVALID, "null pointer");
+  const uintptr_t ptrs = (uintptr_t)x | (uintptr_t)y | (y_skip ? (uintptr_t)y_skip : 0);
+  const int vec = (c % 4 == 0) && ((ptrs & 15) == 0);
+  const int64_t total = (int64_t)n * (d / 2) * (h / 2) * (w / 2) * (vec ? c / 4 : c);
+  if (vec)
+    hipLaunchKernelGGL(gn_avgpool_kernel<4>, dim3(elementwise_blocks(total)), dim3(256), 0, (hipStream_t)stream,
+                       n, d, h, w, c, x, affine, silu, y, y_skip);
+  else
+    hipLaunchKernelGGL(gn_avgpool_kernel<1>, dim3(elementwise_blocks(total)), dim3(256), 0, (hipStream_t)stream,
+                       n, d, h, w, c, x, affine, silu, y, y_skip);
+  return check_launch("gn_avgpool");
 }
 
 int ctmr_resample(int32_t op, int32_t n, int32_t d, int32_t h, int32_t w, int32_t c,

@@ -630,8 +630,10 @@ def residual_block(
         return pointwise_conv(skip, weights["skip_connection.conv.weight"], weights["skip_connection.conv.bias"])
 
     if down:
-        skip = project_skip(avg_pool3d(x))
-        hidden = avg_pool3d(group_norm(x, *norm1, num_groups=num_groups, eps=eps, apply_silu=True))
+        # both pools (of norm1 + SiLU, and of x for the skip) from one read of x (ctmr_gn_avgpool)
+        affine = group_norm_affine(x, *norm1, groups=num_groups, eps=eps)
+        hidden, pooled = ops.gn_avgpool(_require(x, "x").contiguous(), affine, True)
+        skip = project_skip(pooled)
         hidden = norm_conv3d(hidden, weights["conv1.conv.weight"], bias1, norm=None, num_groups=num_groups,
                              eps=eps, apply_silu=False, out_gn_groups=num_groups)
     else:

@@ -356,6 +356,29 @@ def _(x, op):
     return x.new_empty((n, 2 * d, 2 * h, 2 * w, c))
 
 
+@torch.library.custom_op("ctmr::gn_avgpool", mutates_args=())
+def gn_avgpool(x: Tensor, affine: Tensor, silu: bool) -> tuple[Tensor, Tensor]:
+    """``(avg_pool(silu?(x * scale + offset)), avg_pool(x))`` of an NDHWC tensor from one read of ``x``
+    (the down-sampling residual block's two inputs); bit-identical to ``gn_apply`` then ``resample``."""
+    _require_device(x, affine)
+    n, d, h, w, c = (int(v) for v in x.shape)
+    shape = (n, d // 2, h // 2, w // 2, c)
+    y = torch.empty(shape, device=x.device, dtype=torch.float32)
+    y_skip = torch.empty(shape, device=x.device, dtype=torch.float32)
+    _lib.check(
+        _lib.lib().ctmr_gn_avgpool(n, d, h, w, c, x.data_ptr(), affine.data_ptr(), int(silu), y.data_ptr(),
+                                   y_skip.data_ptr(), _stream(x.device)),
+        "ctmr_gn_avgpool",
+    )
+    return y, y_skip
+
+
+@gn_avgpool.register_fake
+def _(x, affine, silu):
+    n, d, h, w, c = x.shape
+    return x.new_empty((n, d // 2, h // 2, w // 2, c)), x.new_empty((n, d // 2, h // 2, w // 2, c))
+
+
 # ---------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------

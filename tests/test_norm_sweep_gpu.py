@@ -69,3 +69,34 @@ def test_random_group_norm_matches_float64(ctmr, dev, case):
     print(f"{case['id']}: norm max rel error {err:.3e}", flush=True)
     assert err <= REL
     assert torch.equal(f.group_norm(xt, gt, bt, num_groups=groups, eps=eps, apply_silu=case["silu"]), y)
+
+
+@pytest.mark.parametrize(("shape", "silu"), [
+    ((2, 64, 64, 32, 64), True),    # UNet top-level down block input
+    ((1, 9, 7, 11, 48), True),      # odd extents: the last plane, row and column are dropped
+    ((2, 6, 4, 8, 6), False),       # channels not a multiple of 4 (scalar path)
+])
+def test_gn_avgpool_equals_gn_apply_then_pool(ctmr, dev, shape, silu):
+    """``ctmr_gn_avgpool`` (the down-sampling residual block's norm + SiLU + pool and the pool of its
+    input, from one read) equals ``gn_apply`` followed by the average pool, and the pool of the input,
+    bit for bit; both within the float64 bar."""
+    print(f"gn_avgpool {shape} silu={silu}", flush=True)
+    ops = ctmr.ops
+    g = torch.Generator(device=dev).manual_seed(sum(shape))
+    x = 1.5 * torch.randn(*shape, device=dev, generator=g) + 0.25
+    n, c = shape[0], shape[-1]
+    affine = torch.stack([1 + 0.2 * torch.randn(n, c, device=dev, generator=g),
+                          0.3 * torch.randn(n, c, device=dev, generator=g)], dim=-1).contiguous()
+    y, y_skip = ops.gn_avgpool(x, affine, silu)
+    assert torch.equal(y, ops.resample(ops.gn_apply(x, affine, silu), ctmr._lib.AVGPOOL2))
+    assert torch.equal(y_skip, ops.resample(x, ctmr._lib.AVGPOOL2))
+    y2, _ = ops.gn_avgpool(x, affine, silu)
+    assert torch.equal(y, y2)
+    xh, ah = x.double().cpu().numpy(), affine.double().cpu().numpy()
+    t = xh * ah[:, None, None, None, :, 0] + ah[:, None, None, None, :, 1]
+    if silu:
+        t = t / (1 + np.exp(-t))
+    d2, h2, w2 = (v // 2 for v in shape[1:4])
+    pool = lambda a: a[:, :2 * d2, :2 * h2, :2 * w2].reshape(n, d2, 2, h2, 2, w2, 2, c).mean(axis=(2, 4, 6))
+    assert rm.max_rel_error(y.cpu().numpy(), pool(t)) <= REL
+    assert rm.max_rel_error(y_skip.cpu().numpy(), pool(xh)) <= REL
