@@ -2978,7 +2978,7 @@ static int conv3d_run(const ctmr_conv_desc* desc, const float* x, const float* x
   int rc = geometry(desc, g);
   if (rc) return rc;
   if (!x || !packed || !y || (g.cat && !x2)) return fail(CTMR_E_INVALID, "null input, weight or output");
-  if (g.lds || g.lds_small) {  // no pack stage: the LDS GEMMs read x and the caller's affine table directly
+  if (g.lds || g.lds_small || g.small_out) {  // no pack stage: these read x and the caller's affine table directly
     if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
     return conv3d_gemm_impl(desc, x, x2, packed, bias, affine, residual, y, workspace, workspace_bytes, 0,
                             nullptr, stream);
@@ -3019,7 +3019,7 @@ static int conv3d_gn_run(const ctmr_conv_desc* desc, const float* x, const float
     return fail(CTMR_E_INVALID, "null input, weight, output or stats");
   if (gn_stats_tiles(desc, g, groups) == 0)
     return fail(CTMR_E_UNSUPPORTED, "this convolution cannot produce group-norm partials");
-  const bool direct_affine = g.lds || g.lds_small;
+  const bool direct_affine = g.lds || g.lds_small || g.small_out;
   if (direct_affine) {
     if ((desc->flags & CTMR_F_AFFINE) && !affine) return fail(CTMR_E_INVALID, "affine flag without affine");
   } else if ((rc = pack_impl(desc, x, x2, affine, workspace, workspace_bytes, stream))) {
