@@ -619,7 +619,7 @@ def profile_only(pkg, dev, what, steps, warmup):
         t = torch.full((2,), 500.0, device=dev)
         cls = torch.tensor([9, 0], device=dev)
         fn = lambda: m.controlnet_residuals(x, t, cls, None, w, constructor=cc, conditioning_embedding=emb)
-    elif what == "decode":
+    elif what in ("decode", "decode_bf16"):
         vc = m.PRODUCTION_VAE_CONSTRUCTOR
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
         z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 20, 64, 64, 4), dtype=np.float32)).to(dev)
@@ -670,7 +670,7 @@ def profile_only(pkg, dev, what, steps, warmup):
         b = torch.zeros(128, device=dev)
         g, z0 = torch.ones(128, device=dev), torch.zeros(128, device=dev)
         fn = lambda: f.vae_resblock([x], (w1, b), (w1, b), (g, z0), (g, z0), None, num_groups=32, eps=1e-6)
-    with f.precision("bf16" if what == "unet_bf16" else "fp32"):
+    with f.precision("bf16" if what.endswith("_bf16") else "fp32"):
         warm_up(fn, warmup)
         ms = _wall_ms(fn, steps)
     print(json.dumps({"only": what, "ms": round(ms, 3), "steps": steps}), flush=True)
@@ -686,8 +686,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "unet_bf16", "controlnet", "decode", "resblock", "attention",
-                                       "pointwise", "gemms", "gemms_stream", "config2a", "config2b"],
+    ap.add_argument("--only", choices=["unet", "unet_bf16", "controlnet", "decode", "decode_bf16", "resblock",
+                                       "attention", "pointwise", "gemms", "gemms_stream", "config2a", "config2b"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")

@@ -139,6 +139,347 @@ __global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
   }
 }
 
+// GN affine (scale, offset) pairs of channels ch..ch+3 of batch item b: two
+// 16-byte loads (the host checks the table's 16-byte alignment).
+__device__ __forceinline__ void load_affine4(const PackArgs& a, int b, int ch, f4& s, f4& o) {
+  const f4* p = reinterpret_cast<const f4*>(a.affine + ((int64_t)b * a.c + ch) * 2);
+  const f4 p0 = p[0], p1 = p[1];
+  s = f4{p0[0], p0[2], p1[0], p1[2]};
+  o = f4{p0[1], p0[3], p1[1], p1[3]};
+}
+
+// The pack transform of one interior vector: affine, then SiLU (the order and
+// operations of pack_value4).
+__device__ __forceinline__ f4 pack_transform4(const PackArgs& a, f4 v, f4 s, f4 o) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float t = v[k];
+    if (a.affine_on) t = fmaf(t, s[k], o[k]);
+    if (a.silu_on) t = silu_f(t);
+    v[k] = t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ unsigned bf16_pair(float lo, float hi) {
+  return (unsigned)f32_to_bf16_bits(lo) | ((unsigned)f32_to_bf16_bits(hi) << 16);
+}
+
+// Store one packed item: V vectors of 4 channels, as V f4 (fp32) or one
+// 16-byte store of 8 rounded values (bf16, V = 2).
+template <int V>
+__device__ __forceinline__ void store_packed(const PackArgs& a, int64_t idx, const f4* v) {
+  if constexpr (V == 2) {
+    u4 packed;
+    packed.x = bf16_pair(v[0][0], v[0][1]);
+    packed.y = bf16_pair(v[0][2], v[0][3]);
+    packed.z = bf16_pair(v[1][0], v[1][1]);
+    packed.w = bf16_pair(v[1][2], v[1][3]);
+    reinterpret_cast<u4*>(a.out)[idx] = packed;
+  } else {
+    reinterpret_cast<f4*>(a.out)[idx] = v[0];
+  }
+}
+
+// Non-resampled pack for c % 4 == 0 (the common case): same values as
+// pack_input_kernel.  A thread takes one (row, column, channel group) item of
+// the padded plane over PZ consecutive padded planes and issues all their
+// source loads before its first store (PZ times the bytes in flight per wave
+// of a one-item thread); the group's affine pairs are read once per batch item
+// as 16-byte vectors.
+template <int V, int PZ>
+__global__ __launch_bounds__(256) void pack_planes_kernel(PackArgs a) {
+  const int cgn = a.cp / (4 * V);
+  const int PW = a.gw + 2 * a.halo, PH = a.gh + 2 * a.halo, PD = a.gd + 2 * a.halo;
+  const unsigned plane = (unsigned)PH * (unsigned)PW * (unsigned)cgn;
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= plane) return;
+  const int cg = (int)(i % (unsigned)cgn);
+  const unsigned r = i / (unsigned)cgn;
+  const int x = (int)(r % (unsigned)PW) - a.halo, y = (int)(r / (unsigned)PW) - a.halo;
+  const bool row_in = x >= 0 && x < a.gw && y >= 0 && y < a.gh;
+  const int total = a.n * PD;
+  for (int bz0 = blockIdx.y * PZ; bz0 < total; bz0 += gridDim.y * PZ) {
+    f4 v[PZ][V];
+    bool in[PZ];
+#pragma unroll
+    for (int s = 0; s < PZ; ++s) {
+      const int bz = bz0 + s;
+      const int b = bz / PD, z = bz - b * PD - a.halo;
+      in[s] = bz < total && row_in && z >= 0 && z < a.gd;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const int ch = cg * 4 * V + 4 * k;
+        v[s][k] = f4{0.f, 0.f, 0.f, 0.f};
+        if (in[s] && ch < a.c) {
+          const int64_t vox = (((int64_t)b * a.gd + z) * a.gh + y) * a.gw + x;
+          v[s][k] = ch < a.c1 ? *reinterpret_cast<const f4*>(a.x + vox * a.c1 + ch)
+                              : *reinterpret_cast<const f4*>(a.x2 + vox * (a.c - a.c1) + (ch - a.c1));
+        }
+      }
+    }
+    int cur_b = -1;
+    f4 sc[V], of[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) sc[k] = of[k] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < PZ; ++s) {
+      const int bz = bz0 + s;
+      if (bz >= total) break;
+      const int b = bz / PD;
+      if (a.affine_on && b != cur_b) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          const int ch = cg * 4 * V + 4 * k;
+          if (ch < a.c) load_affine4(a, b, ch, sc[k], of[k]);
+        }
+        cur_b = b;
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k)
+        if (in[s] && cg * 4 * V + 4 * k < a.c) v[s][k] = pack_transform4(a, v[s][k], sc[k], of[k]);
+      store_packed<V>(a, (int64_t)bz * plane + i, v[s]);
+    }
+  }
+}
+
+// Trilinear-2x pack for c % 4 == 0 (one source tensor): same values as
+// pack_input_kernel.  A thread takes one 4-channel group of one source cell
+// column (cy, cx) and marches ZC cells cz along z; cells run over [-1, n] on
+// each axis, and cell (cz, cy, cx) owns the padded copy's 2x2x2 block of
+// 2x-grid voxels (2cz + dz, 2cy + dy, 2cx + dx): voxels at -1 and 2n are the
+// zero halo, -2 and 2n + 1 lie past the copy.  A column's voxels have fixed
+// x and y source pairs (tri_axis), so the thread keeps three x-then-y-
+// interpolated source planes (clamped planes cz - 1, cz, cz + 1) and computes
+// one new plane per cell: 9 loads where cy and cx lie in [1, n - 2] (the four
+// voxel columns share the 3x3 source rows), 16 at the faces, against 8 per
+// voxel.  Each voxel is then the z blend of two of those planes with
+// tri_axis's weights: the expression trilinear_sample4 evaluates, with the
+// same operands (a plane repeated by the clamp holds the same bits in either
+// slot), so the two agree bitwise.
+struct TriPlane {
+  f4 p[2][2];  // [dy][dx]
+};
+
+// Column geometry of pack_trilinear_kernel's thread: its cell (cy, cx), its
+// channel offset, and its voxels' y/x source pairs and weights.
+struct TriColumn {
+  int cy, cx, ch;
+  int ya[2], yb[2], xa[2], xb[2];
+  float ly[2], lx[2];
+};
+
+// The 3x3 source vectors of an inner column's plane (clamped into the
+// volume): rows cy - 1 .. cy + 1, columns cx - 1 .. cx + 1.
+struct TriRows {
+  f4 v[3][3];
+};
+
+__device__ __forceinline__ TriRows tri_rows(const PackArgs& a, const TriColumn& t, const float* src, int zs) {
+  TriRows o;
+  zs = min(max(zs, 0), a.id - 1);
+  const float* pl = src + (int64_t)zs * a.ih * a.iw * a.c;
+#pragma unroll
+  for (int ys = 0; ys < 3; ++ys) {
+    const float* row = pl + ((int64_t)(t.cy - 1 + ys) * a.iw + (t.cx - 1)) * a.c;
+#pragma unroll
+    for (int xs = 0; xs < 3; ++xs) o.v[ys][xs] = *reinterpret_cast<const f4*>(row + xs * a.c);
+  }
+  return o;
+}
+
+// x-then-y interpolation of an inner column's plane: the four voxel columns
+// share the 3x3 source rows (x pairs (cx - 1, cx), (cx, cx + 1); y likewise).
+__device__ __forceinline__ TriPlane tri_inner_plane(const TriColumn& t, const TriRows& s) {
+#pragma clang fp contract(off)
+  TriPlane o;
+  f4 rr[3][2];  // [source row][dx]
+#pragma unroll
+  for (int ys = 0; ys < 3; ++ys)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      rr[ys][0][q] = fmaf(1.0f - t.lx[0], s.v[ys][0][q], t.lx[0] * s.v[ys][1][q]);
+      rr[ys][1][q] = fmaf(1.0f - t.lx[1], s.v[ys][1][q], t.lx[1] * s.v[ys][2][q]);
+    }
+#pragma unroll
+  for (int dx = 0; dx < 2; ++dx)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o.p[0][dx][q] = fmaf(1.0f - t.ly[0], rr[0][dx][q], t.ly[0] * rr[1][dx][q]);
+      o.p[1][dx][q] = fmaf(1.0f - t.ly[1], rr[1][dx][q], t.ly[1] * rr[2][dx][q]);
+    }
+  return o;
+}
+
+// x-then-y-interpolated source plane zs (clamped into the volume) of a face
+// column: its four voxel columns' y/x pairs loaded apart (16 loads).
+__device__ __forceinline__ TriPlane tri_face_plane(const PackArgs& a, const TriColumn& t, const float* src, int zs) {
+#pragma clang fp contract(off)
+  TriPlane o;
+  zs = min(max(zs, 0), a.id - 1);
+  const float* pl = src + (int64_t)zs * a.ih * a.iw * a.c;
+#pragma unroll
+  for (int dy = 0; dy < 2; ++dy) {
+    const float* r0 = pl + (int64_t)t.ya[dy] * a.iw * a.c;
+    const float* r1 = pl + (int64_t)t.yb[dy] * a.iw * a.c;
+#pragma unroll
+    for (int dx = 0; dx < 2; ++dx) {
+      const f4 a0 = *reinterpret_cast<const f4*>(r0 + (int64_t)t.xa[dx] * a.c);
+      const f4 a1 = *reinterpret_cast<const f4*>(r0 + (int64_t)t.xb[dx] * a.c);
+      const f4 b0 = *reinterpret_cast<const f4*>(r1 + (int64_t)t.xa[dx] * a.c);
+      const f4 b1 = *reinterpret_cast<const f4*>(r1 + (int64_t)t.xb[dx] * a.c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float ra = fmaf(1.0f - t.lx[dx], a0[q], t.lx[dx] * a1[q]);
+        const float rb = fmaf(1.0f - t.lx[dx], b0[q], t.lx[dx] * b1[q]);
+        o.p[dy][dx][q] = fmaf(1.0f - t.ly[dy], ra, t.ly[dy] * rb);
+      }
+    }
+  }
+  return o;
+}
+
+// One column's march over cells [cz0, cz1) of batch item b (see
+// pack_trilinear_kernel): blend, transform and store each cell's 2x2x2 voxels.
+template <bool BF16, bool INNER>
+__device__ __forceinline__ void tri_march(const PackArgs& a, const TriColumn& t, int b, int cz0, int cz1) {
+#pragma clang fp contract(off)
+  const int PW = a.gw + 2, PH = a.gh + 2, PD = a.gd + 2;
+  const float* src = a.x + (int64_t)b * a.id * a.ih * a.iw * a.c + t.ch;
+  f4 sc = {0.f, 0.f, 0.f, 0.f}, of = {0.f, 0.f, 0.f, 0.f};
+  if (a.affine_on) load_affine4(a, b, t.ch, sc, of);
+  // inner columns load the next plane's rows one cell ahead of its blend
+  TriPlane pm, p0;
+  TriRows next;
+  if constexpr (INNER) {
+    pm = tri_inner_plane(t, tri_rows(a, t, src, cz0 - 1));
+    next = tri_rows(a, t, src, cz0 + 1);
+    p0 = tri_inner_plane(t, tri_rows(a, t, src, cz0));
+  } else {
+    pm = tri_face_plane(a, t, src, cz0 - 1);
+    p0 = tri_face_plane(a, t, src, cz0);
+  }
+  for (int cz = cz0; cz < cz1; ++cz) {
+    TriPlane p1;
+    if constexpr (INNER) {
+      p1 = tri_inner_plane(t, next);
+      if (cz + 1 < cz1) next = tri_rows(a, t, src, cz + 2);
+    } else {
+      p1 = tri_face_plane(a, t, src, cz + 1);
+    }
+    f4 out[8];
+    if (cz >= 1 && cz <= a.id - 2) {
+      // both voxels' z pairs are unclamped: (cz - 1, cz) and (cz, cz + 1)
+      float lz[2];
+      int z0, z1;
+      tri_axis(2 * cz, a.id, z0, z1, lz[0]);
+      tri_axis(2 * cz + 1, a.id, z0, z1, lz[1]);
+#pragma unroll
+      for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+        for (int dx = 0; dx < 2; ++dx)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            out[dy * 2 + dx][q] = fmaf(1.0f - lz[0], pm.p[dy][dx][q], lz[0] * p0.p[dy][dx][q]);
+            out[4 + dy * 2 + dx][q] = fmaf(1.0f - lz[1], p0.p[dy][dx][q], lz[1] * p1.p[dy][dx][q]);
+          }
+    } else {
+      // near the z faces: pick each voxel's two planes among the clamped
+      // planes cz - 1, cz, cz + 1 (equal clamped planes hold equal bits; the
+      // halo cells' voxels are not stored from these)
+      const int zlo = max(cz - 1, 0), zmid = min(max(cz, 0), a.id - 1);
+#pragma unroll
+      for (int dz = 0; dz < 2; ++dz) {
+        int z0, z1;
+        float lz;
+        tri_axis(2 * cz + dz, a.id, z0, z1, lz);
+        const int sa = z0 == zlo ? 0 : z0 == zmid ? 1 : 2, sb = z1 == zlo ? 0 : z1 == zmid ? 1 : 2;
+#pragma unroll
+        for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+          for (int dx = 0; dx < 2; ++dx)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float va = sa == 0 ? pm.p[dy][dx][q] : sa == 1 ? p0.p[dy][dx][q] : p1.p[dy][dx][q];
+              const float vb = sb == 0 ? pm.p[dy][dx][q] : sb == 1 ? p0.p[dy][dx][q] : p1.p[dy][dx][q];
+              out[dz * 4 + dy * 2 + dx][q] = fmaf(1.0f - lz, va, lz * vb);
+            }
+      }
+    }
+    pm = p0;
+    p0 = p1;
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+      const int oz = 2 * cz + (o >> 2), oy = 2 * t.cy + ((o >> 1) & 1), ox = 2 * t.cx + (o & 1);
+      if (oz < -1 || oz > a.gd || oy < -1 || oy > a.gh || ox < -1 || ox > a.gw) continue;
+      const bool inside = oz >= 0 && oz < a.gd && oy >= 0 && oy < a.gh && ox >= 0 && ox < a.gw;
+      const f4 v = inside ? pack_transform4(a, out[o], sc, of) : f4{0.f, 0.f, 0.f, 0.f};
+      const int64_t vox = (((int64_t)b * PD + oz + 1) * PH + oy + 1) * PW + ox + 1;
+      if constexpr (BF16) {
+        uint2 packed;
+        packed.x = bf16_pair(v[0], v[1]);
+        packed.y = bf16_pair(v[2], v[3]);
+        *reinterpret_cast<uint2*>(reinterpret_cast<unsigned*>(a.out) + (vox * a.cp + t.ch) / 2) = packed;
+      } else {
+        *reinterpret_cast<f4*>(reinterpret_cast<float*>(a.out) + vox * a.cp + t.ch) = v;
+      }
+    }
+  }
+}
+
+// Zeros of the padded copy for a column's channel group past the source
+// channels, over cells [cz0, cz1) of batch item b.
+template <bool BF16>
+__device__ __forceinline__ void tri_zero(const PackArgs& a, const TriColumn& t, int b, int cz0, int cz1) {
+  const int PW = a.gw + 2, PH = a.gh + 2, PD = a.gd + 2;
+  for (int cz = cz0; cz < cz1; ++cz)
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+      const int oz = 2 * cz + (o >> 2), oy = 2 * t.cy + ((o >> 1) & 1), ox = 2 * t.cx + (o & 1);
+      if (oz < -1 || oz > a.gd || oy < -1 || oy > a.gh || ox < -1 || ox > a.gw) continue;
+      const int64_t vox = (((int64_t)b * PD + oz + 1) * PH + oy + 1) * PW + ox + 1;
+      if constexpr (BF16)
+        *reinterpret_cast<uint2*>(reinterpret_cast<unsigned*>(a.out) + (vox * a.cp + t.ch) / 2) = uint2{0u, 0u};
+      else
+        *reinterpret_cast<f4*>(reinterpret_cast<float*>(a.out) + vox * a.cp + t.ch) = f4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+template <bool BF16, int ZC>
+__global__ __launch_bounds__(256) void pack_trilinear_kernel(PackArgs a) {
+  const int cgn = a.cp >> 2;
+  const int CW = a.iw + 2, CH = a.ih + 2, CD = a.id + 2;
+  const unsigned cells = (unsigned)CH * (unsigned)CW * (unsigned)cgn;
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= cells) return;
+  TriColumn t;
+  t.ch = (int)(i % (unsigned)cgn) * 4;
+  const unsigned r = i / (unsigned)cgn;
+  t.cx = (int)(r % (unsigned)CW) - 1;
+  t.cy = (int)(r / (unsigned)CW) - 1;
+  // the halo cells' pairs are clamped into the volume: their voxels are
+  // zeros or lie past the copy, only the loads need to stay in bounds
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    tri_axis(2 * t.cy + d, a.ih, t.ya[d], t.yb[d], t.ly[d]);
+    tri_axis(2 * t.cx + d, a.iw, t.xa[d], t.xb[d], t.lx[d]);
+    t.ya[d] = min(t.ya[d], a.ih - 1);
+    t.xa[d] = min(t.xa[d], a.iw - 1);
+  }
+  const bool inner = t.cy >= 1 && t.cy <= a.ih - 2 && t.cx >= 1 && t.cx <= a.iw - 2;
+  const int chunks = (CD + ZC - 1) / ZC;
+  for (int bc = blockIdx.y; bc < a.n * chunks; bc += gridDim.y) {
+    const int b = bc / chunks, cz0 = (bc - b * chunks) * ZC - 1;
+    const int cz1 = min(cz0 + ZC, a.id + 1);
+    if (t.ch >= a.c)
+      tri_zero<BF16>(a, t, b, cz0, cz1);
+    else if (inner)
+      tri_march<BF16, true>(a, t, b, cz0, cz1);
+    else
+      tri_march<BF16, false>(a, t, b, cz0, cz1);
+  }
+}
+
 // Small-cin packing (cin below one K block): one row per output voxel holding
 // every tap's channels, K index tap*cin + c (tap = kd*9 + kh*3 + kw), so the
 // GEMM runs ceil(27*cin / K block) steps instead of 27 padded ones.  Values
@@ -2710,6 +3051,39 @@ static int pack_impl(const ctmr_conv_desc* desc, const float* x, const float* x2
   const int64_t plane_items = (int64_t)(g.th + 2 * g.halo) * (g.tw + 2 * g.halo) * (g.cp / (pa.bf16 ? 8 : 4));
   const int64_t planes = (int64_t)desc->n * (g.td + 2 * g.halo);
   if (plane_items >= (1ll << 31)) return fail(CTMR_E_UNSUPPORTED, "padded plane too large for the pack");
+  const bool vec = (desc->cin & 3) == 0 && (!pa.affine_on || ((uintptr_t)affine & 15) == 0);
+  if (vec && pa.trilinear && !g.cat && g.halo == 1) {
+    // one thread per (source cell, channel group), cells over [-1, n] per axis
+    // runs of 8 cells along z; one cell per thread where runs of 8 would
+    // leave under ~4 waves per SIMD (no serial chain of loads)
+    const int64_t cells = (int64_t)(desc->h + 2) * (desc->w + 2) * (g.cp / 4);
+    if (cells >= (1ll << 31)) return fail(CTMR_E_UNSUPPORTED, "source plane too large for the pack");
+    const bool long_runs = cells * desc->n * ceil_div(desc->d + 2, 8) >= (1ll << 18);
+    const int zc = long_runs ? 8 : 1;
+    const int64_t runs = (int64_t)desc->n * ceil_div(desc->d + 2, zc);
+    const dim3 grid((unsigned)ceil_div(cells, 256), (unsigned)std::min<int64_t>(runs, 65535));
+    if (long_runs) {
+      if (pa.bf16)
+        hipLaunchKernelGGL((pack_trilinear_kernel<true, 8>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+      else
+        hipLaunchKernelGGL((pack_trilinear_kernel<false, 8>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+    } else {
+      if (pa.bf16)
+        hipLaunchKernelGGL((pack_trilinear_kernel<true, 1>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+      else
+        hipLaunchKernelGGL((pack_trilinear_kernel<false, 1>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+    }
+    return check_launch("pack_trilinear");
+  }
+  if (vec && !pa.trilinear) {
+    constexpr int PZ = 4;
+    const dim3 grid((unsigned)ceil_div(plane_items, 256), (unsigned)std::min<int64_t>(ceil_div(planes, PZ), 65535));
+    if (pa.bf16)
+      hipLaunchKernelGGL((pack_planes_kernel<2, PZ>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+    else
+      hipLaunchKernelGGL((pack_planes_kernel<1, PZ>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+    return check_launch("pack_planes");
+  }
   hipLaunchKernelGGL(pack_input_kernel,
                      dim3((unsigned)ceil_div(plane_items, 256), (unsigned)std::min<int64_t>(planes, 65535)),
                      dim3(256), 0, (hipStream_t)stream, pa);
