@@ -216,13 +216,29 @@ def pack_upsample_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tens
     return ops.pack_weight(w, int(w.shape[1]), int(w.shape[0]), 3, _lib.MODE_NEAREST2X, code)
 
 
+def _keeps_fp32(weight: Tensor) -> bool:
+    """Convs that stay fp32 under ``precision("bf16")``, where the bf16 form costs more than it saves:
+    every bf16 GEMM reads a bf16 copy of its input made by a conversion pass.
+
+    * 1x1x1 convs: the pass costs more than the fp32 GEMM it would speed up (the UNet's skip
+      projections read their input once, at 2 MFLOP per byte moved);
+    * at most 4 output channels (the UNet and VAE output convs): the fp32 direct kernel (GN affine +
+      SiLU staged, VALU FMAs) takes 77 us at the UNet's 2x64x64x32 and 0.63 ms at the decoder's
+      80x256x256, where the bf16 tap-expanded GEMM, its tap sum and the pass take ~0.1 and ~0.9 ms;
+    * at most 8 input channels (the 4-channel input convs, the condition encoder's 8-channel convs):
+      the fp32 LDS-staged im2col GEMM takes 53 us for the UNet's conv_in, the bf16 im2col rows and
+      GEMM 130 us."""
+    if weight.dim() != 5:
+        return False
+    o, c, k = (int(v) for v in weight.shape[:3])
+    return k == 1 or o <= 4 or c <= 8
+
+
 def _pack(weight: Tensor, mode: int) -> Tensor:
-    """Packed weight for the active precision.  1x1x1 convs stay fp32 under ``precision("bf16")``: their
-    bf16 form needs a conversion pass over the input that costs more than the fp32 GEMM it would save
-    (the UNet's skip projections read the input once, at 2 MFLOP per byte moved)."""
+    """Packed weight for the active precision (``_keeps_fp32`` convs stay fp32 under bf16)."""
     if not isinstance(weight, Tensor) or weight.device.type != "cuda":
         raise ValueError("conv weight must be a torch.Tensor on the GPU (there is no CPU path)")
-    code = _lib.DT_F32 if weight.dim() == 5 and int(weight.shape[2]) == 1 else _dtype_code()
+    code = _lib.DT_F32 if _keeps_fp32(weight) else _dtype_code()
     dtype = "bf16" if code == _lib.DT_BF16 else "fp32"
     packer = pack_upsample_weight if mode == _lib.MODE_NEAREST2X else pack_weight
     return cached_derived(_packed, _packed_lock, ("conv", mode, code, id(weight)), (weight,),

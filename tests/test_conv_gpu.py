@@ -444,9 +444,13 @@ def test_small_cin_im2col_conv(ctmr, dev, cin, cout, stride, fused):
         y = f.conv3d(_t(x, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
         expected = rm.conv3d(x, w, b, stride=stride)
     _assert_rel(_h(y), expected, FP32_REL, f"im2col {cin}->{cout} s{stride}")
-    with f.precision("bf16"):
-        y16 = f.conv3d(_t(x, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
+    # explicit bf16 packing reaches the bf16 im2col GEMM (precision("bf16") keeps cin <= 8 convs fp32)
+    y16 = f.implicit_gemm_conv3d(_t(x, dev), f.pack_weight(_t(w, dev), dtype="bf16"), _t(b, dev), cout=cout,
+                                 stride=stride)
     _assert_rel(_h(y16), rm.conv3d(x, w, b, stride=stride), BF16_REL, f"bf16 im2col {cin}->{cout}")
+    with f.precision("bf16"):
+        y_mode = f.conv3d(_t(x, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
+    _assert_rel(_h(y_mode), rm.conv3d(x, w, b, stride=stride), FP32_REL, f"bf16 mode, fp32 {cin}->{cout}")
 
 
 @pytest.mark.parametrize(("shape", "cout", "stride", "mode"), [
@@ -472,6 +476,11 @@ def test_bf16_variant_within_2e2(ctmr, dev, shape, cout, stride, mode):
             y = f.conv3d(_t(xn, dev), _t(w, dev), _t(b, dev), padding=1, stride=stride)
             expected = rm.conv3d(xn, w, b, stride=stride)
     _assert_rel(_h(y), expected, BF16_REL, f"bf16 {shape}->{cout} {mode}")
+    if mode == "plain":
+        # explicit bf16 packing: the bf16 GEMMs also for the shapes the mode keeps fp32 (cout <= 4, cin <= 8)
+        y16 = f.implicit_gemm_conv3d(_t(xn, dev), f.pack_weight(_t(w, dev), dtype="bf16"), _t(b, dev), cout=cout,
+                                     stride=stride)
+        _assert_rel(_h(y16), expected, BF16_REL, f"explicit bf16 {shape}->{cout}")
 
 
 def test_group_norm_affine_and_apply(ctmr, dev):

@@ -222,9 +222,9 @@ def _production_unet(ctmr, dev, seed=7):
 
 def test_config3_unet_step_matches_cpu_oracle(ctmr, dev):
     """Config 3 at full size: production UNet, latent 64x64x32x4, batch 2 (CFG pair),
-    random init; max relative error vs the PyTorch-CPU fp32 oracle <= 1e-4.  The same step with
-    every conv in bf16 (bf16 operands, fp32 accumulation) stays within the per-layer bf16 bar,
-    2e-2, end to end (measured 5.8e-3 on MI355X)."""
+    random init; max relative error vs the PyTorch-CPU fp32 oracle <= 1e-4.  The same step under
+    precision("bf16") (bf16 operands, fp32 accumulation for every 3x3x3 conv with more than 8 input and
+    4 output channels) stays within the per-layer bf16 bar, 2e-2, end to end."""
     m = ctmr.maisi
     host, w = _production_unet(ctmr, dev)
     rng = np.random.default_rng(3)
