@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <type_traits>
 
 namespace ctmr {
 
@@ -1148,24 +1149,29 @@ constexpr int kStageIters = (kHaloVox * 4 + 255) / 256;  // 16-byte pieces per t
 // transposed accumulators: lane l of block (ms, ns) holds voxel (z0 + wave,
 // y0 + ms + 4*((l/8)%2), x0 + l%8) of the 4x8x8 brick and output columns
 // n0 + ns*16 + 4*(l/16) .. +3 (cout % 64 == 0), stored -- bias first, then the
-// residual -- as 16 bytes.  Group-norm column sums go through `red` (4 KiB of
+// residual -- as 16 bytes.  UP: the brick is of the source grid (p.d, p.h,
+// p.w) and voxel (z, y, x) of parity `phase` = 4a + 2b + c is output voxel
+// (2z + a, 2y + b, 2x + c) of the doubled grid; statistics tiles are
+// (brick, parity) pairs.  Group-norm column sums go through `red` (4 KiB of
 // LDS, which may alias the kernel's staging buffers: a barrier precedes it).
-template <typename Args>
+template <bool UP = false, typename Args>
 __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int b, int split_id, int z0, int y0,
                                             int x0, int n0, int wave, int lane, int tile_id,
-                                            double (*red)[64][2]) {
+                                            double (*red)[64][2], int phase = 0) {
   const int lrow = lane & 15, lgrp = lane >> 4;
   const bool partial = p.split > 1;
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
   const int z = z0 + wave, x = x0 + (lrow & 7);
+  constexpr int S = UP ? 2 : 1;
+  const int pa = UP ? phase >> 2 : 0, pb = UP ? (phase >> 1) & 1 : 0, pc = UP ? phase & 1 : 0;
   bool row_ok[4];
   int64_t base[4];
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
     const int y = y0 + ms + 4 * (lrow >> 3);
     row_ok[ms] = z < p.d && y < p.h && x < p.w;
-    base[ms] = ((((int64_t)b * p.d + min(z, p.d - 1)) * p.h + min(y, p.h - 1)) * p.w + min(x, p.w - 1)) * p.cout +
-               n0 + 4 * lgrp;
+    const int oz = S * min(z, p.d - 1) + pa, oy = S * min(y, p.h - 1) + pb, ox = S * min(x, p.w - 1) + pc;
+    base[ms] = ((((int64_t)b * (S * p.d) + oz) * (S * p.h) + oy) * (S * p.w) + ox) * p.cout + n0 + 4 * lgrp;
   }
   if (!partial && p.has_bias) {
     const float* bias_b = p.bias + (p.batch_bias ? (int64_t)b * p.cout : 0) + n0 + 4 * lgrp;
@@ -1198,7 +1204,7 @@ __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int 
     column_sums<4>(acc, row_ok, col_ok, red, wave, lane);
     __syncthreads();
     combine_gn_partials<4, 4, 1>(red, n0, p.cout, p.gn_cpg, p.gn_groups,
-                                 p.stats + ((int64_t)b * p.tz * p.ty * p.tx + tile_id) * p.gn_groups * 2);
+                                 p.stats + ((int64_t)b * p.tz * p.ty * p.tx * S * S * S + tile_id) * p.gn_groups * 2);
   }
 }
 
@@ -1826,11 +1832,12 @@ struct Lds16Frag {
   u4 a[4], b[4];
 };
 
-// Reads tap (kd, kh, kw) of the halo and of weight row `brow` into `f`.  A row
-// (lane % 16) is brick column x = lane % 8 of line ms + 4 * ((lane / 8) % 2),
-// K piece lane / 16; at tap (kd, kh, kw) it reads halo column x + kw of halo
-// line ms + 4 * ((lane / 8) % 2) + kh.
-template <int KD, int KH, int KW>
+// Reads tap (kd, kh, kw) of the halo and slot BS of weight row `brow` (the
+// row's tap kw for the 3x3x3 GEMM) into `f`.  A row (lane % 16) is brick
+// column x = lane % 8 of line ms + 4 * ((lane / 8) % 2), K piece lane / 16; at
+// tap (kd, kh, kw) it reads halo column x + kw of halo line
+// ms + 4 * ((lane / 8) % 2) + kh.
+template <int KD, int KH, int KW, int BS = KW>
 __device__ __forceinline__ void lds16_load(Lds16Frag& f, const char* brow, const char* halo_p,
                                            const int (&abase)[4], const int (&bbase)[4], int lane) {
   const int h = (lane >> 3) & 1, g = (lane >> 4) & 3;
@@ -1841,7 +1848,7 @@ __device__ __forceinline__ void lds16_load(Lds16Frag& f, const char* brow, const
     f.a[ms] = *reinterpret_cast<const u4*>(halo_p + (abase[ms] | (piece << 4)) + off);
   }
 #pragma unroll
-  for (int ns = 0; ns < 4; ++ns) f.b[ns] = *reinterpret_cast<const u4*>(brow + KW * kB16TapBytes + bbase[ns]);
+  for (int ns = 0; ns < 4; ++ns) f.b[ns] = *reinterpret_cast<const u4*>(brow + BS * kB16TapBytes + bbase[ns]);
 }
 
 // B^T A^T (operands exchanged: the same dot products) so that a lane's result
@@ -1882,6 +1889,34 @@ __device__ __forceinline__ void lds16_row(f4 (&acc)[4][4], Lds16Frag (&fr)[2], c
   lds16_mma(acc, fr[P]);
 }
 
+// Tap row (KD, KH) of the nearest-2x parity GEMM in conv_lds_bf16_kernel<true>:
+// halo taps (KD, KH, KW0) and (KD, KH, KW0 + 1), B from slots 0 and 1 of this
+// row's weight buffer `brow`; its first tap is already in fr[0].  Barrier and
+// refill as in lds16_row: the barrier follows the row's last ds_read; after
+// it `after_barrier` refills `brow`, and the next row's first tap (NEXT: halo
+// tap (NKD, NKH, KW0), buffer `brow_next`) is read into fr[0] while this
+// row's second products run.
+template <int KD, int KH, int KW0, bool NEXT, int NKD, int NKH, typename AfterBarrier>
+__device__ __forceinline__ void lds16_row2(f4 (&acc)[4][4], Lds16Frag (&fr)[2], const char* brow,
+                                           const char* brow_next, const char* halo_p, const int (&abase)[4],
+                                           const int (&bbase)[4], int lane, AfterBarrier&& after_barrier) {
+  lds16_load<KD, KH, KW0 + 1, 1>(fr[1], brow, halo_p, abase, bbase, lane);
+  lds16_mma(acc, fr[0]);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  after_barrier();
+  if constexpr (NEXT) lds16_load<NKD, NKH, KW0, 0>(fr[0], brow_next, halo_p, abase, bbase, lane);
+  lds16_mma(acc, fr[1]);
+}
+
+// UP: nearest-2x upsampling folded into 8 parity filters of 2x2x2 taps
+// (pack_weight_kernel's [phase][tap] layout).  Parity (a, b, c) of source
+// brick (z0, y0, x0) computes output voxels (2(z0 + z) + a, 2(y0 + y) + b,
+// 2(x0 + x) + c) from the same halo of the packed source copy as the 3x3x3
+// GEMM, reading its taps (a + td, b + th, c + tw), td, th, tw in {0, 1}: four
+// two-tap rows per 32-channel chunk.  The parity is part of the workgroup
+// index, so one launch covers all eight.
+template <bool UP>
 __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   __shared__ __attribute__((aligned(256))) char halo[kB16HaloBytes];
   __shared__ __attribute__((aligned(256))) char bbuf[2][3 * kB16TapBytes];
@@ -1898,6 +1933,11 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   rest /= p.ty;
   const int bz = rest % p.tz;
   rest /= p.tz;
+  int phase = 0;
+  if constexpr (UP) {
+    phase = rest & 7;
+    rest >>= 3;
+  }
   const int b = rest % p.n;
   const int split_id = rest / p.n;
   const int z0 = bz * kBD, y0 = by * kBH, x0 = bx * kBW;
@@ -1931,7 +1971,7 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   // of tap j of the row.
   const int tap_bytes = p.kb * p.np * 64;  // packed bytes between consecutive taps
   int woff[kB16RowIters];
-  const unsigned wload = (1u << kB16RowIters) - 1;
+  const unsigned wload = UP ? 3u : (1u << kB16RowIters) - 1;  // two taps per row with UP
 #pragma unroll
   for (int j = 0; j < kB16RowIters; ++j)
     woff[j] = j * tap_bytes + (n0 + (tid >> 2)) * 64 + 16 * ((tid & 3) ^ row64_swizzle((tid >> 2) & 15));
@@ -1943,8 +1983,11 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (lds_ptr_t)(halo + (i * 256 + wave * 64) * 16), 16,
                                                  hoff[i], so, 0, 0);
   };
+  // First tap of weight row `row`: 3 * row of the 27 (or 8 * phase + 2 * row
+  // with UP), K block `chunk`.
   auto row_so = [&](int chunk, int row) {
-    return __builtin_amdgcn_readfirstlane((row * 3 * p.kb + chunk) * p.np * 64);
+    const int tap = UP ? 8 * phase + 2 * row : 3 * row;
+    return __builtin_amdgcn_readfirstlane((tap * p.kb + chunk) * p.np * 64);
   };
 
   int abase[4];
@@ -1977,6 +2020,42 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   fill_row(c_begin, 0, 0);
   if (c_end - c_begin > 0) fill_row(c_begin, 1, 1);
   int k = 0;
+  if constexpr (UP) {
+    // Rows R = 2 td + th of a chunk; row k refills its buffer with row k + 2.
+    auto chunks = [&](auto pa, auto pb, auto pc) {
+      constexpr int A = decltype(pa)::value, B = decltype(pb)::value, C = decltype(pc)::value;
+      for (int chunk = c_begin; chunk < c_end; ++chunk) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        const bool more = chunk + 1 < c_end;
+        Lds16Frag fr[2];
+        lds16_load<A, B, C, 0>(fr[0], &bbuf[k & 1][0], halo, abase, bbase, lane);
+#define CTMR_LDS16_UP_ROW(R, NEXT)                                                                        \
+        lds16_row2<A + (R) / 2, B + (R) % 2, C, NEXT, A + ((R) + 1) / 2, B + ((R) + 1) % 2>(                \
+            acc, fr, &bbuf[k & 1][0], &bbuf[(k + 1) & 1][0], halo, abase, bbase, lane, [&]() {               \
+              if ((R) < 2) fill_row(chunk, (R) + 2, k & 1);                                                 \
+              else if (more) fill_row(chunk + 1, (R) - 2, k & 1);                                           \
+              if ((R) == 3 && more) fill_halo(chunk + 1);                                                   \
+            });                                                                                             \
+        ++k;
+        CTMR_LDS16_UP_ROW(0, true) CTMR_LDS16_UP_ROW(1, true) CTMR_LDS16_UP_ROW(2, true)
+        CTMR_LDS16_UP_ROW(3, false)
+#undef CTMR_LDS16_UP_ROW
+      }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    switch (phase) {
+      case 0: chunks(I0{}, I0{}, I0{}); break;
+      case 1: chunks(I0{}, I0{}, I1{}); break;
+      case 2: chunks(I0{}, I1{}, I0{}); break;
+      case 3: chunks(I0{}, I1{}, I1{}); break;
+      case 4: chunks(I1{}, I0{}, I0{}); break;
+      case 5: chunks(I1{}, I0{}, I1{}); break;
+      case 6: chunks(I1{}, I1{}, I0{}); break;
+      default: chunks(I1{}, I1{}, I1{}); break;
+    }
+  } else
   for (int chunk = c_begin; chunk < c_end; ++chunk) {
     // The chunk's halo (and the first weight rows) must have landed.
     __builtin_amdgcn_s_waitcnt(0);
@@ -1998,8 +2077,8 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
 #undef CTMR_LDS16_ROW
   }
 
-  store_brick(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, (bz * p.ty + by) * p.tx + bx,
-              reinterpret_cast<double (*)[64][2]>(halo));  // the reduction buffer reuses the halo
+  store_brick<UP>(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, ((bz * p.ty + by) * p.tx + bx) * (UP ? 8 : 1) + phase,
+                  reinterpret_cast<double (*)[64][2]>(halo), phase);  // the reduction buffer reuses the halo
 }
 
 // ---------------------------------------------------------------------------
@@ -2636,16 +2715,18 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     return CTMR_OK;
   }
   // LDS-staged bf16 GEMM: stride-1 bf16 convs (plain or trilinear-2x, both
-  // sampled by the pack) with 64-wide column tiles whose 4x8x8 bricks are at
-  // least 3/4 full; the halo fill's 32-bit offsets span 6 packed planes.
+  // sampled by the pack, or nearest-2x as 8 parity GEMMs over the packed
+  // source) with 64-wide column tiles whose 4x8x8 bricks (of the source grid
+  // for nearest-2x) are at least 3/4 full; the halo fill's 32-bit offsets span
+  // 6 packed planes.
   g.lds16 = false;
   g.small_out = false;
-  if (g.layout == WL_TAPS && d->dtype == CTMR_BF16 && d->ksize == 3 && d->stride == 1 && plain_weights &&
-      d->cout % 64 == 0 && !(d->flags & CTMR_F_STREAM)) {
+  if (g.layout == WL_TAPS && d->dtype == CTMR_BF16 && d->ksize == 3 && d->stride == 1 && d->cout % 64 == 0 &&
+      !(d->flags & CTMR_F_STREAM)) {
     const int tz = (int)ceil_div(g.gd, kBD), ty = (int)ceil_div(g.gh, kBH), tx = (int)ceil_div(g.gw, kBW);
     const int64_t slots = (int64_t)tz * ty * tx * kBD * kBH * kBW;
     const int64_t planes = (int64_t)kHD * g.P * g.cp * 2;
-    const int64_t w_bytes = (int64_t)27 * g.kblocks * g.np * 64;
+    const int64_t w_bytes = (int64_t)g.taps * g.phases * g.kblocks * g.np * 64;
     if (4 * S >= 3 * slots && planes < (1ll << 31) && w_bytes < (1ll << 31)) {
       g.lds16 = true;
       g.tz = tz; g.ty = ty; g.tx = tx;
@@ -2686,7 +2767,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     g.split = 1;
   } else if (g.lds16) {  // chunk-range split, as the fp32 LDS GEMM
     if (d->split > g.kblocks) return fail(CTMR_E_INVALID, "split must not exceed the 32-channel chunk count");
-    const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n;
+    const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases;
     g.split = d->split > 0 ? d->split
                            : (base < 512 ? (int)std::min<int64_t>(ceil_div(512, base), g.kblocks) : 1);
   } else if (d->split > 0) {
@@ -2766,7 +2847,7 @@ static int gn_stats_tiles(const ctmr_conv_desc* d, const Geometry& g, int groups
   }
   const int width = g.lds ? 64 : g.wn * g.nsub * 16;
   if (cpg > width || width % cpg != 0) return 0;
-  return (g.lds || g.lds16) ? g.tz * g.ty * g.tx : g.m_tiles * g.phases;
+  return (g.lds || g.lds16) ? g.tz * g.ty * g.tx * g.phases : g.m_tiles * g.phases;
 }
 
 // The K-split reduction, with group-norm partials when `stats` is set.
@@ -3241,7 +3322,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.res = residual;
     a.rows_per_batch = g.rows_per_batch;
     a.x_bytes = (int64_t)desc->n * g.rows_per_batch * g.cp * 2;
-    a.w_bytes = (int64_t)27 * g.kblocks * g.np * 64;
+    a.w_bytes = (int64_t)g.taps * g.phases * g.kblocks * g.np * 64;
     a.plane = (int64_t)desc->n * s_out * desc->cout;
     a.d = g.gd; a.h = g.gh; a.w = g.gw;
     a.P = g.P; a.Q = g.Q;
@@ -3259,8 +3340,11 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     float* part = (float*)((char*)workspace + g.pack_bytes);
     a.y = g.split > 1 ? part : y;
     if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
-    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.split;
-    hipLaunchKernelGGL(conv_lds_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
+    if (g.phases == 8)
+      hipLaunchKernelGGL(conv_lds_bf16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(conv_lds_bf16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, a);
     if ((rc = check_launch("conv_lds_bf16"))) return rc;
     if (g.split > 1) {
       launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);

@@ -243,6 +243,8 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     assert tiles(2, 1, 16, 16, 16, 256, 256, flags=L.F_STREAM, split=1) == 16**3 // 128
     # nearest-2x upsample: one tile per (parity phase, source M tile)
     assert tiles(3, 1, 4, 4, 4, 32, 48, mode=L.MODE_NEAREST2X, split=1) == 8
+    # bf16 nearest-2x on the LDS GEMM: one per (4x8x8 source brick, parity)
+    assert tiles(32, 2, 32, 32, 16, 128, 128, mode=L.MODE_NEAREST2X, dtype=L.DT_BF16, split=1) == (32 // 4) * (32 // 8) * (16 // 8) * 8
     assert tiles(2, 1, 4, 4, 4, 32, 48, mode=L.MODE_NEAREST2X, split=1) == 0  # 24-wide groups vs 64 columns
     d = L.conv_desc(1, 8, 8, 8, 64, 1)
     fake = 0x1000  # never dereferenced: the checks fail first
@@ -267,6 +269,9 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     ((1, 64, 64, 64, 128), 256, {"ksize": 1}, "pointwise"),               # config 2c
     ((1, 64, 64, 64, 64), 64, {"flags": 16}, "stream_direct"),            # CTMR_F_STREAM
     ((1, 64, 64, 64, 64), 64, {"dtype": 1}, "lds_bf16"),
+    ((2, 32, 32, 16, 128), 128, {"dtype": 1, "mode": 1}, "lds_bf16"),     # bf16 nearest-2x: 8 parity GEMMs
+    ((2, 32, 32, 16, 128), 128, {"mode": 1}, "stream"),                   # fp32 nearest-2x
+    ((2, 32, 32, 16, 128), 128, {"dtype": 1, "mode": 1, "flags": 16}, "stream"),  # CTMR_F_STREAM
     ((2, 4, 8, 8, 512), 512, {}, "split_waves"),                          # deep UNet level
     ((1, 20, 64, 64, 64), 1, {"flags": 3}, "small_cout"),                 # decoder output conv (GN + SiLU)
     ((2, 64, 64, 32, 64), 4, {"flags": 3}, "small_cout"),                 # UNet output conv

@@ -188,11 +188,16 @@ def test_lds_staged_and_streaming_gemms_match_float64(ctmr, dev, shape, cout, fu
     ((2, 8, 8, 8, 48), 64, {"split": 1}),                       # 48 channels packed to 64 (zero chunk half)
     ((1, 4, 8, 8, 32), 64, {"trilinear": True, "split": 1}),    # trilinear-2x sampled by the pack
     ((2, 8, 16, 16, 128), 128, {"fused": True, "split": 1}),    # GN affine + SiLU, batch bias, residual
+    ((2, 4, 8, 8, 64), 64, {"upsample": True, "split": 1}),     # nearest-2x: 8 parity GEMMs per brick
+    ((1, 7, 16, 15, 64), 128, {"upsample": True, "split": 1}),  # nearest-2x, ragged source bricks
+    ((1, 4, 8, 8, 128), 64, {"upsample": True, "split": 4}),    # nearest-2x, 4-way chunk split
+    ((2, 4, 8, 16, 96), 64, {"upsample": True, "fused": True, "split": 1}),  # nearest-2x, GN + SiLU, residual
 ])
 def test_bf16_lds_gemm_matches_streaming_bf16(ctmr, dev, shape, cout, kw):
-    """The LDS-staged bf16 GEMM (direct-to-LDS halo and weight fills) against the register-streaming bf16
-    GEMM: same bf16 operands from the same pack, fp32 accumulation in two fixed orders, so they agree to
-    fp32 rounding (1e-5); both within the bf16 bar of float64; repeat runs bit-identical."""
+    """The LDS-staged bf16 GEMM (direct-to-LDS halo and weight fills; for nearest-2x the eight parity
+    GEMMs over the packed source) against the register-streaming bf16 GEMM: same bf16 operands from the
+    same pack, fp32 accumulation in two fixed orders, so they agree to fp32 rounding (1e-5); both within
+    the bf16 bar of float64; repeat runs bit-identical."""
     print(f"bf16 lds {shape}->{cout} {kw}", flush=True)
     kw = dict(kw)
     fused = kw.pop("fused", False)
@@ -202,7 +207,8 @@ def test_bf16_lds_gemm_matches_streaming_bf16(ctmr, dev, shape, cout, kw):
     w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
     bias = rng.standard_normal((n, cout)).astype(np.float32)
     f = ctmr.fast_fp32
-    packed = f.pack_weight(_t(w, dev), dtype="bf16")
+    up = kw.get("upsample", False)
+    packed = (f.pack_upsample_weight if up else f.pack_weight)(_t(w, dev), dtype="bf16")
     xin = rm.upsample_trilinear(x) if kw.get("trilinear") else x
     affine = res = None
     if fused:
@@ -210,8 +216,16 @@ def test_bf16_lds_gemm_matches_streaming_bf16(ctmr, dev, shape, cout, kw):
         gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
         affine = f.group_norm_affine(_t(x, dev), _t(gw, dev), _t(gb, dev), groups=8, eps=1e-6)
         xin = rm.group_norm(x, gw, gb, 8, 1e-6, apply_silu=True)
-        res = rng.standard_normal((*shape[:-1], cout)).astype(np.float32)
+    if up:
+        xin = rm.upsample_nearest(xin)
+    if fused:
+        res = rng.standard_normal((*xin.shape[:-1], cout)).astype(np.float32)
     expected = rm.conv3d(xin, w) + bias[:, None, None, None, :] + (0 if res is None else res)
+    L = ctmr._lib
+    mode = L.MODE_NEAREST2X if up else (L.MODE_TRILINEAR2X if kw.get("trilinear") else L.MODE_PLAIN)
+    flags = (L.F_AFFINE | L.F_SILU | L.F_RESIDUAL) if fused else 0
+    desc = ctmr.ops.make_desc(shape, cout, 3, 1, mode, flags, L.DT_BF16, kw.get("split", 0))
+    assert L.conv_kernel(desc) == "lds_bf16"
     outs = []
     for stream_gemm in (False, True):
         run = lambda: f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), cout=cout, affine=affine,

@@ -46,6 +46,9 @@ CASES = [
     ("stride 2", (1, 8, 16, 16, 32), 64, 16, {"stride": 2, "split": 1}),
     ("bf16", (2, 8, 16, 16, 64), 64, 32, {"bf16": True, "split": 1}),
     ("bf16 split", (2, 8, 16, 16, 64), 64, 32, {"bf16": True}),
+    ("bf16 nearest-2x LDS parities", (2, 4, 8, 8, 64), 64, 32, {"bf16": True, "upsample": True, "split": 1}),
+    ("bf16 nearest-2x LDS fused ragged", (1, 7, 16, 15, 64), 128, 16,
+     {"bf16": True, "upsample": True, "split": 1, "fused": True}),
 ]
 
 
