@@ -1145,6 +1145,12 @@ constexpr int kHaloVox = kHD * kHH * kHW;                 // 600
 constexpr int kLdsRow = 80;
 constexpr int kStageIters = (kHaloVox * 4 + 255) / 256;  // 16-byte pieces per thread
 
+// Cache-policy operand of the output stores of the brick GEMMs and the
+// persistent 1x1 GEMM: SC1 (device scope).  Same values; measured on MI355X
+// against the default policy, A/B in one run: config-2c 1x1 0.165 -> 0.160 ms,
+// config-1 block 26.57 -> 26.40 ms, decoder window -0.25 %, UNet step unchanged.
+constexpr int kOutStorePolicy = 2;
+
 // Epilogue of the brick GEMMs (conv_lds_kernel, conv_lds_bf16_kernel) from
 // transposed accumulators: lane l of block (ms, ns) holds voxel (z0 + wave,
 // y0 + ms + 4*((l/8)%2), x0 + l%8) of the 4x8x8 brick and output columns
@@ -1193,11 +1199,22 @@ __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int 
 #pragma unroll
       for (int ns = 0; ns < 4; ++ns) acc[ms][ns] += rq[ms][ns];
   }
+  {
+    // Buffer stores relative to the brick's first output plane (its rows lie
+    // within S * 4 planes of it, so the offsets stay 32-bit), with the device-
+    // scope cache policy (kOutStorePolicy).
+    const int64_t origin = ((int64_t)b * (S * p.d) + S * min(z0, p.d - 1)) * (S * p.h) * (int64_t)(S * p.w) * p.cout;
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+        out + origin, (short)0, (int)min(max((int64_t)p.plane - origin, (int64_t)0) * 4, (int64_t)0x7fffffff),
+        0x00020000);
 #pragma unroll
-  for (int ms = 0; ms < 4; ++ms)
+    for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-    for (int ns = 0; ns < 4; ++ns)
-      if (row_ok[ms]) *reinterpret_cast<f4*>(out + base[ms] + ns * 16) = acc[ms][ns];
+      for (int ns = 0; ns < 4; ++ns)
+        if (row_ok[ms])
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[ms][ns]), ors,
+                                                 (int)((base[ms] - origin + ns * 16) * 4), 0, kOutStorePolicy);
+  }
   if (p.stats) {  // a kernel argument: every thread reaches the barriers
     __syncthreads();
     const bool col_ok[4] = {true, true, true, true};
@@ -2313,7 +2330,7 @@ __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[ms][ns]), orsrc,
-                                               q_off[ns] + ms * 16 * p.cout * 4, 0, 0);
+                                               q_off[ns] + ms * 16 * p.cout * 4, 0, kOutStorePolicy);
     if (p.stats) {  // a kernel argument: every thread reaches the barriers
       bool row_ok[4], col_ok[NSUB];
 #pragma unroll
@@ -3260,7 +3277,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.y = y;
     a.x_bytes = (int64_t)desc->n * desc->d * desc->h * desc->w * desc->cin * 4;
     a.w_bytes = (int64_t)g.kblocks * g.np * 64;
-    a.plane = 0;
+    a.plane = (int64_t)desc->n * s_out * desc->cout;  // the output (store_brick's store range)
     a.n = desc->n; a.d = desc->d; a.h = desc->h; a.w = desc->w;
     a.cin = desc->cin; a.cout = desc->cout; a.np = g.np; a.kb = g.kblocks;
     a.tz = g.tz; a.ty = g.ty; a.tx = g.tx;
