@@ -817,7 +817,18 @@ __device__ __forceinline__ void load_bias(const ConvArgs& p, int b, int n0, int 
 // load would wait for the stores before it (the compiler cannot prove the
 // output and its inputs apart).  Rows past the grid are clamped for the loads
 // and masked for the stores.
-template <int NSUB, int WM, int WN, typename OutVoxel>
+// Cache-policy operand of the GEMMs' output stores: SC1 (device scope).  Same
+// values; measured on MI355X against the default policy, A/B in one run: the
+// brick GEMMs and the persistent 1x1 GEMM -- config-2c 1x1 0.165 -> 0.160 ms,
+// config-1 block 26.57 -> 26.40 ms, decoder window -0.25 %; the streaming
+// GEMM's contiguous-row epilogue -- config 2a 0.860 -> 0.844 ms, UNet step
+// -0.2 %.
+constexpr int kOutStorePolicy = 2;
+
+// IDENT: GEMM row v of batch item b is output voxel b * s_out + v (every route
+// but the nearest-2x parity phases), so a wave's 64 rows are contiguous and
+// its stores go through one buffer descriptor with the cache policy above.
+template <int NSUB, int WM, int WN, bool IDENT, typename OutVoxel>
 __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB], const f4 (&bq)[NSUB], int b,
                                            int m0, int n0, int S, int split_id, int wave, int lane, int col0,
                                            int tile_id, OutVoxel out_voxel) {
@@ -861,6 +872,14 @@ __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB]
 #pragma unroll
       for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += rq[ms][ns];
   }
+  int64_t vbase = 0;
+  __amdgpu_buffer_rsrc_t ors;
+  if constexpr (IDENT) {
+    vbase = out_voxel(min(m0, S - 1));  // the wave's first row; the others follow it
+    ors = __builtin_amdgcn_make_buffer_rsrc(out + vbase * p.cout, (short)0,
+                                            (int)min(max((int64_t)p.plane - vbase * p.cout, (int64_t)0) * 4,
+                                                     (int64_t)0x7fffffff), 0x00020000);
+  }
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
@@ -868,7 +887,13 @@ __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB]
       const int c0 = n0 + ns * 16 + 4 * lgrp;
       const f4 val = acc[ms][ns];
       if (wide) {
-        if (row_ok[ms] && col_ok[ns]) *reinterpret_cast<f4*>(out + vox[ms] * p.cout + c0) = val;
+        if constexpr (IDENT) {
+          if (row_ok[ms] && col_ok[ns])
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, val), ors,
+                                                   (int)(((vox[ms] - vbase) * p.cout + c0) * 4), 0, kOutStorePolicy);
+        } else {
+          if (row_ok[ms] && col_ok[ns]) *reinterpret_cast<f4*>(out + vox[ms] * p.cout + c0) = val;
+        }
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -1111,7 +1136,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
   f4 bq[NSUB];
   load_bias<NSUB>(p, b, n0, lane, bq);
-  store_tile<NSUB, WM, WN>(p, acc, bq, b, m0, n0, S, split_id, wave, lane, n_tile * (WN * NSUB * 16), tile_id,
+  store_tile<NSUB, WM, WN, !UP>(p, acc, bq, b, m0, n0, S, split_id, wave, lane, n_tile * (WN * NSUB * 16), tile_id,
                            [&](int v) -> int64_t {
                              int o = v;
                              if (UP) {
@@ -1145,11 +1170,6 @@ constexpr int kHaloVox = kHD * kHH * kHW;                 // 600
 constexpr int kLdsRow = 80;
 constexpr int kStageIters = (kHaloVox * 4 + 255) / 256;  // 16-byte pieces per thread
 
-// Cache-policy operand of the output stores of the brick GEMMs and the
-// persistent 1x1 GEMM: SC1 (device scope).  Same values; measured on MI355X
-// against the default policy, A/B in one run: config-2c 1x1 0.165 -> 0.160 ms,
-// config-1 block 26.57 -> 26.40 ms, decoder window -0.25 %, UNet step unchanged.
-constexpr int kOutStorePolicy = 2;
 
 // Epilogue of the brick GEMMs (conv_lds_kernel, conv_lds_bf16_kernel) from
 // transposed accumulators: lane l of block (ms, ns) holds voxel (z0 + wave,
