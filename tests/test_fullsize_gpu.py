@@ -280,3 +280,34 @@ def test_config4_256_decode_blend_and_int16(ctmr, dev):
     np.testing.assert_array_equal(img, np.trunc(np.maximum(y * np.float32(1000.0), 0)).astype(np.int16))
     ct = m.output_intensities(y, configuration="ct")
     assert ct.dtype == np.int16 and ct.min() >= -1000 and ct.max() <= 1000
+
+
+def test_outputs_beyond_2gib(ctmr, dev):
+    """A conv whose output exceeds 2 GiB (1x80x256x256x64 -> 128 channels: 2.68 GB) on the fp32 LDS-staged
+    GEMM, the fp32 streaming GEMM and the bf16 LDS-staged GEMM. Their epilogues store through buffer
+    descriptors based at each brick's first output plane (LDS GEMMs) or each wave's first output row
+    (streaming GEMM), so byte offsets stay within 32 bits; checked on every corner, edge and face of the
+    volume (its last planes, 2.6 GB past the start, included) and interior voxels against float64."""
+    f, L = ctmr.fast_fp32, ctmr._lib
+    rng = np.random.default_rng(5)
+    shape, cout = (1, 80, 256, 256, 64), 128
+    x = rng.standard_normal(shape, dtype=np.float32)
+    w = (rng.standard_normal((cout, shape[-1], 3, 3, 3)) / np.sqrt(27 * shape[-1])).astype(np.float32)
+    b = (0.01 * rng.standard_normal(cout)).astype(np.float32)
+    assert np.prod(shape[:-1]) * cout * 4 > 2**31
+    pts = rm.boundary_points(1, shape[1:4], 1024, seed=5)
+    expected = rm.conv3d_points(x, w, b, pts)
+    xg, wg, bg = _g(x, dev), _g(w, dev), _g(b, dev)
+    idx = tuple(torch.from_numpy(pts[:, a]).to(dev) for a in range(4))
+    for name, dtype, stream, route, bound in (("fp32 LDS GEMM", "fp32", False, "lds", FP32_REL),
+                                              ("fp32 streaming GEMM", "fp32", True, "stream", FP32_REL),
+                                              ("bf16 LDS GEMM", "bf16", False, "lds_bf16", 2e-2)):
+        desc = ctmr.ops.make_desc(shape, cout, 3, 1, L.MODE_PLAIN, L.F_STREAM if stream else 0,
+                                  L.DT_BF16 if dtype == "bf16" else L.DT_F32, 0)
+        assert L.conv_kernel(desc) in (route, route + "_direct"), (name, L.conv_kernel(desc))
+        print(f"case {name}: route {L.conv_kernel(desc)}", flush=True)
+        y = f.implicit_gemm_conv3d(xg, f.pack_weight(wg, dtype=dtype), bg, cout=cout, stream_gemm=stream)
+        got = _h(y[idx])
+        del y
+        torch.cuda.empty_cache()
+        _check(got, expected, bound, f"{name}, output beyond 2 GiB, points vs float64")
