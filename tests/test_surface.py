@@ -128,3 +128,20 @@ def test_channel_cat_validation(ctmr):
         f.ChannelCat(a.numpy(), a)
     out = f.concat_channels(torch.zeros(1, 2, 2, 2, 8), torch.ones(1, 2, 2, 2, 8))
     assert isinstance(out, torch.Tensor) and tuple(out.shape) == (1, 2, 2, 2, 16)
+
+
+@pytest.mark.parametrize(("shape", "keeps"), [
+    ((64, 64, 3, 3, 3), False),   # UNet / VAE 3x3x3 convs: bf16 under precision("bf16")
+    ((128, 256, 3, 3, 3), False),
+    ((64, 4, 3, 3, 3), True),     # 4-channel input conv: fp32 LDS-staged im2col GEMM
+    ((32, 8, 3, 3, 3), True),     # 8-channel condition-encoder conv
+    ((64, 16, 3, 3, 3), False),   # 16 input channels: bf16
+    ((4, 64, 3, 3, 3), True),     # UNet output conv (cout 4): fp32 direct conv
+    ((1, 64, 3, 3, 3), True),     # VAE output conv
+    ((5, 64, 3, 3, 3), False),
+    ((256, 128, 1, 1, 1), True),  # 1x1 skip projections
+])
+def test_bf16_precision_keeps_small_convs_fp32(ctmr, shape, keeps):
+    """Which convs keep fp32 operands under ``precision("bf16")`` (a function of the weight shape only):
+    1x1 convs, at most 8 input channels, at most 4 output channels."""
+    assert ctmr.fast_fp32._keeps_fp32(torch.empty(shape)) is keeps
