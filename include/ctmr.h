@@ -160,10 +160,11 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  * cout % 64 == 0, no resampling, CTMR_F_STREAM not set), stages 16-channel chunks of the input
  * with their halo (affine + SiLU and zero padding applied while staging) and
  * visits chunks ascending (outer), taps ascending (inner).  The LDS-staged
- * bf16 GEMM, chosen for stride-1 bf16 convs (plain or trilinear-2x) with
- * cout % 64 == 0 and bricks at least 3/4 full (CTMR_F_STREAM not set), reads the
- * bf16 packed copy and visits 32-channel chunks ascending (outer), taps
- * ascending (inner).  Deep small grids split by the library's policy (split of
+ * bf16 GEMM, chosen for stride-1 bf16 convs (plain, trilinear-2x, or
+ * nearest-2x as the eight parity GEMMs of the fold) with cout % 64 == 0 and
+ * 4x8x8 bricks at least half full (CTMR_F_STREAM not set), reads the bf16
+ * packed copy and visits 32-channel chunks ascending (outer), taps ascending
+ * (inner).  Deep small grids split by the library's policy (split of
  * at least 4 for the 128-wide tiles) run 64 x 64 tiles whose four waves sum
  * four contiguous quarters of each split range, added in ascending order
  * before the partial plane is stored; ctmr_conv3d_split reports the planes.

@@ -270,6 +270,8 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     ((1, 64, 64, 64, 64), 64, {"flags": 16}, "stream_direct"),            # CTMR_F_STREAM
     ((1, 64, 64, 64, 64), 64, {"dtype": 1}, "lds_bf16"),
     ((2, 32, 32, 16, 128), 128, {"dtype": 1, "mode": 1}, "lds_bf16"),     # bf16 nearest-2x: 8 parity GEMMs
+    ((2, 8, 8, 4, 512), 512, {"dtype": 1}, "lds_bf16"),                   # bf16, bricks half full (w = 4)
+    ((2, 8, 8, 3, 512), 512, {"dtype": 1}, "split_waves"),                # bf16, bricks under half full
     ((2, 32, 32, 16, 128), 128, {"mode": 1}, "stream"),                   # fp32 nearest-2x
     ((2, 32, 32, 16, 128), 128, {"dtype": 1, "mode": 1, "flags": 16}, "stream"),  # CTMR_F_STREAM
     ((2, 4, 8, 8, 512), 512, {}, "split_waves"),                          # deep UNet level

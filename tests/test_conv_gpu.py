@@ -192,6 +192,8 @@ def test_lds_staged_and_streaming_gemms_match_float64(ctmr, dev, shape, cout, fu
     ((1, 7, 16, 15, 64), 128, {"upsample": True, "split": 1}),  # nearest-2x, ragged source bricks
     ((1, 4, 8, 8, 128), 64, {"upsample": True, "split": 4}),    # nearest-2x, 4-way chunk split
     ((2, 4, 8, 16, 96), 64, {"upsample": True, "fused": True, "split": 1}),  # nearest-2x, GN + SiLU, residual
+    ((2, 8, 8, 4, 256), 256, {}),                                # half-full bricks (w = 4), policy chunk split
+    ((2, 8, 8, 4, 128), 128, {"upsample": True}),               # nearest-2x from half-full source bricks
 ])
 def test_bf16_lds_gemm_matches_streaming_bf16(ctmr, dev, shape, cout, kw):
     """The LDS-staged bf16 GEMM (direct-to-LDS halo and weight fills; for nearest-2x the eight parity
