@@ -2643,6 +2643,12 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   const int64_t s_out = (int64_t)g.od * g.oh * g.ow;
   if (S > (1ll << 30) || s_out * d->cout > (1ll << 40))
     return fail(CTMR_E_UNSUPPORTED, "volume too large for 32-bit voxel indexing");
+  // The brick GEMMs' epilogues (store_brick) store at 32-bit byte offsets from
+  // the brick's first output plane: the kBD output planes of a brick (2 kBD
+  // for the nearest-2x phases) must span under 2 GiB, or the route is not
+  // taken (outputs past that span would be dropped by the buffer range).
+  const bool brick_out_fits =
+      (int64_t)kBD * (g.phases == 8 ? 2 : 1) * g.oh * g.ow * d->cout * 4 < (1ll << 31);
   // LDS-staged im2col GEMM: the im2col formulation of stride-1 fp32 convs with
   // 4 or 8 input channels, its rows read from a halo brick in LDS instead of
   // HBM (same K blocks and products: bit-identical outputs); 64-column tiles
@@ -2658,7 +2664,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     const int tz = (int)ceil_div(d->d, kBD), ty = (int)ceil_div(d->h, kBH), tx = (int)ceil_div(d->w, kBW);
     const int64_t slots = (int64_t)tz * ty * tx * kBD * kBH * kBW;
     const int64_t planes = (int64_t)kHD * d->h * d->w * d->cin * 4;
-    if (4 * S >= 3 * slots && planes < (1ll << 31)) {
+    if (4 * S >= 3 * slots && planes < (1ll << 31) && brick_out_fits) {
       g.lds_small = true;
       g.pack = false;
       g.tz = tz; g.ty = ty; g.tx = tx;
@@ -2728,7 +2734,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     const int64_t base = (int64_t)g.tz * g.ty * g.tx * (d->cout / 64) * d->n;
     const int64_t policy_split = lds_policy_split(base, d->cin / 16);
     const int64_t split = d->split > 0 ? d->split : policy_split;
-    if (4 * S >= 3 * slots && planes < (1ll << 31) && (d->cin / 16) / split >= 4) g.lds = true;
+    if (4 * S >= 3 * slots && planes < (1ll << 31) && brick_out_fits && (d->cin / 16) / split >= 4) g.lds = true;
   }
   if (g.lds) {
     g.pack = false;
@@ -2766,7 +2772,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     const int64_t slots = (int64_t)tz * ty * tx * kBD * kBH * kBW;
     const int64_t planes = (int64_t)kHD * g.P * g.cp * 2;
     const int64_t w_bytes = (int64_t)g.taps * g.phases * g.kblocks * g.np * 64;
-    if (2 * S >= slots && planes < (1ll << 31) && w_bytes < (1ll << 31)) {
+    if (2 * S >= slots && planes < (1ll << 31) && w_bytes < (1ll << 31) && brick_out_fits) {
       g.lds16 = true;
       g.tz = tz; g.ty = ty; g.tx = tx;
     }

@@ -283,6 +283,16 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     ((1, 256, 256, 256, 8), 8, {}, "lds_small"),                          # condition encoder 8 -> 8
     ((1, 256, 256, 256, 8), 32, {"stride": 2}, "stream"),                 # stride 2: im2col rows in HBM
     ((2, 64, 64, 32, 4), 64, {"flags": 16}, "stream"),                    # CTMR_F_STREAM: the im2col GEMM
+    # brick epilogues store at 32-bit offsets from the brick's first output plane: the brick's output
+    # planes (4, or 8 for nearest-2x) must span under 2 GiB; at 2 GiB the route moves off the brick GEMMs
+    ((1, 8, 256, 256, 64), 1024, {}, "lds"),                              # 4 x 256 x 256 x 1024 x 4 B = 1 GiB
+    ((1, 8, 256, 256, 64), 2048, {}, "stream_direct"),                    # 2 GiB
+    ((1, 8, 256, 256, 64), 1024, {"dtype": 1}, "lds_bf16"),
+    ((1, 8, 256, 256, 64), 2048, {"dtype": 1}, "stream"),
+    ((1, 8, 128, 128, 64), 512, {"dtype": 1, "mode": 1}, "lds_bf16"),     # 8 x 256 x 256 x 512 x 4 B = 1 GiB
+    ((1, 8, 128, 128, 64), 1024, {"dtype": 1, "mode": 1}, "stream"),      # 2 GiB
+    ((1, 8, 256, 256, 4), 1024, {}, "lds_small"),
+    ((1, 8, 256, 256, 4), 2048, {}, "pointwise"),                         # the im2col GEMM
 ])
 def test_conv_kernel_route(ctmr, shape, cout, kw, expected):
     """``ctmr_conv3d_kernel`` names the formulation the library picks (a function of the desc only)."""
