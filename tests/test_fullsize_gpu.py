@@ -311,3 +311,41 @@ def test_outputs_beyond_2gib(ctmr, dev):
         del y
         torch.cuda.empty_cache()
         _check(got, expected, bound, f"{name}, output beyond 2 GiB, points vs float64")
+
+
+@pytest.mark.parametrize(("name", "shape", "cout", "mode", "dtype", "route", "bound"), [
+    ("fp32 LDS GEMM, 4 planes of 256x256x1984", (1, 8, 256, 256, 64), 1984, "plain", "fp32", "lds", FP32_REL),
+    ("bf16 nearest-2x LDS GEMM, 8 planes of 256x256x960", (1, 8, 128, 128, 64), 960, "nearest", "bf16", "lds_bf16",
+     2e-2),
+])
+def test_brick_output_span_near_2gib(ctmr, dev, name, shape, cout, mode, dtype, route, bound):
+    """Brick epilogues store at 32-bit byte offsets from the brick's first output plane, and the library
+    keeps a brick route only while a brick's output planes (4; 8 for the nearest-2x phases) span under
+    2 GiB. Here that span is 1.94-1.88 GiB (outputs 4.2 / 4.0 GB): the far corners of each brick, the
+    last channel of the volume's last voxel among them, against float64."""
+    f, L = ctmr.fast_fp32, ctmr._lib
+    rng = np.random.default_rng(11)
+    n, d, h, w, c = shape
+    up = mode == "nearest"
+    s = 2 if up else 1
+    span = 4 * s * (s * h) * (s * w) * cout * 4
+    assert 0.9 * 2**31 < span < 2**31, span
+    x = rng.standard_normal(shape, dtype=np.float32)
+    wt = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    b = (0.01 * rng.standard_normal(cout)).astype(np.float32)
+    out_sp = (s * d, s * h, s * w)
+    pts = rm.boundary_points(1, out_sp, 512, seed=11)
+    last = np.array([[0, s * d - 1 - dz, s * h - 1, s * w - 1] for dz in range(4 * s)])  # a brick's far corners
+    pts = np.concatenate([pts, last])
+    expected = rm.conv3d_points(x, wt, b, pts, upsample=up)
+    m = L.MODE_NEAREST2X if up else L.MODE_PLAIN
+    desc = ctmr.ops.make_desc(shape, cout, 3, 1, m, 0, L.DT_BF16 if dtype == "bf16" else L.DT_F32, 0)
+    assert L.conv_kernel(desc) == route, (name, L.conv_kernel(desc))
+    print(f"case {name}: route {route}, brick span {span / 2**30:.3f} GiB", flush=True)
+    packed = (f.pack_upsample_weight if up else f.pack_weight)(_g(wt, dev), dtype=dtype)
+    y = f.implicit_gemm_conv3d(_g(x, dev), packed, _g(b, dev), cout=cout, upsample=up)
+    idx = tuple(torch.from_numpy(pts[:, a]).to(dev) for a in range(4))
+    got = _h(y[idx])
+    del y
+    torch.cuda.empty_cache()
+    _check(got, expected, bound, f"{name}, points vs float64")
