@@ -24,10 +24,10 @@
  *   ctmr_gn_apply             <- fast_fp32.group_norm_ncdhw (fast_fp32.py:102-118)
  *   ctmr_conv3d (ksize 1)     <- fast_fp32.pointwise_conv_ncdhw (fast_fp32.py:121-130)
  *   ctmr_resample             <- medmlx_core.ops.avg_pool3d_ncdhw / upsample_nearest_ncdhw
- *   ctmr_gn_avgpool           <- the down branch of fast_fp32.residual_block_ncdhw
- *                                (fast_fp32.py:250-255: group norm + SiLU, then pooling)
  *                                (fast_fp32.py:48-59) and source_vae.upsample_trilinear_ncdhw
  *                                (fast_fp32.py:66-68; formula at _nax_conv.py:115-142)
+ *   ctmr_gn_avgpool           <- the down branch of fast_fp32.residual_block_ncdhw
+ *                                (fast_fp32.py:250-255: group norm + SiLU, then pooling)
  *   ctmr_flash_attention      <- _flash_attention.flash_attention (_flash_attention.py:320-360),
  *                                selected by flash_eligible (_flash_attention.py:276-289) from
  *                                fast_fp32.self_attention_tokens (fast_fp32.py:352-392)
@@ -208,9 +208,16 @@ int ctmr_conv3d_cat(const ctmr_conv_desc* desc, const float* x1, const float* x2
  * ctmr_conv3d.  A convolution whose ctmr_conv3d_workspace_bytes exceeds the
  * limit returns CTMR_E_WORKSPACE (256 MiB covers every conv of the MAISI UNet
  * and ControlNet steps at a 64x64x32 latent, batch 2; not the decoder's
- * full-resolution levels).  Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU (other streams, other threads) race.  Call
- * with the stream's device current.
+ * full-resolution levels).  Every call on one GPU shares that GPU's array, so
+ * the library orders them: each call's stream first waits for a per-device
+ * event (created once, with the array's address lookup, on the first call on
+ * that device) that the previous call recorded after its kernels, so calls
+ * from any streams and host threads run on the GPU one after another, in the
+ * order the host issued them.  Calls enqueued under stream capture are not
+ * chained (the graph orders its own nodes): replays of such graphs that
+ * overlap with each other or with other calls on the same GPU race on the
+ * array, and ordering them is the caller's job.  The stream's device must be
+ * current (CTMR_E_INVALID otherwise).
  */
 #define CTMR_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
 int ctmr_conv3d_noalloc(const ctmr_conv_desc* desc, const float* x, const void* packed, const float* bias,
@@ -312,7 +319,7 @@ int ctmr_resample(int32_t op, int32_t n, int32_t d, int32_t h, int32_t w, int32_
  * 32 (the MAISI UNet's num_head_channels).  Any lq, lk >= 1.  query_tiles
  * picks 16 (1) or 32 (2) queries per wave, 0 = the library's policy; results
  * are bit-identical either way (keys are visited in the same fixed order:
- * ascending 64-key blocks, or -- for grids of under two waves per SIMD, decided
+ * ascending 32-key blocks, or -- for grids of under two waves per SIMD, decided
  * from n, lq, lk and heads only -- two such runs over the key halves, combined
  * first half first). */
 typedef struct ctmr_attn_desc {

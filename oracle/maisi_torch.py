@@ -12,10 +12,12 @@ HIP composition it checks:
   CT from mask     from_mask.py:177-338 (sampling loop), condition.py:20-43 (label bits),
                    decode.py:248-259 (HU)
 Pinned by the reference goldens in tests/golden (tests/test_oracle_networks.py).  The ControlNet
-has no recorded outputs in the reference fixtures (its boundary arrays live outside the repository);
-its shared down path is pinned through the UNet goldens and an identity invariant, its conditioning
-encoder and zero convolutions are plain conv/SiLU/1x1 compositions of pinned primitives — the
-ControlNet as a whole is "parity unpinned" against a recording.
+has no recorded outputs in the reference fixtures (its boundary arrays live outside the repository),
+so it is pinned without a recording: its shared down path through the UNet goldens and an identity
+invariant (identity zero convs and a zero condition give the UNet's skips), its conditioning encoder
+against a brute-force loop, its first residual against conv_in plus the embedding, and the
+conditioning scale against a closed form, each with planted mistakes that must fail
+(tests/test_oracle_networks.py).
 """
 
 from __future__ import annotations

@@ -2,13 +2,20 @@
 
 Its workspace is the library's own per-GPU scratch array; the output must equal ``ctmr_conv3d``'s
 (caller workspace, same kernels) bit for bit, on consecutive calls whose second input is smaller
-(the scratch keeps the previous call's contents), and a convolution whose workspace exceeds the
-scratch limit must be refused before anything is launched.
+(the scratch keeps the previous call's contents), on calls alternating between two streams (the
+library chains them through a per-device event), and when recorded in a HIP graph (with and
+without an eager call first); a convolution whose workspace exceeds the scratch limit must be
+refused before anything is launched.
 """
 
 from __future__ import annotations
 
 import ctypes
+import os
+import subprocess
+import sys
+import textwrap
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -84,3 +91,83 @@ def test_noalloc_refuses_workspace_above_the_limit(ctmr, dev):
     rc = L.lib().ctmr_conv3d_noalloc(ctypes.byref(desc), None, None, None, None, None, None, None)
     assert rc == L.E_WORKSPACE
     assert "scratch limit" in L.last_error() and str(L.NOALLOC_SCRATCH_BYTES) in L.last_error()
+
+
+def test_noalloc_two_streams_alternating(ctmr, dev):
+    """Two different convs issued alternately on two streams, with no host synchronisation between
+    them: both use the one scratch array (partial planes of a K split; a padded nearest-2x copy), so
+    only the library's event chain keeps them apart.  Every output equals ``ctmr_conv3d``'s."""
+    L = ctmr._lib
+    da, ia, ra = _case(ctmr, dev, 71, (2, 8, 8, 4, 512), 512)
+    db, ib, rb = _case(ctmr, dev, 72, (1, 6, 8, 10, 64), 48, mode=L.MODE_NEAREST2X)
+    assert L.conv_split(da) > 1 and L.workspace_bytes(db) > 0
+    outs_a = [torch.full_like(ra, float("nan")) for _ in range(4)]
+    outs_b = [torch.full_like(rb, float("nan")) for _ in range(4)]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for oa, ob in zip(outs_a, outs_b):
+        with torch.cuda.stream(s1):
+            assert _noalloc(ctmr, da, ia, oa) == L.OK, L.last_error()
+        with torch.cuda.stream(s2):
+            assert _noalloc(ctmr, db, ib, ob) == L.OK, L.last_error()
+    torch.cuda.synchronize()
+    for i, (oa, ob) in enumerate(zip(outs_a, outs_b)):
+        assert torch.equal(oa, ra), f"stream 1 call {i}"
+        assert torch.equal(ob, rb), f"stream 2 call {i}"
+
+
+def test_noalloc_in_a_graph_after_an_eager_call(ctmr, dev):
+    """Recorded in a HIP graph (after an eager call set the device up) and replayed three times with
+    other eager work in between: every replay equals ``ctmr_conv3d`` bit for bit."""
+    L = ctmr._lib
+    desc, inputs, ref = _case(ctmr, dev, 73, (2, 8, 8, 4, 512), 512)
+    out = torch.full_like(ref, float("nan"))
+    assert _noalloc(ctmr, desc, inputs, out) == L.OK, L.last_error()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert _noalloc(ctmr, desc, inputs, out) == L.OK, L.last_error()
+    for i in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}"
+        _case(ctmr, dev, 74 + i, (1, 6, 8, 10, 64), 48)  # eager convs between the replays
+
+
+_FRESH_PROCESS_GRAPH = """
+import ctypes, importlib, sys
+import numpy as np, torch
+sys.path.insert(0, {repo!r})
+sys.path.insert(0, {tests!r})
+ctmr = importlib.import_module("mlx-generate-ctmr_amd")
+import test_zz_no_alloc as t
+dev = torch.device("cuda:0")
+L = ctmr._lib
+desc, inputs, ref = t._case(ctmr, dev, 77, (2, 8, 8, 4, 512), 512)
+out = torch.full_like(ref, float("nan"))
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the process's first noalloc call: set-up happens inside the capture
+    rc = t._noalloc(ctmr, desc, inputs, out)
+assert rc == L.OK, L.last_error()
+for i in range(3):
+    out.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), i
+print("fresh-process graph ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_a_graph_capture(ctmr, dev):
+    """In a fresh process, the first ``ctmr_conv3d_noalloc`` call (which looks up the scratch
+    address and creates the ordering event) is made under graph capture; replays equal
+    ``ctmr_conv3d``."""
+    tests = Path(__file__).resolve().parent
+    code = _FRESH_PROCESS_GRAPH.format(repo=str(tests.parent), tests=str(tests))
+    print("noalloc fresh-process graph capture: starting child", flush=True)
+    proc = subprocess.run([sys.executable, "-c", textwrap.dedent(code)], capture_output=True, text=True,
+                          timeout=300, env=dict(os.environ))
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-4000:]
+    assert "fresh-process graph ok" in proc.stdout
