@@ -446,11 +446,11 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         from oracle import cpu_baseline as cb
 
         host_v = {k: v.cpu().numpy() for k, v in vw.items()}
-        win = cb.vae_window_seconds(host_v, vc, np.ascontiguousarray(z[:, :20].cpu().numpy()))
+        full = cb.vae_decode_seconds(host_v, vc, np.ascontiguousarray(z.cpu().numpy()), (20, 64, 64), 0.25)
         out["config4_vae_decode_256^3_4windows"].update(
-            {"cpu_window_s": round(win, 2), "cpu_decode_s_est": round(4 * win, 2), "cpu_cores": cb.cores(),
-             "cpu_sample": "one 20x64x64 window (PyTorch fp32 decoder), one run after a small warm-up; x4 "
-                           "windows for the estimate (the blend is negligible)"})
+            {"cpu_decode_s": round(full, 2), "cpu_cores": cb.cores(), "cpu_repetitions": 1,
+             "cpu_sample": "the full 256^3 decode (4 windows of 20x64x64 latent, Gaussian blend, int16) with "
+                           "the PyTorch fp32 decoder, one timed run after a small warm-up window"})
     del z
     if generation:
         # full 256^3 generation: 30 rflow steps with batched CFG at a 64^3 latent, then decode

@@ -130,18 +130,20 @@ def config_legs(reps: int = 3) -> dict:
     return out
 
 
-def vae_window_seconds(weights_host: dict, constructor: dict, z_window) -> float:
-    """One decoder window on the CPU (PyTorch fp32, the restated MAISI decoder): seconds, one run
-    after a warm-up on a 1/8-size window (the full window takes several seconds)."""
+def vae_decode_seconds(weights_host: dict, constructor: dict, z, roi, overlap: float) -> float:
+    """One full sliding-window decode on the CPU (PyTorch fp32, the restated MAISI decoder and
+    Gaussian blend of decode.py:104-245, then the int16 conversion of image.py:85-87): seconds of
+    one run after a warm-up on a 1/8-size window (the full decode takes tens of seconds)."""
     import torch
 
     from . import maisi_torch as mt
 
     torch.set_num_threads(cores())
     w = mt.to_torch(weights_host, dtype=torch.float32, strip="")
-    z = torch.from_numpy(z_window).permute(0, 4, 1, 2, 3).contiguous()
+    zt = torch.from_numpy(z).permute(0, 4, 1, 2, 3).contiguous()
     with torch.no_grad():
-        mt.vae_decode(z[:, :, :10, :32, :32].contiguous(), w, constructor)
+        mt.vae_decode(zt[:, :, :10, :32, :32].contiguous(), w, constructor)
         t0 = time.perf_counter()
-        mt.vae_decode(z, w, constructor)
+        y = mt.sliding_window_decode(zt, w, constructor, roi, overlap, scale_factor=1.0)
+        torch.clamp(y * 1000.0, min=0.0).to(torch.int16)
         return time.perf_counter() - t0

@@ -226,29 +226,57 @@ def _decoder(ctmr, dev):
     return ctor, host, {k: _g(v, dev) for k, v in host.items()}
 
 
-def test_config4_full_window_matches_cpu_oracle(ctmr, dev):
+BF16_REL = 2e-2  # north-star per-layer bar of the bf16-in / fp32-accumulate variant
+
+
+@pytest.fixture(scope="module")
+def cpu_window(ctmr):
+    """bench.py's first config-4 window (latent 20x64x64x4) and its PyTorch CPU fp32 decode (NDHWC),
+    computed once for the fp32 and bf16 window checks."""
+    m = ctmr.maisi
+    ctor = m.PRODUCTION_VAE_CONSTRUCTOR
+    host = m.random_weights(m.vae_decoder_weight_shapes(ctor), seed=11)  # bench.py's seed
+    z = np.random.default_rng(4).standard_normal((1, 64, 64, 64, 4), dtype=np.float32)  # bench.py's latent
+    window = np.ascontiguousarray(z[:, 0:20])
+    with torch.no_grad():
+        _, ref = mt.vae_decode(torch.from_numpy(np.moveaxis(window, -1, 1).copy()),
+                               mt.to_torch(host, dtype=torch.float32, strip=""), ctor)
+    return window, np.moveaxis(ref.numpy(), 1, -1)
+
+
+def test_config4_full_window_matches_cpu_oracle(ctmr, dev, cpu_window):
     """One full config-4 window (latent 20x64x64x4 -> 80x256x256, production decoder, random init):
     the top level convolves 5.2M voxels x 64 channels and normalizes groups of 10.5M values.  The
     window bench.py decodes first, against the PyTorch CPU fp32 decoder, <= 1e-4."""
     m = ctmr.maisi
-    ctor, host, w = _decoder(ctmr, dev)
-    z = np.random.default_rng(4).standard_normal((1, 64, 64, 64, 4), dtype=np.float32)  # bench.py's latent
-    window = np.ascontiguousarray(z[:, 0:20])
+    ctor, _, w = _decoder(ctmr, dev)
+    window, ref = cpu_window
     post, y = m.decode_vae(_g(window, dev), w, constructor=ctor)
     assert tuple(y.shape) == (1, 80, 256, 256, 1)
     y = _h(y)
     del post
-    with torch.no_grad():
-        _, ref = mt.vae_decode(torch.from_numpy(np.moveaxis(window, -1, 1).copy()),
-                               mt.to_torch(host, dtype=torch.float32, strip=""), ctor)
-    _check(y, np.moveaxis(ref.numpy(), 1, -1), BLOCK_REL, "config4 window vs torch CPU fp32 decoder")
+    _check(y, ref, BLOCK_REL, "config4 window vs torch CPU fp32 decoder")
 
 
-def test_config4_256_decode_blend_and_int16(ctmr, dev):
-    """bench.py's config-4 decode (64^3 latent, roi 20x64x64, overlap 0.25 -> 4 windows along D,
-    256^3 output, int16): finite; equal, at every voxel, to the Gaussian blend of the four windows
-    decoded separately recomputed in float64 (so continuous across each seam); the int16 image
-    is the truncation of max(1000 x, 0) with no value outside the int16 range."""
+def test_config4_full_window_bf16_matches_cpu_oracle(ctmr, dev, cpu_window):
+    """The same window decoded under ``precision("bf16")`` -- the variant bench.py times as
+    ``config4 ... bf16_s`` (3x3x3 convs on bf16 MFMA with fp32 accumulation, the LDS-staged bf16
+    GEMM, its nearest/trilinear packs) -- against the PyTorch CPU fp32 decoder, <= 2e-2, and
+    bit-identical run to run."""
+    m, f = ctmr.maisi, ctmr.fast_fp32
+    ctor, _, w = _decoder(ctmr, dev)
+    window, ref = cpu_window
+    with f.precision("bf16"):
+        _, y = m.decode_vae(_g(window, dev), w, constructor=ctor)
+        _, y2 = m.decode_vae(_g(window, dev), w, constructor=ctor)
+    assert tuple(y.shape) == (1, 80, 256, 256, 1)
+    assert torch.equal(y, y2)
+    _check(_h(y), ref, BF16_REL, "config4 window bf16 vs torch CPU fp32 decoder")
+
+
+def _check_256_decode(ctmr, dev, tag):
+    """bench.py's config-4 decode under the active precision: finite; equal, at every voxel, to the
+    float64 Gaussian blend of the four windows decoded separately; int16 = truncation, in range."""
     m = ctmr.maisi
     ctor, _, w = _decoder(ctmr, dev)
     z = np.random.default_rng(4).standard_normal((1, 64, 64, 64, 4), dtype=np.float32)
@@ -271,15 +299,31 @@ def test_config4_256_decode_blend_and_int16(ctmr, dev):
         num[4 * a:4 * a + 80] += pred[0, ..., 0].astype(np.float64) * gw
         den[4 * a:4 * a + 80] += gw
     blend = num / den
-    _check(y[0, ..., 0], blend, GN_REL, "config4 256^3 decode vs float64 blend of its windows")
+    _check(y[0, ..., 0], blend, GN_REL, f"config4 256^3 {tag} decode vs float64 blend of its windows")
     for a in starts[1:]:  # the rows either side of each window start
         seam = slice(4 * a - 2, 4 * a + 2)
-        _check(y[0, seam, ..., 0], blend[seam], GN_REL, f"config4 seam at depth {4 * a}")
+        _check(y[0, seam, ..., 0], blend[seam], GN_REL, f"config4 {tag} seam at depth {4 * a}")
     scaled = np.maximum(y.astype(np.float64) * 1000.0, 0.0)
     assert scaled.max() < 32767.0, f"MR-scaled intensities overflow int16: max {scaled.max():.1f}"
     np.testing.assert_array_equal(img, np.trunc(np.maximum(y * np.float32(1000.0), 0)).astype(np.int16))
     ct = m.output_intensities(y, configuration="ct")
     assert ct.dtype == np.int16 and ct.min() >= -1000 and ct.max() <= 1000
+
+
+def test_config4_256_decode_blend_and_int16(ctmr, dev):
+    """bench.py's config-4 decode (64^3 latent, roi 20x64x64, overlap 0.25 -> 4 windows along D,
+    256^3 output, int16): finite; equal, at every voxel, to the Gaussian blend of the four windows
+    decoded separately recomputed in float64 (so continuous across each seam); the int16 image
+    is the truncation of max(1000 x, 0) with no value outside the int16 range."""
+    _check_256_decode(ctmr, dev, "fp32")
+
+
+def test_config4_256_decode_bf16_blend_and_int16(ctmr, dev):
+    """The bf16 variant of the same 256^3 decode (the one bench.py times as ``bf16_s``): the same
+    blend, seam and int16 checks, with every window decoded under ``precision("bf16")`` (each
+    window itself is checked against the fp32 CPU decoder, <= 2e-2, above)."""
+    with ctmr.fast_fp32.precision("bf16"):
+        _check_256_decode(ctmr, dev, "bf16")
 
 
 def test_outputs_beyond_2gib(ctmr, dev):
