@@ -20,7 +20,8 @@ E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_LAUNCH = -1, -2, -3, -4
 MODE_PLAIN, MODE_NEAREST2X, MODE_TRILINEAR2X = 0, 1, 2
 F_AFFINE, F_SILU, F_BATCH_BIAS, F_RESIDUAL, F_STREAM = 1, 2, 4, 8, 16
 DT_F32, DT_BF16 = 0, 1
-K_STREAM, K_STREAM_DIRECT, K_LDS, K_LDS_BF16, K_POINTWISE, K_SPLIT_WAVES, K_TAP_EXPAND, K_LDS_SMALL = range(8)
+(K_STREAM, K_STREAM_DIRECT, K_LDS, K_LDS_BF16, K_POINTWISE, K_SPLIT_WAVES, K_TAP_EXPAND, K_LDS_SMALL,
+ K_SMALL_COUT) = range(9)
 KERNEL_NAMES = ("stream", "stream_direct", "lds", "lds_bf16", "pointwise", "split_waves", "tap_expand", "lds_small",
                 "small_cout")
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2

@@ -153,8 +153,14 @@ _packed_lock = threading.RLock()  # re-entrant: a weakref eviction may run insid
 _retained = threading.local()
 
 
+def _version(t: Tensor) -> int:
+    """``t._version``, or -1 for an inference tensor (created under ``torch.inference_mode``), which
+    has no version counter; such a tensor cannot be modified in place outside inference mode."""
+    return -1 if t.is_inference() else t._version
+
+
 def _sources_match(refs: tuple[weakref.ref, ...], versions: tuple[int, ...], sources: tuple[Tensor, ...]) -> bool:
-    return all(r() is t and v == t._version for r, v, t in zip(refs, versions, sources))
+    return all(r() is t and v == _version(t) for r, v, t in zip(refs, versions, sources))
 
 
 def _note_use(*derived: Optional[Tensor]) -> None:
@@ -194,7 +200,7 @@ def cached_derived(cache: dict, lock: threading.Lock, key: tuple, sources: tuple
             cache.pop(key, None)
 
     with lock:
-        cache[key] = (tuple(weakref.ref(t, _evict) for t in sources), tuple(t._version for t in sources), value)
+        cache[key] = (tuple(weakref.ref(t, _evict) for t in sources), tuple(_version(t) for t in sources), value)
     _note_use(*(value if isinstance(value, tuple) else (value,)))
     return value
 
@@ -343,7 +349,10 @@ def implicit_gemm_conv3d(
         residual = _require(residual, "residual")
         if tuple(residual.shape) != out_shape:
             raise ValueError(f"residual shape {tuple(residual.shape)} != output {out_shape}")
-    if gn_groups > 0 and ops.conv_stats_tiles(tuple(x.shape), cout, ksize, stride, mode, code, split,
+    # Statistics ride on the output tensor, valid while its version counter is unchanged; under
+    # torch.inference_mode the output is an inference tensor without one, so nothing is attached and
+    # the group norm reading it makes its own pass.
+    if gn_groups > 0 and not torch.is_inference_mode_enabled() and ops.conv_stats_tiles(tuple(x.shape), cout, ksize, stride, mode, code, split,
                                               stream_gemm, int(gn_groups), cin2) > 0:
         y, stats = ops.conv3d_gn(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split,
                                  stream_gemm, int(gn_groups), x2)
@@ -357,7 +366,7 @@ def conv_output_stats(x: Tensor, groups: int) -> Optional[Tensor]:
     """The ``(N, tiles, groups, 2)`` group-norm partials a conv epilogue wrote for ``x``, or None if
     ``x`` carries none for ``groups`` or was modified in place since."""
     info = getattr(x, "_ctmr_gn_stats", None)
-    if info is None or info[0] != groups or info[2] != x._version:
+    if info is None or x.is_inference() or info[0] != groups or info[2] != x._version:
         return None
     return info[1]
 

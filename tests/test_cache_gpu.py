@@ -147,3 +147,36 @@ def test_graph_keeps_cached_weights_after_drop(ctmr, dev):
         torch.cuda.synchronize()
         assert torch.equal(y, eager)
     del junk
+
+
+def test_inference_mode_weights_and_residual_block(ctmr, dev):
+    """Weights created under ``torch.inference_mode`` (inference tensors have no version counter)
+    pack and cache; a residual block run under inference mode (its outputs are inference tensors,
+    so no epilogue statistics ride on them and each group norm makes its own pass) matches the same
+    block run outside it."""
+    f = ctmr.fast_fp32
+    rng = np.random.default_rng(58)
+    c = 64
+    x = _g(rng.standard_normal((1, 6, 8, 8, c)).astype(np.float32), dev)
+    emb = _g(rng.standard_normal((1, 32)).astype(np.float32), dev)
+    arrays = {
+        "norm1.weight": 1 + 0.1 * rng.standard_normal(c), "norm1.bias": 0.1 * rng.standard_normal(c),
+        "norm2.weight": 1 + 0.1 * rng.standard_normal(c), "norm2.bias": 0.1 * rng.standard_normal(c),
+        "conv1.conv.weight": rng.standard_normal((c, c, 3, 3, 3)) / np.sqrt(27 * c),
+        "conv1.conv.bias": 0.01 * rng.standard_normal(c),
+        "conv2.conv.weight": rng.standard_normal((c, c, 3, 3, 3)) / np.sqrt(27 * c),
+        "conv2.conv.bias": 0.01 * rng.standard_normal(c),
+        "time_emb_proj.weight": rng.standard_normal((c, 32)) / np.sqrt(32),
+        "time_emb_proj.bias": 0.01 * rng.standard_normal(c),
+    }
+    plain = {k: _g(v.astype(np.float32), dev) for k, v in arrays.items()}
+    want = f.residual_block(x, emb, plain, num_groups=32, eps=1e-6)
+    with torch.inference_mode():
+        inf = {k: _g(v.astype(np.float32), dev) for k, v in arrays.items()}
+        assert all(t.is_inference() for t in inf.values())
+        got = f.residual_block(x, emb, inf, num_groups=32, eps=1e-6)
+        again = f.residual_block(x, emb, inf, num_groups=32, eps=1e-6)  # cache hits on inference tensors
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
+    scale = float(want.abs().max())
+    assert float((got - want).abs().max()) <= 1e-6 * scale

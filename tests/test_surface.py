@@ -145,3 +145,41 @@ def test_bf16_precision_keeps_small_convs_fp32(ctmr, shape, keeps):
     """Which convs keep fp32 operands under ``precision("bf16")`` (a function of the weight shape only):
     1x1 convs, at most 8 input channels, at most 4 output channels."""
     assert ctmr.fast_fp32._keeps_fp32(torch.empty(shape)) is keeps
+
+
+def test_derived_cache_accepts_inference_tensors(ctmr):
+    """The derived-weight cache keys on each source's version counter; inference tensors (made under
+    ``torch.inference_mode``) have none, and must still build once and then hit (CPU: host logic
+    only; the build function stands in for a pack)."""
+    import threading
+
+    f = ctmr.fast_fp32
+    cache, lock, builds = {}, threading.Lock(), []
+
+    def build():
+        builds.append(1)
+        return torch.zeros(3)
+
+    with torch.inference_mode():
+        w = torch.ones(4)
+    assert w.is_inference()
+    first = f.cached_derived(cache, lock, ("k",), (w,), build)
+    second = f.cached_derived(cache, lock, ("k",), (w,), build)
+    assert first is second and len(builds) == 1
+    v = torch.ones(4)  # an ordinary tensor: an in-place change still forces a rebuild
+    f.cached_derived(cache, lock, ("v",), (v,), build)
+    v.add_(1)
+    f.cached_derived(cache, lock, ("v",), (v,), build)
+    assert len(builds) == 3
+
+
+def test_python_kernel_constants_match_header(ctmr):
+    """Every ``CTMR_K_*`` route of include/ctmr.h has its Python constant, in enum order."""
+    import re
+
+    L = ctmr._lib
+    text = L.HEADER_PATH.read_text()
+    names = re.findall(r"CTMR_K_(\w+)\s*=\s*(\d+)", text)
+    assert len(names) == len(L.KERNEL_NAMES)
+    for name, value in names:
+        assert getattr(L, "K_" + name) == int(value), name
