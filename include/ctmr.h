@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define CTMR_ABI_VERSION 2
+#define CTMR_ABI_VERSION 3
 
 enum ctmr_status {
   CTMR_OK = 0,
@@ -71,9 +71,21 @@ enum ctmr_conv_flags {
 };
 
 enum ctmr_dtype {
-  CTMR_F32 = 0,  /* fp32 operands, FP32 MFMA (v_mfma_f32_16x16x4_f32) */
-  CTMR_BF16 = 1  /* bf16 operands, fp32 accumulate (v_mfma_f32_16x16x32_bf16);
-                    activations and outputs stay fp32 in memory */
+  CTMR_F32 = 0,   /* fp32 operands, FP32 MFMA (v_mfma_f32_16x16x4_f32) */
+  CTMR_BF16 = 1,  /* bf16 operands, fp32 accumulate (v_mfma_f32_16x16x32_bf16);
+                     activations and outputs stay fp32 in memory */
+  CTMR_F16X2 = 2  /* split fp16, the reference's "exact" mode for fp32 tensors
+                     (_nax_conv.py:27-35): each fp32 input value is held as
+                     hi = fp16(v) and lo = fp16((v - hi) * 2^11), each weight
+                     (scaled per output column by a power of two) as hi and
+                     lo = fp16(w - hi), and every product is summed as
+                     hi*hi + (lo*hi)*2^-11 + hi*lo on fp16 MFMA
+                     (v_mfma_f32_16x16x32_f16) with fp32 accumulation: about
+                     2^-22 relative per product, against 2^-24 for fp32.  Values
+                     must stay below 65504 in magnitude (fp16 range of hi).
+                     Stride-1 3x3x3 convs with cout % 64 == 0 and bricks at
+                     least half full only (the LDS-staged 16-bit GEMM);
+                     CTMR_E_UNSUPPORTED otherwise. */
 };
 
 typedef struct ctmr_conv_desc {
@@ -103,7 +115,10 @@ const char* ctmr_last_error(void);
 /* Output spatial extent of a conv described by `desc` (out[0..2] = D', H', W'). */
 int ctmr_conv3d_output_dims(const ctmr_conv_desc* desc, int32_t out[3]);
 
-/* Packed-weight element count (fp32 for CTMR_F32, bf16 for CTMR_BF16). */
+/* Packed-weight element count (fp32 for CTMR_F32, bf16 for CTMR_BF16, 16-bit
+ * elements for CTMR_F16X2: per (phase, tap, 16-channel block, column) 48
+ * halves -- hi, hi * 2^-11 and lo of the scaled weight -- then one fp32
+ * power-of-two column scale per packed column). */
 int64_t ctmr_packed_weight_elems(const ctmr_conv_desc* desc);
 
 /* Scratch bytes ctmr_conv3d needs for `desc` (padded input copy + split planes). */
@@ -125,7 +140,8 @@ enum ctmr_conv_kernel {
   CTMR_K_SPLIT_WAVES = 5,   /* 64 x 64 tiles, each split range over the four waves */
   CTMR_K_TAP_EXPAND = 6,    /* cout <= 4: 27*cout-column GEMM + tap sum */
   CTMR_K_LDS_SMALL = 7,     /* cin 4 / 8: im2col rows read from an LDS halo brick */
-  CTMR_K_SMALL_COUT = 8     /* cout <= 4: direct FMA conv from an LDS halo brick */
+  CTMR_K_SMALL_COUT = 8,    /* cout <= 4: direct FMA conv from an LDS halo brick */
+  CTMR_K_LDS_F16X2 = 9      /* split-fp16 LDS-staged GEMM over the packed hi/lo copy */
 };
 int ctmr_conv3d_kernel(const ctmr_conv_desc* desc);
 

@@ -19,13 +19,13 @@ OK = 0
 E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_LAUNCH = -1, -2, -3, -4
 MODE_PLAIN, MODE_NEAREST2X, MODE_TRILINEAR2X = 0, 1, 2
 F_AFFINE, F_SILU, F_BATCH_BIAS, F_RESIDUAL, F_STREAM = 1, 2, 4, 8, 16
-DT_F32, DT_BF16 = 0, 1
+DT_F32, DT_BF16, DT_F16X2 = 0, 1, 2
 (K_STREAM, K_STREAM_DIRECT, K_LDS, K_LDS_BF16, K_POINTWISE, K_SPLIT_WAVES, K_TAP_EXPAND, K_LDS_SMALL,
- K_SMALL_COUT) = range(9)
+ K_SMALL_COUT, K_LDS_F16X2) = range(10)
 KERNEL_NAMES = ("stream", "stream_direct", "lds", "lds_bf16", "pointwise", "split_waves", "tap_expand", "lds_small",
-                "small_cout")
+                "small_cout", "lds_f16x2")
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 NOALLOC_SCRATCH_BYTES = 256 << 20  # CTMR_NOALLOC_SCRATCH_BYTES
 
 

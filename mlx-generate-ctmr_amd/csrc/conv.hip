@@ -60,8 +60,38 @@ struct PackArgs {
   int c, cp;            // source / packed channels
   int id, ih, iw;       // source grid (trilinear)
   int affine_on, silu_on, trilinear, bf16;
+  int split16;          // split-fp16 copy (CTMR_F16X2): per 16-channel block [hi 0..15 | lo 0..15]
   int n;                // batch items
 };
+
+// Packed-copy formats: fp32, bf16, or split fp16 (CTMR_F16X2), whose 16-channel
+// blocks hold the hi halves of channels 0..15 and then their lo halves (64
+// bytes, the size of the fp32 copy's block).
+enum { PF_F32 = 0, PF_BF16 = 1, PF_SPLIT = 2 };
+
+// Byte offset of channel ch (a multiple of 4) of packed voxel `vox` in the
+// split-fp16 copy of cp channels: its hi half; the lo half lies 32 bytes on.
+__device__ __forceinline__ int64_t split_offset(int64_t vox, int cp, int ch) {
+  return vox * cp * 4 + (ch >> 4) * 64 + (ch & 15) * 2;
+}
+
+// Split-fp16 store of 4 channels (8-byte halves) and of 8 (16-byte halves,
+// ch % 8 == 0) at a split_offset.
+__device__ __forceinline__ void store_split4(void* out, int64_t off, f4 v) {
+  h4 hi, lo;
+  split_f16x4(v, hi, lo);
+  char* p = reinterpret_cast<char*>(out) + off;
+  *reinterpret_cast<h4*>(p) = hi;
+  *reinterpret_cast<h4*>(p + 32) = lo;
+}
+__device__ __forceinline__ void store_split8(void* out, int64_t off, f4 v0, f4 v1) {
+  h4 hi0, lo0, hi1, lo1;
+  split_f16x4(v0, hi0, lo0);
+  split_f16x4(v1, hi1, lo1);
+  char* p = reinterpret_cast<char*>(out) + off;
+  *reinterpret_cast<h8*>(p) = h8{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
+  *reinterpret_cast<h8*>(p + 32) = h8{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
+}
 
 // The packed value of channels ch..ch+3 at padded voxel (pz, py, px) of batch
 // item b: zero in the halo and past the source channels, else the source (or
@@ -112,9 +142,10 @@ __device__ __forceinline__ f4 pack_value4(const PackArgs& a, int b, int pz, int 
 // and the thread the plane's (row, column, channel group) items, so the index
 // arithmetic is 32-bit (the host checks a plane holds < 2^31 items).  A
 // thread packs 4 channels (fp32: one 16-byte store) or 8 (bf16: one 16-byte
-// store of 8 rounded values; the bf16 copy's cp is a multiple of 32).
+// store of 8 rounded values; the bf16 copy's cp is a multiple of 32), or 8
+// (split fp16: 16-byte hi and lo stores; cp a multiple of 16).
 __global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
-  const int G = a.bf16 ? 2 : 1;
+  const int G = (a.bf16 || a.split16) ? 2 : 1;
   const int cgn = (a.cp >> 2) / G;
   const int PW = a.gw + 2 * a.halo, PH = a.gh + 2 * a.halo, PD = a.gd + 2 * a.halo;
   const unsigned plane = (unsigned)PH * (unsigned)PW * (unsigned)cgn;
@@ -126,7 +157,10 @@ __global__ __launch_bounds__(256) void pack_input_kernel(PackArgs a) {
   for (int bz = blockIdx.y; bz < a.n * PD; bz += gridDim.y) {
     const int b = bz / PD, pz = bz - b * PD;
     const int64_t idx = (int64_t)bz * plane + i;
-    if (a.bf16) {
+    if (a.split16) {
+      const f4 v0 = pack_value4(a, b, pz, py, px, cg * 8), v1 = pack_value4(a, b, pz, py, px, cg * 8 + 4);
+      store_split8(a.out, split_offset((idx - cg) / cgn, a.cp, cg * 8), v0, v1);
+    } else if (a.bf16) {
       const f4 v0 = pack_value4(a, b, pz, py, px, cg * 8), v1 = pack_value4(a, b, pz, py, px, cg * 8 + 4);
       u4 packed;
       packed.x = (unsigned)f32_to_bf16_bits(v0[0]) | ((unsigned)f32_to_bf16_bits(v0[1]) << 16);
@@ -166,11 +200,16 @@ __device__ __forceinline__ unsigned bf16_pair(float lo, float hi) {
   return (unsigned)f32_to_bf16_bits(lo) | ((unsigned)f32_to_bf16_bits(hi) << 16);
 }
 
-// Store one packed item: V vectors of 4 channels, as V f4 (fp32) or one
-// 16-byte store of 8 rounded values (bf16, V = 2).
-template <int V>
-__device__ __forceinline__ void store_packed(const PackArgs& a, int64_t idx, const f4* v) {
-  if constexpr (V == 2) {
+// Store one packed item: V vectors of 4 channels, as V f4 (fp32), one
+// 16-byte store of 8 rounded values (bf16, V = 2), or 16-byte hi and lo
+// stores of channel group cg's 8 values (split fp16, V = 2: a voxel's cp / 8
+// groups occupy cp * 4 = 32 * (cp / 8) bytes).
+template <int V, bool SPLIT = false>
+__device__ __forceinline__ void store_packed(const PackArgs& a, int64_t idx, int cg, const f4* v) {
+  if constexpr (SPLIT) {
+    static_assert(V == 2, "split-fp16 packing stores 8 channels per item");
+    store_split8(a.out, (idx - cg) * 32 + (cg >> 1) * 64 + (cg & 1) * 16, v[0], v[1]);
+  } else if constexpr (V == 2) {
     u4 packed;
     packed.x = bf16_pair(v[0][0], v[0][1]);
     packed.y = bf16_pair(v[0][2], v[0][3]);
@@ -188,7 +227,7 @@ __device__ __forceinline__ void store_packed(const PackArgs& a, int64_t idx, con
 // source loads before its first store (PZ times the bytes in flight per wave
 // of a one-item thread); the group's affine pairs are read once per batch item
 // as 16-byte vectors.
-template <int V, int PZ>
+template <int V, int PZ, bool SPLIT = false>
 __global__ __launch_bounds__(256) void pack_planes_kernel(PackArgs a) {
   const int cgn = a.cp / (4 * V);
   const int PW = a.gw + 2 * a.halo, PH = a.gh + 2 * a.halo, PD = a.gd + 2 * a.halo;
@@ -239,7 +278,7 @@ __global__ __launch_bounds__(256) void pack_planes_kernel(PackArgs a) {
 #pragma unroll
       for (int k = 0; k < V; ++k)
         if (in[s] && cg * 4 * V + 4 * k < a.c) v[s][k] = pack_transform4(a, v[s][k], sc[k], of[k]);
-      store_packed<V>(a, (int64_t)bz * plane + i, v[s]);
+      store_packed<V, SPLIT>(a, (int64_t)bz * plane + i, cg, v[s]);
     }
   }
 }
@@ -342,7 +381,7 @@ __device__ __forceinline__ TriPlane tri_face_plane(const PackArgs& a, const TriC
 
 // One column's march over cells [cz0, cz1) of batch item b (see
 // pack_trilinear_kernel): blend, transform and store each cell's 2x2x2 voxels.
-template <bool BF16, bool INNER>
+template <int FMT, bool INNER>
 __device__ __forceinline__ void tri_march(const PackArgs& a, const TriColumn& t, int b, int cz0, int cz1) {
 #pragma clang fp contract(off)
   const int PW = a.gw + 2, PH = a.gh + 2, PD = a.gd + 2;
@@ -416,7 +455,9 @@ __device__ __forceinline__ void tri_march(const PackArgs& a, const TriColumn& t,
       const bool inside = oz >= 0 && oz < a.gd && oy >= 0 && oy < a.gh && ox >= 0 && ox < a.gw;
       const f4 v = inside ? pack_transform4(a, out[o], sc, of) : f4{0.f, 0.f, 0.f, 0.f};
       const int64_t vox = (((int64_t)b * PD + oz + 1) * PH + oy + 1) * PW + ox + 1;
-      if constexpr (BF16) {
+      if constexpr (FMT == PF_SPLIT) {
+        store_split4(a.out, split_offset(vox, a.cp, t.ch), v);
+      } else if constexpr (FMT == PF_BF16) {
         uint2 packed;
         packed.x = bf16_pair(v[0], v[1]);
         packed.y = bf16_pair(v[2], v[3]);
@@ -430,7 +471,7 @@ __device__ __forceinline__ void tri_march(const PackArgs& a, const TriColumn& t,
 
 // Zeros of the padded copy for a column's channel group past the source
 // channels, over cells [cz0, cz1) of batch item b.
-template <bool BF16>
+template <int FMT>
 __device__ __forceinline__ void tri_zero(const PackArgs& a, const TriColumn& t, int b, int cz0, int cz1) {
   const int PW = a.gw + 2, PH = a.gh + 2, PD = a.gd + 2;
   for (int cz = cz0; cz < cz1; ++cz)
@@ -439,14 +480,16 @@ __device__ __forceinline__ void tri_zero(const PackArgs& a, const TriColumn& t, 
       const int oz = 2 * cz + (o >> 2), oy = 2 * t.cy + ((o >> 1) & 1), ox = 2 * t.cx + (o & 1);
       if (oz < -1 || oz > a.gd || oy < -1 || oy > a.gh || ox < -1 || ox > a.gw) continue;
       const int64_t vox = (((int64_t)b * PD + oz + 1) * PH + oy + 1) * PW + ox + 1;
-      if constexpr (BF16)
+      if constexpr (FMT == PF_SPLIT)
+        store_split4(a.out, split_offset(vox, a.cp, t.ch), f4{0.f, 0.f, 0.f, 0.f});
+      else if constexpr (FMT == PF_BF16)
         *reinterpret_cast<uint2*>(reinterpret_cast<unsigned*>(a.out) + (vox * a.cp + t.ch) / 2) = uint2{0u, 0u};
       else
         *reinterpret_cast<f4*>(reinterpret_cast<float*>(a.out) + vox * a.cp + t.ch) = f4{0.f, 0.f, 0.f, 0.f};
     }
 }
 
-template <bool BF16, int ZC>
+template <int FMT, int ZC>
 __global__ __launch_bounds__(256) void pack_trilinear_kernel(PackArgs a) {
   const int cgn = a.cp >> 2;
   const int CW = a.iw + 2, CH = a.ih + 2, CD = a.id + 2;
@@ -473,11 +516,11 @@ __global__ __launch_bounds__(256) void pack_trilinear_kernel(PackArgs a) {
     const int b = bc / chunks, cz0 = (bc - b * chunks) * ZC - 1;
     const int cz1 = min(cz0 + ZC, a.id + 1);
     if (t.ch >= a.c)
-      tri_zero<BF16>(a, t, b, cz0, cz1);
+      tri_zero<FMT>(a, t, b, cz0, cz1);
     else if (inner)
-      tri_march<BF16, true>(a, t, b, cz0, cz1);
+      tri_march<FMT, true>(a, t, b, cz0, cz1);
     else
-      tri_march<BF16, false>(a, t, b, cz0, cz1);
+      tri_march<FMT, false>(a, t, b, cz0, cz1);
   }
 }
 
@@ -586,6 +629,8 @@ struct WPackArgs {
   int64_t total;
   int cout, cin, ks, np, kblocks, kstep, taps, up, bf16;
   int layout;      // WL_TAPS, or WL_EXPAND / WL_IM2COL with taps = 1
+  int phases;
+  float* colscale; // split fp16: (np) power-of-two column scales after the packed blocks, else null
 };
 
 // Packed-weight layouts.  WL_TAPS: K = (tap, channel).  WL_EXPAND (cout <= 4):
@@ -601,19 +646,9 @@ __device__ __forceinline__ void fold_range(int p, int t, int& lo, int& hi) {
   hi = (p == 0) ? (t == 0 ? 0 : 2) : (t == 0 ? 1 : 2);
 }
 
-__global__ __launch_bounds__(256) void pack_weight_kernel(WPackArgs a) {
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-  int64_t t = idx;
-  const int e = (int)(t % a.kstep);
-  t /= a.kstep;
-  const int col = (int)(t % a.np);
-  t /= a.np;
-  const int kb = (int)(t % a.kblocks);
-  t /= a.kblocks;
-  const int tap = (int)(t % a.taps);
-  const int phase = (int)(t / a.taps);
-  const int c = kb * a.kstep + e;
+// Packed value of channel c (K index for WL_IM2COL) of column col at tap `tap`
+// of parity `phase`: zero past the weight's channels / columns.
+__device__ __forceinline__ float packed_weight_value(const WPackArgs& a, int phase, int tap, int c, int col) {
   float val = 0.f;
   if (a.layout == WL_EXPAND) {
     if (col < 27 * a.cout && c < a.cin) val = a.w[((int64_t)(col % a.cout) * a.cin + c) * 27 + col / a.cout];
@@ -638,10 +673,72 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(WPackArgs a) {
       val = s;
     }
   }
-  if (a.bf16)
-    reinterpret_cast<unsigned short*>(a.out)[idx] = f32_to_bf16_bits(val);
-  else
-    reinterpret_cast<float*>(a.out)[idx] = val;
+  return val;
+}
+
+__global__ __launch_bounds__(256) void pack_weight_kernel(WPackArgs a) {
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    int64_t t = idx;
+    const int e = (int)(t % a.kstep);
+    t /= a.kstep;
+    const int col = (int)(t % a.np);
+    t /= a.np;
+    const int kb = (int)(t % a.kblocks);
+    t /= a.kblocks;
+    const int tap = (int)(t % a.taps);
+    const int phase = (int)(t / a.taps);
+    const float val = packed_weight_value(a, phase, tap, kb * a.kstep + e, col);
+    if (a.bf16)
+      reinterpret_cast<unsigned short*>(a.out)[idx] = f32_to_bf16_bits(val);
+    else
+      reinterpret_cast<float*>(a.out)[idx] = val;
+  }
+}
+
+// Split-fp16 weights (CTMR_F16X2), step 1: the power-of-two scale 2^-k of
+// each packed column, k chosen so that the column's largest magnitude m
+// (over every phase, tap and channel of the packed values, nearest-2x folds
+// included) times 2^k lies in [2^14, 2^15): fp16 holds the scaled weights'
+// hi and lo halves as normal numbers.  k = 0 for an all-zero column; k is
+// kept within [-100, 100].
+__global__ __launch_bounds__(256) void weight_colscale_kernel(WPackArgs a) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= a.np) return;
+  float m = 0.f;
+  for (int phase = 0; phase < a.phases; ++phase)
+    for (int tap = 0; tap < a.taps; ++tap)
+      for (int c = 0; c < a.cin; ++c) m = fmaxf(m, fabsf(packed_weight_value(a, phase, tap, c, col)));
+  int k = 0;
+  if (m > 0.f) {
+    const int e = (int)((__float_as_uint(m) >> 23) & 0xff) - 127;  // floor(log2 m) for normal m
+    k = min(max(14 - e, -100), 100);
+  }
+  a.colscale[col] = ldexpf(1.0f, -k);
+}
+
+// Split-fp16 weights, step 2: per (phase, tap, 16-channel block, column) 96
+// bytes -- hi (channels 0..15), hi * 2^-11 (the same, for the input's lo
+// halves, which carry 2^11), lo -- of the column-scaled weight ws = w * 2^k:
+// hi = fp16(ws), lo = fp16(ws - hi); ws - hi is exact in fp32.
+__global__ __launch_bounds__(256) void pack_weight_split_kernel(WPackArgs a) {
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    int64_t t = idx;
+    const int e = (int)(t % 16);
+    t /= 16;
+    const int col = (int)(t % a.np);
+    t /= a.np;
+    const int kb = (int)(t % a.kblocks);
+    t /= a.kblocks;
+    const int tap = (int)(t % a.taps);
+    const int phase = (int)(t / a.taps);
+    const float ws = packed_weight_value(a, phase, tap, kb * 16 + e, col) / a.colscale[col];  // exact: 2^k
+    const _Float16 hi = (_Float16)ws;
+    _Float16* block = reinterpret_cast<_Float16*>(a.out) + (idx - e) * 3;  // 48 halves per 16 channels
+    block[e] = hi;
+    block[16 + e] = (_Float16)((float)hi * (1.0f / 2048.0f));
+    block[32 + e] = (_Float16)(ws - (float)hi);
   }
 }
 
@@ -817,17 +914,20 @@ __device__ __forceinline__ void load_bias(const ConvArgs& p, int b, int n0, int 
 // load would wait for the stores before it (the compiler cannot prove the
 // output and its inputs apart).  Rows past the grid are clamped for the loads
 // and masked for the stores.
-// Cache-policy operand of the GEMMs' output stores: SC1 (device scope).  Same
-// values; measured on MI355X against the default policy, A/B in one run: the
-// brick GEMMs and the persistent 1x1 GEMM -- config-2c 1x1 0.165 -> 0.160 ms,
-// config-1 block 26.57 -> 26.40 ms, decoder window -0.25 %; the streaming
-// GEMM's contiguous-row epilogue -- config 2a 0.860 -> 0.844 ms, UNet step
-// -0.2 %.
-constexpr int kOutStorePolicy = 2;
+// Cache-policy operands of the GEMMs' output stores (gfx950 encoding: bit 1 =
+// NT, non-temporal; bit 4 = SC1, device scope).  Same values under every
+// policy; measured on MI355X, default / NT / SC1, A/B twice in one run: the
+// brick GEMMs (fp32 and bf16 LDS-staged) and the streaming GEMM take SC1
+// (config-0 fp32 + bf16 GEMMs 0.462 / 0.505 / 0.451 ms, UNet step 17.72 /
+// 17.80 / 17.69 ms, config-1 block 26.18 / 26.17 / 26.14 ms, config 2a and
+// the decoder window within 0.5 % either way); the persistent 1x1 GEMM takes
+// NT (config 2c 0.165 / 0.160 / 0.171 ms).
+constexpr int kStoreSC1 = 16;
+constexpr int kStoreNT = 2;
 
 // IDENT: GEMM row v of batch item b is output voxel b * s_out + v (every route
 // but the nearest-2x parity phases), so a wave's 64 rows are contiguous and
-// its stores go through one buffer descriptor with the cache policy above.
+// its stores go through one buffer descriptor with the SC1 cache policy.
 template <int NSUB, int WM, int WN, bool IDENT, typename OutVoxel>
 __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB], const f4 (&bq)[NSUB], int b,
                                            int m0, int n0, int S, int split_id, int wave, int lane, int col0,
@@ -890,7 +990,7 @@ __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB]
         if constexpr (IDENT) {
           if (row_ok[ms] && col_ok[ns])
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, val), ors,
-                                                   (int)(((vox[ms] - vbase) * p.cout + c0) * 4), 0, kOutStorePolicy);
+                                                   (int)(((vox[ms] - vbase) * p.cout + c0) * 4), 0, kStoreSC1);
         } else {
           if (row_ok[ms] && col_ok[ns]) *reinterpret_cast<f4*>(out + vox[ms] * p.cout + c0) = val;
         }
@@ -1222,7 +1322,7 @@ __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int 
   {
     // Buffer stores relative to the brick's first output plane (its rows lie
     // within S * 4 planes of it, so the offsets stay 32-bit), with the device-
-    // scope cache policy (kOutStorePolicy).
+    // scope cache policy (kStoreSC1).
     const int64_t origin = ((int64_t)b * (S * p.d) + S * min(z0, p.d - 1)) * (S * p.h) * (int64_t)(S * p.w) * p.cout;
     const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
         out + origin, (short)0, (int)min(max((int64_t)p.plane - origin, (int64_t)0) * 4, (int64_t)0x7fffffff),
@@ -1233,7 +1333,7 @@ __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int 
       for (int ns = 0; ns < 4; ++ns)
         if (row_ok[ms])
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[ms][ns]), ors,
-                                                 (int)((base[ms] - origin + ns * 16) * 4), 0, kOutStorePolicy);
+                                                 (int)((base[ms] - origin + ns * 16) * 4), 0, kStoreSC1);
   }
   if (p.stats) {  // a kernel argument: every thread reaches the barriers
     __syncthreads();
@@ -1828,21 +1928,51 @@ constexpr int kB16HaloBytes = kHaloVox * 64;                 // 38400
 constexpr int kB16HaloSlots = kHaloVox * 4;                  // 2400
 constexpr int kB16HaloIters = (kB16HaloSlots + 255) / 256;   // 10
 constexpr int kB16TapBytes = 64 * 64;                        // one tap's 64 columns
-constexpr int kB16RowIters = 3;                              // 768 slots of a 3-tap row
+
+// Split fp16 (CTMR_F16X2) on the same GEMM.  A K block is 16 input channels
+// whose packed voxel holds [hi 0..15 | lo 0..15] (64 bytes, as a bf16 chunk),
+// so the halo fill and the A reads are the bf16 ones; lane group g (K 8g ..
+// 8g + 7 of the MFMA) reads hi 0..7, hi 8..15, lo 0..7, lo 8..15.  A packed
+// weight column holds 96 bytes per K block: Bh = [hi | hi * 2^-11] (64 bytes,
+// laid out and swizzled like a bf16 column) and Bl = [lo] (32 bytes; lane
+// groups 2 and 3 read a zeroed 16-byte slot instead).  Per (tap, row block,
+// column block) two MFMAs: Bh^T A^T adds hi*hi + (lo * 2^11)(hi * 2^-11), Bl^T
+// A^T adds lo*hi -- every product of the split but the 2^-22-relative lo*lo.
+// In LDS a tap is 384 16-byte slots (Bh 256, Bl 128) followed by a zeroed
+// 16-byte slot, which lane groups 2 and 3 read for Bl at the same tap offset
+// as groups 0 and 1 (so a Bl address is one register per column block, as for
+// Bh).  A fill wave writes 64 consecutive slots, and 384 = 6 * 64, so no
+// wave's slots straddle a tap: wave block q of a row lands at slot 64 q +
+// q / 6.  4.5 fill iterations per three-tap row, exactly 3 per two-tap
+// nearest-2x row.  Bl rows of 32 bytes need no swizzle: under the
+// ds_read_b128 service order (four cycles of 16 lanes, equal bit 5 and equal
+// parity of bits 2-4) a cycle's lanes of groups 0 and 1 hit 16 distinct bank
+// groups 2 * column + piece (mod 16), and groups 2 and 3 read one zero slot.
+constexpr int kF2TapBytes = 385 * 16;                        // 6160: Bh, Bl, zero slot
+constexpr int kF2BlOff = 256 * 16;                           // Bl after the tap's Bh
+constexpr int kF2ZeroOff = 384 * 16;                         // the tap's zero slot
+
+template <int DT>
+struct Lds16Cfg {
+  static constexpr int tap_bytes = DT == CTMR_F16X2 ? kF2TapBytes : kB16TapBytes;  // LDS bytes per tap
+  static constexpr int row_bytes = 3 * tap_bytes;
+  static constexpr int col_bytes = DT == CTMR_F16X2 ? 96 : 64;                     // packed bytes per column
+  static constexpr int row_iters = DT == CTMR_F16X2 ? 5 : 3;                       // fill iterations per row
+};
 
 __host__ __device__ constexpr int lds16_halo_swizzle(int hy) { return ((hy >> 2) & 1) << 1; }
 __host__ __device__ constexpr int row64_swizzle(int c) { return ((c >> 3) & 1) * 3; }
 
 struct Lds16Args {
-  const char* xp;       // bf16 packed copy (n, d+2, h+2, w+2, cp)
-  const char* wp;       // packed bf16 weight [tap][kblock][np][64 bytes]
+  const char* xp;       // bf16 / split-fp16 packed copy (n, d+2, h+2, w+2, cp)
+  const char* wp;       // packed weight [tap][kblock][np][64 or 96 bytes]
   const float* bias;
   const float* res;
   float* y;             // output, or split partial planes
   int64_t x_bytes, w_bytes, plane, rows_per_batch;
   int d, h, w;          // output grid = packed interior
   int P, Q;             // padded plane / row pitch in voxels
-  int vbytes;           // bytes per packed voxel (cp * 2)
+  int vbytes;           // bytes per packed voxel (cp * 2 bf16, cp * 4 split fp16)
   int cout, np, kb, n;
   int tz, ty, tx, n_tiles, split;
   int batch_bias, has_res, has_bias;
@@ -1864,39 +1994,65 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, unsigned lds_addr) {
                : "memory", "m0");
 }
 
-// Operand fragments of one tap: A (4 row blocks) and B (4 column blocks).
+// Operand fragments of one tap: A (4 row blocks), B (4 column blocks) and,
+// for split fp16, the Bl column blocks.
 struct Lds16Frag {
-  u4 a[4], b[4];
+  u4 a[4], b[4], c[4];
 };
 
 // Reads tap (kd, kh, kw) of the halo and slot BS of weight row `brow` (the
 // row's tap kw for the 3x3x3 GEMM) into `f`.  A row (lane % 16) is brick
 // column x = lane % 8 of line ms + 4 * ((lane / 8) % 2), K piece lane / 16; at
 // tap (kd, kh, kw) it reads halo column x + kw of halo line
-// ms + 4 * ((lane / 8) % 2) + kh.
-template <int KD, int KH, int KW, int BS = KW>
+// ms + 4 * ((lane / 8) % 2) + kh.  Split fp16: cbase[ns] is the lane's Bl
+// offset within a tap (lane groups 0, 1) or the tap's zero slot (2, 3).
+template <int DT, int KD, int KH, int KW, int BS = KW>
 __device__ __forceinline__ void lds16_load(Lds16Frag& f, const char* brow, const char* halo_p,
-                                           const int (&abase)[4], const int (&bbase)[4], int lane) {
+                                           const int (&abase)[4], const int (&bbase)[4], const int (&cbase)[4],
+                                           int lane) {
   const int h = (lane >> 3) & 1, g = (lane >> 4) & 3;
   constexpr int off = ((KD * kHH + KH) * kHW + KW) * 64;
+  constexpr int tb = Lds16Cfg<DT>::tap_bytes;
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
     const int piece = g ^ lds16_halo_swizzle(ms + 4 * h + KH);
     f.a[ms] = *reinterpret_cast<const u4*>(halo_p + (abase[ms] | (piece << 4)) + off);
   }
 #pragma unroll
-  for (int ns = 0; ns < 4; ++ns) f.b[ns] = *reinterpret_cast<const u4*>(brow + BS * kB16TapBytes + bbase[ns]);
+  for (int ns = 0; ns < 4; ++ns) f.b[ns] = *reinterpret_cast<const u4*>(brow + BS * tb + bbase[ns]);
+  if constexpr (DT == CTMR_F16X2) {
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) f.c[ns] = *reinterpret_cast<const u4*>(brow + BS * tb + cbase[ns]);
+  }
+}
+
+__device__ __forceinline__ void mfma_f16(f4& acc, const u4& a, const u4& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), acc, 0, 0, 0);
 }
 
 // B^T A^T (operands exchanged: the same dot products) so that a lane's result
-// registers are four adjacent output columns of one voxel.
+// registers are four adjacent output columns of one voxel.  Split fp16: the
+// sixteen Bh products, then the sixteen Bl ones (no MFMA waits on the one
+// before it).
+template <int DT>
 __device__ __forceinline__ void lds16_mma(f4 (&acc)[4][4], const Lds16Frag& f) {
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_setprio(1);
+  if constexpr (DT == CTMR_F16X2) {
 #pragma unroll
-  for (int ms = 0; ms < 4; ++ms)
+    for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-    for (int ns = 0; ns < 4; ++ns) mfma_step<CTMR_BF16>(acc[ms][ns], f.b[ns], f.a[ms]);
+      for (int ns = 0; ns < 4; ++ns) mfma_f16(acc[ms][ns], f.b[ns], f.a[ms]);
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) mfma_f16(acc[ms][ns], f.c[ns], f.a[ms]);
+  } else {
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) mfma_step<CTMR_BF16>(acc[ms][ns], f.b[ns], f.a[ms]);
+  }
   __builtin_amdgcn_s_setprio(0);
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -1909,41 +2065,82 @@ __device__ __forceinline__ void lds16_mma(f4 (&acc)[4][4], const Lds16Frag& f) {
 // so `after_barrier` can refill it with the row two ahead -- a fill has three
 // taps of products to arrive.  The next row's first tap (NEXT) is read into
 // fr[(R + 1) % 2] while this row's last products run.
-template <int R, bool NEXT, typename AfterBarrier>
+template <int DT, int R, bool NEXT, typename AfterBarrier>
 __device__ __forceinline__ void lds16_row(f4 (&acc)[4][4], Lds16Frag (&fr)[2], const char* brow,
                                           const char* brow_next, const char* halo_p, const int (&abase)[4],
-                                          const int (&bbase)[4], int lane, AfterBarrier&& after_barrier) {
+                                          const int (&bbase)[4], const int (&cbase)[4], int lane,
+                                          AfterBarrier&& after_barrier) {
   constexpr int KD = R / 3, KH = R % 3, P = R & 1;
-  lds16_load<KD, KH, 1>(fr[P ^ 1], brow, halo_p, abase, bbase, lane);
-  lds16_mma(acc, fr[P]);
-  lds16_load<KD, KH, 2>(fr[P], brow, halo_p, abase, bbase, lane);
-  lds16_mma(acc, fr[P ^ 1]);
+  lds16_load<DT, KD, KH, 1>(fr[P ^ 1], brow, halo_p, abase, bbase, cbase, lane);
+  lds16_mma<DT>(acc, fr[P]);
+  lds16_load<DT, KD, KH, 2>(fr[P], brow, halo_p, abase, bbase, cbase, lane);
+  lds16_mma<DT>(acc, fr[P ^ 1]);
   // Every read of this row has returned and this wave's fills have landed.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   after_barrier();
-  if (NEXT) lds16_load<(R + 1) / 3, (R + 1) % 3, 0>(fr[P ^ 1], brow_next, halo_p, abase, bbase, lane);
-  lds16_mma(acc, fr[P]);
+  if (NEXT)
+    lds16_load<DT, (R + 1) / 3, (R + 1) % 3, 0>(fr[P ^ 1], brow_next, halo_p, abase, bbase, cbase, lane);
+  lds16_mma<DT>(acc, fr[P]);
 }
 
-// Tap row (KD, KH) of the nearest-2x parity GEMM in conv_lds_bf16_kernel<true>:
+// Tap row (KD, KH) of the nearest-2x parity GEMM in conv_lds_bf16_kernel<.., true>:
 // halo taps (KD, KH, KW0) and (KD, KH, KW0 + 1), B from slots 0 and 1 of this
 // row's weight buffer `brow`; its first tap is already in fr[0].  Barrier and
 // refill as in lds16_row: the barrier follows the row's last ds_read; after
 // it `after_barrier` refills `brow`, and the next row's first tap (NEXT: halo
 // tap (NKD, NKH, KW0), buffer `brow_next`) is read into fr[0] while this
 // row's second products run.
-template <int KD, int KH, int KW0, bool NEXT, int NKD, int NKH, typename AfterBarrier>
+template <int DT, int KD, int KH, int KW0, bool NEXT, int NKD, int NKH, typename AfterBarrier>
 __device__ __forceinline__ void lds16_row2(f4 (&acc)[4][4], Lds16Frag (&fr)[2], const char* brow,
                                            const char* brow_next, const char* halo_p, const int (&abase)[4],
-                                           const int (&bbase)[4], int lane, AfterBarrier&& after_barrier) {
-  lds16_load<KD, KH, KW0 + 1, 1>(fr[1], brow, halo_p, abase, bbase, lane);
-  lds16_mma(acc, fr[0]);
+                                           const int (&bbase)[4], const int (&cbase)[4], int lane,
+                                           AfterBarrier&& after_barrier) {
+  lds16_load<DT, KD, KH, KW0 + 1, 1>(fr[1], brow, halo_p, abase, bbase, cbase, lane);
+  lds16_mma<DT>(acc, fr[0]);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   after_barrier();
-  if constexpr (NEXT) lds16_load<NKD, NKH, KW0, 0>(fr[0], brow_next, halo_p, abase, bbase, lane);
-  lds16_mma(acc, fr[1]);
+  if constexpr (NEXT) lds16_load<DT, NKD, NKH, KW0, 0>(fr[0], brow_next, halo_p, abase, bbase, cbase, lane);
+  lds16_mma<DT>(acc, fr[1]);
+}
+
+// Halo-fill geometry of a thread of conv_lds_bf16_kernel.
+struct Lds16Geo {
+  int tid, y0, x0, pd_max, ph_max, pw_max, P, Q, vbytes;
+};
+
+// Packed-copy byte offset (from the brick's first padded plane) of halo slot
+// tid + 256 i: slot s % 4 of halo voxel s / 4, coordinates past the padded
+// volume clamped (they feed only masked output rows).
+__device__ __forceinline__ int lds16_halo_offset(const Lds16Geo& g, int i) {
+  const int sl = g.tid + 256 * i;
+  const int v = sl >> 2, q = sl & 3;
+  const int hz = v / (kHH * kHW), hr = v - hz * (kHH * kHW);
+  const int hy = hr / kHW, hx = hr - hy * kHW;
+  const int pz = min(hz, g.pd_max), py = min(g.y0 + hy, g.ph_max), px = min(g.x0 + hx, g.pw_max);
+  return ((pz * g.P + py * g.Q + px) * g.vbytes) + 16 * (q ^ lds16_halo_swizzle(hy));
+}
+
+// Packed-weight byte offset (from a row's first tap) of weight-row fill slot
+// tid + 256 j.  bf16: slot s % 4 of column (s / 4) % 64 of tap j.  Split
+// fp16: slot s is in tap s / 384; its first 256 slots are the Bh pieces (slot
+// r: piece r % 4 of column r / 4, swizzled as bf16), the next 128 the Bl
+// pieces (piece r % 2 of column r / 2).
+template <int DT>
+__device__ __forceinline__ int lds16_weight_offset(int tid, int j, int n0, int tap_bytes) {
+  const int s = tid + 256 * j;
+  if constexpr (DT == CTMR_F16X2) {
+    const int t = s / 384, r = s - 384 * t;
+    if (r < 256) {
+      const int col = r >> 2;
+      return t * tap_bytes + (n0 + col) * 96 + 16 * ((r & 3) ^ row64_swizzle(col & 15));
+    }
+    const int col = (r - 256) >> 1;
+    return t * tap_bytes + (n0 + col) * 96 + 64 + 16 * (r & 1);
+  } else {
+    return j * tap_bytes + (n0 + (tid >> 2)) * 64 + 16 * ((tid & 3) ^ row64_swizzle((tid >> 2) & 15));
+  }
 }
 
 // UP: nearest-2x upsampling folded into 8 parity filters of 2x2x2 taps
@@ -1951,12 +2148,15 @@ __device__ __forceinline__ void lds16_row2(f4 (&acc)[4][4], Lds16Frag (&fr)[2], 
 // brick (z0, y0, x0) computes output voxels (2(z0 + z) + a, 2(y0 + y) + b,
 // 2(x0 + x) + c) from the same halo of the packed source copy as the 3x3x3
 // GEMM, reading its taps (a + td, b + th, c + tw), td, th, tw in {0, 1}: four
-// two-tap rows per 32-channel chunk.  The parity is part of the workgroup
-// index, so one launch covers all eight.
-template <bool UP>
+// two-tap rows per chunk.  The parity is part of the workgroup index, so one
+// launch covers all eight.  DT: CTMR_BF16 (32-channel chunks) or CTMR_F16X2
+// (16-channel chunks of hi/lo pairs, outputs scaled back by the packed
+// weight's power-of-two column scales before the epilogue).
+template <int DT, bool UP>
 __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
+  using Cfg = Lds16Cfg<DT>;
   __shared__ __attribute__((aligned(256))) char halo[kB16HaloBytes];
-  __shared__ __attribute__((aligned(256))) char bbuf[2][3 * kB16TapBytes];
+  __shared__ __attribute__((aligned(256))) char bbuf[2][Cfg::row_bytes];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nb = gridDim.x, bid = blockIdx.x;
@@ -1980,6 +2180,11 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   const int z0 = bz * kBD, y0 = by * kBH, x0 = bx * kBW;
   const int lrow = lane & 15, lgrp = lane >> 4;
   const int n0 = n_tile * 64;
+  if constexpr (DT == CTMR_F16X2) {
+    // the taps' zero slots read by lane groups 2 and 3 for Bl (published by
+    // the first chunk's barrier; fills never write them)
+    if (tid < 6) *reinterpret_cast<u4*>(&bbuf[tid / 3][(tid % 3) * kF2TapBytes + kF2ZeroOff]) = u4{0u, 0u, 0u, 0u};
+  }
 
   // Halo fill: slot s = tid + 256 i is slot s % 4 of halo voxel s / 4.  The
   // brick's halo origin in padded coordinates is (z0, y0, x0); coordinates
@@ -1989,51 +2194,52 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.xp + xbase), (short)0, (int)min(p.x_bytes - xbase, (int64_t)0x7fffffff), 0x00020000);
   const int pd_max = p.d + 1 - z0, ph_max = p.h + 1, pw_max = p.w + 1;
+  const Lds16Geo geo{tid, y0, x0, pd_max, ph_max, pw_max, p.P, p.Q, p.vbytes};
+  // Split fp16 holds more operand registers (the Bl fragments): its fill
+  // offsets are recomputed per fill (a few VALU operations per chunk or row)
+  // instead of being kept in 15 registers.
+  constexpr bool kKeepOffsets = DT != CTMR_F16X2;
   int hoff[kB16HaloIters];
   unsigned hload = 0;
 #pragma unroll
   for (int i = 0; i < kB16HaloIters; ++i) {
-    const int sl = tid + 256 * i;
-    const int v = sl >> 2, q = sl & 3;
     hoff[i] = 0;
-    if (sl < kB16HaloSlots) {
+    if (tid + 256 * i < kB16HaloSlots) {
       hload |= 1u << i;
-      const int hz = v / (kHH * kHW), hr = v - hz * (kHH * kHW);
-      const int hy = hr / kHW, hx = hr - hy * kHW;
-      const int pz = min(hz, pd_max), py = min(y0 + hy, ph_max), px = min(x0 + hx, pw_max);
-      hoff[i] = ((pz * p.P + py * p.Q + px) * p.vbytes) + 16 * (q ^ lds16_halo_swizzle(hy));
+      if constexpr (kKeepOffsets) hoff[i] = lds16_halo_offset(geo, i);
     }
   }
-  // Weight-row fill: slot s = tid + 256 j is slot s % 4 of column (s / 4) % 64
-  // of tap j of the row.
-  const int tap_bytes = p.kb * p.np * 64;  // packed bytes between consecutive taps
-  int woff[kB16RowIters];
-  const unsigned wload = UP ? 3u : (1u << kB16RowIters) - 1;  // two taps per row with UP
+  // Weight-row fill (lds16_weight_offset).
+  const int tap_bytes = p.kb * p.np * Cfg::col_bytes;  // packed bytes between consecutive taps
+  constexpr int row_slots = (UP ? 2 : 3) * (DT == CTMR_F16X2 ? 384 : Cfg::tap_bytes / 16);
+  int woff[Cfg::row_iters];
 #pragma unroll
-  for (int j = 0; j < kB16RowIters; ++j)
-    woff[j] = j * tap_bytes + (n0 + (tid >> 2)) * 64 + 16 * ((tid & 3) ^ row64_swizzle((tid >> 2) & 15));
+  for (int j = 0; j < Cfg::row_iters; ++j) woff[j] = kKeepOffsets ? lds16_weight_offset<DT>(tid, j, n0, tap_bytes) : 0;
   auto fill_halo = [&](int chunk) {
     const int so = __builtin_amdgcn_readfirstlane(chunk * 64);
 #pragma unroll
     for (int i = 0; i < kB16HaloIters; ++i)
       if ((hload >> i) & 1u)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (lds_ptr_t)(halo + (i * 256 + wave * 64) * 16), 16,
-                                                 hoff[i], so, 0, 0);
+                                                 kKeepOffsets ? hoff[i] : lds16_halo_offset(geo, i), so, 0, 0);
   };
   // First tap of weight row `row`: 3 * row of the 27 (or 8 * phase + 2 * row
   // with UP), K block `chunk`.
   auto row_so = [&](int chunk, int row) {
     const int tap = UP ? 8 * phase + 2 * row : 3 * row;
-    return __builtin_amdgcn_readfirstlane((tap * p.kb + chunk) * p.np * 64);
+    return __builtin_amdgcn_readfirstlane((tap * p.kb + chunk) * p.np * Cfg::col_bytes);
   };
 
   int abase[4];
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms)
     abase[ms] = ((wave * kHH + ms + 4 * (lrow >> 3)) * kHW + (lrow & 7)) * 64;
-  int bbase[4];
+  int bbase[4], cbase[4];
 #pragma unroll
-  for (int ns = 0; ns < 4; ++ns) bbase[ns] = (ns * 16 + lrow) * 64 + 16 * (lgrp ^ row64_swizzle(lrow));
+  for (int ns = 0; ns < 4; ++ns) {
+    bbase[ns] = (ns * 16 + lrow) * 64 + 16 * (lgrp ^ row64_swizzle(lrow));
+    cbase[ns] = lgrp < 2 ? kF2BlOff + (ns * 16 + lrow) * 32 + 16 * lgrp : kF2ZeroOff;
+  }
 
   f4 acc[4][4];
 #pragma unroll
@@ -2049,9 +2255,13 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
   auto fill_row = [&](int chunk, int row, int buf) {
     const char* src = p.wp + row_so(chunk, row);
 #pragma unroll
-    for (int j = 0; j < kB16RowIters; ++j)
-      if ((wload >> j) & 1u)
-        lds_dma16(src + woff[j], (unsigned)(uintptr_t)(lds_ptr_t)(&bbuf[buf][0] + (j * 256 + wave * 64) * 16));
+    for (int j = 0; j < Cfg::row_iters; ++j)
+      if (j * 256 + wave * 64 < row_slots) {  // wave-uniform
+        const int q = 4 * j + wave;  // wave block of 64 slots; split fp16 skips each tap's zero slot
+        const int slot0 = 64 * q + (DT == CTMR_F16X2 ? q / 6 : 0);
+        lds_dma16(src + (kKeepOffsets ? woff[j] : lds16_weight_offset<DT>(tid, j, n0, tap_bytes)),
+                  (unsigned)(uintptr_t)(lds_ptr_t)(&bbuf[buf][0] + slot0 * 16));
+      }
   };
   fill_halo(c_begin);
   fill_row(c_begin, 0, 0);
@@ -2066,10 +2276,10 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
         __syncthreads();
         const bool more = chunk + 1 < c_end;
         Lds16Frag fr[2];
-        lds16_load<A, B, C, 0>(fr[0], &bbuf[k & 1][0], halo, abase, bbase, lane);
+        lds16_load<DT, A, B, C, 0>(fr[0], &bbuf[k & 1][0], halo, abase, bbase, cbase, lane);
 #define CTMR_LDS16_UP_ROW(R, NEXT)                                                                        \
-        lds16_row2<A + (R) / 2, B + (R) % 2, C, NEXT, A + ((R) + 1) / 2, B + ((R) + 1) % 2>(                \
-            acc, fr, &bbuf[k & 1][0], &bbuf[(k + 1) & 1][0], halo, abase, bbase, lane, [&]() {               \
+        lds16_row2<DT, A + (R) / 2, B + (R) % 2, C, NEXT, A + ((R) + 1) / 2, B + ((R) + 1) % 2>(            \
+            acc, fr, &bbuf[k & 1][0], &bbuf[(k + 1) & 1][0], halo, abase, bbase, cbase, lane, [&]() {        \
               if ((R) < 2) fill_row(chunk, (R) + 2, k & 1);                                                 \
               else if (more) fill_row(chunk + 1, (R) - 2, k & 1);                                           \
               if ((R) == 3 && more) fill_halo(chunk + 1);                                                   \
@@ -2099,10 +2309,10 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
     __syncthreads();
     const bool more = chunk + 1 < c_end;
     Lds16Frag fr[2];
-    lds16_load<0, 0, 0>(fr[0], &bbuf[k & 1][0], halo, abase, bbase, lane);
+    lds16_load<DT, 0, 0, 0>(fr[0], &bbuf[k & 1][0], halo, abase, bbase, cbase, lane);
 #define CTMR_LDS16_ROW(R)                                                                                   \
-    lds16_row<(R), (R) < 8>(acc, fr, &bbuf[k & 1][0], &bbuf[(k + 1) & 1][0], halo, abase, bbase, lane,     \
-                            [&]() {                                                                        \
+    lds16_row<DT, (R), (R) < 8>(acc, fr, &bbuf[k & 1][0], &bbuf[(k + 1) & 1][0], halo, abase, bbase, cbase,  \
+                                lane, [&]() {                                                               \
       if ((R) < 7) fill_row(chunk, (R) + 2, k & 1);                                                        \
       else if (more) fill_row(chunk + 1, (R) - 7, k & 1);                                                  \
       if ((R) == 8 && more) fill_halo(chunk + 1);                                                          \
@@ -2114,6 +2324,16 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
 #undef CTMR_LDS16_ROW
   }
 
+  if constexpr (DT == CTMR_F16X2) {
+    // undo the weights' power-of-two column scales (exact), per partial plane alike
+    const float* colscale = reinterpret_cast<const float*>(p.wp + p.w_bytes);
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) {
+      const f4 sc = *reinterpret_cast<const f4*>(colscale + n0 + ns * 16 + 4 * lgrp);
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) acc[ms][ns] *= sc;
+    }
+  }
   store_brick<UP>(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, ((bz * p.ty + by) * p.tx + bx) * (UP ? 8 : 1) + phase,
                   reinterpret_cast<double (*)[64][2]>(halo), phase);  // the reduction buffer reuses the halo
 }
@@ -2350,7 +2570,7 @@ __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[ms][ns]), orsrc,
-                                               q_off[ns] + ms * 16 * p.cout * 4, 0, kOutStorePolicy);
+                                               q_off[ns] + ms * 16 * p.cout * 4, 0, kStoreNT);
     if (p.stats) {  // a kernel argument: every thread reaches the barriers
       bool row_ok[4], col_ok[NSUB];
 #pragma unroll
@@ -2543,7 +2763,8 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   if (!d) return fail(CTMR_E_INVALID, "null descriptor");
   if (d->n <= 0 || d->d <= 0 || d->h <= 0 || d->w <= 0 || d->cin <= 0 || d->cout <= 0)
     return fail(CTMR_E_INVALID, "non-positive dimension");
-  if (d->dtype != CTMR_F32 && d->dtype != CTMR_BF16) return fail(CTMR_E_INVALID, "bad dtype");
+  if (d->dtype != CTMR_F32 && d->dtype != CTMR_BF16 && d->dtype != CTMR_F16X2)
+    return fail(CTMR_E_INVALID, "bad dtype");
   if (d->ksize != 1 && d->ksize != 3) return fail(CTMR_E_UNSUPPORTED, "ksize must be 1 or 3");
   if (d->stride != 1 && d->stride != 2) return fail(CTMR_E_UNSUPPORTED, "stride must be 1 or 2");
   if (d->mode < CTMR_MODE_PLAIN || d->mode > CTMR_MODE_TRILINEAR2X)
@@ -2561,8 +2782,8 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   if (g.cat && d->mode != CTMR_MODE_PLAIN)
     return fail(CTMR_E_UNSUPPORTED, "a two-source input supports only CTMR_MODE_PLAIN");
   g.ks = d->ksize;
-  g.kstep = d->dtype == CTMR_F32 ? 16 : 32;
-  g.esize = d->dtype == CTMR_F32 ? 4 : 2;
+  g.kstep = d->dtype == CTMR_BF16 ? 32 : 16;
+  g.esize = d->dtype == CTMR_BF16 ? 2 : 4;  // packed-copy bytes per channel (split fp16: hi + lo)
   g.np = (int)round_up(d->cout, 16);
   g.phases = 1;
   if (d->ksize == 3) {
@@ -2766,17 +2987,22 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // the halo fill's 32-bit offsets span 6 packed planes.
   g.lds16 = false;
   g.small_out = false;
-  if (g.layout == WL_TAPS && d->dtype == CTMR_BF16 && d->ksize == 3 && d->stride == 1 && d->cout % 64 == 0 &&
-      !(d->flags & CTMR_F_STREAM)) {
+  if (g.layout == WL_TAPS && (d->dtype == CTMR_BF16 || d->dtype == CTMR_F16X2) && d->ksize == 3 &&
+      d->stride == 1 && d->cout % 64 == 0 && !(d->flags & CTMR_F_STREAM)) {
     const int tz = (int)ceil_div(g.gd, kBD), ty = (int)ceil_div(g.gh, kBH), tx = (int)ceil_div(g.gw, kBW);
     const int64_t slots = (int64_t)tz * ty * tx * kBD * kBH * kBW;
-    const int64_t planes = (int64_t)kHD * g.P * g.cp * 2;
-    const int64_t w_bytes = (int64_t)g.taps * g.phases * g.kblocks * g.np * 64;
+    const int64_t planes = (int64_t)kHD * g.P * g.cp * g.esize;
+    const int64_t w_bytes = (int64_t)g.taps * g.phases * g.kblocks * g.np * (d->dtype == CTMR_F16X2 ? 96 : 64);
     if (2 * S >= slots && planes < (1ll << 31) && w_bytes < (1ll << 31) && brick_out_fits) {
       g.lds16 = true;
       g.tz = tz; g.ty = ty; g.tx = tx;
     }
   }
+  // Split fp16 runs only on the LDS-staged 16-bit GEMM.
+  if (d->dtype == CTMR_F16X2 && !g.lds16)
+    return fail(CTMR_E_UNSUPPORTED,
+                "split fp16 (CTMR_F16X2) needs a stride-1 3x3x3 conv with cin >= 16, cout % 64 == 0, 4x8x8 bricks "
+                "at least half full and no CTMR_F_STREAM");
   // Plain fp32 3x3x3 convs whose channels fill whole 16-channel K blocks
   // need no packed copy: the streaming GEMM reads x itself, with out-of-range
   // offsets for taps outside the volume (the padded copy's zeros).  Its lane
@@ -2811,7 +3037,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     if (d->split > 1) return fail(CTMR_E_INVALID, "split must be 1 for the cout <= 4 tap-expanded GEMM");
     g.split = 1;
   } else if (g.lds16) {  // chunk-range split, as the fp32 LDS GEMM
-    if (d->split > g.kblocks) return fail(CTMR_E_INVALID, "split must not exceed the 32-channel chunk count");
+    if (d->split > g.kblocks) return fail(CTMR_E_INVALID, "split must not exceed the chunk count");
     const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases;
     g.split = d->split > 0 ? d->split
                            : (base < 512 ? (int)std::min<int64_t>(ceil_div(512, base), g.kblocks) : 1);
@@ -3027,7 +3253,31 @@ int ctmr_conv3d_output_dims(const ctmr_conv_desc* desc, int32_t out[3]) {
   return CTMR_OK;
 }
 
+// Packed-weight geometry of a split-fp16 (CTMR_F16X2) weight, which does not
+// depend on the input grid: [phase][tap][16-channel block][np][96 bytes], then
+// np fp32 column scales.
+static int split_weight_layout(const ctmr_conv_desc* d, int& phases, int& taps, int& kblocks, int& np,
+                               int64_t& block_bytes) {
+  if (!d) return fail(CTMR_E_INVALID, "null descriptor");
+  if (d->cin <= 0 || d->cout <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (d->ksize != 3) return fail(CTMR_E_UNSUPPORTED, "split fp16 (CTMR_F16X2) supports only 3x3x3 weights");
+  if (d->mode < CTMR_MODE_PLAIN || d->mode > CTMR_MODE_TRILINEAR2X) return fail(CTMR_E_INVALID, "bad mode");
+  phases = d->mode == CTMR_MODE_NEAREST2X ? 8 : 1;
+  taps = d->mode == CTMR_MODE_NEAREST2X ? 8 : 27;
+  kblocks = (int)ceil_div(d->cin, 16);
+  np = (int)round_up(d->cout, 16);
+  block_bytes = (int64_t)phases * taps * kblocks * np * 96;
+  return CTMR_OK;
+}
+
 int64_t ctmr_packed_weight_elems(const ctmr_conv_desc* desc) {
+  if (desc && desc->dtype == CTMR_F16X2) {
+    int phases, taps, kblocks, np;
+    int64_t bytes;
+    const int rc = split_weight_layout(desc, phases, taps, kblocks, np, bytes);
+    if (rc) return rc;
+    return (bytes + (int64_t)np * 4) / 2;
+  }
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
@@ -3055,7 +3305,7 @@ int ctmr_conv3d_kernel(const ctmr_conv_desc* desc) {
   if (rc) return rc;
   if (g.lds) return CTMR_K_LDS;
   if (g.lds_small) return CTMR_K_LDS_SMALL;
-  if (g.lds16) return CTMR_K_LDS_BF16;
+  if (g.lds16) return desc->dtype == CTMR_F16X2 ? CTMR_K_LDS_F16X2 : CTMR_K_LDS_BF16;
   if (g.small_out) return CTMR_K_SMALL_COUT;
   if (g.layout == WL_EXPAND) return CTMR_K_TAP_EXPAND;
   if (g.kws) return CTMR_K_SPLIT_WAVES;
@@ -3065,6 +3315,34 @@ int ctmr_conv3d_kernel(const ctmr_conv_desc* desc) {
 
 static int pack_weight_impl(const ctmr_conv_desc* desc, const float* weight, void* packed,
                             void* stream, bool up) {
+  if (desc && desc->dtype == CTMR_F16X2) {
+    WPackArgs a;
+    int64_t bytes;
+    int rc = split_weight_layout(desc, a.phases, a.taps, a.kblocks, a.np, bytes);
+    if (rc) return rc;
+    if (!weight || !packed) return fail(CTMR_E_INVALID, "null pointer");
+    if (up != (desc->mode == CTMR_MODE_NEAREST2X))
+      return fail(CTMR_E_INVALID, up ? "ctmr_pack_upsample_weight needs CTMR_MODE_NEAREST2X"
+                                     : "use ctmr_pack_upsample_weight for CTMR_MODE_NEAREST2X");
+    if (((uintptr_t)packed & 15) != 0) return fail(CTMR_E_INVALID, "packed weight must be 16-byte aligned");
+    a.w = weight;
+    a.out = packed;
+    a.cout = desc->cout;
+    a.cin = desc->cin;
+    a.ks = 3;
+    a.kstep = 16;
+    a.up = up ? 1 : 0;
+    a.bf16 = 0;
+    a.layout = WL_TAPS;
+    a.colscale = reinterpret_cast<float*>(reinterpret_cast<char*>(packed) + bytes);
+    a.total = (int64_t)a.phases * a.taps * a.kblocks * a.np * 16;
+    hipLaunchKernelGGL(weight_colscale_kernel, dim3((unsigned)ceil_div(a.np, 256)), dim3(256), 0,
+                       (hipStream_t)stream, a);
+    if ((rc = check_launch("weight_colscale"))) return rc;
+    hipLaunchKernelGGL(pack_weight_split_kernel, dim3(elementwise_blocks(a.total)), dim3(256), 0,
+                       (hipStream_t)stream, a);
+    return check_launch("pack_weight_split");
+  }
   Geometry g;
   int rc = geometry(desc, g);
   if (rc) return rc;
@@ -3073,6 +3351,8 @@ static int pack_weight_impl(const ctmr_conv_desc* desc, const float* weight, voi
     return fail(CTMR_E_INVALID, up ? "ctmr_pack_upsample_weight needs CTMR_MODE_NEAREST2X"
                                    : "use ctmr_pack_upsample_weight for CTMR_MODE_NEAREST2X");
   WPackArgs a;
+  a.phases = g.phases;
+  a.colscale = nullptr;
   a.w = weight;
   a.out = packed;
   a.cout = desc->cout;
@@ -3172,9 +3452,11 @@ static int pack_impl(const ctmr_conv_desc* desc, const float* x, const float* x2
   pa.silu_on = (desc->flags & CTMR_F_SILU) != 0;
   pa.trilinear = desc->mode == CTMR_MODE_TRILINEAR2X;
   pa.bf16 = desc->dtype == CTMR_BF16;
+  pa.split16 = desc->dtype == CTMR_F16X2;
   pa.total4 = (int64_t)desc->n * g.rows_per_batch * (g.cp / 4);
   pa.n = desc->n;
-  const int64_t plane_items = (int64_t)(g.th + 2 * g.halo) * (g.tw + 2 * g.halo) * (g.cp / (pa.bf16 ? 8 : 4));
+  const int64_t plane_items =
+      (int64_t)(g.th + 2 * g.halo) * (g.tw + 2 * g.halo) * (g.cp / (pa.bf16 || pa.split16 ? 8 : 4));
   const int64_t planes = (int64_t)desc->n * (g.td + 2 * g.halo);
   if (plane_items >= (1ll << 31)) return fail(CTMR_E_UNSUPPORTED, "padded plane too large for the pack");
   const bool vec = (desc->cin & 3) == 0 && (!pa.affine_on || ((uintptr_t)affine & 15) == 0);
@@ -3188,23 +3470,24 @@ static int pack_impl(const ctmr_conv_desc* desc, const float* x, const float* x2
     const int zc = long_runs ? 8 : 1;
     const int64_t runs = (int64_t)desc->n * ceil_div(desc->d + 2, zc);
     const dim3 grid((unsigned)ceil_div(cells, 256), (unsigned)std::min<int64_t>(runs, 65535));
+    const hipStream_t ts = (hipStream_t)stream;
     if (long_runs) {
-      if (pa.bf16)
-        hipLaunchKernelGGL((pack_trilinear_kernel<true, 8>), grid, dim3(256), 0, (hipStream_t)stream, pa);
-      else
-        hipLaunchKernelGGL((pack_trilinear_kernel<false, 8>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+      if (pa.split16) hipLaunchKernelGGL((pack_trilinear_kernel<PF_SPLIT, 8>), grid, dim3(256), 0, ts, pa);
+      else if (pa.bf16) hipLaunchKernelGGL((pack_trilinear_kernel<PF_BF16, 8>), grid, dim3(256), 0, ts, pa);
+      else hipLaunchKernelGGL((pack_trilinear_kernel<PF_F32, 8>), grid, dim3(256), 0, ts, pa);
     } else {
-      if (pa.bf16)
-        hipLaunchKernelGGL((pack_trilinear_kernel<true, 1>), grid, dim3(256), 0, (hipStream_t)stream, pa);
-      else
-        hipLaunchKernelGGL((pack_trilinear_kernel<false, 1>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+      if (pa.split16) hipLaunchKernelGGL((pack_trilinear_kernel<PF_SPLIT, 1>), grid, dim3(256), 0, ts, pa);
+      else if (pa.bf16) hipLaunchKernelGGL((pack_trilinear_kernel<PF_BF16, 1>), grid, dim3(256), 0, ts, pa);
+      else hipLaunchKernelGGL((pack_trilinear_kernel<PF_F32, 1>), grid, dim3(256), 0, ts, pa);
     }
     return check_launch("pack_trilinear");
   }
   if (vec && !pa.trilinear) {
     constexpr int PZ = 4;
     const dim3 grid((unsigned)ceil_div(plane_items, 256), (unsigned)std::min<int64_t>(ceil_div(planes, PZ), 65535));
-    if (pa.bf16)
+    if (pa.split16)
+      hipLaunchKernelGGL((pack_planes_kernel<2, PZ, true>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+    else if (pa.bf16)
       hipLaunchKernelGGL((pack_planes_kernel<2, PZ>), grid, dim3(256), 0, (hipStream_t)stream, pa);
     else
       hipLaunchKernelGGL((pack_planes_kernel<1, PZ>), grid, dim3(256), 0, (hipStream_t)stream, pa);
@@ -3366,12 +3649,13 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.bias = bias;
     a.res = residual;
     a.rows_per_batch = g.rows_per_batch;
-    a.x_bytes = (int64_t)desc->n * g.rows_per_batch * g.cp * 2;
-    a.w_bytes = (int64_t)g.taps * g.phases * g.kblocks * g.np * 64;
+    const bool f16x2 = desc->dtype == CTMR_F16X2;
+    a.x_bytes = (int64_t)desc->n * g.rows_per_batch * g.cp * g.esize;
+    a.w_bytes = (int64_t)g.taps * g.phases * g.kblocks * g.np * (f16x2 ? 96 : 64);
     a.plane = (int64_t)desc->n * s_out * desc->cout;
     a.d = g.gd; a.h = g.gh; a.w = g.gw;
     a.P = g.P; a.Q = g.Q;
-    a.vbytes = g.cp * 2;
+    a.vbytes = g.cp * g.esize;
     a.cout = desc->cout; a.np = g.np; a.kb = g.kblocks; a.n = desc->n;
     a.tz = g.tz; a.ty = g.ty; a.tx = g.tx;
     a.n_tiles = g.n_tiles;
@@ -3386,10 +3670,15 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.y = g.split > 1 ? part : y;
     if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
     const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
-    if (g.phases == 8)
-      hipLaunchKernelGGL(conv_lds_bf16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL(conv_lds_bf16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    if (f16x2 && ((uintptr_t)packed & 15) != 0) return fail(CTMR_E_INVALID, "packed weight must be 16-byte aligned");
+    const dim3 grid((unsigned)blocks), block(256);
+    if (f16x2) {
+      if (g.phases == 8) hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_F16X2, true>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_F16X2, false>), grid, block, 0, st, a);
+    } else {
+      if (g.phases == 8) hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_BF16, true>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_BF16, false>), grid, block, 0, st, a);
+    }
     if ((rc = check_launch("conv_lds_bf16"))) return rc;
     if (g.split > 1) {
       launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);

@@ -15,6 +15,8 @@ namespace ctmr {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 // Message for the last failing call on this thread (ctmr_last_error).
 void set_error(const char* fmt, ...);
@@ -51,6 +53,19 @@ __device__ __forceinline__ unsigned short f32_to_bf16_bits(float v) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (unsigned short)(u >> 16);
+}
+
+// Split-fp16 operand of an fp32 value v (CTMR_F16X2): hi = fp16(v) and
+// lo = fp16((v - hi) * 2^11), both rounded to nearest even.  v - hi is exact
+// in fp32 (at most 13 significant bits) and the 2^11 scale keeps lo a normal
+// fp16 for |v| down to about 2^-14, so hi + lo * 2^-11 holds v to about 2^-22
+// relative.  |v| must stay below 65504 (the fp16 range of hi).
+__device__ __forceinline__ void split_f16x4(f4 v, h4& hi, h4& lo) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    hi[k] = (_Float16)v[k];
+    lo[k] = (_Float16)((v[k] - (float)hi[k]) * 2048.0f);
+  }
 }
 
 // SiLU y * sigmoid(y) = y / (1 + e^-y), with e^-y = 2^(-y log2 e) on the

@@ -9,7 +9,9 @@ hand-written HIP kernels of ``libctmr_hip.so``:
 * padding-1 3x3x3 convolutions (stride 1/2, nearest-2x folded into parity
   weights, trilinear-2x computed while packing the input) and 1x1x1
   convolutions are implicit GEMMs on FP32 MFMA (or bf16 MFMA with fp32
-  accumulation inside ``precision("bf16")``);
+  accumulation inside ``precision("bf16")``, or split fp16 -- the reference's
+  "exact" mode for fp32 tensors, _nax_conv.py:27-35 -- on fp16 MFMA inside
+  ``precision("f16x2")``);
 * a preceding group norm + SiLU is applied while packing the convolution
   input; bias, the residual block's per-batch time-embedding bias and the
   residual join the fp32 sum before the single store;
@@ -25,6 +27,7 @@ linear ``(O, I)``.
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import math
 import threading
 import weakref
@@ -40,15 +43,24 @@ from . import _lib, ops
 
 # ---------------------------------------------------------------------------
 # precision selection (the reference's request-scoped arithmetic switch,
-# arithmetic_mode.py:28-60, reduced to the two MFMA variants of this path)
+# arithmetic_mode.py:28-60, reduced to the MFMA variants of this path)
 # ---------------------------------------------------------------------------
-PRECISIONS = ("fp32", "bf16")
+PRECISIONS = ("fp32", "bf16", "f16x2")
+_DTYPE_CODES = {"fp32": _lib.DT_F32, "bf16": _lib.DT_BF16, "f16x2": _lib.DT_F16X2}
+_PACKED_DTYPES = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16X2}
 _precision: ContextVar[str] = ContextVar("ctmr_precision", default="fp32")
 
 
 @contextlib.contextmanager
 def precision(mode: str) -> Iterator[None]:
-    """Select ``"fp32"`` (FP32 MFMA) or ``"bf16"`` (bf16 MFMA, fp32 accumulate) convs."""
+    """Select ``"fp32"`` (FP32 MFMA), ``"bf16"`` (bf16 MFMA, fp32 accumulate) or ``"f16x2"`` convs.
+
+    ``"f16x2"`` is the reference's exact mode for fp32 tensors (``_nax_conv.py:27-35``): each fp32
+    value is split into an fp16 high half and an fp16 low half scaled by 2^11, weights are scaled per
+    output column by a power of two, and every product is summed as hi*hi + lo*hi + hi*lo on fp16
+    MFMA with fp32 accumulation (about 2^-22 relative per product).  It applies to the stride-1
+    3x3x3 convs the LDS-staged 16-bit GEMM takes (cout a multiple of 64, at least 16 input
+    channels); every other conv runs on FP32 MFMA.  Values must stay below 65504 in magnitude."""
     if mode not in PRECISIONS:
         raise ValueError(f"precision must be one of {PRECISIONS}; got {mode!r}")
     token = _precision.set(mode)
@@ -63,7 +75,7 @@ def active_precision() -> str:
 
 
 def _dtype_code() -> int:
-    return _lib.DT_BF16 if _precision.get() == "bf16" else _lib.DT_F32
+    return _DTYPE_CODES[_precision.get()]
 
 
 # ---------------------------------------------------------------------------
@@ -206,8 +218,9 @@ def cached_derived(cache: dict, lock: threading.Lock, key: tuple, sources: tuple
 
 
 def pack_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tensor:
-    """Packed ``(O, C, k, k, k)`` weight for ``implicit_gemm_conv3d`` (``_nax_conv.pack_weight``)."""
-    code = _lib.DT_BF16 if (dtype or _precision.get()) == "bf16" else _lib.DT_F32
+    """Packed ``(O, C, k, k, k)`` weight for ``implicit_gemm_conv3d`` (``_nax_conv.pack_weight``);
+    ``dtype`` one of ``PRECISIONS`` (default: the active precision)."""
+    code = _DTYPE_CODES[dtype or _precision.get()]
     w = weight.to(torch.float32).contiguous()
     o, c, k = int(w.shape[0]), int(w.shape[1]), int(w.shape[2])
     return ops.pack_weight(w, c, o, k, _lib.MODE_PLAIN, code)
@@ -215,7 +228,7 @@ def pack_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tensor:
 
 def pack_upsample_weight(weight: Tensor, *, dtype: Optional[str] = None) -> Tensor:
     """Eight 2x2x2 nearest-2x parity filters folded in fp32 (``_nax_conv.pack_upsample_weight``)."""
-    code = _lib.DT_BF16 if (dtype or _precision.get()) == "bf16" else _lib.DT_F32
+    code = _DTYPE_CODES[dtype or _precision.get()]
     w = weight.to(torch.float32).contiguous()
     if tuple(w.shape[2:]) != (3, 3, 3):
         raise ValueError("upsample packing needs a 3x3x3 weight")
@@ -240,12 +253,35 @@ def _keeps_fp32(weight: Tensor) -> bool:
     return k == 1 or o <= 4 or c <= 8
 
 
-def _pack(weight: Tensor, mode: int) -> Tensor:
-    """Packed weight for the active precision (``_keeps_fp32`` convs stay fp32 under bf16)."""
+_split_routes: dict[tuple, bool] = {}
+
+
+def _f16x2_route(x_shape: tuple[int, ...], cout: int, mode: int, stride: int, cin2: int) -> bool:
+    """Whether a conv of this shape runs on the split-fp16 GEMM (``ctmr_conv3d_kernel`` accepts the
+    descriptor with ``CTMR_F16X2``); a function of the shape only, cached."""
+    key = (x_shape, cout, mode, stride, cin2)
+    hit = _split_routes.get(key)
+    if hit is None:
+        desc = ops.make_desc(x_shape, cout, 3, stride, mode, 0, _lib.DT_F16X2, 0, cin2)
+        hit = _lib.lib().ctmr_conv3d_kernel(ctypes.byref(desc)) == _lib.K_LDS_F16X2
+        _split_routes[key] = hit
+    return hit
+
+
+def _pack(weight: Tensor, mode: int, x=None, stride: int = 1) -> Tensor:
+    """Packed weight for the active precision (``_keeps_fp32`` convs stay fp32 under bf16; under
+    f16x2 only convs of ``x``'s shape that the split-fp16 GEMM takes are packed for it)."""
     if not isinstance(weight, Tensor) or weight.device.type != "cuda":
         raise ValueError("conv weight must be a torch.Tensor on the GPU (there is no CPU path)")
     code = _lib.DT_F32 if _keeps_fp32(weight) else _dtype_code()
-    dtype = "bf16" if code == _lib.DT_BF16 else "fp32"
+    if code == _lib.DT_F16X2:
+        first, second = (x.first, x.second) if isinstance(x, ChannelCat) else (x, None)
+        ok = (first is not None and weight.dim() == 5 and int(weight.shape[2]) == 3 and
+              _f16x2_route(tuple(int(v) for v in first.shape), int(weight.shape[0]), mode, stride,
+                           0 if second is None else int(second.shape[-1])))
+        if not ok:
+            code = _lib.DT_F32
+    dtype = {v: k for k, v in _DTYPE_CODES.items()}[code]
     packer = pack_upsample_weight if mode == _lib.MODE_NEAREST2X else pack_weight
     return cached_derived(_packed, _packed_lock, ("conv", mode, code, id(weight)), (weight,),
                           lambda: packer(weight, dtype=dtype))
@@ -329,13 +365,15 @@ def implicit_gemm_conv3d(
     if ksize == 1 and (upsample or trilinear or stride != 1):
         raise ValueError("1x1x1 convolution supports only stride 1 without resampling")
     mode = _lib.MODE_NEAREST2X if upsample else (_lib.MODE_TRILINEAR2X if trilinear else _lib.MODE_PLAIN)
-    code = _lib.DT_BF16 if packed.dtype == torch.bfloat16 else _lib.DT_F32
+    code = _PACKED_DTYPES.get(packed.dtype)
+    if code is None:
+        raise ValueError(f"packed weight dtype {packed.dtype} is not one this library writes")
     desc = ops.make_desc(tuple(x.shape), cout, ksize, stride, mode, _lib.F_STREAM if stream_gemm else 0, code,
                          split, cin2)
     if packed.numel() != _lib.packed_weight_elems(desc):
         raise ValueError(
             f"packed weight of {packed.numel()} elements does not fit {cin} input / {cout} output "
-            f"channels ({'nearest-2x' if upsample else 'plain'}, {'bf16' if code else 'fp32'})"
+            f"channels ({'nearest-2x' if upsample else 'plain'}, {('fp32', 'bf16', 'f16x2')[code]})"
         )
     bias = _vec(bias, cout, "bias", x.device)
     if bias is not None and bias.dim() == 2 and bias.shape[0] != n:
@@ -385,7 +423,7 @@ def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], *, padding: int, s
         raise ValueError("1x1x1 convolution supports only stride 1")
     if int(weight.shape[1]) != int(x.shape[-1]):
         raise ValueError(f"weight expects {int(weight.shape[1])} input channels; x has {int(x.shape[-1])}")
-    return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_PLAIN), bias, cout=int(weight.shape[0]),
+    return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_PLAIN, x, stride), bias, cout=int(weight.shape[0]),
                                 ksize=k, stride=stride, gn_groups=gn_groups)
 
 
@@ -464,13 +502,13 @@ def norm_conv3d(
         x = _require(x, "x")
     affine = None if norm is None else group_norm_affine(x, norm[0], norm[1], groups=num_groups, eps=eps)
     mode = _lib.MODE_NEAREST2X if upsample else _lib.MODE_PLAIN
-    return implicit_gemm_conv3d(x, _pack(weight, mode), bias, cout=int(weight.shape[0]), affine=affine,
+    return implicit_gemm_conv3d(x, _pack(weight, mode, x), bias, cout=int(weight.shape[0]), affine=affine,
                                 silu=apply_silu, upsample=upsample, residual=residual, gn_groups=out_gn_groups)
 
 
 def trilinear_conv3d(x: Tensor, weight: Tensor, bias: Tensor, *, gn_groups: int = 0) -> Tensor:
     """Padding-1 3x3x3 conv of the trilinear 2x upsampling, sampled while packing (:339-349)."""
-    return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_PLAIN), bias, cout=int(weight.shape[0]),
+    return implicit_gemm_conv3d(x, _pack(weight, _lib.MODE_TRILINEAR2X, x), bias, cout=int(weight.shape[0]),
                                 trilinear=True, gn_groups=gn_groups)
 
 

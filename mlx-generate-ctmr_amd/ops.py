@@ -74,14 +74,18 @@ def _cin2(x2: Optional[Tensor]) -> int:
 # ---------------------------------------------------------------------------
 # weight packing
 # ---------------------------------------------------------------------------
+# element type of a packed weight per ctmr_dtype (split fp16: 16-bit halves and the fp32 column
+# scales, as raw 16-bit elements)
+_PACKED_TORCH_DTYPES = {_lib.DT_F32: torch.float32, _lib.DT_BF16: torch.bfloat16, _lib.DT_F16X2: torch.float16}
+
+
 @torch.library.custom_op("ctmr::pack_weight", mutates_args=())
 def pack_weight(weight: Tensor, cin: int, cout: int, ksize: int, mode: int, dtype: int) -> Tensor:
     """Packed conv weight (``ctmr_pack_weight`` / ``ctmr_pack_upsample_weight``)."""
     _require_device(weight)
     desc = _lib.conv_desc(1, 2, 2, 2, cin, cout, ksize=ksize, mode=mode, dtype=dtype)
     elems = _lib.packed_weight_elems(desc)
-    out = torch.empty(elems, device=weight.device,
-                      dtype=torch.float32 if dtype == _lib.DT_F32 else torch.bfloat16)
+    out = torch.empty(elems, device=weight.device, dtype=_PACKED_TORCH_DTYPES[dtype])
     fn = _lib.lib().ctmr_pack_upsample_weight if mode == _lib.MODE_NEAREST2X else _lib.lib().ctmr_pack_weight
     _lib.check(fn(ctypes.byref(desc), weight.data_ptr(), out.data_ptr(), _stream(weight.device)),
                "ctmr_pack_weight")
@@ -91,8 +95,7 @@ def pack_weight(weight: Tensor, cin: int, cout: int, ksize: int, mode: int, dtyp
 @pack_weight.register_fake
 def _(weight, cin, cout, ksize, mode, dtype):
     desc = _lib.conv_desc(1, 2, 2, 2, cin, cout, ksize=ksize, mode=mode, dtype=dtype)
-    return weight.new_empty(_lib.packed_weight_elems(desc),
-                            dtype=torch.float32 if dtype == _lib.DT_F32 else torch.bfloat16)
+    return weight.new_empty(_lib.packed_weight_elems(desc), dtype=_PACKED_TORCH_DTYPES[dtype])
 
 
 # ---------------------------------------------------------------------------
