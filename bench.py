@@ -41,6 +41,9 @@ sys.path.insert(0, str(REPO))
 FP32_PEAK = 157.3e12
 BF16_PEAK = 2516.6e12
 HBM_PEAK = 8.0e12
+# split fp16 (CTMR_F16X2): per fp32 multiply-add two K=32 fp16 MFMAs over 16 channels (hi and lo of the
+# input against the weight's hi, then against its lo): 4 fp16 MFMA FLOPs per algorithmic FLOP
+F16X2_PEAK = BF16_PEAK / 4
 
 
 def progress(msg):
@@ -179,6 +182,13 @@ def secondary(pkg, dev, steps, cpu=False):
     progress(f"config 1 {ms:.3f} ms")
     out["config1_vae_resblock_128c_128^3"] = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 2),
                                               "frac_fp32_peak": round(flops / ms / 1e-3 / FP32_PEAK, 4)}
+    with f.precision("f16x2"):
+        for _ in range(2):
+            block()
+        msx = _wall_ms(block, max(2, steps // 4))
+    out["config1_vae_resblock_128c_128^3"].update({"f16x2_ms": round(msx, 3),
+                                                   "f16x2_tflops": round(flops / msx / 1e9, 2),
+                                                   "f16x2_frac_peak": round(flops / msx / 1e-3 / F16X2_PEAK, 4)})
     del x
     # config 2a: stride-2 conv 64->128, 128^3 -> 64^3
     xa = torch.from_numpy(rng.standard_normal((1, 128, 128, 128, 64), dtype=np.float32)).to(dev)
@@ -365,10 +375,22 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         gms16 = _wall_ms(gstep, max(3, steps // 2))
         del graph
     floor16 = (conv_f / BF16_PEAK + attn_f / FP32_PEAK) * 1e3
+    # split fp16 (the reference's exact mode): same floor rule with every conv at the split peak
+    with pkg.fast_fp32.precision("f16x2"):
+        for _ in range(2):
+            step()
+        msx = _wall_ms(step, max(3, steps // 2))
+        graph = m.UNetGraph(x, t, classes, spacing, uw, constructor=uc)
+        gmsx = _wall_ms(gstep, max(3, steps // 2))
+        del graph
+    progress(f"config 3 UNet step f16x2 {msx:.3f} ms, graph {gmsx:.3f} ms")
+    floorx = (conv_f / F16X2_PEAK + attn_f / FP32_PEAK) * 1e3
     out["config3_unet_step_batch2_64x64x32"].update(
         {"graph_ms": round(gms, 3), "graph_frac_roofline": round(floor_ms / gms, 4),
          "bf16_ms": round(ms16, 3), "bf16_graph_ms": round(gms16, 3), "bf16_roofline_ms": round(floor16, 3),
-         "bf16_frac_roofline": round(floor16 / min(ms16, gms16), 4)})
+         "bf16_frac_roofline": round(floor16 / min(ms16, gms16), 4),
+         "f16x2_ms": round(msx, 3), "f16x2_graph_ms": round(gmsx, 3), "f16x2_roofline_ms": round(floorx, 3),
+         "f16x2_frac_roofline": round(floorx / min(msx, gmsx), 4)})
     # CT from mask: ControlNetMaisi (production constructor, conditioning embedding computed once per
     # generation) + the UNet with its residuals, per denoising step
     cc = m.PRODUCTION_CONTROLNET_CONSTRUCTOR
@@ -384,12 +406,19 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         ct_step()
     ct_ms = _wall_ms(ct_step, max(3, steps // 2))
     ctrl_ms = _wall_ms(ctrl, max(3, steps // 2))
+    with pkg.fast_fp32.precision("f16x2"):
+        for _ in range(2):
+            ct_step()
+        ct_msx = _wall_ms(ct_step, max(3, steps // 2))
     cconv, cattn = controlnet_flops(cc, 2, 64, 64, 32)
     ct_flop = conv_f + attn_f + cconv + cattn
+    ct_floorx = ((conv_f + cconv) / F16X2_PEAK + (attn_f + cattn) / FP32_PEAK) * 1e3
     out["ct_controlnet_unet_step_batch2_64x64x32"] = {
         "ms": round(ct_ms, 3), "controlnet_ms": round(ctrl_ms, 3),
         "controlnet_tflop": round((cconv + cattn) / 1e12, 4), "tflops": round(ct_flop / ct_ms / 1e9, 2),
-        "roofline_ms": round(ct_flop / FP32_PEAK * 1e3, 3), "frac_roofline": round(ct_flop / FP32_PEAK * 1e3 / ct_ms, 4)}
+        "roofline_ms": round(ct_flop / FP32_PEAK * 1e3, 3), "frac_roofline": round(ct_flop / FP32_PEAK * 1e3 / ct_ms, 4),
+        "f16x2_ms": round(ct_msx, 3), "f16x2_roofline_ms": round(ct_floorx, 3),
+        "f16x2_frac_roofline": round(ct_floorx / ct_msx, 4)}
     del cw, cond_emb
     if cpu:
         from oracle import cpu_baseline as cb
@@ -439,9 +468,14 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         "output": [1, 256, 256, 256, 1]}
     with pkg.fast_fp32.precision("bf16"):
         sec16, _ = timed(decode)
+    with pkg.fast_fp32.precision("f16x2"):
+        secx, _ = timed(decode)
+    progress(f"config 4 decode f16x2 {secx:.3f} s")
     out["config4_vae_decode_256^3_4windows"].update(
         {"bf16_s": round(sec16, 4), "bf16_roofline_s": round(dec_f / BF16_PEAK, 4),
-         "bf16_frac_roofline": round(dec_f / BF16_PEAK / sec16, 4)})
+         "bf16_frac_roofline": round(dec_f / BF16_PEAK / sec16, 4),
+         "f16x2_s": round(secx, 4), "f16x2_roofline_s": round(dec_f / F16X2_PEAK, 4),
+         "f16x2_frac_roofline": round(dec_f / F16X2_PEAK / secx, 4)})
     if cpu:
         from oracle import cpu_baseline as cb
 
@@ -474,10 +508,19 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
 
         total, peak = timed(generate)
         progress(f"256^3 MR generation {total:.3f} s")
+        phases32 = list(phases)
+        phases.clear()
+        with pkg.fast_fp32.precision("f16x2"):
+            totalx, _ = timed(generate)
+        progress(f"256^3 MR generation f16x2 {totalx:.3f} s")
         gen_f = 30 * sum(unet_flops(uc, 2, 64, 64, 64)) + dec_f
+        gen_attn = 30 * unet_flops(uc, 2, 64, 64, 64)[1]
+        gen_floorx = (gen_f - gen_attn) / F16X2_PEAK + gen_attn / FP32_PEAK
         out["generation_256^3_30steps_cfg"] = {
-            "s": round(total, 3), "sampling_s": round(float(np.median(phases[1:])), 3), "tflop": round(gen_f / 1e12, 2),
+            "s": round(total, 3), "sampling_s": round(float(np.median(phases32[1:])), 3), "tflop": round(gen_f / 1e12, 2),
             "roofline_s": round(gen_f / FP32_PEAK, 3), "frac_roofline": round(gen_f / FP32_PEAK / total, 4),
+            "f16x2_s": round(totalx, 3), "f16x2_sampling_s": round(float(np.median(phases[1:])), 3),
+            "f16x2_roofline_s": round(gen_floorx, 3), "f16x2_frac_roofline": round(gen_floorx / totalx, 4),
             "target_s": 60, "timing": "median of 3 after 1 warm-up", "peak_device_GiB": round(peak / 2**30, 2),
             "image_dtype": "torch.int16"}
         del lat
@@ -601,7 +644,7 @@ def profile_only(pkg, dev, what, steps, warmup):
     import torch
 
     m, f = pkg.maisi, pkg.fast_fp32
-    if what in ("unet", "unet_bf16"):
+    if what in ("unet", "unet_bf16", "unet_f16x2"):
         uc = m.PRODUCTION_UNET_CONSTRUCTOR
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.unet_weight_shapes(uc), seed=7).items()}
         x = torch.from_numpy(np.random.default_rng(3).standard_normal((2, 64, 64, 32, 4), dtype=np.float32)).to(dev)
@@ -609,7 +652,7 @@ def profile_only(pkg, dev, what, steps, warmup):
         cls = torch.tensor([9, 0], device=dev)
         sp = m.spacing_tensor([0.94, 0.94, 1.36], device=dev).repeat(2, 1)
         fn = lambda: m.denoise_unet(x, t, cls, sp, w, constructor=uc)
-    elif what == "controlnet":
+    elif what in ("controlnet", "controlnet_f16x2"):
         # the CT step's ControlNet (production constructor, batch 2, conditioning embedding precomputed)
         cc = m.PRODUCTION_CONTROLNET_CONSTRUCTOR
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.controlnet_weight_shapes(cc), seed=13).items()}
@@ -619,20 +662,21 @@ def profile_only(pkg, dev, what, steps, warmup):
         t = torch.full((2,), 500.0, device=dev)
         cls = torch.tensor([9, 0], device=dev)
         fn = lambda: m.controlnet_residuals(x, t, cls, None, w, constructor=cc, conditioning_embedding=emb)
-    elif what in ("decode", "decode_bf16"):
+    elif what in ("decode", "decode_bf16", "decode_f16x2"):
         vc = m.PRODUCTION_VAE_CONSTRUCTOR
         w = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.vae_decoder_weight_shapes(vc), seed=11).items()}
         z = torch.from_numpy(np.random.default_rng(4).standard_normal((1, 20, 64, 64, 4), dtype=np.float32)).to(dev)
         fn = lambda: m.decode_vae(z, w, constructor=vc)
     elif what in ("gemms", "gemms_stream"):
-        # config-0 fp32 and bf16 GEMM kernels alone (one pack each), for counter passes; gemms_stream
-        # forces the register-streaming GEMM for the bf16 stage too (the LDS-staged one otherwise)
+        # config-0 fp32, bf16 and split-fp16 GEMM kernels alone (one pack each), for counter passes;
+        # gemms_stream forces the register-streaming GEMM for the bf16 stage (no split-fp16 stage)
         rng = np.random.default_rng(0)
         x = torch.from_numpy(rng.standard_normal((1, 64, 64, 64, 64), dtype=np.float32)).to(dev)
         w = torch.from_numpy((rng.standard_normal((64, 64, 3, 3, 3)) / np.sqrt(27 * 64)).astype(np.float32)).to(dev)
         b = torch.zeros(64, device=dev)
-        stages = [staged_op(pkg, x, w, b, code, stream_gemm=what == "gemms_stream")
-                  for code in (pkg._lib.DT_F32, pkg._lib.DT_BF16)]
+        codes = (pkg._lib.DT_F32, pkg._lib.DT_BF16) if what == "gemms_stream" else (
+            pkg._lib.DT_F32, pkg._lib.DT_BF16, pkg._lib.DT_F16X2)
+        stages = [staged_op(pkg, x, w, b, code, stream_gemm=what == "gemms_stream") for code in codes]
         for pack, _, _ in stages:
             pack()
 
@@ -670,7 +714,7 @@ def profile_only(pkg, dev, what, steps, warmup):
         b = torch.zeros(128, device=dev)
         g, z0 = torch.ones(128, device=dev), torch.zeros(128, device=dev)
         fn = lambda: f.vae_resblock([x], (w1, b), (w1, b), (g, z0), (g, z0), None, num_groups=32, eps=1e-6)
-    with f.precision("bf16" if what.endswith("_bf16") else "fp32"):
+    with f.precision(what.rsplit("_", 1)[1] if what.endswith(("_bf16", "_f16x2")) else "fp32"):
         warm_up(fn, warmup)
         ms = _wall_ms(fn, steps)
     print(json.dumps({"only": what, "ms": round(ms, 3), "steps": steps}), flush=True)
@@ -686,7 +730,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true", help="skip the config 1/2 measurements")
     ap.add_argument("--no-networks", action="store_true", help="skip configs 3/4 and the full generation")
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
-    ap.add_argument("--only", choices=["unet", "unet_bf16", "controlnet", "decode", "decode_bf16", "resblock",
+    ap.add_argument("--only", choices=["unet", "unet_bf16", "unet_f16x2", "controlnet", "controlnet_f16x2", "decode",
+                                       "decode_bf16", "decode_f16x2", "resblock", "resblock_f16x2",
                                        "attention", "pointwise", "gemms", "gemms_stream", "config2a", "config2b"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -751,6 +796,16 @@ def main() -> int:
         pack16()
         gemm16()
     bf16_ms = gemm_ms_in_context(pack16, gemm16, max(args.steps, 10))
+    # split-fp16 variant (the reference's exact mode on fp16 MFMA): the whole operator (pack + GEMM)
+    # and its GEMM kernel alone
+    with f.precision("f16x2"):
+        warm_up(step, args.warmup, settle_s=0.3)
+        x16_ms = _wall_ms(step, args.steps)
+    packx, gemmx, _keepx = staged_op(pkg, x, w, b, pkg._lib.DT_F16X2)
+    for _ in range(3):
+        packx()
+        gemmx()
+    x16_gemm_ms = gemm_ms_in_context(packx, gemmx, max(args.steps, 10))
 
     result = {
         "metric": "conv3d fp32 TFLOP/s (implicit GEMM, FP32 MFMA)",
@@ -780,7 +835,13 @@ def main() -> int:
         result["roofline"]["traffic"] = json.loads(traffic_file.read_text())["traffic_bytes"]
         result["roofline"]["traffic_source"] = "profiles/conv3d_config0_traffic.json"
     sec = {"config0_bf16_gemm": {"ms": round(bf16_ms, 4), "tflops": round(flops / bf16_ms / 1e9, 2),
-                                 "frac_bf16_peak": round(flops / (bf16_ms * 1e-3) / BF16_PEAK, 4)}}
+                                 "frac_bf16_peak": round(flops / (bf16_ms * 1e-3) / BF16_PEAK, 4)},
+           "config0_f16x2": {"ms": round(x16_ms, 4), "tflops": round(flops / x16_ms / 1e9, 2),
+                             "gemm_ms": round(x16_gemm_ms, 4), "gemm_tflops": round(flops / x16_gemm_ms / 1e9, 2),
+                             "gemm_frac_f16x2_peak": round(flops / (x16_gemm_ms * 1e-3) / F16X2_PEAK, 4),
+                             "f16x2_peak_tflops": round(F16X2_PEAK / 1e12, 1),
+                             "kernel": "conv_lds_bf16_kernel<CTMR_F16X2> (split fp16: 4 fp16 MFMA FLOPs per fp32 "
+                                       "FLOP; whole op = split pack + GEMM)"}}
     if not args.no_secondary:
         sec.update(secondary(pkg, dev, args.steps, cpu=not args.no_cpu))
     if not args.no_networks:

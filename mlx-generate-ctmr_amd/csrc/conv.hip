@@ -701,20 +701,30 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(WPackArgs a) {
 // (over every phase, tap and channel of the packed values, nearest-2x folds
 // included) times 2^k lies in [2^14, 2^15): fp16 holds the scaled weights'
 // hi and lo halves as normal numbers.  k = 0 for an all-zero column; k is
-// kept within [-100, 100].
+// kept within [-100, 100].  One workgroup per column (a max is exact in any
+// order).
 __global__ __launch_bounds__(256) void weight_colscale_kernel(WPackArgs a) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= a.np) return;
+  const int col = blockIdx.x;
+  const int count = a.phases * a.taps * a.cin;
   float m = 0.f;
-  for (int phase = 0; phase < a.phases; ++phase)
-    for (int tap = 0; tap < a.taps; ++tap)
-      for (int c = 0; c < a.cin; ++c) m = fmaxf(m, fabsf(packed_weight_value(a, phase, tap, c, col)));
-  int k = 0;
-  if (m > 0.f) {
-    const int e = (int)((__float_as_uint(m) >> 23) & 0xff) - 127;  // floor(log2 m) for normal m
-    k = min(max(14 - e, -100), 100);
+  for (int i = threadIdx.x; i < count; i += 256) {
+    const int c = i % a.cin, t = i / a.cin;
+    m = fmaxf(m, fabsf(packed_weight_value(a, t / a.taps, t % a.taps, c, col)));
   }
-  a.colscale[col] = ldexpf(1.0f, -k);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __shared__ float wmax[4];
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int k = 0;
+    if (m > 0.f) {
+      const int e = (int)((__float_as_uint(m) >> 23) & 0xff) - 127;  // floor(log2 m) for normal m
+      k = min(max(14 - e, -100), 100);
+    }
+    a.colscale[col] = ldexpf(1.0f, -k);
+  }
 }
 
 // Split-fp16 weights, step 2: per (phase, tap, 16-channel block, column) 96
@@ -3336,8 +3346,7 @@ static int pack_weight_impl(const ctmr_conv_desc* desc, const float* weight, voi
     a.layout = WL_TAPS;
     a.colscale = reinterpret_cast<float*>(reinterpret_cast<char*>(packed) + bytes);
     a.total = (int64_t)a.phases * a.taps * a.kblocks * a.np * 16;
-    hipLaunchKernelGGL(weight_colscale_kernel, dim3((unsigned)ceil_div(a.np, 256)), dim3(256), 0,
-                       (hipStream_t)stream, a);
+    hipLaunchKernelGGL(weight_colscale_kernel, dim3((unsigned)a.np), dim3(256), 0, (hipStream_t)stream, a);
     if ((rc = check_launch("weight_colscale"))) return rc;
     hipLaunchKernelGGL(pack_weight_split_kernel, dim3(elementwise_blocks(a.total)), dim3(256), 0,
                        (hipStream_t)stream, a);

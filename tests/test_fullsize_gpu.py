@@ -100,6 +100,35 @@ def test_config0_conv_full_volume(ctmr, dev):
     _check(y, _torch_conv_cpu(x, w, b), FP32_REL, "config0 whole volume vs torch CPU fp32")
 
 
+def test_config0_conv_full_volume_f16x2(ctmr, dev):
+    """Config 0 under ``precision("f16x2")`` (the reference's exact mode: split fp16 on fp16 MFMA, the
+    LDS-staged 16-bit GEMM over the packed hi/lo copy) -- the step bench.py reports as the split
+    variant -- against PyTorch CPU fp32 and float64 points at the fp32 bar, and as the two C-ABI
+    stages its roofline times."""
+    f = ctmr.fast_fp32
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, 64, 64, 64, 64), dtype=np.float32)
+    w = (rng.standard_normal((64, 64, 3, 3, 3)) / np.sqrt(27 * 64)).astype(np.float32)
+    b = (0.01 * rng.standard_normal(64)).astype(np.float32)
+    desc = ctmr.ops.make_desc(x.shape, 64, 3, 1, ctmr._lib.MODE_PLAIN, 0, ctmr._lib.DT_F16X2, 0)
+    assert ctmr._lib.conv_kernel(desc) == "lds_f16x2" and ctmr._lib.conv_split(desc) == 1
+    xg, wg, bg = _g(x, dev), _g(w, dev), _g(b, dev)
+    with f.precision("f16x2"):
+        y = f.conv3d(xg, wg, bg, padding=1)
+        assert torch.equal(y, f.conv3d(xg, wg, bg, padding=1))
+    import bench
+
+    pack, gemm, keep = bench.staged_op(ctmr, xg, wg, bg, ctmr._lib.DT_F16X2)
+    pack()
+    gemm()
+    torch.cuda.synchronize()
+    assert torch.equal(keep[2], y)
+    y = _h(y)
+    pts = rm.boundary_points(1, (64, 64, 64), 4096, seed=0)
+    _check(rm.gather_points(y, pts), rm.conv3d_points(x, w, b, pts), FP32_REL, "config0 f16x2 points vs float64")
+    _check(y, _torch_conv_cpu(x, w, b), FP32_REL, "config0 f16x2 whole volume vs torch CPU fp32")
+
+
 def test_config1_vae_resblock_full_size(ctmr, dev):
     """Config 1 at 128^3 x 128: GN(32) + SiLU + conv 128->128, twice, + identity skip (bench.py's
     ``vae_resblock`` call), checked per stage: the input's GN statistics (groups of 8.4M values)
@@ -274,6 +303,18 @@ def test_config4_full_window_bf16_matches_cpu_oracle(ctmr, dev, cpu_window):
     _check(_h(y), ref, BF16_REL, "config4 window bf16 vs torch CPU fp32 decoder")
 
 
+def test_config4_full_window_f16x2_matches_cpu_oracle(ctmr, dev, cpu_window):
+    """The window under ``precision("f16x2")`` against the PyTorch CPU fp32 decoder at the fp32 bar,
+    1e-4 (the decoder's 3x3x3 convs with 64 or more output channels on the split-fp16 GEMM, the
+    64 -> 1 output conv and the 1x1 shortcuts on FP32)."""
+    m, f = ctmr.maisi, ctmr.fast_fp32
+    ctor, _, w = _decoder(ctmr, dev)
+    window, ref = cpu_window
+    with f.precision("f16x2"):
+        _, y = m.decode_vae(_g(window, dev), w, constructor=ctor)
+    _check(_h(y), ref, BLOCK_REL, "config4 window f16x2 vs torch CPU fp32 decoder")
+
+
 def _check_256_decode(ctmr, dev, tag):
     """bench.py's config-4 decode under the active precision: finite; equal, at every voxel, to the
     float64 Gaussian blend of the four windows decoded separately; int16 = truncation, in range."""
@@ -316,6 +357,12 @@ def test_config4_256_decode_blend_and_int16(ctmr, dev):
     decoded separately recomputed in float64 (so continuous across each seam); the int16 image
     is the truncation of max(1000 x, 0) with no value outside the int16 range."""
     _check_256_decode(ctmr, dev, "fp32")
+
+
+def test_config4_256_decode_f16x2_blend_and_int16(ctmr, dev):
+    """The split-fp16 variant of the same 256^3 decode: blend, seam and int16 checks."""
+    with ctmr.fast_fp32.precision("f16x2"):
+        _check_256_decode(ctmr, dev, "f16x2")
 
 
 def test_config4_256_decode_bf16_blend_and_int16(ctmr, dev):
