@@ -552,14 +552,24 @@ def ct_generation(pkg, dev, uw, vw, timed):
 
     sec, peak = timed(run)
     progress(f"CT from mask generation {sec:.3f} s")
+    stages32 = list(results)
+    results.clear()
+    with pkg.fast_fp32.precision("f16x2"):
+        secx, _ = timed(run)
+    progress(f"CT from mask generation f16x2 {secx:.3f} s")
     windows = len(m.dense_patch_slices((64, 64, 64), (48, 48, 64), m.scan_interval((64, 64, 64), (48, 48, 64), 0.6666)))
     unet_f = sum(unet_flops(uc, 1, 64, 64, 64))
     ctrl_f = sum(controlnet_flops(cc, 1, 64, 64, 64))
     flop = controlnet_cond_flops(cc, 1, 256, 256, 256) + 30 * (unet_f + ctrl_f) + windows * vae_decoder_flops(
         vc, 48, 48, 64)
-    stages = {k: round(float(np.median([r[k] for r in results[1:]])), 3) for k in results[0]}
+    stages = {k: round(float(np.median([r[k] for r in stages32[1:]])), 3) for k in stages32[0]}
+    stagesx = {k: round(float(np.median([r[k] for r in results[1:]])), 3) for k in results[0]}
+    attn = 30 * (unet_flops(uc, 1, 64, 64, 64)[1] + controlnet_flops(cc, 1, 64, 64, 64)[1])
+    floorx = (flop - attn) / F16X2_PEAK + attn / FP32_PEAK
     return {"s": round(sec, 3), "stages_s": stages, "tflop": round(flop / 1e12, 2), "decode_windows": windows,
             "roofline_s": round(flop / FP32_PEAK, 3), "frac_roofline": round(flop / FP32_PEAK / sec, 4),
+            "f16x2_s": round(secx, 3), "f16x2_stages_s": stagesx, "f16x2_roofline_s": round(floorx, 3),
+            "f16x2_frac_roofline": round(floorx / secx, 4),
             "timing": "median of 3 after 1 warm-up, label upload to HU download", "peak_device_GiB":
             round(peak / 2**30, 2)}
 
