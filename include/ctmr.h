@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define CTMR_ABI_VERSION 3
+#define CTMR_ABI_VERSION 4
 
 enum ctmr_status {
   CTMR_OK = 0,
@@ -301,6 +301,34 @@ int ctmr_gn_affine(int32_t n, int64_t s, int32_t c, int32_t groups, float eps, c
 int ctmr_gn_affine_cat(int32_t n, int64_t s, int32_t c1, int32_t c2, int32_t groups, float eps, const float* x1,
                        const float* x2, const float* gamma, const float* beta, float* affine, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/*
+ * Group norm from statistics at a finer grouping than the norm's, over one tensor
+ * or the channel concatenation of two (the up-path norm1 over cat([hidden, skip]),
+ * unet.py:444, when both halves' producers wrote statistics; the reference reads
+ * the concatenated tensor in a medmlx-core pass, fast_fp32.py:185-189).  No
+ * counterpart entry point exists in the reference.
+ *   ctmr_gn_affine_from_stats2: source k (k = 1, 2) holds partials
+ *     stats_k[((b * tiles_k + tile) * sgroups_k + sg) * 2 + {0, 1}] over its c_k
+ *     channels in sgroups_k equal stat groups (ctmr_conv3d_gn's layout; per channel
+ *     when sgroups_k = c_k); source 2 is channels [c1, c1 + c2) of the normalised
+ *     tensor (c2 = 0: one source, stats2 unused).  Every norm group's share of a
+ *     source must be a union of its stat groups, else CTMR_E_INVALID.  count =
+ *     voxels * (c1 + c2) / groups.  The items are summed in a fixed order (source
+ *     1's tiles, then source 2's; stat groups ascending in each tile).
+ *   ctmr_add_gn_partials: y = a + b (NDHWC fp32, c % 4 == 0, c <= 1024, 16-byte
+ *     aligned; bit-identical to the fp32 sum) and per-channel partials of y into
+ *     workspace, (n, tiles, c, 2) with tiles = workspace size of
+ *     ctmr_gn_workspace_bytes(n, s, c) / (n * c * 16): a source for
+ *     ctmr_gn_affine_from_stats2 with sgroups = c.  For the UNet skips to which
+ *     ControlNet residuals are added (controlnet.py:160-163, unet.py:426-431).
+ */
+int ctmr_gn_affine_from_stats2(int32_t n, int32_t groups, int64_t count, float eps, const double* stats1,
+                               int32_t tiles1, int32_t c1, int32_t sgroups1, const double* stats2, int32_t tiles2,
+                               int32_t c2, int32_t sgroups2, const float* gamma, const float* beta, float* affine,
+                               void* stream);
+int ctmr_add_gn_partials(int32_t n, int64_t s, int32_t c, const float* a, const float* b, float* y,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* y = silu?(x*scale + offset) with affine from ctmr_gn_affine; y may equal x. */
 int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,

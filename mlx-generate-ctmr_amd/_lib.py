@@ -25,7 +25,7 @@ DT_F32, DT_BF16, DT_F16X2 = 0, 1, 2
 KERNEL_NAMES = ("stream", "stream_direct", "lds", "lds_bf16", "pointwise", "split_waves", "tap_expand", "lds_small",
                 "small_cout", "lds_f16x2")
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 NOALLOC_SCRATCH_BYTES = 256 << 20  # CTMR_NOALLOC_SCRATCH_BYTES
 
 
@@ -74,6 +74,9 @@ _PROTOTYPES = {
     "ctmr_gn_affine_cat": (_c_int, [_c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _f, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                     _vp]),
     "ctmr_gn_affine_from_stats": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _f, _vp, _vp, _vp, _vp, _vp]),
+    "ctmr_gn_affine_from_stats2": (_c_int, [_c_i32, _c_i32, _c_i64, _f, _vp, _c_i32, _c_i32, _c_i32, _vp, _c_i32,
+                                            _c_i32, _c_i32, _vp, _vp, _vp, _vp]),
+    "ctmr_add_gn_partials": (_c_int, [_c_i32, _c_i64, _c_i32, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ctmr_gn_apply": (_c_int, [_c_i32, _c_i64, _c_i32, _vp, _vp, _c_i32, _vp, _vp]),
     "ctmr_silu": (_c_int, [_c_i64, _vp, _vp, _vp]),
     "ctmr_resample": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp]),

@@ -59,11 +59,14 @@ __device__ __forceinline__ double wave_butterfly_sum(double v) {
 // A two-source input (x2 non-null) is the channel concatenation of x
 // (channels [0, c1)) and x2 (channels [c1, c)); a thread's channels lie in one
 // of them (c1 % VEC == 0) and it reads the same values in the same order as
-// from the concatenated tensor.
+// from the concatenated tensor.  With `addend` (single source, VEC 4) the
+// statistics are those of x + addend, which the kernel also stores to y.
 template <int VEC>
 __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict__ x, const float* __restrict__ x2,
                                                          int c1, int64_t s, int c, int64_t chunk_vox, int chunks,
-                                                         double* __restrict__ part) {
+                                                         double* __restrict__ part,
+                                                         const float* __restrict__ addend = nullptr,
+                                                         float* __restrict__ y = nullptr) {
   const int chunk = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int cgn = c / VEC;
   const int vl_count = 256 / cgn;
@@ -94,10 +97,23 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict
     const int stride = x2 == nullptr ? c : (second ? c - c1 : c1);
     const float* xb = second ? x2 + (int64_t)b * s * stride + (cg * VEC - c1) : x + (int64_t)b * s * stride + cg * VEC;
     const int64_t step = vl_count;
-    for (int64_t v = v0 + vl; v < v1; v += step) {
-      float q[VEC];
-      load(xb + v * stride, q);
-      add(q);
+    if (addend != nullptr) {
+      const int64_t off = (int64_t)b * s * stride + cg * VEC;
+      for (int64_t v = v0 + vl; v < v1; v += step) {
+        float q[VEC], r[VEC];
+        load(xb + v * stride, q);
+        load(addend + off + v * stride, r);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) q[k] += r[k];
+        if constexpr (VEC == 4) *reinterpret_cast<f4*>(y + off + v * stride) = f4{q[0], q[1], q[2], q[3]};
+        add(q);
+      }
+    } else {
+      for (int64_t v = v0 + vl; v < v1; v += step) {
+        float q[VEC];
+        load(xb + v * stride, q);
+        add(q);
+      }
     }
   }
   double* out = part + (((int64_t)b * chunks + chunk) * c) * 2;
@@ -198,6 +214,45 @@ __global__ __launch_bounds__(256) void gn_tiles_finalize_kernel(const double* __
     const double* p = part + (((int64_t)b * tiles + i) * groups + g) * 2;
     sm += p[0];
     sq += p[1];
+  }
+  gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
+}
+
+// Partials of one source of ctmr_gn_affine_from_stats2: (n, tiles, sgroups, 2)
+// fp64 (sum, sum of squares) over its c channels, channels [c0, c0 + c) of the
+// normalised (possibly concatenated) tensor.
+struct StatSource {
+  const double* stats;
+  int tiles, c, sgroups, c0;
+};
+
+// Affine of norm group g of batch item b from the stat groups of one or two
+// sources that tile its channels (checked on the host): the items (source,
+// tile, stat group) strided over the threads in a fixed order -- source 1's
+// tiles then source 2's, each tile's stat groups ascending -- then the fixed
+// combine of gn_group_affine.
+__global__ __launch_bounds__(256) void gn_stats_finalize_kernel(StatSource s1, StatSource s2, int c, int groups,
+                                                                int64_t count, const float* __restrict__ gamma,
+                                                                const float* __restrict__ beta, float eps,
+                                                                float* __restrict__ affine) {
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int cpg = c / groups, lo = g * cpg, hi = lo + cpg;
+  double sm = 0, sq = 0;
+  const StatSource* src[2] = {&s1, &s2};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const StatSource& s = *src[k];
+    if (s.c == 0) continue;
+    const int a = max(lo, s.c0) - s.c0, e = min(hi, s.c0 + s.c) - s.c0;  // source-local channel range
+    if (a >= e) continue;
+    const int scpg = s.c / s.sgroups, g0 = a / scpg, ng = (e - a) / scpg;
+    const int64_t items = (int64_t)s.tiles * ng;
+    for (int64_t i = t; i < items; i += 256) {
+      const int tile = (int)(i / ng), sg = g0 + (int)(i % ng);
+      const double* p = s.stats + (((int64_t)b * s.tiles + tile) * s.sgroups + sg) * 2;
+      sm += p[0];
+      sq += p[1];
+    }
   }
   gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
 }
@@ -464,6 +519,56 @@ int ctmr_gn_affine_from_stats(int32_t n, int32_t tiles, int32_t c, int32_t group
   hipLaunchKernelGGL(gn_tiles_finalize_kernel, dim3(groups, n), dim3(256), 0, (hipStream_t)stream, stats, tiles,
                      c, groups, count, gamma, beta, eps, affine);
   return check_launch("gn_tiles_finalize");
+}
+
+int ctmr_add_gn_partials(int32_t n, int64_t s, int32_t c, const float* a, const float* b, float* y,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (n <= 0 || s <= 0 || c <= 0) return fail(CTMR_E_INVALID, "non-positive dimension");
+  if (c % 4 != 0 || c > 1024) return fail(CTMR_E_UNSUPPORTED, "add with statistics needs c % 4 == 0 and c <= 1024");
+  if (!a || !b || !y) return fail(CTMR_E_INVALID, "null pointer");
+  if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)y) & 15) != 0)
+    return fail(CTMR_E_INVALID, "a, b and y must be 16-byte aligned");
+  const GnChunks ch = gn_chunks(n, s, c);
+  const int64_t need = (int64_t)n * ch.count * c * 2 * (int64_t)sizeof(double);
+  if ((int64_t)workspace_bytes < need || !workspace) {
+    set_error("statistics workspace %zu bytes < required %lld", workspace_bytes, (long long)need);
+    return CTMR_E_WORKSPACE;
+  }
+  if (ch.count >= (1 << 30) || n > 65535) return fail(CTMR_E_UNSUPPORTED, "volume too large");
+  hipLaunchKernelGGL(gn_partial_kernel<4>, dim3((unsigned)ch.count, n), dim3(256), 0, (hipStream_t)stream, a,
+                     nullptr, c, s, c, ch.vox, (int)ch.count, (double*)workspace, b, y);
+  return check_launch("add_gn_partials");
+}
+
+// Whether the stat groups of a source tile every norm group's share of it.
+static bool stats_tile_groups(int c0, int c, int sgroups, int ctot, int groups) {
+  if (c == 0) return true;
+  if (sgroups <= 0 || c % sgroups != 0) return false;
+  const int scpg = c / sgroups, cpg = ctot / groups;
+  for (int g = 0; g < groups; ++g) {
+    const int a = std::max(g * cpg, c0) - c0, e = std::min((g + 1) * cpg, c0 + c) - c0;
+    if (a < e && (a % scpg != 0 || e % scpg != 0)) return false;
+  }
+  return true;
+}
+
+int ctmr_gn_affine_from_stats2(int32_t n, int32_t groups, int64_t count, float eps, const double* stats1,
+                               int32_t tiles1, int32_t c1, int32_t sgroups1, const double* stats2, int32_t tiles2,
+                               int32_t c2, int32_t sgroups2, const float* gamma, const float* beta, float* affine,
+                               void* stream) {
+  if (n <= 0 || groups <= 0 || count <= 0 || c1 <= 0 || tiles1 <= 0 || c2 < 0 || (c2 > 0 && tiles2 <= 0))
+    return fail(CTMR_E_INVALID, "non-positive dimension");
+  const int c = c1 + c2;
+  if (c % groups != 0) return fail(CTMR_E_INVALID, "channels must be divisible by groups");
+  if (n > 65535 || groups > 65535) return fail(CTMR_E_UNSUPPORTED, "too many batch items or groups");
+  if (!stats_tile_groups(0, c1, sgroups1, c, groups) || !stats_tile_groups(c1, c2, sgroups2, c, groups))
+    return fail(CTMR_E_INVALID, "the sources' statistic groups do not tile the norm's groups");
+  if (!stats1 || (c2 > 0 && !stats2) || !gamma || !beta || !affine) return fail(CTMR_E_INVALID, "null pointer");
+  const StatSource s1{stats1, tiles1, c1, sgroups1, 0};
+  const StatSource s2{c2 > 0 ? stats2 : nullptr, c2 > 0 ? tiles2 : 0, c2, c2 > 0 ? sgroups2 : 1, c1};
+  hipLaunchKernelGGL(gn_stats_finalize_kernel, dim3(groups, n), dim3(256), 0, (hipStream_t)stream, s1, s2, c, groups,
+                     count, gamma, beta, eps, affine);
+  return check_launch("gn_stats_finalize");
 }
 
 int ctmr_gn_apply(int32_t n, int64_t s, int32_t c, const float* x, const float* affine,

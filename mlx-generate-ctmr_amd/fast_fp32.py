@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import functools
 import math
 import threading
 import weakref
@@ -345,8 +346,10 @@ def implicit_gemm_conv3d(
     fp32 rounding with different fixed summation orders.  ``gn_groups`` asks
     the epilogue for the group-norm statistics of the output over that many
     groups (``ctmr_conv3d_gn``; same output bits); a later ``group_norm_affine``
-    of the unmodified output with the same groups uses them instead of reading
-    the output again.  Shapes that cannot produce them are computed without.
+    of the unmodified output, alone or in a ``ChannelCat``, uses them instead of
+    reading the output again when its groups are unions of these (``gn_groups =
+    cout`` gives per-channel statistics, usable by any grouping).  Shapes that
+    cannot produce them are computed without.
 
     Raises:
         ValueError: on a packed weight that does not fit, unsupported option
@@ -390,8 +393,9 @@ def implicit_gemm_conv3d(
     # Statistics ride on the output tensor, valid while its version counter is unchanged; under
     # torch.inference_mode the output is an inference tensor without one, so nothing is attached and
     # the group norm reading it makes its own pass.
-    if gn_groups > 0 and not torch.is_inference_mode_enabled() and ops.conv_stats_tiles(tuple(x.shape), cout, ksize, stride, mode, code, split,
-                                              stream_gemm, int(gn_groups), cin2) > 0:
+    if (gn_groups > 0 and not torch.is_inference_mode_enabled()
+            and ops.conv_stats_tiles(tuple(x.shape), cout, ksize, stride, mode, code, split, stream_gemm,
+                                     int(gn_groups), cin2) > 0):
         y, stats = ops.conv3d_gn(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, code, split,
                                  stream_gemm, int(gn_groups), x2)
         y._ctmr_gn_stats = (int(gn_groups), stats, y._version)
@@ -400,13 +404,47 @@ def implicit_gemm_conv3d(
                       stream_gemm, x2)
 
 
+def _attached_stats(x: Tensor) -> Optional[tuple[int, Tensor]]:
+    """``(stat groups, (N, tiles, stat groups, 2) partials)`` written for ``x`` by the op that produced
+    it, or None if there are none or ``x`` was modified in place since."""
+    info = getattr(x, "_ctmr_gn_stats", None)
+    if info is None or x.is_inference() or info[2] != x._version:
+        return None
+    return info[0], info[1]
+
+
 def conv_output_stats(x: Tensor, groups: int) -> Optional[Tensor]:
     """The ``(N, tiles, groups, 2)`` group-norm partials a conv epilogue wrote for ``x``, or None if
     ``x`` carries none for ``groups`` or was modified in place since."""
-    info = getattr(x, "_ctmr_gn_stats", None)
-    if info is None or x.is_inference() or info[0] != groups or info[2] != x._version:
-        return None
-    return info[1]
+    info = _attached_stats(x)
+    return info[1] if info is not None and info[0] == groups else None
+
+
+@functools.lru_cache(maxsize=1024)
+def _stats_tile_groups(c0: int, c: int, sgroups: int, total: int, groups: int) -> bool:
+    """Whether ``sgroups`` equal stat groups over channels ``[c0, c0 + c)`` of a ``total``-channel
+    tensor tile every share of its ``groups`` norm groups (``ctmr_gn_affine_from_stats2``'s rule)."""
+    if sgroups <= 0 or c % sgroups:
+        return False
+    scpg, cpg = c // sgroups, total // groups
+    for g in range(groups):
+        a, e = max(g * cpg, c0) - c0, min((g + 1) * cpg, c0 + c) - c0
+        if a < e and (a % scpg or e % scpg):
+            return False
+    return True
+
+
+def add_with_stats(a: Tensor, b: Tensor) -> Tensor:
+    """``a + b`` (NDHWC fp32, same shape) with per-channel group-norm partials attached, so a group
+    norm of the sum, or of a ``ChannelCat`` holding it, reads no statistics pass (the ControlNet
+    residuals added to the UNet skips, ``controlnet.py:160-163``).  Same bits as ``a + b``."""
+    if (a.shape != b.shape or a.dim() != 5 or int(a.shape[-1]) % 4 or int(a.shape[-1]) > 1024
+            or torch.is_inference_mode_enabled()):
+        return a + b  # broadcasting or unsupported shapes: the plain sum, without statistics
+    a, b = _require(a, "a"), _require(b, "b")
+    y, stats = ops.add_gn(a, b)
+    y._ctmr_gn_stats = (int(a.shape[-1]), stats, y._version)
+    return y
 
 
 nax_conv3d = implicit_gemm_conv3d  # the reference orchestrator's name (_nax_conv.py:475)
@@ -436,21 +474,31 @@ def pointwise_conv(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
 
 def group_norm_affine(x: Tensor, weight: Tensor, bias: Tensor, *, groups: int, eps: float) -> Tensor:
     """``(N, C, 2)`` scale/offset pairs of a group norm of NDHWC ``x`` (``medmlx_core.group_norm_affine``).
-    Uses the statistics a convolution epilogue wrote for ``x`` when there are any; ``x`` may be a
-    ``ChannelCat``."""
+    Uses the statistics a convolution epilogue (or ``add_with_stats``) wrote for ``x`` when there are
+    any at this grouping or a finer one; ``x`` may be a ``ChannelCat``, whose halves' statistics are
+    used when both have them."""
     x, x2 = _split_input(x)
     c = int(x.shape[-1]) + (0 if x2 is None else int(x2.shape[-1]))
     if c % groups != 0:
         raise ValueError(f"{c} channels are not divisible by {groups} groups")
     gamma = _vec(weight, c, "norm weight", x.device)
     beta = _vec(bias, c, "norm bias", x.device)
-    if x2 is not None:
-        return ops.gn_affine(x, gamma, beta, int(groups), float(eps), x2)
-    stats = conv_output_stats(x, int(groups))
-    if stats is not None:
-        count = (x.numel() // (int(x.shape[0]) * c)) * (c // int(groups))
-        return ops.gn_affine_from_stats(stats, gamma, beta, count, float(eps))
-    return ops.gn_affine(x, gamma, beta, int(groups), float(eps))
+    groups, c1 = int(groups), int(x.shape[-1])
+    count = (x.numel() // (int(x.shape[0]) * c1)) * (c // groups)
+    first = _attached_stats(x)
+    if x2 is None:
+        if first is None:
+            return ops.gn_affine(x, gamma, beta, groups, float(eps))
+        if first[0] == groups:
+            return ops.gn_affine_from_stats(first[1], gamma, beta, count, float(eps))
+        if _stats_tile_groups(0, c, first[0], c, groups):
+            return ops.gn_affine_from_stats2(first[1], c, gamma, beta, groups, count, float(eps))
+        return ops.gn_affine(x, gamma, beta, groups, float(eps))
+    second = _attached_stats(x2)
+    if (first is not None and second is not None and _stats_tile_groups(0, c1, first[0], c, groups)
+            and _stats_tile_groups(c1, c - c1, second[0], c, groups)):
+        return ops.gn_affine_from_stats2(first[1], c1, gamma, beta, groups, count, float(eps), second[1])
+    return ops.gn_affine(x, gamma, beta, groups, float(eps), x2)
 
 
 def group_norm(x: Tensor, weight: Tensor, bias: Tensor, *, num_groups: int, eps: float,

@@ -101,7 +101,8 @@ def condition_embedding(timesteps: Tensor, class_labels: Optional[Tensor], spaci
 def spatial_attention(x: Tensor, weights: Mapping[str, Tensor], *, num_groups: int, eps: float,
                       num_head_channels: int, include_fc: bool) -> Tensor:
     """Residual self-attention over all voxels of NDHWC ``x`` (attention.py:92-160): group
-    norm (HIP), tokens are the NDHWC rows as they lie, Q/K/V + flash attention + out_proj."""
+    norm (HIP), tokens are the NDHWC rows as they lie, Q/K/V + flash attention + out_proj.  The
+    residual sum carries per-channel statistics for the group norm that reads it next."""
     n, d, h, w, c = x.shape
     if c % num_head_channels != 0:
         raise ValueError("num_channels must be divisible by num_head_channels")
@@ -110,7 +111,7 @@ def spatial_attention(x: Tensor, weights: Mapping[str, Tensor], *, num_groups: i
     hidden = ff.group_norm(x, weights["norm.weight"], weights["norm.bias"], num_groups=num_groups, eps=eps)
     merged = ff.self_attention_tokens(hidden.reshape(n, d * h * w, c), weights, heads=heads, scale=scale,
                                       include_fc=include_fc)
-    return x + merged.reshape(n, d, h, w, c)
+    return ff.add_with_stats(x, merged.reshape(n, d, h, w, c))
 
 
 # ---------------------------------------------------------------------------
@@ -181,12 +182,16 @@ def _blocks(weights: Mapping[str, Tensor], emb: Tensor, groups: int, eps: float,
     index, offsets = _block_major_index(spans, n, int(conv1_bias.shape[1]), conv1_bias.device)
     blocked = conv1_bias.reshape(-1).index_select(0, index)
 
-    def resnet(h, prefix: str, *, normed_next: bool = True, **kw) -> Tensor:
-        """``normed_next``: a group norm reads the output next (its statistics come from conv2)."""
+    def resnet(h, prefix: str, *, stats: Optional[str] = "groups", **kw) -> Tensor:
+        """``stats``: the group-norm statistics conv2's epilogue writes for the output -- ``"groups"``
+        when a group norm over the output alone reads it next, ``"channels"`` (per channel) when it is
+        also read as half of an up-path concatenation, whose norm groups may straddle the halves,
+        None when no group norm reads it."""
         off, width = offsets[prefix]
+        cout = int(_need(weights, f"{prefix}.conv2.conv.weight").shape[0])
         return ff.residual_block(h, emb, _prefixed(weights, prefix), num_groups=groups, eps=eps,
                                  conv1_bias=blocked[off:off + n * width].view(n, width),
-                                 out_gn_groups=groups if normed_next else 0, **kw)
+                                 out_gn_groups={"groups": groups, "channels": cout, None: 0}[stats], **kw)
 
     def attention(h: Tensor, prefix: str, n_heads: int) -> Tensor:
         return spatial_attention(h, _prefixed(weights, prefix), num_groups=groups, eps=eps,
@@ -196,26 +201,28 @@ def _blocks(weights: Mapping[str, Tensor], emb: Tensor, groups: int, eps: float,
 
 
 def _down_path(hidden: Tensor, resnet, attention, res_blocks, attn_levels, heads) -> tuple[Tensor, list[Tensor]]:
-    """Encoder levels; returns the hidden state and every skip (unet.py:274-356)."""
+    """Encoder levels; returns the hidden state and every skip (unet.py:274-356).  Outputs that
+    become skips carry per-channel statistics (the up path's norm1 reads them in a concatenation)."""
     skips = [hidden]
     n_levels = len(res_blocks)
     for index in range(n_levels):
         for r in range(res_blocks[index]):
-            hidden = resnet(hidden, f"down_blocks.{index}.resnets.{r}")
+            hidden = resnet(hidden, f"down_blocks.{index}.resnets.{r}",
+                            stats="groups" if attn_levels[index] else "channels")
             if attn_levels[index]:
                 hidden = attention(hidden, f"down_blocks.{index}.attentions.{r}", heads[index])
             skips.append(hidden)
         if index != n_levels - 1:
-            hidden = resnet(hidden, f"down_blocks.{index}.downsampler", down=True)
+            hidden = resnet(hidden, f"down_blocks.{index}.downsampler", down=True, stats="channels")
             skips.append(hidden)
     return hidden, skips
 
 
-def _mid_block(hidden: Tensor, resnet, attention, n_heads: int) -> Tensor:
-    """resnet -> attention -> resnet (unet.py:359-399)."""
+def _mid_block(hidden: Tensor, resnet, attention, n_heads: int, out_stats: Optional[str] = "channels") -> Tensor:
+    """resnet -> attention -> resnet (unet.py:359-399); the output is concatenated with a skip next."""
     hidden = resnet(hidden, "middle_block.resnet_1")
     hidden = attention(hidden, "middle_block.attention", n_heads)
-    return resnet(hidden, "middle_block.resnet_2", normed_next=False)  # concatenated with a skip next
+    return resnet(hidden, "middle_block.resnet_2", stats=out_stats)
 
 
 def denoise_unet(
@@ -254,8 +261,9 @@ def denoise_unet(
     t_emb, emb = condition_embedding(timesteps, class_labels, spacing, weights, constructor)
     resnet, attention = _blocks(weights, emb, groups, eps, include_fc)
 
-    hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1,
-                       gn_groups=groups)
+    conv_in_w = _need(weights, "conv_in.conv.weight")
+    hidden = ff.conv3d(x, conv_in_w, _need(weights, "conv_in.conv.bias"), padding=1,
+                       gn_groups=int(conv_in_w.shape[0]))  # per channel: the first skip
     hidden, skips = _down_path(hidden, resnet, attention, res_blocks, attn_levels, heads)
     if residuals_ready is not None:
         torch.cuda.current_stream(x.device).wait_event(residuals_ready)
@@ -263,24 +271,27 @@ def denoise_unet(
         extras = list(down_block_additional_residuals)
         if len(extras) != len(skips):
             raise ValueError(f"ControlNet residuals length {len(extras)} != UNet skip count {len(skips)}")
-        skips = [s + e for s, e in zip(skips, extras)]
+        skips = [ff.add_with_stats(s, e) for s, e in zip(skips, extras)]
         hidden = skips[-1]
-    hidden = _mid_block(hidden, resnet, attention, heads[-1])
-    if mid_block_additional_residual is not None:
-        hidden = hidden + mid_block_additional_residual
+    mid_extra = mid_block_additional_residual
+    hidden = _mid_block(hidden, resnet, attention, heads[-1], out_stats=None if mid_extra is not None else "channels")
+    if mid_extra is not None:
+        hidden = ff.add_with_stats(hidden, mid_extra)
     rev_res, rev_attn, rev_heads = res_blocks[::-1], attn_levels[::-1], heads[::-1]
     for index in range(n_levels):
         n_res = rev_res[index] + 1
         samples, skips = skips[-n_res:], skips[:-n_res]
         for r in range(n_res):
             skip = samples.pop()
-            # cat([hidden, skip]) (unet.py:444) read in place by the block's norm and convolutions
+            # cat([hidden, skip]) (unet.py:444) read in place by the block's norm and convolutions; an
+            # output concatenated next carries per-channel statistics, one normalised alone next
+            # (by attention, the up-sampler or the output norm) the groups'
             hidden = resnet(ff.concat_channels(hidden, skip), f"up_blocks.{index}.resnets.{r}",
-                            normed_next=rev_attn[index] or r == n_res - 1)
+                            stats="groups" if rev_attn[index] or r == n_res - 1 else "channels")
             if rev_attn[index]:
                 hidden = attention(hidden, f"up_blocks.{index}.attentions.{r}", rev_heads[index])
         if index != n_levels - 1:
-            hidden = resnet(hidden, f"up_blocks.{index}.upsampler", up=True)
+            hidden = resnet(hidden, f"up_blocks.{index}.upsampler", up=True, stats="channels")
     if skips:
         raise ValueError(f"UNet skip list leftover after up blocks: {len(skips)}")
     y = ff.norm_conv3d(hidden, _need(weights, "out.2.conv.weight"), _need(weights, "out.2.conv.bias"),
@@ -465,7 +476,7 @@ def controlnet_residuals(
     hidden = ff.conv3d(x, _need(weights, "conv_in.conv.weight"), _need(weights, "conv_in.conv.bias"), padding=1)
     embedding = (encode_controlnet_condition(cond, weights, constructor=constructor)
                  if conditioning_embedding is None else conditioning_embedding)
-    hidden = hidden + embedding
+    hidden = ff.add_with_stats(hidden, embedding)  # with the statistics of the first block's norm1
     hidden, skips = _down_path(hidden, resnet, attention, res_blocks, attn_levels, heads)
     hidden = _mid_block(hidden, resnet, attention, heads[-1])
     down = [_zero_conv(s, weights, f"controlnet_down_blocks.{i}") for i, s in enumerate(skips)]

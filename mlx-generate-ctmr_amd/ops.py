@@ -5,17 +5,59 @@ allocator, passes raw device pointers and the current HIP stream to the
 library, and raises on a non-zero status.  Shapes are validated by the
 callers in ``fast_fp32``; these functions assume contiguous fp32 NDHWC CUDA
 tensors.  Every operator has a fake (meta) implementation so it traces.
+
+An eager call on plain CUDA tensors (no tracing, compilation, dispatch mode or
+autograd input) runs the operator's implementation directly: the dispatcher
+round trip of a Python custom operator costs about 25 us of host time per call,
+more than many of the kernels these operators launch, and an eager network pass
+issues a few hundred of them.  Every other call goes through the registered
+operator.
 """
 
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+import functools
+from typing import Callable, Optional
 
 import torch
 from torch import Tensor
 
 from . import _lib
+
+
+class _CustomOp:
+    """A registered ``ctmr::*`` operator (``.op``) whose eager calls on plain tensors skip the
+    dispatcher."""
+
+    def __init__(self, name: str, fn: Callable):
+        self.op = torch.library.custom_op(name, mutates_args=())(fn)
+        self.fn = fn
+        functools.update_wrapper(self, fn)
+
+    def register_fake(self, fake: Callable) -> Callable:
+        return self.op.register_fake(fake)
+
+    def __call__(self, *args, **kwargs):
+        if _direct(args) and _direct(kwargs.values()):
+            return self.fn(*args, **kwargs)
+        return self.op(*args, **kwargs)
+
+
+def _direct(values) -> bool:
+    """Whether a call with these arguments may bypass the dispatcher: nothing traces or compiles, and
+    every tensor is a plain tensor that autograd does not track."""
+    if torch._C._len_torch_dispatch_stack() or torch.compiler.is_compiling():
+        return False
+    grad = torch.is_grad_enabled()
+    for v in values:
+        if isinstance(v, Tensor) and (type(v) is not Tensor or (grad and v.requires_grad)):
+            return False
+    return True
+
+
+def _custom_op(name: str) -> Callable[[Callable], _CustomOp]:
+    return lambda fn: _CustomOp(name, fn)
 
 
 def _ptr(t: Optional[Tensor]) -> Optional[int]:
@@ -79,7 +121,7 @@ def _cin2(x2: Optional[Tensor]) -> int:
 _PACKED_TORCH_DTYPES = {_lib.DT_F32: torch.float32, _lib.DT_BF16: torch.bfloat16, _lib.DT_F16X2: torch.float16}
 
 
-@torch.library.custom_op("ctmr::pack_weight", mutates_args=())
+@_custom_op("ctmr::pack_weight")
 def pack_weight(weight: Tensor, cin: int, cout: int, ksize: int, mode: int, dtype: int) -> Tensor:
     """Packed conv weight (``ctmr_pack_weight`` / ``ctmr_pack_upsample_weight``)."""
     _require_device(weight)
@@ -101,7 +143,7 @@ def _(weight, cin, cout, ksize, mode, dtype):
 # ---------------------------------------------------------------------------
 # convolution
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("ctmr::conv3d", mutates_args=())
+@_custom_op("ctmr::conv3d")
 def conv3d(
     x: Tensor,
     packed: Tensor,
@@ -167,7 +209,7 @@ def conv_stats_tiles(x_shape: tuple[int, ...], cout: int, ksize: int, stride: in
     return max(int(_lib.lib().ctmr_conv3d_stats_tiles(ctypes.byref(desc), groups)), 0)
 
 
-@torch.library.custom_op("ctmr::conv3d_gn", mutates_args=())
+@_custom_op("ctmr::conv3d_gn")
 def conv3d_gn(
     x: Tensor,
     packed: Tensor,
@@ -238,7 +280,7 @@ def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype,
 # ---------------------------------------------------------------------------
 # group norm
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("ctmr::gn_affine_from_stats", mutates_args=())
+@_custom_op("ctmr::gn_affine_from_stats")
 def gn_affine_from_stats(stats: Tensor, gamma: Tensor, beta: Tensor, count: int, eps: float) -> Tensor:
     """``ctmr_gn_affine_from_stats``: (N, C, 2) (scale, offset) pairs from ``conv3d_gn`` partials
     ``(N, tiles, groups, 2)``; ``count`` is the number of values in one (batch item, group)."""
@@ -260,7 +302,61 @@ def _(stats, gamma, beta, count, eps):
     return stats.new_empty((stats.shape[0], gamma.numel(), 2), dtype=torch.float32)
 
 
-@torch.library.custom_op("ctmr::gn_affine", mutates_args=())
+@_custom_op("ctmr::gn_affine_from_stats2")
+def gn_affine_from_stats2(stats1: Tensor, c1: int, gamma: Tensor, beta: Tensor, groups: int, count: int,
+                          eps: float, stats2: Optional[Tensor] = None) -> Tensor:
+    """``ctmr_gn_affine_from_stats2``: (N, C, 2) (scale, offset) pairs over ``groups`` groups from
+    partials ``(N, tiles, sgroups, 2)`` at a finer grouping: ``stats1`` over the first ``c1``
+    channels and, if given, ``stats2`` over the remaining ``C - c1`` (a channel concatenation)."""
+    _require_device(stats1, gamma, beta, stats2)
+    n, tiles1, sg1 = (int(v) for v in stats1.shape[:3])
+    c = int(gamma.numel())
+    tiles2, sg2 = (0, 1) if stats2 is None else (int(stats2.shape[1]), int(stats2.shape[2]))
+    out = torch.empty((n, c, 2), device=stats1.device, dtype=torch.float32)
+    _lib.check(
+        _lib.lib().ctmr_gn_affine_from_stats2(n, groups, count, float(eps), stats1.data_ptr(), tiles1, c1, sg1,
+                                              _ptr(stats2), tiles2, c - c1, sg2, gamma.data_ptr(),
+                                              beta.data_ptr(), out.data_ptr(), _stream(stats1.device)),
+        "ctmr_gn_affine_from_stats2",
+    )
+    return out
+
+
+@gn_affine_from_stats2.register_fake
+def _(stats1, c1, gamma, beta, groups, count, eps, stats2=None):
+    return stats1.new_empty((stats1.shape[0], gamma.numel(), 2), dtype=torch.float32)
+
+
+@_custom_op("ctmr::add_gn")
+def add_gn(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
+    """``ctmr_add_gn_partials``: ``a + b`` (same NDHWC shape) and its per-channel float64 partials
+    ``(N, tiles, C, 2)``."""
+    _require_device(a, b)
+    if a.shape != b.shape:
+        raise ValueError(f"add_gn operands differ in shape: {tuple(a.shape)} vs {tuple(b.shape)}")
+    a, b = _aligned16(a), _aligned16(b)
+    n, c = int(a.shape[0]), int(a.shape[-1])
+    s = a.numel() // (n * c)
+    ws_bytes = _lib.gn_workspace_bytes(n, s, c)
+    y = torch.empty(a.shape, device=a.device, dtype=torch.float32)
+    stats = torch.empty((n, ws_bytes // (n * c * 16), c, 2), device=a.device, dtype=torch.float64)
+    _lib.check(
+        _lib.lib().ctmr_add_gn_partials(n, s, c, a.data_ptr(), b.data_ptr(), y.data_ptr(), stats.data_ptr(),
+                                        ws_bytes, _stream(a.device)),
+        "ctmr_add_gn_partials",
+    )
+    return y, stats
+
+
+@add_gn.register_fake
+def _(a, b):
+    n, c = int(a.shape[0]), int(a.shape[-1])
+    s = a.numel() // (n * c)
+    tiles = _lib.gn_workspace_bytes(n, s, c) // (n * c * 16)
+    return a.new_empty(a.shape), a.new_empty((n, tiles, c, 2), dtype=torch.float64)
+
+
+@_custom_op("ctmr::gn_affine")
 def gn_affine(x: Tensor, gamma: Tensor, beta: Tensor, groups: int, eps: float,
               x2: Optional[Tensor] = None) -> Tensor:
     """Per-(batch, channel) (scale, offset) pairs, shape ``(N, C, 2)``; with ``x2`` of the channel
@@ -296,7 +392,7 @@ def _(x, gamma, beta, groups, eps, x2=None):
     return x.new_empty((x.shape[0], x.shape[-1] + _cin2(x2), 2))
 
 
-@torch.library.custom_op("ctmr::gn_apply", mutates_args=())
+@_custom_op("ctmr::gn_apply")
 def gn_apply(x: Tensor, affine: Tensor, silu: bool) -> Tensor:
     """``silu?(x * scale + offset)`` with pairs from ``gn_affine``."""
     _require_device(x, affine)
@@ -316,7 +412,7 @@ def _(x, affine, silu):
     return torch.empty_like(x)
 
 
-@torch.library.custom_op("ctmr::silu", mutates_args=())
+@_custom_op("ctmr::silu")
 def silu(x: Tensor) -> Tensor:
     """Elementwise ``x / (1 + exp(-x))``."""
     _require_device(x)
@@ -334,7 +430,7 @@ def _(x):
 # ---------------------------------------------------------------------------
 # resampling
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("ctmr::resample", mutates_args=())
+@_custom_op("ctmr::resample")
 def resample(x: Tensor, op: int) -> Tensor:
     """2x average pool, nearest or trilinear upsampling of an NDHWC tensor."""
     _require_device(x)
@@ -359,7 +455,7 @@ def _(x, op):
     return x.new_empty((n, 2 * d, 2 * h, 2 * w, c))
 
 
-@torch.library.custom_op("ctmr::gn_avgpool", mutates_args=())
+@_custom_op("ctmr::gn_avgpool")
 def gn_avgpool(x: Tensor, affine: Tensor, silu: bool) -> tuple[Tensor, Tensor]:
     """``(avg_pool(silu?(x * scale + offset)), avg_pool(x))`` of an NDHWC tensor from one read of ``x``
     (the down-sampling residual block's two inputs); bit-identical to ``gn_apply`` then ``resample``."""
@@ -385,7 +481,7 @@ def _(x, affine, silu):
 # ---------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("ctmr::flash_attention", mutates_args=())
+@_custom_op("ctmr::flash_attention")
 def flash_attention(q: Tensor, k: Tensor, v: Tensor, heads: int, scale: float, query_tiles: int = 0) -> Tensor:
     """``softmax(q k^T * scale) v`` per head on ``(B, L, heads * 32)`` projections.
 

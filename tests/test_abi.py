@@ -354,3 +354,46 @@ def test_two_source_validation(ctmr, native_loaded):
     rc = native_loaded.ctmr_gn_affine_cat(1, 512, 126, 66, 32, 1e-6, fake, fake, fake, fake, fake, fake, 1 << 20,
                                           None)
     assert rc == L.E_INVALID and "multiples of 4" in L.last_error()
+
+
+def test_group_norm_from_finer_statistics_host_checks(ctmr, native_loaded):
+    """``ctmr_gn_affine_from_stats2`` accepts exactly the stat groupings ``fast_fp32`` routes to it (the
+    tiling rule is checked before the pointers, so a null gamma marks an accepted grouping), and
+    ``ctmr_add_gn_partials`` rejects what its kernel cannot read."""
+    from importlib import import_module
+
+    L = ctmr._lib
+    ff = import_module(ctmr.__name__ + ".fast_fp32")
+    fake = 0x1000
+    fn = native_loaded.ctmr_gn_affine_from_stats2
+    cases = 0
+    for c1, c2, groups in ((64, 64, 32), (256, 128, 32), (128, 64, 32), (64, 0, 32), (96, 0, 32), (256, 256, 32),
+                           (512, 256, 32), (48, 16, 8)):
+        c = c1 + c2
+        for sg1 in sorted({1, 2, 4, 8, 16, 32, 64, c1 // 4, c1 // 2, c1} - {0}):
+            for sg2 in (sorted({1, 4, 16, 32, c2 // 2, c2} - {0}) if c2 else [1]):
+                ok = ff._stats_tile_groups(0, c1, sg1, c, groups) and (
+                    c2 == 0 or ff._stats_tile_groups(c1, c2, sg2, c, groups))
+                rc = fn(1, groups, 64, 1e-6, fake, 4, c1, sg1, fake if c2 else None, 4 if c2 else 0, c2, sg2, None,
+                        fake, fake, None)
+                assert rc == L.E_INVALID
+                assert ("null pointer" if ok else "do not tile") in L.last_error(), (c1, c2, groups, sg1, sg2)
+                cases += 1
+    assert cases > 100
+    # per-channel statistics tile every grouping; the norm's own groups tile it; a 12-wide group straddling
+    # 256 + 128 channels does not split into 8-channel stat groups
+    assert ff._stats_tile_groups(0, 256, 256, 384, 32) and ff._stats_tile_groups(256, 128, 32, 384, 32)
+    assert not ff._stats_tile_groups(0, 256, 32, 384, 32)
+    assert not ff._stats_tile_groups(0, 64, 16, 64, 32)  # stat groups coarser than the norm's
+    rc = fn(1, 5, 64, 1e-6, fake, 4, 64, 64, None, 0, 0, 1, fake, fake, fake, None)
+    assert rc == L.E_INVALID and "divisible" in L.last_error()
+    rc = fn(1, 32, 64, 1e-6, fake, 0, 64, 64, None, 0, 0, 1, fake, fake, fake, None)
+    assert rc == L.E_INVALID
+    add = native_loaded.ctmr_add_gn_partials
+    rc = add(1, 64, 6, fake, fake, fake, fake, 1 << 20, None)
+    assert rc == L.E_UNSUPPORTED
+    rc = add(1, 64, 64, fake + 4, fake, fake, fake, 1 << 20, None)
+    assert rc == L.E_INVALID and "aligned" in L.last_error()
+    rc = add(1, 64, 64, fake, fake, fake, fake, 16, None)
+    assert rc == L.E_WORKSPACE
+    assert add(1, 64, 64, None, fake, fake, fake, 1 << 20, None) == L.E_INVALID

@@ -220,12 +220,14 @@ def _production_unet(ctmr, dev, seed=7):
     return host, {k: _g(v, dev) for k, v in host.items()}
 
 
-def test_config3_unet_step_matches_cpu_oracle(ctmr, dev):
+def test_config3_unet_step_matches_cpu_oracle(ctmr, dev, monkeypatch):
     """Config 3 at full size: production UNet, latent 64x64x32x4, batch 2 (CFG pair),
     random init; max relative error vs the PyTorch-CPU fp32 oracle <= 1e-4.  The same step under
     precision("bf16") (bf16 operands, fp32 accumulation for every 3x3x3 conv with more than 8 input and
-    4 output channels) stays within the per-layer bf16 bar, 2e-2, end to end."""
-    m = ctmr.maisi
+    4 output channels) stays within the per-layer bf16 bar, 2e-2, end to end.  Every group norm of the
+    fp32 step takes its statistics from the producers' epilogues (convs, attention residual sums): no
+    read pass, the up path's concatenations included."""
+    m, ops = ctmr.maisi, ctmr.ops
     host, w = _production_unet(ctmr, dev)
     rng = np.random.default_rng(3)
     x = rng.standard_normal((2, 64, 64, 32, 4)).astype(np.float32)
@@ -234,7 +236,18 @@ def test_config3_unet_step_matches_cpu_oracle(ctmr, dev):
     spacing = np.repeat(np.asarray([[0.94, 0.94, 1.36]], np.float64) * 100, 2, 0).astype(np.float16).astype(np.float32)
     ctor = m.PRODUCTION_UNET_CONSTRUCTOR
     args = (_g(x, dev), _g(t, dev), _g(classes, dev, torch.int64), _g(spacing, dev), w)
-    _, y = m.denoise_unet(*args, constructor=ctor)
+    passes = {"one": 0, "cat": 0}
+    real = ops.gn_affine
+
+    def counted(x, gamma, beta, groups, eps, x2=None):
+        passes["one" if x2 is None else "cat"] += 1
+        return real(x, gamma, beta, groups, eps, x2)
+
+    with monkeypatch.context() as patch:
+        patch.setattr(ops, "gn_affine", counted)
+        _, y = m.denoise_unet(*args, constructor=ctor)
+    print(f"config3 step: statistics read passes {passes}", flush=True)
+    assert passes == {"one": 0, "cat": 0}
     y = _h(y)
     with ctmr.fast_fp32.precision("bf16"):
         _, y16 = m.denoise_unet(*args, constructor=ctor)

@@ -183,3 +183,33 @@ def test_python_kernel_constants_match_header(ctmr):
     assert len(names) == len(L.KERNEL_NAMES)
     for name, value in names:
         assert getattr(L, "K_" + name) == int(value), name
+
+
+def test_custom_operators_are_registered_and_trace(ctmr):
+    """Every ``ctmr::*`` operator is a registered custom op with a fake implementation: under a
+    FakeTensorMode (tracing) the call goes through the dispatcher to the fake and launches nothing; an
+    eager call on plain tensors (and only that) bypasses the dispatcher."""
+    from torch._subclasses.fake_tensor import FakeTensor, FakeTensorMode
+
+    ops = ctmr.ops
+    names = ["pack_weight", "conv3d", "conv3d_gn", "gn_affine_from_stats", "gn_affine_from_stats2", "add_gn",
+             "gn_affine", "gn_apply", "silu", "resample", "gn_avgpool", "flash_attention"]
+    for name in names:
+        wrapper = getattr(ops, name)
+        assert hasattr(torch.ops.ctmr, name) and type(wrapper.op).__name__ == "CustomOpDef", name
+        assert callable(wrapper.fn) and wrapper.__doc__
+    x = torch.zeros(2, 4, 4, 4, 64)
+    assert ops._direct((x, 3, None))
+    assert not ops._direct((x.requires_grad_(),))
+    with torch.no_grad():
+        assert ops._direct((x,))  # autograd records nothing here
+    x = x.detach()
+    with FakeTensorMode():
+        assert not ops._direct((3,))
+        fx = torch.empty(2, 4, 4, 4, 64)
+        a = ops.gn_affine(fx, torch.empty(64), torch.empty(64), 32, 1e-6)
+        y, st = ops.add_gn(fx, fx)
+        s2 = ops.gn_affine_from_stats2(st, 64, torch.empty(128), torch.empty(128), 32, 100, 1e-6, st)
+    assert isinstance(a, FakeTensor) and tuple(a.shape) == (2, 64, 2)
+    assert tuple(y.shape) == tuple(x.shape) and st.dtype == torch.float64 and st.shape[2:] == (64, 2)
+    assert tuple(s2.shape) == (2, 128, 2)
