@@ -525,6 +525,7 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
             "image_dtype": "torch.int16"}
         del lat
         out["ct_from_mask_256^3_30steps"] = ct_generation(pkg, dev, uw, vw, timed)
+        out.update(production_grids(pkg, dev, uw, vw, timed))
     return out
 
 
@@ -572,6 +573,75 @@ def ct_generation(pkg, dev, uw, vw, timed):
             "f16x2_frac_roofline": round(floorx / secx, 4),
             "timing": "median of 3 after 1 warm-up, label upload to HU download", "peak_device_GiB":
             round(peak / 2**30, 2)}
+
+
+def production_grids(pkg, dev, uw, vw, timed):
+    """The reference's other production grids (its configurations table): MR-Brain 256x256x128 with
+    guidance 2 and general MR 128x256x256 with guidance 15 (batched CFG, batch 2 per step), and CT from
+    a 256x256x128 mask (ControlNet + UNet at batch 1); 30 rflow steps each, then the windowed decode
+    with the default window (both latents are below it: one pass).  One timed run after a warm-up,
+    fp32 and split fp16."""
+    import numpy as np
+    import torch
+
+    m = pkg.maisi
+    uc, cc, vc = m.PRODUCTION_UNET_CONSTRUCTOR, m.PRODUCTION_CONTROLNET_CONSTRUCTOR, m.PRODUCTION_VAE_CONSTRUCTOR
+    rng = np.random.default_rng(9)
+    out = {}
+
+    def mr(name, latent, spacing_mm, guidance):
+        lat = torch.from_numpy(rng.standard_normal((1, *latent, 4), dtype=np.float32)).to(dev)
+        sp = m.spacing_tensor(spacing_mm, device=dev)
+        cls = torch.tensor([9], device=dev)
+        times, _ = m.set_timesteps_rflow(num_inference_steps=30, input_img_size_numel=int(np.prod(latent)))
+        vel = lambda s, tt: m.guided_velocity(s, tt, class_labels=cls, spacing=sp, weights=uw, constructor=uc,
+                                              guidance_scale=guidance)
+
+        def generate():
+            final = m.sample_rflow(lat, vel, times)
+            return torch.clamp(m.sliding_window_decode(final, vw, constructor=vc) * 1000.0, min=0.0).to(
+                torch.int16).cpu()
+
+        sec, peak = timed(generate, reps=1)
+        with pkg.fast_fp32.precision("f16x2"):
+            secx, _ = timed(generate, reps=1)
+        progress(f"{name} generation {sec:.3f} s, f16x2 {secx:.3f} s")
+        flop = 30 * sum(unet_flops(uc, 2, *latent)) + vae_decoder_flops(vc, *latent)
+        attn = 30 * unet_flops(uc, 2, *latent)[1]
+        floorx = (flop - attn) / F16X2_PEAK + attn / FP32_PEAK
+        out[name] = {"s": round(sec, 3), "tflop": round(flop / 1e12, 2), "roofline_s": round(flop / FP32_PEAK, 3),
+                     "frac_roofline": round(flop / FP32_PEAK / sec, 4), "f16x2_s": round(secx, 3),
+                     "f16x2_roofline_s": round(floorx, 3), "f16x2_frac_roofline": round(floorx / secx, 4),
+                     "guidance_scale": guidance, "output": [4 * v for v in latent],
+                     "timing": "one run after a warm-up", "peak_device_GiB": round(peak / 2**30, 2)}
+
+    mr("mr_brain_256x256x128_30steps_cfg", (64, 64, 32), [0.94, 0.94, 1.36], 2.0)
+    mr("mr_128x256x256_30steps_cfg", (32, 64, 64), [1.25, 1.0, 1.0], 15.0)
+
+    cw = {k: torch.from_numpy(v).to(dev) for k, v in m.random_weights(m.controlnet_weight_shapes(cc), seed=13).items()}
+    label = rng.choice(np.array(sorted(m.VALID_LABELS)), size=(1, 1, 256, 256, 128)).astype(np.int16)
+    lat = torch.from_numpy(rng.standard_normal((1, 64, 64, 32, 4), dtype=np.float32)).to(dev)
+
+    def ct():
+        r = m.sample_ct_from_mask(label, (1.7, 1.7, 2.0), unet_weights=uw, controlnet_weights=cw, vae_weights=vw,
+                                  unet_constructor=uc, controlnet_constructor=cc, vae_constructor=vc,
+                                  scale_factor=1.0, latent=lat, drop_weights=False)
+        return r.hu.cpu()
+
+    sec, peak = timed(ct, reps=1)
+    with pkg.fast_fp32.precision("f16x2"):
+        secx, _ = timed(ct, reps=1)
+    progress(f"CT 256x256x128 from mask {sec:.3f} s, f16x2 {secx:.3f} s")
+    step_f = sum(unet_flops(uc, 1, 64, 64, 32)) + sum(controlnet_flops(cc, 1, 64, 64, 32))
+    flop = controlnet_cond_flops(cc, 1, 256, 256, 128) + 30 * step_f + vae_decoder_flops(vc, 64, 64, 32)
+    attn = 30 * (unet_flops(uc, 1, 64, 64, 32)[1] + controlnet_flops(cc, 1, 64, 64, 32)[1])
+    floorx = (flop - attn) / F16X2_PEAK + attn / FP32_PEAK
+    out["ct_from_mask_256x256x128_30steps"] = {
+        "s": round(sec, 3), "tflop": round(flop / 1e12, 2), "roofline_s": round(flop / FP32_PEAK, 3),
+        "frac_roofline": round(flop / FP32_PEAK / sec, 4), "f16x2_s": round(secx, 3),
+        "f16x2_roofline_s": round(floorx, 3), "f16x2_frac_roofline": round(floorx / secx, 4),
+        "timing": "one run after a warm-up, label upload to HU download", "peak_device_GiB": round(peak / 2**30, 2)}
+    return out
 
 
 def _sclk_under(fn, seconds=4.0):

@@ -2567,8 +2567,13 @@ __global__ __launch_bounds__(256, 2) void pointwise_kernel(ConvArgs p) {
     const int m0 = it.m_tile * TM + wave_m * 64;
     const int valid_rows = min(max(S - m0, 0), 64);
     float* out = p.y + (p.split > 1 ? (int64_t)it.split_id * p.plane : 0) + ((int64_t)it.b * p.s_out + m0) * p.cout;
-    const __amdgpu_buffer_rsrc_t orsrc =
-        __builtin_amdgcn_make_buffer_rsrc(out, (short)0, valid_rows * p.cout * 4, 0x00020000);
+    // Both descriptor fields are wave-uniform; the compiler cannot prove it (the row count goes
+    // through a VALU clamp) and would wrap every store in a loop over distinct descriptors.
+    const uint64_t oaddr = (uint64_t)out;
+    out = (float*)(((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(oaddr >> 32)) << 32) |
+                   (unsigned)__builtin_amdgcn_readfirstlane((unsigned)oaddr));
+    const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+        out, (short)0, __builtin_amdgcn_readfirstlane(valid_rows * p.cout * 4), 0x00020000);
     if (p.split == 1 && p.has_bias) {
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
