@@ -770,6 +770,20 @@ def profile_only(pkg, dev, what, steps, warmup):
         w = torch.from_numpy((rng.standard_normal((256, 128, 1, 1, 1)) / np.sqrt(128)).astype(np.float32)).to(dev)
         b = torch.zeros(256, device=dev)
         fn = lambda: f.pointwise_conv(x, w, b)
+    elif what == "output_convs":
+        # the cout <= 4 direct convs with GN + SiLU staged: the VAE decoder's 64 -> 1 at a full 80x256x256
+        # window and the UNet's 64 -> 4 at 2x64x64x32
+        rng = np.random.default_rng(1)
+        calls = []
+        for shape, cout in (((1, 80, 256, 256, 64), 1), ((2, 64, 64, 32, 64), 4)):
+            x = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(dev)
+            w = torch.from_numpy((rng.standard_normal((cout, 64, 3, 3, 3)) / np.sqrt(27 * 64)).astype(np.float32)).to(dev)
+            g, z0 = torch.ones(64, device=dev), torch.zeros(64, device=dev)
+            calls.append((x, w, torch.zeros(cout, device=dev), (g, z0)))
+
+        def fn():
+            for x, w, b, norm in calls:
+                f.norm_conv3d(x, w, b, norm=norm, num_groups=32, eps=1e-6, apply_silu=True)
     elif what in ("config2a", "config2b"):
         # config 2a: stride-2 conv 64->128, 128^3 -> 64^3; config 2b: nearest-2x + conv 256->128, 64^3 -> 128^3
         rng = np.random.default_rng(1)
@@ -812,7 +826,8 @@ def main() -> int:
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
     ap.add_argument("--only", choices=["unet", "unet_bf16", "unet_f16x2", "controlnet", "controlnet_f16x2", "decode",
                                        "decode_bf16", "decode_f16x2", "resblock", "resblock_f16x2",
-                                       "attention", "pointwise", "gemms", "gemms_stream", "config2a", "config2b"],
+                                       "attention", "pointwise", "gemms", "gemms_stream", "config2a", "config2b",
+                                       "output_convs"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM-counter scale reference for rocprofv3 --pmc)")
