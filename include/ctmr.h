@@ -65,9 +65,14 @@ enum ctmr_conv_flags {
   CTMR_F_SILU = 2,       /* SiLU after the affine (or on x) before the conv */
   CTMR_F_BATCH_BIAS = 4, /* bias is (N, Cout) instead of (Cout) */
   CTMR_F_RESIDUAL = 8,   /* residual (output-shaped, NDHWC) added before the store */
-  CTMR_F_STREAM = 16     /* use the one-tile-per-workgroup register-streaming GEMM even
+  CTMR_F_STREAM = 16,    /* use the one-tile-per-workgroup register-streaming GEMM even
                             where the LDS-staged or the persistent pointwise one
                             applies (comparisons and tests) */
+  CTMR_F_SPLIT_WAVES = 32 /* the CTMR_K_SPLIT_WAVES form (each split range over the four
+                            waves) with desc->split (2 .. taps * K blocks / 32) ranges,
+                            which the library otherwise picks only by its own policy
+                            (split 0): a depth slab of such a conv keeps its summation
+                            order (CTMR_E_INVALID where the form does not apply) */
 };
 
 enum ctmr_dtype {

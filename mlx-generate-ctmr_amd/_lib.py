@@ -18,7 +18,7 @@ HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "ctmr.h"
 OK = 0
 E_INVALID, E_UNSUPPORTED, E_WORKSPACE, E_LAUNCH = -1, -2, -3, -4
 MODE_PLAIN, MODE_NEAREST2X, MODE_TRILINEAR2X = 0, 1, 2
-F_AFFINE, F_SILU, F_BATCH_BIAS, F_RESIDUAL, F_STREAM = 1, 2, 4, 8, 16
+F_AFFINE, F_SILU, F_BATCH_BIAS, F_RESIDUAL, F_STREAM, F_SPLIT_WAVES = 1, 2, 4, 8, 16, 32
 DT_F32, DT_BF16, DT_F16X2 = 0, 1, 2
 (K_STREAM, K_STREAM_DIRECT, K_LDS, K_LDS_BF16, K_POINTWISE, K_SPLIT_WAVES, K_TAP_EXPAND, K_LDS_SMALL,
  K_SMALL_COUT, K_LDS_F16X2) = range(10)

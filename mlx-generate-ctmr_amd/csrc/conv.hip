@@ -2975,7 +2975,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   g.small_out = false;
   if (g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 && d->stride == 1 &&
       d->mode == CTMR_MODE_PLAIN && d->cin % 16 == 0 && d->cin >= 64 && d->cout % 64 == 0 &&
-      !(d->flags & CTMR_F_STREAM)) {
+      !(d->flags & (CTMR_F_STREAM | CTMR_F_SPLIT_WAVES))) {
     g.tz = (int)ceil_div(d->d, kBD);
     g.ty = (int)ceil_div(d->h, kBH);
     g.tx = (int)ceil_div(d->w, kBW);
@@ -3020,7 +3020,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   g.lds16 = false;
   g.small_out = false;
   if (g.layout == WL_TAPS && (d->dtype == CTMR_BF16 || d->dtype == CTMR_F16X2) && d->ksize == 3 &&
-      d->stride == 1 && d->cout % 64 == 0 && !(d->flags & CTMR_F_STREAM)) {
+      d->stride == 1 && d->cout % 64 == 0 && !(d->flags & (CTMR_F_STREAM | CTMR_F_SPLIT_WAVES))) {
     const int tz = (int)ceil_div(g.gd, kBD), ty = (int)ceil_div(g.gh, kBH), tx = (int)ceil_div(g.gw, kBW);
     const int64_t slots = (int64_t)tz * ty * tx * kBD * kBH * kBW;
     const int64_t planes = (int64_t)kHD * g.P * g.cp * g.esize;
@@ -3097,7 +3097,16 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // least 2 planes (the waves' quarter sums go to a partial plane; the bias,
   // residual and statistics come from the reduction) and 8 steps per wave.
   g.kws = false;
-  if (d->split == 0 && g.layout == WL_TAPS && !g.lds16 && g.KT != 1 && g.split >= 4) {
+  if (d->flags & CTMR_F_SPLIT_WAVES) {  // this form with the caller's split (a depth slab of such a conv)
+    if (g.layout != WL_TAPS || g.lds16 || g.KT == 1 || d->split < 2 || d->split > steps / 32)
+      return fail(CTMR_E_INVALID, "CTMR_F_SPLIT_WAVES needs a 3x3x3 or nearest-2x streaming GEMM and a split of "
+                                  "2 .. (taps * K blocks) / 32");
+    g.kws = true;
+    g.nsub = 4; g.wm = 1; g.wn = 1;
+    g.m_tiles = (int)ceil_div(S, 64);
+    g.n_tiles = (int)ceil_div(g.np, 64);
+    g.split = d->split;
+  } else if (d->split == 0 && g.layout == WL_TAPS && !g.lds16 && g.KT != 1 && g.split >= 4) {
     const int64_t mt = ceil_div(S, 64), nt = ceil_div(g.np, 64);
     const int64_t base1 = mt * nt * d->n * g.phases;
     const int64_t split1 = std::min<int64_t>(ceil_div(512, base1), steps / 32);

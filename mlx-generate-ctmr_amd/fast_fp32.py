@@ -316,6 +316,62 @@ def cache_size() -> int:
 # ---------------------------------------------------------------------------
 # NDHWC-native operators
 # ---------------------------------------------------------------------------
+# Largest conv workspace (padded input copy + split partial planes) built at once,
+# or None: no limit (the default; one MI355X holds 288 GB).  Above it a stride-1
+# conv runs in depth slabs with the whole volume's kernel and split, so it returns
+# the whole volume's bits (the reference's _SLAB_PACK_BYTES, _nax_conv.py:348-349,
+# 667-684, fixed at 512 MiB there for unified-memory Macs).
+SLAB_WORKSPACE_BYTES: Optional[int] = None
+
+
+def _slabs(x: Tensor, x2: Optional[Tensor], *, cout: int, ksize: int, mode: int, flags: int, code: int, split: int,
+           budget: int):
+    """Plan of a depth-slabbed conv: ``(split, [(input planes a:b, kept input planes s0:s1)], extra flags)``, or None
+    when no slab depth keeps the whole volume's kernel and split for every slab (each output's summation
+    order is fixed by those two: the slabs then give the whole volume's bits)."""
+    n, d, h, w, c1 = (int(v) for v in x.shape)
+    cin2 = 0 if x2 is None else int(x2.shape[-1])
+    whole = ops.make_desc(tuple(x.shape), cout, ksize, 1, mode, flags, code, split, cin2)
+    route, whole_split = _lib.conv_kernel(whole), _lib.conv_split(whole)
+    if route == "split_waves":  # a form the library picks by its own policy only: request it explicitly
+        flags |= _lib.F_SPLIT_WAVES
+    halo = 1 if ksize == 3 else 0
+    per_plane = max(1, _lib.workspace_bytes(whole) // d)
+    depth = max(1, budget // per_plane - 2 * halo)
+    for depth in range(min(depth, d - 1), 0, -1):
+        plan = []
+        for s0 in range(0, d, depth):
+            s1 = min(d, s0 + depth)
+            a, b = max(s0 - halo, 0), min(s1 + halo, d)
+            desc = ops.make_desc((n, b - a, h, w, c1), cout, ksize, 1, mode, flags, code, whole_split, cin2)
+            try:
+                same = _lib.conv_kernel(desc) == route and _lib.conv_split(desc) == whole_split
+            except _lib.CtmrError:
+                same = False
+            if not same:
+                break
+            plan.append((a, b, s0, s1))
+        else:
+            return whole_split, plan, flags & _lib.F_SPLIT_WAVES
+    return None
+
+
+def _conv_in_slabs(x, x2, packed, bias, affine, residual, out_shape, *, cout, ksize, mode, silu, code, split,
+                   stream_gemm, scale: int, plan, flags: int) -> Tensor:
+    """Run ``plan`` (``_slabs``): each slab convolves its input planes with a one-plane halo and keeps the
+    planes whose halo is real data (``scale`` output planes per input plane for trilinear-2x)."""
+    y = torch.empty(out_shape, device=x.device, dtype=torch.float32)
+    for a, b, s0, s1 in plan:
+        xs = x[:, a:b].contiguous()
+        xs2 = None if x2 is None else x2[:, a:b].contiguous()
+        res = None if residual is None else residual[:, scale * a:scale * b].contiguous()
+        ys = ops.conv3d(xs, packed, bias, affine, res, cout, ksize, 1, mode, silu, code, split, stream_gemm, xs2,
+                        flags)
+        y[:, scale * s0:scale * s1] = ys[:, scale * (s0 - a):scale * (s1 - a)]
+        del xs, xs2, res, ys
+    return y
+
+
 def implicit_gemm_conv3d(
     x: Tensor,
     packed: Tensor,
@@ -350,6 +406,13 @@ def implicit_gemm_conv3d(
     reading the output again when its groups are unions of these (``gn_groups =
     cout`` gives per-channel statistics, usable by any grouping).  Shapes that
     cannot produce them are computed without.
+
+    With ``SLAB_WORKSPACE_BYTES`` set and a stride-1 conv (plain, trilinear-2x or
+    1x1x1) whose workspace exceeds it, the conv runs in depth slabs, each with
+    the whole volume's kernel and K split, and returns the whole volume's bits
+    (as the reference's slabbed packs, ``_nax_conv.py:571-573,667-684``); such a
+    conv writes no group-norm statistics.  If no slab depth keeps the kernel and
+    split, the volume runs whole.
 
     Raises:
         ValueError: on a packed weight that does not fit, unsupported option
@@ -390,6 +453,18 @@ def implicit_gemm_conv3d(
         residual = _require(residual, "residual")
         if tuple(residual.shape) != out_shape:
             raise ValueError(f"residual shape {tuple(residual.shape)} != output {out_shape}")
+    budget = SLAB_WORKSPACE_BYTES
+    if budget is not None and stride == 1 and not upsample and int(x.shape[1]) > 1:
+        flags = ops._flags(affine is not None, silu, bias is not None and bias.dim() == 2, residual is not None)
+        flags |= _lib.F_STREAM if stream_gemm else 0
+        whole = ops.make_desc(tuple(x.shape), cout, ksize, 1, mode, flags, code, split, cin2)
+        if _lib.workspace_bytes(whole) > int(budget):
+            plan = _slabs(x, x2, cout=cout, ksize=ksize, mode=mode, flags=flags, code=code, split=split,
+                          budget=int(budget))
+            if plan is not None:
+                return _conv_in_slabs(x, x2, packed, bias, affine, residual, out_shape, cout=cout, ksize=ksize,
+                                      mode=mode, silu=silu, code=code, split=plan[0], stream_gemm=stream_gemm,
+                                      scale=2 if trilinear else 1, plan=plan[1], flags=plan[2])
     # Statistics ride on the output tensor, valid while its version counter is unchanged; under
     # torch.inference_mode the output is an inference tensor without one, so nothing is attached and
     # the group norm reading it makes its own pass.

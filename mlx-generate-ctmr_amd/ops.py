@@ -159,14 +159,16 @@ def conv3d(
     split: int,
     stream_gemm: bool = False,
     x2: Optional[Tensor] = None,
+    extra_flags: int = 0,
 ) -> Tensor:
     """``ctmr_conv3d`` on an NDHWC fp32 tensor; returns the NDHWC output.  ``stream_gemm``
     forces the register-streaming GEMM where the LDS-staged one would be chosen.  With ``x2`` the
-    input is the channel concatenation of ``x`` and ``x2`` (``ctmr_conv3d_cat``)."""
+    input is the channel concatenation of ``x`` and ``x2`` (``ctmr_conv3d_cat``).  ``extra_flags``:
+    route flags OR-ed into the descriptor (``CTMR_F_SPLIT_WAVES``)."""
     _require_device(x, packed, bias, affine, residual, x2)
     x, residual, x2 = _aligned16(x), _aligned16(residual), _aligned16(x2)
     batch_bias = bias is not None and bias.dim() == 2
-    flags = _flags(affine is not None, silu, batch_bias, residual is not None)
+    flags = _flags(affine is not None, silu, batch_bias, residual is not None) | int(extra_flags)
     if stream_gemm:
         flags |= _lib.F_STREAM
     desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, flags, dtype, split, _cin2(x2))
@@ -195,8 +197,8 @@ def conv3d(
 
 @conv3d.register_fake
 def _(x, packed, bias, affine, residual, cout, ksize, stride, mode, silu, dtype, split, stream_gemm=False,
-      x2=None):
-    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, 0, dtype, split, _cin2(x2))
+      x2=None, extra_flags=0):
+    desc = make_desc(tuple(x.shape), cout, ksize, stride, mode, int(extra_flags), dtype, split, _cin2(x2))
     od, oh, ow = _lib.output_dims(desc)
     return x.new_empty((x.shape[0], od, oh, ow, cout))
 

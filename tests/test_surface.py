@@ -213,3 +213,51 @@ def test_custom_operators_are_registered_and_trace(ctmr):
     assert isinstance(a, FakeTensor) and tuple(a.shape) == (2, 64, 2)
     assert tuple(y.shape) == tuple(x.shape) and st.dtype == torch.float64 and st.shape[2:] == (64, 2)
     assert tuple(s2.shape) == (2, 128, 2)
+
+
+def test_depth_slab_plan(ctmr):
+    """The depth-slab plan (descriptors only, no GPU work): every input plane is kept by exactly one slab,
+    each slab reads a one-plane halo inside the volume, and each slab's descriptor selects the whole
+    volume's kernel and split; budgets too small for any such slab depth give no plan (the conv then runs
+    whole)."""
+    f, L, ops = ctmr.fast_fp32, ctmr._lib, ctmr.ops
+    for shape, cout, code, stream in (((2, 20, 64, 64, 64), 64, L.DT_F32, False),  # fp32 LDS-staged GEMM
+                                      ((1, 18, 32, 32, 64), 64, L.DT_F32, True),  # four-wave split form
+                                      ((1, 16, 32, 32, 64), 64, L.DT_F16X2, False)):
+        x = torch.empty(shape, device="meta")
+        flags = L.F_AFFINE | L.F_SILU | (L.F_STREAM if stream else 0)
+        whole = ops.make_desc(shape, cout, 3, 1, 0, flags, code, 0)
+        per_plane = max(1, L.workspace_bytes(whole) // shape[1])
+        plans = 0
+        for depth in range(1, 9):
+            out = f._slabs(x, None, cout=cout, ksize=3, mode=0, flags=flags, code=code, split=0,
+                           budget=per_plane * (depth + 2))
+            if out is None:
+                continue
+            plans += 1
+            split, plan, extra = out
+            assert split == L.conv_split(whole)
+            assert extra == (L.F_SPLIT_WAVES if L.conv_kernel(whole) == "split_waves" else 0)
+            assert [p for a, b, s0, s1 in plan for p in range(s0, s1)] == list(range(shape[1]))
+            assert max(s1 - s0 for a, b, s0, s1 in plan) <= depth
+            for a, b, s0, s1 in plan:
+                assert a == max(s0 - 1, 0) and b == min(s1 + 1, shape[1])
+                desc = ops.make_desc((shape[0], b - a, *shape[2:]), cout, 3, 1, 0, flags | extra, code, split)
+                assert L.conv_kernel(desc) == L.conv_kernel(whole) and L.conv_split(desc) == split
+        assert plans > 0, shape
+
+
+def test_split_waves_flag_host_checks(ctmr, native_loaded):
+    """``CTMR_F_SPLIT_WAVES`` selects the four-wave split form with the caller's split, and is refused
+    where that form does not apply (no split, a split over taps * K blocks / 32, 1x1x1, 16-bit LDS GEMMs)."""
+    import ctypes
+
+    L = ctmr._lib
+    d = L.conv_desc(1, 18, 32, 32, 64, 64, flags=L.F_SPLIT_WAVES, split=2)
+    assert L.conv_kernel(d) == "split_waves" and L.conv_split(d) == 2
+    for kw, status in (({"split": 0}, L.E_INVALID), ({"split": 4}, L.E_INVALID), ({"split": 2, "ksize": 1}, L.E_INVALID),
+                       ({"split": 2, "dtype": L.DT_F16X2}, L.E_UNSUPPORTED)):  # split fp16: the LDS GEMM only
+        args = dict(flags=L.F_SPLIT_WAVES)
+        args.update(kw)
+        rc = native_loaded.ctmr_conv3d_kernel(ctypes.byref(L.conv_desc(1, 18, 32, 32, 64, 64, **args)))
+        assert rc == status, kw
