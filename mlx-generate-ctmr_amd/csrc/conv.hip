@@ -1374,8 +1374,10 @@ struct LdsArgs {
 };
 
 // TWO: the input is two tensors (ctmr_conv3d_cat); the one-tensor kernel keeps
-// precomputed byte offsets and a single descriptor.
-template <bool TWO>
+// precomputed byte offsets and a single descriptor.  XF: the staging
+// transform, bit 0 the GN affine and bit 1 SiLU (p.affine_on, p.silu_on), as
+// template flags so the transform is branch-free code.
+template <bool TWO, int XF>
 __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
   __shared__ __attribute__((aligned(16))) char lds[kHaloVox * kLdsRow];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1477,28 +1479,36 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
     for (int i = 0; i < kStageIters; ++i)
       stage[i] = __builtin_amdgcn_raw_buffer_load_b128(c.rs, piece_off(i, c), c.so, 0);
   };
-  auto commit = [&](int chunk) {
-    f4 sc = {1.f, 1.f, 1.f, 1.f}, of = {0.f, 0.f, 0.f, 0.f};
-    if (p.affine_on) {
+  // GN affine of this thread's four channels of a chunk: (scale, offset) pairs.
+  auto load_affine = [&](int chunk, f4& sc, f4& of) {
+    sc = f4{1.f, 1.f, 1.f, 1.f};
+    of = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr ((XF & 1) != 0) {
       const f4* q = reinterpret_cast<const f4*>(p.affine + ((int64_t)b * p.cin + chunk * 16 + part * 4) * 2);
       const f4 a0 = q[0], a1 = q[1];
       sc = f4{a0[0], a0[2], a1[0], a1[2]};
       of = f4{a0[1], a0[3], a1[1], a1[3]};
     }
+  };
+  // Piece i as staged: GN affine, SiLU, zero outside the volume.
+  auto transform = [&](int i, const f4& sc, const f4& of) {
+    f4 v = __builtin_bit_cast(f4, stage[i]);
+    const bool in = (valid >> i) & 1u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float t = v[j];
+      if constexpr ((XF & 1) != 0) t = fmaf(t, sc[j], of[j]);
+      if constexpr ((XF & 2) != 0) t = silu_f(t);
+      v[j] = in ? t : 0.f;
+    }
+    stage[i] = __builtin_bit_cast(u4, v);
+  };
+  auto commit = [&]() {
 #pragma unroll
     for (int i = 0; i < kStageIters; ++i) {
       const int hv = (tid >> 2) + 64 * i;
       if (hv >= kHaloVox) continue;
-      f4 v = __builtin_bit_cast(f4, stage[i]);
-      const bool in = (valid >> i) & 1u;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float t = v[j];
-        if (p.affine_on) t = fmaf(t, sc[j], of[j]);
-        if (p.silu_on) t = silu_f(t);
-        v[j] = in ? t : 0.f;
-      }
-      *reinterpret_cast<f4*>(lds + hv * kLdsRow + part * 16) = v;
+      *reinterpret_cast<u4*>(lds + hv * kLdsRow + part * 16) = stage[i];
     }
   };
   auto load_a = [&](f4 (&A)[4], int tap) {
@@ -1522,17 +1532,38 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
                                                              acc[ms][ns], 0, 0, 0);  // B^T A^T: see store_brick
   };
 
+  // Without affine or SiLU the staging transform is the zero mask alone: it
+  // runs inside the previous chunk's tap loop, among the MFMAs, and the
+  // commit between the barriers only writes LDS (config 0: 409-412 -> 405-406
+  // us).  With affine + SiLU the same placement measured ~1 % slower than
+  // transforming at the commit, which those variants keep.
+  constexpr bool kInLoop = XF == 0;
   fetch(c_begin);
+  if constexpr (kInLoop) {
+    f4 sc, of;
+    load_affine(c_begin, sc, of);
+#pragma unroll
+    for (int i = 0; i < kStageIters; ++i) transform(i, sc, of);
+  }
   for (int chunk = c_begin; chunk < c_end; ++chunk) {
     __syncthreads();  // every wave has finished reading the previous chunk
-    commit(chunk);
+    if constexpr (!kInLoop) {
+      f4 sc, of;
+      load_affine(chunk, sc, of);
+#pragma unroll
+      for (int i = 0; i < kStageIters; ++i) transform(i, sc, of);
+    }
+    commit();
     __syncthreads();
     f4 A[2][4];
     u4 B[2][4];
     load_b(B[0], 0, chunk);
     load_a(A[0], 0);
     // Unconditional (see conv_kernel): the last chunk re-reads itself.
-    const ChunkSrc nx = chunk_src(min(chunk + 1, c_end - 1));
+    const int next = min(chunk + 1, c_end - 1);
+    const ChunkSrc nx = chunk_src(next);
+    f4 nsc, nof;
+    load_affine(next, nsc, nof);
 #pragma unroll
     for (int t = 0; t < 27; ++t) {
       if (t + 1 < 27) {
@@ -1549,6 +1580,10 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
       // operands are ready wins issue slots over waves in their staging code.
       __builtin_amdgcn_s_setprio(1);
       mma(A[t & 1], B[t & 1]);
+      // Piece i, loaded at tap 2i + 1, is masked at tap 2i + 6.
+      if (kInLoop && t >= 6 && !(t & 1) && ((t - 6) >> 1) < kStageIters) {
+        transform((t - 6) >> 1, nsc, nof);
+      }
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -3609,8 +3644,23 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.y = g.split > 1 ? part : y;
     if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
     const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.split;
-    if (a.x2) hipLaunchKernelGGL(conv_lds_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(conv_lds_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    const dim3 grid((unsigned)blocks);
+    const int xf = (a.affine_on ? 1 : 0) | (a.silu_on ? 2 : 0);
+    if (a.x2) {
+      switch (xf) {
+        case 0: hipLaunchKernelGGL((conv_lds_kernel<true, 0>), grid, dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((conv_lds_kernel<true, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((conv_lds_kernel<true, 2>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((conv_lds_kernel<true, 3>), grid, dim3(256), 0, st, a); break;
+      }
+    } else {
+      switch (xf) {
+        case 0: hipLaunchKernelGGL((conv_lds_kernel<false, 0>), grid, dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((conv_lds_kernel<false, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((conv_lds_kernel<false, 2>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((conv_lds_kernel<false, 3>), grid, dim3(256), 0, st, a); break;
+      }
+    }
     if ((rc = check_launch("conv_lds"))) return rc;
     if (g.split > 1) {
       launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
