@@ -862,11 +862,35 @@ __device__ __forceinline__ void mma_block(f4 (&acc)[4][NSUB], const u4 (&A)[4], 
   }
 }
 
+// One DPP lane move of an fp64 value (two 32-bit halves; every source lane
+// lies inside the lane's row of 16).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(unsigned)u, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+// Sum over the 16 lanes of a row, in the tree of an xor butterfly (partners
+// 1, 2, 4, 8): quad_perm [1,0,3,2] and [2,3,0,1] are xor 1 and xor 2; after
+// them lane 7 - i of a half row holds the value lane i ^ 4 holds (fp32/fp64
+// addition commutes), so the half-row mirror is the xor-4 step and the row
+// mirror the xor-8 step.  VALU moves instead of LDS permutes.
+__device__ __forceinline__ double row16_sum(double v) {
+  v += dpp_f64<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f64<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f64<0x141>(v);  // row_half_mirror
+  v += dpp_f64<0x140>(v);  // row_mirror
+  return v;
+}
+
 // Column sums over a wave's 64 rows of a transposed accumulator block set
 // (lane l of block (ms, ns): row ms*16 + l%16, columns ns*16 + 4*(l/16) .. +3),
 // masked by row_ok[ms] and col_ok[ns]: per block ns the 4 row blocks in the
-// lane, then xor butterflies over l%16; lanes l%16 == 0 publish the fp64
-// (sum, sum of squares) of their 4 columns in red[wave][column].  A fixed order.
+// lane, then the butterfly tree over l%16 (row16_sum); lanes l%16 == 0
+// publish the fp64 (sum, sum of squares) of their 4 columns in
+// red[wave][column].  A fixed order.
 template <int NSUB>
 __device__ __forceinline__ void column_sums(const f4 (&acc)[4][NSUB], const bool (&row_ok)[4],
                                             const bool (&col_ok)[NSUB], double (*red)[64][2], int wave, int lane) {
@@ -885,12 +909,10 @@ __device__ __forceinline__ void column_sums(const f4 (&acc)[4][NSUB], const bool
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) {
-        q1[r] += __shfl_xor(q1[r], m);
-        q2[r] += __shfl_xor(q2[r], m);
-      }
+    for (int r = 0; r < 4; ++r) {
+      q1[r] = row16_sum(q1[r]);
+      q2[r] = row16_sum(q2[r]);
+    }
     if (lrow == 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
