@@ -174,6 +174,35 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict
   }
 }
 
+// Thread t's sums of items t, t + 256, t + 512, .. (ascending, one running
+// (sum, sum of squares) pair): pair(i) is item i's partial pair.  Eight items'
+// loads are issued before their adds, so the loop waits for memory once per
+// eight items instead of once per item; the order of the adds is unchanged.
+template <typename Pair>
+__device__ __forceinline__ void strided_pair_sums(int64_t items, Pair pair, double& sm, double& sq) {
+  constexpr int kDepth = 8;
+  int64_t i = threadIdx.x;
+  for (; i + (kDepth - 1) * 256 < items; i += kDepth * 256) {
+    double a[kDepth], q[kDepth];
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) {
+      const double* p = pair(i + u * 256);
+      a[u] = p[0];
+      q[u] = p[1];
+    }
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) {
+      sm += a[u];
+      sq += q[u];
+    }
+  }
+  for (; i < items; i += 256) {
+    const double* p = pair(i);
+    sm += p[0];
+    sq += p[1];
+  }
+}
+
 // Fixed-order combine of the 256 per-thread (sum, sum of squares) of group g of
 // batch item b (a butterfly across each wave, then the four waves in order),
 // then that group's (scale, offset) pairs.
@@ -187,16 +216,14 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(const double* __restri
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta,
                                                           float eps, float* __restrict__ affine) {
-  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int g = blockIdx.x, b = blockIdx.y;
   const int cpg = c / groups;
   const int64_t items = (int64_t)chunks * cpg;
   double sm = 0, sq = 0;
-  for (int64_t i = t; i < items; i += 256) {
+  strided_pair_sums(items, [&](int64_t i) {
     const int chunk = (int)(i / cpg), cc = (int)(i % cpg);
-    const double* p = part + (((int64_t)b * chunks + chunk) * c + g * cpg + cc) * 2;
-    sm += p[0];
-    sq += p[1];
-  }
+    return part + (((int64_t)b * chunks + chunk) * c + g * cpg + cc) * 2;
+  }, sm, sq);
   gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
 }
 
@@ -208,13 +235,9 @@ __global__ __launch_bounds__(256) void gn_tiles_finalize_kernel(const double* __
                                                                 const float* __restrict__ gamma,
                                                                 const float* __restrict__ beta, float eps,
                                                                 float* __restrict__ affine) {
-  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int g = blockIdx.x, b = blockIdx.y;
   double sm = 0, sq = 0;
-  for (int i = t; i < tiles; i += 256) {
-    const double* p = part + (((int64_t)b * tiles + i) * groups + g) * 2;
-    sm += p[0];
-    sq += p[1];
-  }
+  strided_pair_sums(tiles, [&](int64_t i) { return part + (((int64_t)b * tiles + i) * groups + g) * 2; }, sm, sq);
   gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
 }
 
@@ -235,7 +258,7 @@ __global__ __launch_bounds__(256) void gn_stats_finalize_kernel(StatSource s1, S
                                                                 int64_t count, const float* __restrict__ gamma,
                                                                 const float* __restrict__ beta, float eps,
                                                                 float* __restrict__ affine) {
-  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int g = blockIdx.x, b = blockIdx.y;
   const int cpg = c / groups, lo = g * cpg, hi = lo + cpg;
   double sm = 0, sq = 0;
   const StatSource* src[2] = {&s1, &s2};
@@ -247,12 +270,10 @@ __global__ __launch_bounds__(256) void gn_stats_finalize_kernel(StatSource s1, S
     if (a >= e) continue;
     const int scpg = s.c / s.sgroups, g0 = a / scpg, ng = (e - a) / scpg;
     const int64_t items = (int64_t)s.tiles * ng;
-    for (int64_t i = t; i < items; i += 256) {
+    strided_pair_sums(items, [&](int64_t i) {
       const int tile = (int)(i / ng), sg = g0 + (int)(i % ng);
-      const double* p = s.stats + (((int64_t)b * s.tiles + tile) * s.sgroups + sg) * 2;
-      sm += p[0];
-      sq += p[1];
-    }
+      return s.stats + (((int64_t)b * s.tiles + tile) * s.sgroups + sg) * 2;
+    }, sm, sq);
   }
   gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
 }
