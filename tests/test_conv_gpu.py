@@ -181,6 +181,48 @@ def test_lds_staged_and_streaming_gemms_match_float64(ctmr, dev, shape, cout, fu
     assert rm.max_rel_error(outs[0], outs[1]) <= 2 * FP32_REL
 
 
+@pytest.mark.parametrize("two_source", [False, True])
+@pytest.mark.parametrize(("affine_on", "silu"), [(False, False), (True, False), (False, True), (True, True)])
+def test_lds_gemm_staging_transforms_match_float64(ctmr, dev, affine_on, silu, two_source):
+    """Each staging transform of the fp32 LDS GEMM (no transform, GN affine alone, SiLU alone, both; a
+    template instance each, one- and two-source) against float64 and against the streaming GEMM over
+    the packed copy, which applies the same transform in its pack."""
+    rng = np.random.default_rng(43 + 2 * affine_on + silu)
+    shape, c2, cout = (2, 8, 16, 15, 64), 32 if two_source else 0, 64
+    n, c1 = shape[0], shape[-1]
+    c = c1 + c2
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    x2 = (rng.standard_normal((*shape[:-1], c2)) - 0.25).astype(np.float32) if c2 else None
+    xc = np.concatenate([x, x2], -1) if c2 else x
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal(cout).astype(np.float32)
+    f = ctmr.fast_fp32
+    packed = f.pack_weight(_t(w, dev))
+    xin = f.ChannelCat(_t(x, dev), _t(x2, dev)) if c2 else _t(x, dev)
+    prepared = xc.astype(np.float64)
+    affine = None
+    if affine_on:
+        gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+        affine = f.group_norm_affine(xin, _t(gw, dev), _t(gb, dev), groups=8, eps=1e-6)
+        a = _h(affine).astype(np.float64)  # (n, c, 2): the GEMMs apply exactly these fp32 pairs
+        prepared = prepared * a[:, None, None, None, :, 0] + a[:, None, None, None, :, 1]
+    if silu:
+        prepared = prepared / (1.0 + np.exp(-prepared))
+    expected = rm.conv3d(prepared, w) + bias
+    outs = []
+    for stream_gemm in (False, True):
+        y = f.implicit_gemm_conv3d(xin, packed, _t(bias, dev), cout=cout, affine=affine, silu=silu,
+                                   split=1, stream_gemm=stream_gemm)
+        _assert_rel(_h(y), expected, FP32_REL, f"affine={affine_on} silu={silu} two={two_source} "
+                                               f"{'streaming' if stream_gemm else 'lds'}")
+        outs.append(_h(y))
+    desc = ctmr.ops.make_desc(tuple(shape), cout, 3, 1, 0, ctmr.ops._flags(affine_on, silu, False, False),
+                              0, 1, c2)
+    assert ctmr._lib.conv_kernel(desc) == "lds"  # the route of split=1 above
+    assert rm.max_rel_error(outs[0], outs[1]) <= 2 * FP32_REL
+
+
 @pytest.mark.parametrize(("shape", "cout", "kw"), [
     ((2, 8, 16, 16, 64), 64, {}),                               # config-0 channels, policy chunk split
     ((1, 7, 16, 15, 128), 128, {"split": 1}),                   # ragged bricks (clamped halo, masked rows)
