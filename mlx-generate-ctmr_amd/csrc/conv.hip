@@ -1307,15 +1307,20 @@ constexpr int kStageIters = (kHaloVox * 4 + 255) / 256;  // 16-byte pieces per t
 // transposed accumulators: lane l of block (ms, ns) holds voxel (z0 + wave,
 // y0 + ms + 4*((l/8)%2), x0 + l%8) of the 4x8x8 brick and output columns
 // n0 + ns*16 + 4*(l/16) .. +3 (cout % 64 == 0), stored -- bias first, then the
-// residual -- as 16 bytes.  UP: the brick is of the source grid (p.d, p.h,
+// residual -- as 16 bytes (`after_bias` adds any term that follows the bias:
+// a second K range).  UP: the brick is of the source grid (p.d, p.h,
 // p.w) and voxel (z, y, x) of parity `phase` = 4a + 2b + c is output voxel
 // (2z + a, 2y + b, 2x + c) of the doubled grid; statistics tiles are
 // (brick, parity) pairs.  Group-norm column sums go through `red` (4 KiB of
 // LDS, which may alias the kernel's staging buffers: a barrier precedes it).
-template <bool UP = false, typename Args>
+struct NoTerm {
+  __device__ void operator()(f4 (&)[4][4]) const {}
+};
+
+template <bool UP = false, typename Args, typename AfterBias = NoTerm>
 __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int b, int split_id, int z0, int y0,
                                             int x0, int n0, int wave, int lane, int tile_id,
-                                            double (*red)[64][2], int phase = 0) {
+                                            double (*red)[64][2], int phase = 0, AfterBias after_bias = {}) {
   const int lrow = lane & 15, lgrp = lane >> 4;
   const bool partial = p.split > 1;
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
@@ -1340,6 +1345,7 @@ __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int 
       for (int ms = 0; ms < 4; ++ms) acc[ms][ns] += bq;
     }
   }
+  after_bias(acc);
   if (!partial && p.has_res) {  // every residual load before the first store
     f4 rq[4][4];
 #pragma unroll
@@ -1398,11 +1404,18 @@ struct LdsArgs {
 // TWO: the input is two tensors (ctmr_conv3d_cat); the one-tensor kernel keeps
 // precomputed byte offsets and a single descriptor.  XF: the staging
 // transform, bit 0 the GN affine and bit 1 SiLU (p.affine_on, p.silu_on), as
-// template flags so the transform is branch-free code.
-template <bool TWO, int XF>
-__global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
-  __shared__ __attribute__((aligned(16))) char lds[kHaloVox * kLdsRow];
-  const int tid = threadIdx.x, lane = tid & 63;
+// template flags so the transform is branch-free code.  WS = 2: a K split of
+// two ranges inside the workgroup -- wave set s (waves 4s .. 4s + 3, each set
+// with its own halo buffer) runs the chunks of range s of one brick, and set
+// 0 adds set 1's sums after the bias, the order of the split reduction
+// (bias, range 0, range 1, residual), with no partial planes in memory.
+template <bool TWO, int XF, int WS>
+__global__ __launch_bounds__(256 * WS, WS == 1 ? 2 : 1) void conv_lds_kernel(LdsArgs p) {
+  static_assert(WS == 1 || WS == 2, "one or two wave sets");
+  __shared__ __attribute__((aligned(16))) char lds_sets[WS * kHaloVox * kLdsRow];
+  const int set = WS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+  char* const lds = lds_sets + set * (kHaloVox * kLdsRow);
+  const int tid = threadIdx.x & 255, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // XCD-aware order (as conv_kernel): neighbouring bricks share halo planes.
   const int nb = gridDim.x, bid = blockIdx.x;
@@ -1491,8 +1504,9 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int c_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)split_id * p.kb / p.split));
-  const int c_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(split_id + 1) * p.kb / p.split));
+  const int kpart = split_id * WS + set, kparts = p.split * WS;
+  const int c_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)kpart * p.kb / kparts));
+  const int c_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(kpart + 1) * p.kb / kparts));
 
   u4 stage[kStageIters];
   auto fetch = [&](int chunk) {
@@ -1612,7 +1626,30 @@ __global__ __launch_bounds__(256, 2) void conv_lds_kernel(LdsArgs p) {
   }
 
   __shared__ double red[4][64][2];
-  store_brick(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, (bz * p.ty + by) * p.tx + bx, red);
+  const int tile_id = (bz * p.ty + by) * p.tx + bx;
+  if constexpr (WS == 2) {
+    // Set 1 hands its sums to set 0 through the halo buffers (64 KiB of the
+    // 2 x 47 KiB) once every wave has finished reading them, then ends; the
+    // barriers after that wait only for set 0's waves.
+    f4* const xs = reinterpret_cast<f4*>(lds_sets);
+    __syncthreads();
+    if (set == 1) {
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) xs[(wave * 16 + ms * 4 + ns) * 64 + lane] = acc[ms][ns];
+    }
+    __syncthreads();
+    if (set == 1) return;
+    store_brick(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, tile_id, red, 0, [&](f4 (&a)[4][4]) {
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) a[ms][ns] += xs[(wave * 16 + ms * 4 + ns) * 64 + lane];
+    });
+  } else {
+    store_brick(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, tile_id, red);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2816,6 +2853,7 @@ struct Geometry {
   int split;
   int nsub, wm, wn, m_tiles, n_tiles;
   bool lds;              // LDS-staged GEMM (conv_lds_kernel)
+  int wsets;             // its K ranges as wave sets of one workgroup (2: a split of 2 without partial planes)
   bool lds16;            // LDS-staged bf16 GEMM over the packed copy (conv_lds_bf16_kernel)
   bool small_out;        // direct cout <= 4 conv from an LDS halo (conv_small_cout_kernel)
   bool lds_small;        // LDS-staged im2col GEMM for cin 4 / 8 (conv_lds_small_kernel)
@@ -3028,6 +3066,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   // barriers dominate), 64-wide column tiles, at least 4 chunks per split, and
   // 6 staged planes within 32-bit buffer offsets.
   g.lds = false;
+  g.wsets = 1;
   g.lds16 = false;
   g.small_out = false;
   if (g.layout == WL_TAPS && d->dtype == CTMR_F32 && d->ksize == 3 && d->stride == 1 &&
@@ -3061,9 +3100,13 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
       const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n;
       g.split = (int)lds_policy_split(base, chunks);
     }
+    // A split of two over an even chunk count runs as two wave sets of one
+    // workgroup (the same K ranges and output bits, no partial planes and no
+    // reduction launch; group-norm partials per brick as without a split).
+    g.wsets = (g.split == 2 && chunks % 2 == 0) ? 2 : 1;
     g.pack_bytes = (d->flags & CTMR_F_AFFINE) ? round_up((int64_t)d->n * d->cin * 2 * 4, 256) : 0;
-    g.part_bytes = g.split > 1 ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
-    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * g.split;
+    g.part_bytes = (g.split > 1 && g.wsets == 1) ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * (g.wsets == 2 ? 1 : g.split) * g.wsets;
     if (blocks * 256 >= (1ll << 32)) return fail(CTMR_E_UNSUPPORTED, "grid too large");
     return CTMR_OK;
   }
@@ -3208,7 +3251,7 @@ static int gn_stats_tiles(const ctmr_conv_desc* d, const Geometry& g, int groups
     return (g.nsub == 4 && cpg <= 64 && 64 % cpg == 0) ? g.tz * g.ty * g.tx : 0;
   }
   const int cpg = d->cout / groups;
-  if (g.split > 1) {
+  if (g.split > 1 && g.wsets == 1) {
     if (d->cout % 64 != 0 || 64 % cpg != 0) return 0;
     const int64_t s_out = (int64_t)g.od * g.oh * g.ow, per = 16 * (int64_t)split_gn_rows(d, g);
     const int64_t chunks = (s_out + per - 1) / per;
@@ -3236,6 +3279,18 @@ static void launch_split_reduce(const ctmr_conv_desc* d, const Geometry& g, cons
 }
 
 typedef void (*ConvFn)(dim3, dim3, hipStream_t, const ConvArgs&);
+
+// conv_lds_kernel for a staging transform xf (bit 0 affine, bit 1 SiLU).
+template <bool TWO, int WS>
+static void launch_lds(int xf, dim3 grid, hipStream_t st, const LdsArgs& a) {
+  const dim3 block(256 * WS);
+  switch (xf) {
+    case 0: hipLaunchKernelGGL((conv_lds_kernel<TWO, 0, WS>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((conv_lds_kernel<TWO, 1, WS>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((conv_lds_kernel<TWO, 2, WS>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((conv_lds_kernel<TWO, 3, WS>), grid, block, 0, st, a); break;
+  }
+}
 
 // The 64-column register-streaming GEMM is tuned for two resident workgroups
 // per CU (two waves per SIMD; its split policy and round sizes assume 512 per
@@ -3659,32 +3714,28 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
     a.has_bias = bias != nullptr;
     a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
-    a.stats = g.split > 1 ? nullptr : stats;  // a split's partial planes: the reduce writes them
+    // A split's partial planes: the reduce writes outputs and statistics (one
+    // in two wave sets: the kernel does).
+    const bool partial = g.split > 1 && g.wsets == 1;
+    a.stats = partial ? nullptr : stats;
     a.gn_groups = stats ? groups : 0;
     a.gn_cpg = stats ? desc->cout / groups : 1;
     float* part = (float*)((char*)workspace + g.pack_bytes);
-    a.y = g.split > 1 ? part : y;
-    if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
-    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.split;
+    a.y = partial ? part : y;
+    if (partial) { a.res = nullptr; a.has_res = 0; }
+    if (g.wsets == 2) a.split = 1;  // the kernel's two K ranges are its wave sets
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * a.split;
     const dim3 grid((unsigned)blocks);
     const int xf = (a.affine_on ? 1 : 0) | (a.silu_on ? 2 : 0);
     if (a.x2) {
-      switch (xf) {
-        case 0: hipLaunchKernelGGL((conv_lds_kernel<true, 0>), grid, dim3(256), 0, st, a); break;
-        case 1: hipLaunchKernelGGL((conv_lds_kernel<true, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((conv_lds_kernel<true, 2>), grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL((conv_lds_kernel<true, 3>), grid, dim3(256), 0, st, a); break;
-      }
+      if (g.wsets == 2) launch_lds<true, 2>(xf, grid, st, a);
+      else launch_lds<true, 1>(xf, grid, st, a);
     } else {
-      switch (xf) {
-        case 0: hipLaunchKernelGGL((conv_lds_kernel<false, 0>), grid, dim3(256), 0, st, a); break;
-        case 1: hipLaunchKernelGGL((conv_lds_kernel<false, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((conv_lds_kernel<false, 2>), grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL((conv_lds_kernel<false, 3>), grid, dim3(256), 0, st, a); break;
-      }
+      if (g.wsets == 2) launch_lds<false, 2>(xf, grid, st, a);
+      else launch_lds<false, 1>(xf, grid, st, a);
     }
     if ((rc = check_launch("conv_lds"))) return rc;
-    if (g.split > 1) {
+    if (partial) {
       launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
       if ((rc = check_launch("split_reduce"))) return rc;
     }

@@ -122,7 +122,10 @@ def test_split_policy_is_shape_only(ctmr):
     # 256-channel level, 320 bricks x 4 column tiles = 1280 workgroups (2.5 rounds -> 5 whole rounds);
     # whole rounds (1024) and grids of 4 rounds or more do not
     assert L.conv_split(L.conv_desc(1, 20, 64, 64, 256, 256)) == 2
-    assert L.workspace_bytes(L.conv_desc(1, 20, 64, 64, 256, 256)) == 2 * 20 * 64 * 64 * 256 * 4
+    # two K ranges over an even chunk count run as two wave sets of one workgroup: no partial planes
+    assert L.workspace_bytes(L.conv_desc(1, 20, 64, 64, 256, 256)) == 0
+    # three ranges keep the partial planes
+    assert L.workspace_bytes(L.conv_desc(1, 20, 64, 64, 256, 256, split=3)) == 3 * 20 * 64 * 64 * 256 * 4
     assert L.conv_split(L.conv_desc(2, 64, 64, 32, 64, 64)) == 1  # 1024
     assert L.conv_split(L.conv_desc(1, 40, 128, 128, 128, 128)) == 1  # 5120
     # an explicit split may be any count up to the K step count (27 taps x 32
@@ -233,7 +236,11 @@ def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     assert tiles(32, 1, 64, 64, 64, 64, 64) == 64**3 // 256  # streaming: one per 256-voxel M tile
     # K split: the reduction writes them, one per chunk of 16 * rows output voxels (rows keeps ~1024 blocks)
     assert tiles(32, 2, 4, 8, 8, 512, 512) == 256 // 16
-    assert tiles(32, 2, 16, 32, 32, 128, 128) == 16 * 32 * 32 // (16 * 4)
+    assert tiles(32, 2, 16, 32, 32, 128, 128, split=4) == 16 * 32 * 32 // (16 * 4)
+    # a split of two over an even chunk count runs as two wave sets of one LDS-GEMM workgroup, whose
+    # epilogue writes them: one per 4x8x8 brick
+    assert L.conv_split(L.conv_desc(2, 16, 32, 32, 128, 128)) == 2
+    assert tiles(32, 2, 16, 32, 32, 128, 128) == 4 * 4 * 4
     assert tiles(3, 1, 8, 8, 8, 256, 96, split=4) == 0  # split reduce works on 64-column tiles
     assert tiles(2, 1, 8, 8, 8, 256, 256, split=4) == 0  # 128-wide groups
     assert tiles(1, 1, 8, 8, 8, 64, 1) == 0  # cout <= 4: outputs come from the tap sum
