@@ -960,10 +960,16 @@ constexpr int kStoreNT = 2;
 // IDENT: GEMM row v of batch item b is output voxel b * s_out + v (every route
 // but the nearest-2x parity phases), so a wave's 64 rows are contiguous and
 // its stores go through one buffer descriptor with the SC1 cache policy.
-template <int NSUB, int WM, int WN, bool IDENT, typename OutVoxel>
+// No term after the bias (the epilogues' default `after_bias`).
+struct NoTerm {
+  template <typename Acc>
+  __device__ void operator()(Acc&) const {}
+};
+
+template <int NSUB, int WM, int WN, bool IDENT, typename OutVoxel, typename AfterBias = NoTerm>
 __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB], const f4 (&bq)[NSUB], int b,
                                            int m0, int n0, int S, int split_id, int wave, int lane, int col0,
-                                           int tile_id, OutVoxel out_voxel) {
+                                           int tile_id, OutVoxel out_voxel, AfterBias after_bias = {}) {
   const int lrow = lane & 15, lgrp = lane >> 4;
   const bool partial = p.split > 1;
   float* out = p.y + (partial ? (int64_t)split_id * p.plane : 0);
@@ -985,6 +991,7 @@ __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB]
 #pragma unroll
       for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += bq[ns];
   }
+  after_bias(acc);  // a second K range, between the bias and the residual
   if (add_res) {
     f4 rq[4][NSUB];
 #pragma unroll
@@ -1062,14 +1069,21 @@ __device__ __forceinline__ void store_tile(const ConvArgs& p, f4 (&acc)[4][NSUB]
 // KWS = 4 (small K-split grids, a 64 x 64 tile per workgroup): the four waves
 // sum four contiguous quarters of the workgroup's K range for the same tile and
 // combine them through LDS in ascending order, so a launch needs a quarter of
-// the split partial planes (and their reduction traffic).
-template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false, int KWS = 1>
-__global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
-  static_assert(WM * WN * KWS == 4, "four waves per workgroup");
+// the split partial planes (and their reduction traffic).  SETS = 2 with it:
+// a split of two inside the workgroup -- wave set s (waves 4s .. 4s + 3) sums
+// K range s as above, and set 0 adds set 1's sum after the bias (the split
+// reduction's order: bias, range 0, range 1, residual), so the launch writes
+// the outputs and their group-norm partials with no partial planes.
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false, int KWS = 1,
+          int SETS = 1>
+__global__ __launch_bounds__(256 * SETS, SETS == 1 ? 2 : 1) void conv_kernel(ConvArgs p) {
+  static_assert(WM * WN * KWS == 4, "four waves per wave set");
+  static_assert(SETS == 1 || (SETS == 2 && KWS == 4), "two wave sets only with the four-wave K split");
   static_assert(!DIRECT || (KT == 3 && !UP && DT == CTMR_F32), "direct reads: plain fp32 3x3x3 convs");
   const int lane = threadIdx.x & 63;
   // Wave index made provably uniform so every address base below lives in SGPRs.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int set = wave_all >> 2, wave = wave_all & 3;
   const int wave_mn = wave % (WM * WN), wave_k = wave / (WM * WN);
   const int wave_m = wave_mn % WM, wave_n = wave_mn / WM;
 
@@ -1154,8 +1168,9 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
   const int steps = p.taps * p.kb;
   // Wave-uniform (readfirstlane) so the loop counter and the load cursor
   // derived from them stay in SGPRs.
-  const int g_begin = (int)((int64_t)split_id * steps / p.split);
-  const int g_end = (int)((int64_t)(split_id + 1) * steps / p.split);
+  const int kpart = split_id * SETS + set, kparts = p.split * SETS;
+  const int g_begin = (int)((int64_t)kpart * steps / kparts);
+  const int g_end = (int)((int64_t)(kpart + 1) * steps / kparts);
   const int s_begin = __builtin_amdgcn_readfirstlane(g_begin + (g_end - g_begin) * wave_k / KWS);
   const int s_end = __builtin_amdgcn_readfirstlane(g_begin + (g_end - g_begin) * (wave_k + 1) / KWS);
   const int bstep = p.np * 64;
@@ -1245,16 +1260,34 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
+  auto out_voxel = [&](int v) -> int64_t {
+    int o = v;
+    if (UP) {
+      const int d = v / ghw, rr = v - d * ghw;
+      const int h = rr / p.gw, w = rr - h * p.gw;
+      o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
+    }
+    return (int64_t)b * p.s_out + o;
+  };
+  auto finish = [&](auto after_bias) {
+    f4 bq[NSUB];
+    load_bias<NSUB>(p, b, n0, lane, bq);
+    store_tile<NSUB, WM, WN, !UP>(p, acc, bq, b, m0, n0, S, split_id, wave, lane, n_tile * (WN * NSUB * 16),
+                                  tile_id, out_voxel, after_bias);
+  };
   if constexpr (KWS > 1) {
-    // Quarters 1..3 hand their sums to wave 0, which adds them in ascending
-    // order; the result is a split partial plane (no bias, residual or
-    // statistics: the host uses KWS only with a split), stored by wave 0.
-    __shared__ f4 xk[KWS - 1][4][NSUB][64];
+    // Quarters 1..3 of a set hand their sums to the set's wave 0, which adds
+    // them in ascending order (with one set and a split: a split partial
+    // plane, whose bias, residual and statistics come from the reduction).
+    // With two sets, set 1's wave 0 then hands its sum to set 0's (the
+    // barriers wait only for the waves still running).
+    __shared__ f4 xk[SETS][KWS - 1][4][NSUB][64];
     if (wave_k > 0) {
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-        for (int ns = 0; ns < NSUB; ++ns) xk[wave_k - 1][ms][ns][lane] = acc[ms][ns];
+        for (int ns = 0; ns < NSUB; ++ns) xk[set][wave_k - 1][ms][ns][lane] = acc[ms][ns];
     }
     __syncthreads();
     if (wave_k > 0) return;
@@ -1263,21 +1296,28 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(ConvArgs p) {
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms)
 #pragma unroll
-        for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += xk[w][ms][ns][lane];
+        for (int ns = 0; ns < NSUB; ++ns) acc[ms][ns] += xk[set][w][ms][ns][lane];
+    if constexpr (SETS == 2) {
+      if (set == 1) {
+#pragma unroll
+        for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+          for (int ns = 0; ns < NSUB; ++ns) xk[1][0][ms][ns][lane] = acc[ms][ns];
+      }
+      __syncthreads();
+      if (set == 1) return;
+      finish([&](f4 (&a)[4][NSUB]) {
+#pragma unroll
+        for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+          for (int ns = 0; ns < NSUB; ++ns) a[ms][ns] += xk[1][0][ms][ns][lane];
+      });
+    } else {
+      finish(NoTerm{});
+    }
+  } else {
+    finish(NoTerm{});
   }
-  const int tile_id = UP ? phase * p.m_tiles + m_tile : m_tile;
-  f4 bq[NSUB];
-  load_bias<NSUB>(p, b, n0, lane, bq);
-  store_tile<NSUB, WM, WN, !UP>(p, acc, bq, b, m0, n0, S, split_id, wave, lane, n_tile * (WN * NSUB * 16), tile_id,
-                           [&](int v) -> int64_t {
-                             int o = v;
-                             if (UP) {
-                               const int d = v / ghw, rr = v - d * ghw;
-                               const int h = rr / p.gw, w = rr - h * p.gw;
-                               o = ((2 * d + pd) * p.oh + 2 * h + ph) * p.ow + 2 * w + pw;
-                             }
-                             return (int64_t)b * p.s_out + o;
-                           });
 }
 
 // ---------------------------------------------------------------------------
@@ -1313,10 +1353,6 @@ constexpr int kStageIters = (kHaloVox * 4 + 255) / 256;  // 16-byte pieces per t
 // (2z + a, 2y + b, 2x + c) of the doubled grid; statistics tiles are
 // (brick, parity) pairs.  Group-norm column sums go through `red` (4 KiB of
 // LDS, which may alias the kernel's staging buffers: a barrier precedes it).
-struct NoTerm {
-  __device__ void operator()(f4 (&)[4][4]) const {}
-};
-
 template <bool UP = false, typename Args, typename AfterBias = NoTerm>
 __device__ __forceinline__ void store_brick(const Args& p, f4 (&acc)[4][4], int b, int split_id, int z0, int y0,
                                             int x0, int n0, int wave, int lane, int tile_id,
@@ -3206,6 +3242,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     g.m_tiles = (int)ceil_div(S, 64);
     g.n_tiles = (int)ceil_div(g.np, 64);
     g.split = d->split;
+    g.wsets = g.split == 2 ? 2 : 1;
   } else if (d->split == 0 && g.layout == WL_TAPS && !g.lds16 && g.KT != 1 && g.split >= 4) {
     const int64_t mt = ceil_div(S, 64), nt = ceil_div(g.np, 64);
     const int64_t base1 = mt * nt * d->n * g.phases;
@@ -3216,6 +3253,9 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
       g.m_tiles = (int)mt;
       g.n_tiles = (int)nt;
       g.split = (int)split1;
+      // A split of two runs as two wave sets of one workgroup: the same K
+      // ranges and output bits, no partial planes and no reduction launch.
+      g.wsets = g.split == 2 ? 2 : 1;
     }
   }
   const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases * g.split;
@@ -3226,7 +3266,7 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
   g.pointwise = g.KT == 1 && g.nsub == 4 && g.layout != WL_EXPAND && d->cout % 4 == 0 &&
                 !(d->flags & (CTMR_F_STREAM | CTMR_F_BATCH_BIAS | CTMR_F_RESIDUAL));
   g.pack_bytes = g.pack ? round_up((int64_t)d->n * g.rows_per_batch * g.cp * g.esize, 256) : 0;
-  g.part_bytes = g.split > 1 ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
+  g.part_bytes = (g.split > 1 && g.wsets == 1) ? (int64_t)g.split * d->n * s_out * d->cout * 4 : 0;
   if (g.layout == WL_EXPAND) g.z_bytes = (int64_t)g.ncols * d->n * g.rows_per_batch * 4;
   return CTMR_OK;
 }
@@ -3299,11 +3339,13 @@ static void launch_lds(int xf, dim3 grid, hipStream_t st, const LdsArgs& a) {
 // not use: 60 KiB + 4 KiB of partial buffers per workgroup, two per 160 KiB CU.
 constexpr size_t kConvTwoPerCuLds = 60 * 1024;
 
-template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false, int KWS = 1>
-static void launch_conv(dim3 grid, dim3 block, hipStream_t st, const ConvArgs& a) {
-  // KWS = 4 holds 48 KiB of quarter sums in LDS: 8 KiB more keeps it at two per CU.
-  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP, DIRECT, KWS>), grid, block,
-                     KWS > 1 ? 8 * 1024 : NSUB == 4 ? kConvTwoPerCuLds : 0, st, a);
+template <int DT, int NSUB, int WM, int WN, int KT, int STRIDE, bool UP, bool DIRECT = false, int KWS = 1,
+          int SETS = 1>
+static void launch_conv(dim3 grid, dim3, hipStream_t st, const ConvArgs& a) {
+  // KWS = 4 holds 48 KiB of quarter sums in LDS: 8 KiB more keeps it at two per CU.  Two wave sets (512
+  // threads, 96 KiB of quarter sums) run one per CU.
+  hipLaunchKernelGGL((conv_kernel<DT, NSUB, WM, WN, KT, STRIDE, UP, DIRECT, KWS, SETS>), grid, dim3(256 * SETS),
+                     SETS == 2 ? 0 : KWS > 1 ? 8 * 1024 : NSUB == 4 ? kConvTwoPerCuLds : 0, st, a);
 }
 
 // Compute units of the current device (cached per device).
@@ -3347,7 +3389,16 @@ static ConvFn pick_kind(int KT, int stride, bool up) {
 
 template <int DT, int NSUB, int WM, int WN>
 static ConvFn pick_kind(const Geometry& g, int stride, bool up) {
-  if constexpr (WM * WN == 1) {  // the K split over the four waves (g.kws)
+  if constexpr (WM * WN == 1) {  // the K split over the four waves (g.kws), in one or two wave sets
+    if (g.wsets == 2) {
+      if constexpr (DT == CTMR_F32) {
+        if (g.direct) return stride == 2 ? launch_conv<DT, NSUB, 1, 1, 3, 2, false, true, 4, 2>
+                                         : launch_conv<DT, NSUB, 1, 1, 3, 1, false, true, 4, 2>;
+      }
+      if (up) return launch_conv<DT, NSUB, 1, 1, 2, 1, true, false, 4, 2>;
+      if (stride == 2) return launch_conv<DT, NSUB, 1, 1, 3, 2, false, false, 4, 2>;
+      return launch_conv<DT, NSUB, 1, 1, 3, 1, false, false, 4, 2>;
+    }
     if constexpr (DT == CTMR_F32) {
       if (g.direct) return stride == 2 ? launch_conv<DT, NSUB, 1, 1, 3, 2, false, true, 4>
                                        : launch_conv<DT, NSUB, 1, 1, 3, 1, false, true, 4>;
@@ -3879,13 +3930,15 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
   a.n_tiles = g.n_tiles;
   a.planar = 0;
   a.zstride = 0;
-  a.stats = g.split > 1 ? nullptr : stats;
+  const bool partial = g.split > 1 && g.wsets == 1;  // partial planes and a reduction launch
+  a.stats = partial ? nullptr : stats;
   a.gn_groups = stats ? groups : 0;
   a.gn_cpg = stats ? desc->cout / groups : 1;
   a.stats_tiles = tiles;
   float* part = (float*)((char*)workspace + g.pack_bytes);
-  a.y = g.split > 1 ? part : y;
-  if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
+  a.y = partial ? part : y;
+  if (partial) { a.res = nullptr; a.has_res = 0; }
+  if (g.wsets == 2) a.split = 1;  // the kernel's two K ranges are its wave sets
   float* z = (float*)((char*)workspace + g.pack_bytes + g.part_bytes);
   if (g.layout == WL_EXPAND) {
     // GEMM over every padded row into planar tap columns; bias and residual
@@ -3902,7 +3955,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.res = nullptr;
     a.has_res = 0;
   }
-  const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
+  const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * a.split;
   a.items = g.pointwise ? (int)((int64_t)g.m_tiles * desc->n * g.split) : 0;  // launch_pointwise sizes its grid
   a.in_d = desc->d;
   a.in_h = desc->h;
@@ -3918,7 +3971,7 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
                        (desc->flags & CTMR_F_RESIDUAL) ? residual : nullptr, y);
     return check_launch("tap_sum");
   }
-  if (g.split > 1) {
+  if (partial) {
     launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
     if ((rc = check_launch("split_reduce"))) return rc;
   }
