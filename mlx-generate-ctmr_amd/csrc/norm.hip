@@ -174,13 +174,24 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float* __restrict
   }
 }
 
+// Norm group of finalize workgroup `idx` of `groups` (grid x = groups, so the
+// hardware deals workgroups idx, idx + 8, .. to one XCD): each XCD takes a
+// contiguous run of groups, whose partials share 128-byte lines of the
+// (tile, group) layout -- the lines are fetched by one or two XCDs' L2s
+// instead of all eight.  The order inside a group is unchanged.
+__device__ __forceinline__ int finalize_group(int idx, int groups) {
+  if (groups % 8 != 0) return idx;
+  return (idx % 8) * (groups / 8) + idx / 8;
+}
+
 // Thread t's sums of items t, t + 256, t + 512, .. (ascending, one running
-// (sum, sum of squares) pair): pair(i) is item i's partial pair.  Eight items'
-// loads are issued before their adds, so the loop waits for memory once per
-// eight items instead of once per item; the order of the adds is unchanged.
+// (sum, sum of squares) pair): pair(i) is item i's partial pair.  Sixteen
+// items' loads are issued before their adds, so the loop waits for memory once
+// per sixteen items instead of once per item; the order of the adds is
+// unchanged.
 template <typename Pair>
 __device__ __forceinline__ void strided_pair_sums(int64_t items, Pair pair, double& sm, double& sq) {
-  constexpr int kDepth = 8;
+  constexpr int kDepth = 16;
   int64_t i = threadIdx.x;
   for (; i + (kDepth - 1) * 256 < items; i += kDepth * 256) {
     double a[kDepth], q[kDepth];
@@ -216,7 +227,7 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(const double* __restri
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta,
                                                           float eps, float* __restrict__ affine) {
-  const int g = blockIdx.x, b = blockIdx.y;
+  const int g = finalize_group(blockIdx.x, groups), b = blockIdx.y;
   const int cpg = c / groups;
   const int64_t items = (int64_t)chunks * cpg;
   double sm = 0, sq = 0;
@@ -235,7 +246,7 @@ __global__ __launch_bounds__(256) void gn_tiles_finalize_kernel(const double* __
                                                                 const float* __restrict__ gamma,
                                                                 const float* __restrict__ beta, float eps,
                                                                 float* __restrict__ affine) {
-  const int g = blockIdx.x, b = blockIdx.y;
+  const int g = finalize_group(blockIdx.x, groups), b = blockIdx.y;
   double sm = 0, sq = 0;
   strided_pair_sums(tiles, [&](int64_t i) { return part + (((int64_t)b * tiles + i) * groups + g) * 2; }, sm, sq);
   gn_group_affine(sm, sq, g, b, c, groups, count, gamma, beta, eps, affine);
@@ -258,7 +269,7 @@ __global__ __launch_bounds__(256) void gn_stats_finalize_kernel(StatSource s1, S
                                                                 int64_t count, const float* __restrict__ gamma,
                                                                 const float* __restrict__ beta, float eps,
                                                                 float* __restrict__ affine) {
-  const int g = blockIdx.x, b = blockIdx.y;
+  const int g = finalize_group(blockIdx.x, groups), b = blockIdx.y;
   const int cpg = c / groups, lo = g * cpg, hi = lo + cpg;
   double sm = 0, sq = 0;
   const StatSource* src[2] = {&s1, &s2};
