@@ -188,7 +188,11 @@ int ctmr_pack_upsample_weight(const ctmr_conv_desc* desc, const float* weight, v
  * (inner).  Deep small grids split by the library's policy (split of
  * at least 4 for the 128-wide tiles) run 64 x 64 tiles whose four waves sum
  * four contiguous quarters of each split range, added in ascending order
- * before the partial plane is stored; ctmr_conv3d_split reports the planes.
+ * before the partial plane is stored; ctmr_conv3d_split reports the ranges.
+ * A split of two of those (and of the fp32 LDS-staged GEMM, over an even
+ * count of 16-channel chunks) runs inside one 512-thread workgroup as two
+ * wave sets: the second range's sum is added after the bias, the order of
+ * the split reduction, with no partial planes in the workspace.
  * One-tap GEMMs (1x1x1, im2col rows) with cout % 4 == 0 and
  * no per-batch bias or residual run on a persistent grid with the streaming
  * GEMM's per-output order, so their outputs equal the CTMR_F_STREAM ones bit
@@ -271,8 +275,8 @@ int ctmr_conv3d_gemm(const ctmr_conv_desc* desc, const float* x, const void* pac
  *     produce them (cout <= 4, groups not dividing cout, a group that does not
  *     divide the GEMM's column tile; on a K split, cout not a multiple of 64 or
  *     a group wider than 64 channels); use ctmr_gn_affine on the output then.
- *     A tile is a GEMM output tile, or on a K split a chunk of output voxels
- *     of the reduction.
+ *     A tile is a GEMM output tile, or on a K split with partial planes a
+ *     chunk of output voxels of the reduction.
  *   ctmr_conv3d_gn: ctmr_conv3d that also writes fp64 (sum, sum of squares) of
  *     the stored output per (batch item, tile, group), each summed in a fixed
  *     order, into stats[((b * tiles + tile) * groups + g) * 2 + {0, 1}].  The
