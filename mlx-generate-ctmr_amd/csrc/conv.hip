@@ -2308,13 +2308,23 @@ __device__ __forceinline__ int lds16_weight_offset(int tid, int j, int n0, int t
 // two-tap rows per chunk.  The parity is part of the workgroup index, so one
 // launch covers all eight.  DT: CTMR_BF16 (32-channel chunks) or CTMR_F16X2
 // (16-channel chunks of hi/lo pairs, outputs scaled back by the packed
-// weight's power-of-two column scales before the epilogue).
-template <int DT, bool UP>
-__global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
+// weight's power-of-two column scales before the epilogue).  WS = 2: a K
+// split of two inside the workgroup, as conv_lds_kernel's wave sets (each set
+// its own halo and weight rows; every barrier is the workgroup's, and both
+// sets run the same chunk count).
+template <int DT, bool UP, int WS>
+__global__ __launch_bounds__(256 * WS, WS == 1 ? 2 : 1) void conv_lds_bf16_kernel(Lds16Args p) {
   using Cfg = Lds16Cfg<DT>;
-  __shared__ __attribute__((aligned(256))) char halo[kB16HaloBytes];
-  __shared__ __attribute__((aligned(256))) char bbuf[2][Cfg::row_bytes];
-  const int tid = threadIdx.x, lane = tid & 63;
+  static_assert(WS == 1 || WS == 2, "one or two wave sets");
+  // A set's region: the halo, then the two weight rows; regions start on
+  // 256-byte boundaries, as the single set's arrays did.
+  constexpr int kSetBytes = (kB16HaloBytes + 2 * Cfg::row_bytes + 255) / 256 * 256;
+  static_assert(kB16HaloBytes % 256 == 0 && Cfg::row_bytes % 16 == 0, "aligned halo and weight rows");
+  __shared__ __attribute__((aligned(256))) char lds_sets[WS * kSetBytes];
+  const int set = WS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+  char* const halo = lds_sets + set * kSetBytes;
+  char (*const bbuf)[Cfg::row_bytes] = reinterpret_cast<char (*)[Cfg::row_bytes]>(halo + kB16HaloBytes);
+  const int tid = threadIdx.x & 255, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nb = gridDim.x, bid = blockIdx.x;
   const int xcd = bid & 7, slot = bid >> 3, per = nb >> 3, rem = nb & 7;
@@ -2404,8 +2414,9 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int c_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)split_id * p.kb / p.split));
-  const int c_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(split_id + 1) * p.kb / p.split));
+  const int kpart = split_id * WS + set, kparts = p.split * WS;
+  const int c_begin = __builtin_amdgcn_readfirstlane((int)((int64_t)kpart * p.kb / kparts));
+  const int c_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(kpart + 1) * p.kb / kparts));
 
   // Weight rows are numbered k = 9 * (chunk - c_begin) + row and live in
   // buffer k & 1; row k refills its own buffer with row k + 2.
@@ -2491,8 +2502,32 @@ __global__ __launch_bounds__(256, 2) void conv_lds_bf16_kernel(Lds16Args p) {
       for (int ms = 0; ms < 4; ++ms) acc[ms][ns] *= sc;
     }
   }
-  store_brick<UP>(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, ((bz * p.ty + by) * p.tx + bx) * (UP ? 8 : 1) + phase,
-                  reinterpret_cast<double (*)[64][2]>(halo), phase);  // the reduction buffer reuses the halo
+  const int tile_id = ((bz * p.ty + by) * p.tx + bx) * (UP ? 8 : 1) + phase;
+  // The statistics' reduction buffer reuses set 0's halo (its first 4 KiB).
+  double (*const red)[64][2] = reinterpret_cast<double (*)[64][2]>(lds_sets);
+  if constexpr (WS == 2) {
+    // Set 1 hands its sums to set 0 through LDS past that buffer (64 KiB of
+    // the two sets' regions) once every wave has finished its last chunk.
+    f4* const xs = reinterpret_cast<f4*>(lds_sets + 4096);
+    static_assert(4096 + 4 * 16 * 64 * 16 <= WS * kSetBytes, "hand-over buffer");
+    __syncthreads();
+    if (set == 1) {
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) xs[(wave * 16 + ms * 4 + ns) * 64 + lane] = acc[ms][ns];
+    }
+    __syncthreads();
+    if (set == 1) return;
+    store_brick<UP>(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, tile_id, red, phase, [&](f4 (&a)[4][4]) {
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) a[ms][ns] += xs[(wave * 16 + ms * 4 + ns) * 64 + lane];
+    });
+  } else {
+    store_brick<UP>(p, acc, b, split_id, z0, y0, x0, n0, wave, lane, tile_id, red, phase);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -3209,6 +3244,9 @@ static int geometry(const ctmr_conv_desc* d, Geometry& g) {
     const int64_t base = (int64_t)g.m_tiles * g.n_tiles * d->n * g.phases;
     g.split = d->split > 0 ? d->split
                            : (base < 512 ? (int)std::min<int64_t>(ceil_div(512, base), g.kblocks) : 1);
+    // A split of two over an even chunk count runs as two wave sets of one
+    // workgroup (same output bits, no partial planes, no reduction launch).
+    g.wsets = (g.split == 2 && g.kblocks % 2 == 0) ? 2 : 1;
   } else if (d->split > 0) {
     if (d->split > steps) return fail(CTMR_E_INVALID, "split must not exceed the K step count");
     g.split = d->split;
@@ -3319,6 +3357,13 @@ static void launch_split_reduce(const ctmr_conv_desc* d, const Geometry& g, cons
 }
 
 typedef void (*ConvFn)(dim3, dim3, hipStream_t, const ConvArgs&);
+
+// conv_lds_bf16_kernel, nearest-2x parity form or not.
+template <int DT, int WS>
+static void launch_lds16(bool up, dim3 grid, hipStream_t st, const Lds16Args& a) {
+  if (up) hipLaunchKernelGGL((conv_lds_bf16_kernel<DT, true, WS>), grid, dim3(256 * WS), 0, st, a);
+  else hipLaunchKernelGGL((conv_lds_bf16_kernel<DT, false, WS>), grid, dim3(256 * WS), 0, st, a);
+}
 
 // conv_lds_kernel for a staging transform xf (bit 0 affine, bit 1 SiLU).
 template <bool TWO, int WS>
@@ -3877,24 +3922,26 @@ static int conv3d_gemm_impl(const ctmr_conv_desc* desc, const float* x, const fl
     a.batch_bias = (desc->flags & CTMR_F_BATCH_BIAS) != 0;
     a.has_bias = bias != nullptr;
     a.has_res = (desc->flags & CTMR_F_RESIDUAL) != 0;
-    a.stats = g.split > 1 ? nullptr : stats;
+    const bool partial = g.split > 1 && g.wsets == 1;  // partial planes and a reduction launch
+    a.stats = partial ? nullptr : stats;
     a.gn_groups = stats ? groups : 0;
     a.gn_cpg = stats ? desc->cout / groups : 1;
     float* part = (float*)((char*)workspace + g.pack_bytes);
-    a.y = g.split > 1 ? part : y;
-    if (g.split > 1) { a.res = nullptr; a.has_res = 0; }
-    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * g.split;
+    a.y = partial ? part : y;
+    if (partial) { a.res = nullptr; a.has_res = 0; }
+    if (g.wsets == 2) a.split = 1;  // the kernel's two K ranges are its wave sets
+    const int64_t blocks = (int64_t)g.m_tiles * g.n_tiles * desc->n * g.phases * a.split;
     if (f16x2 && ((uintptr_t)packed & 15) != 0) return fail(CTMR_E_INVALID, "packed weight must be 16-byte aligned");
-    const dim3 grid((unsigned)blocks), block(256);
+    const dim3 grid((unsigned)blocks);
     if (f16x2) {
-      if (g.phases == 8) hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_F16X2, true>), grid, block, 0, st, a);
-      else hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_F16X2, false>), grid, block, 0, st, a);
+      if (g.wsets == 2) launch_lds16<CTMR_F16X2, 2>(g.phases == 8, grid, st, a);
+      else launch_lds16<CTMR_F16X2, 1>(g.phases == 8, grid, st, a);
     } else {
-      if (g.phases == 8) hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_BF16, true>), grid, block, 0, st, a);
-      else hipLaunchKernelGGL((conv_lds_bf16_kernel<CTMR_BF16, false>), grid, block, 0, st, a);
+      if (g.wsets == 2) launch_lds16<CTMR_BF16, 2>(g.phases == 8, grid, st, a);
+      else launch_lds16<CTMR_BF16, 1>(g.phases == 8, grid, st, a);
     }
     if ((rc = check_launch("conv_lds_bf16"))) return rc;
-    if (g.split > 1) {
+    if (partial) {
       launch_split_reduce(desc, g, part, a.plane, bias, a.batch_bias, residual, y, s_out, groups, stats, st);
       if ((rc = check_launch("split_reduce"))) return rc;
     }
