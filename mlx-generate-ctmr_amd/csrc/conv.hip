@@ -3731,14 +3731,23 @@ static int pack_impl(const ctmr_conv_desc* desc, const float* x, const float* x2
     return check_launch("pack_trilinear");
   }
   if (vec && !pa.trilinear) {
-    constexpr int PZ = 4;
-    const dim3 grid((unsigned)ceil_div(plane_items, 256), (unsigned)std::min<int64_t>(ceil_div(planes, PZ), 65535));
-    if (pa.split16)
-      hipLaunchKernelGGL((pack_planes_kernel<2, PZ, true>), grid, dim3(256), 0, (hipStream_t)stream, pa);
-    else if (pa.bf16)
-      hipLaunchKernelGGL((pack_planes_kernel<2, PZ>), grid, dim3(256), 0, (hipStream_t)stream, pa);
-    else
-      hipLaunchKernelGGL((pack_planes_kernel<1, PZ>), grid, dim3(256), 0, (hipStream_t)stream, pa);
+    // Four planes per thread; copies that would then fill under four
+    // workgroups per CU (the deep levels' 1-4 MB copies) take one plane per
+    // thread, four times the workgroups and a quarter of each thread's chain.
+    const int64_t gx = ceil_div(plane_items, 256);
+    const bool one = gx * ceil_div(planes, 4) < 4 * (int64_t)device_cus();
+    const dim3 grid((unsigned)gx, (unsigned)std::min<int64_t>(ceil_div(planes, one ? 1 : 4), 65535));
+    const hipStream_t ps = (hipStream_t)stream;
+    if (pa.split16) {
+      if (one) hipLaunchKernelGGL((pack_planes_kernel<2, 1, true>), grid, dim3(256), 0, ps, pa);
+      else hipLaunchKernelGGL((pack_planes_kernel<2, 4, true>), grid, dim3(256), 0, ps, pa);
+    } else if (pa.bf16) {
+      if (one) hipLaunchKernelGGL((pack_planes_kernel<2, 1>), grid, dim3(256), 0, ps, pa);
+      else hipLaunchKernelGGL((pack_planes_kernel<2, 4>), grid, dim3(256), 0, ps, pa);
+    } else {
+      if (one) hipLaunchKernelGGL((pack_planes_kernel<1, 1>), grid, dim3(256), 0, ps, pa);
+      else hipLaunchKernelGGL((pack_planes_kernel<1, 4>), grid, dim3(256), 0, ps, pa);
+    }
     return check_launch("pack_planes");
   }
   hipLaunchKernelGGL(pack_input_kernel,
