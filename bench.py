@@ -919,7 +919,7 @@ def main() -> int:
                    "flop_per_step": flops, "step": "implicit-GEMM conv reading x directly"},
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": FP32_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK, 4), "traffic": None,
-                     "kernel": "conv_lds_kernel<false, 0> (fp32 LDS-staged implicit GEMM, one input tensor, no staging transform, reads x directly)",
+                     "kernel": "conv_lds_kernel<false, 0, 1> (fp32 LDS-staged implicit GEMM, one input tensor, no staging transform, one wave set, reads x directly)",
                      "kernel_ms": round(gemm_ms, 4), "kernel_timing": "HIP events around each GEMM launch "
                      "of pack+GEMM rounds on the launch stream"},
     }
