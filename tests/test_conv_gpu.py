@@ -609,6 +609,49 @@ def test_validation_errors(ctmr, dev):
         f.implicit_gemm_conv3d(torch.zeros((1, 4, 4, 4, 32), device=dev), packed, None, cout=16)
 
 
+@pytest.mark.parametrize("precision", ["fp32", "f16x2", "bf16"])
+def test_split_of_two_as_wave_sets(ctmr, dev, precision):
+    """A K split of two on the LDS GEMMs (fp32; 16-bit for split fp16 and bf16) runs as two wave sets of
+    one workgroup: no partial planes in the workspace, within the bar of float64 with GN affine + SiLU,
+    per-batch bias and a residual, within fp32 rounding of a four-range split over partial planes, the
+    same bits with statistics as without, and statistics that sum the stored outputs."""
+    f, L, ops = ctmr.fast_fp32, ctmr._lib, ctmr.ops
+    rng = np.random.default_rng(77)
+    shape, cout = (2, 8, 16, 16, 128), 128
+    n, c = shape[0], shape[-1]
+    x = (2 * rng.standard_normal(shape) + 0.5).astype(np.float32)
+    w = (rng.standard_normal((cout, c, 3, 3, 3)) / np.sqrt(27 * c)).astype(np.float32)
+    bias = rng.standard_normal((n, cout)).astype(np.float32)
+    res = rng.standard_normal((*shape[:-1], cout)).astype(np.float32)
+    gw = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    gb = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    affine = f.group_norm_affine(_t(x, dev), _t(gw, dev), _t(gb, dev), groups=32, eps=1e-6)
+    expected = (rm.conv3d(rm.group_norm(x, gw, gb, 32, 1e-6, apply_silu=True), w)
+                + bias[:, None, None, None, :] + res)
+    packed = f.pack_weight(_t(w, dev), dtype=precision)
+    code = f._PACKED_DTYPES[packed.dtype]
+    flags = ops._flags(True, True, True, True)
+    ws = {s: L.workspace_bytes(ops.make_desc(shape, cout, 3, 1, 0, flags, code, s)) for s in (2, 4)}
+    route = L.conv_kernel(ops.make_desc(shape, cout, 3, 1, 0, flags, code, 2))
+    assert route == ("lds" if precision == "fp32" else "lds_f16x2" if precision == "f16x2" else "lds_bf16")
+    assert ws[2] < ws[4]  # the four-range split keeps partial planes, the split of two none
+    call = dict(cout=cout, affine=affine, silu=True, residual=_t(res, dev))
+    y2 = f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), split=2, **call)
+    assert torch.equal(y2, f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), split=2, **call))
+    bar = {"fp32": FP32_REL, "f16x2": FP32_REL, "bf16": BF16_REL}[precision]
+    _assert_rel(_h(y2), expected, bar, f"split of two as wave sets ({precision})")
+    y4 = f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), split=4, **call)
+    assert rm.max_rel_error(_h(y2), _h(y4)) <= FP32_REL
+    y_gn = f.implicit_gemm_conv3d(_t(x, dev), packed, _t(bias, dev), split=2, gn_groups=32, **call)
+    assert torch.equal(y_gn, y2)
+    stats = f.conv_output_stats(y_gn, 32)
+    assert stats is not None
+    yh = _h(y2).astype(np.float64).reshape(n, -1, 32, cout // 32)
+    totals = stats.cpu().numpy().sum(axis=1)
+    assert rm.max_rel_error(totals[..., 0], yh.sum(axis=(1, 3))) <= 1e-12
+    assert rm.max_rel_error(totals[..., 1], (yh * yh).sum(axis=(1, 3))) <= 1e-12
+
+
 KWS_CASES = [
     # (name, x shape NDHWC, cout, keyword arguments): deep small grids the library splits over K,
     # where the four waves of a 64 x 64 tile sum quarters of each split range
