@@ -44,6 +44,8 @@ HBM_PEAK = 8.0e12
 # split fp16 (CTMR_F16X2): per fp32 multiply-add two K=32 fp16 MFMAs over 16 channels (hi and lo of the
 # input against the weight's hi, then against its lo): 4 fp16 MFMA FLOPs per algorithmic FLOP
 F16X2_PEAK = BF16_PEAK / 4
+# split-fp16 attention: three fp16 MFMA products (hi*hi, hi*lo, lo*hi) per algorithmic multiply-add
+ATTN_F16X2_PEAK = BF16_PEAK / 3
 
 
 def progress(msg):
@@ -223,6 +225,23 @@ def secondary(pkg, dev, steps, cpu=False):
                                           "hbm_GBps": round(nbytes / ms / 1e6, 1),
                                           "frac_hbm": round(nbytes / ms / 1e-3 / HBM_PEAK, 4)}
     del xc
+    # flash attention at the production UNet's 2048-token level (16x16x8 latent, 8 heads of 32, batch 2):
+    # FP32 MFMA, and the reference's split-fp16 kernel (whole operator: the split pass and the kernel)
+    g = torch.Generator(device=dev).manual_seed(0)
+    qkv = torch.randn(2, 2048, 768, device=dev, generator=g)
+    q, k, v = qkv[..., :256], qkv[..., 256:512], qkv[..., 512:]
+    run = lambda: f.flash_attention(q, k, v, heads=8, scale=32 ** -0.5)
+    flops = 4.0 * 2048 * 2048 * 32 * 8 * 2
+    warm_up(run, 5, settle_s=0.3)
+    ms = _wall_ms(run, 4 * steps)
+    with f.precision("f16x2"):
+        warm_up(run, 5, settle_s=0.3)
+        msx = _wall_ms(run, 4 * steps)
+    out["attention_level2_2048tok_8h"] = {"ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 2),
+                                          "frac_fp32_peak": round(flops / ms / 1e-3 / FP32_PEAK, 4),
+                                          "f16x2_ms": round(msx, 4), "f16x2_tflops": round(flops / msx / 1e9, 2),
+                                          "f16x2_frac_peak": round(flops / msx / 1e-3 / ATTN_F16X2_PEAK, 4)}
+    del qkv
     if cpu:
         from oracle import cpu_baseline as cb
 
@@ -384,7 +403,7 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         gmsx = _wall_ms(gstep, max(3, steps // 2))
         del graph
     progress(f"config 3 UNet step f16x2 {msx:.3f} ms, graph {gmsx:.3f} ms")
-    floorx = (conv_f / F16X2_PEAK + attn_f / FP32_PEAK) * 1e3
+    floorx = (conv_f / F16X2_PEAK + attn_f / ATTN_F16X2_PEAK) * 1e3
     out["config3_unet_step_batch2_64x64x32"].update(
         {"graph_ms": round(gms, 3), "graph_frac_roofline": round(floor_ms / gms, 4),
          "bf16_ms": round(ms16, 3), "bf16_graph_ms": round(gms16, 3), "bf16_roofline_ms": round(floor16, 3),
@@ -412,7 +431,7 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         ct_msx = _wall_ms(ct_step, max(3, steps // 2))
     cconv, cattn = controlnet_flops(cc, 2, 64, 64, 32)
     ct_flop = conv_f + attn_f + cconv + cattn
-    ct_floorx = ((conv_f + cconv) / F16X2_PEAK + (attn_f + cattn) / FP32_PEAK) * 1e3
+    ct_floorx = ((conv_f + cconv) / F16X2_PEAK + (attn_f + cattn) / ATTN_F16X2_PEAK) * 1e3
     out["ct_controlnet_unet_step_batch2_64x64x32"] = {
         "ms": round(ct_ms, 3), "controlnet_ms": round(ctrl_ms, 3),
         "controlnet_tflop": round((cconv + cattn) / 1e12, 4), "tflops": round(ct_flop / ct_ms / 1e9, 2),
@@ -515,7 +534,7 @@ def networks(pkg, dev, steps, generation=True, cpu=False):
         progress(f"256^3 MR generation f16x2 {totalx:.3f} s")
         gen_f = 30 * sum(unet_flops(uc, 2, 64, 64, 64)) + dec_f
         gen_attn = 30 * unet_flops(uc, 2, 64, 64, 64)[1]
-        gen_floorx = (gen_f - gen_attn) / F16X2_PEAK + gen_attn / FP32_PEAK
+        gen_floorx = (gen_f - gen_attn) / F16X2_PEAK + gen_attn / ATTN_F16X2_PEAK
         out["generation_256^3_30steps_cfg"] = {
             "s": round(total, 3), "sampling_s": round(float(np.median(phases32[1:])), 3), "tflop": round(gen_f / 1e12, 2),
             "roofline_s": round(gen_f / FP32_PEAK, 3), "frac_roofline": round(gen_f / FP32_PEAK / total, 4),
@@ -566,7 +585,7 @@ def ct_generation(pkg, dev, uw, vw, timed):
     stages = {k: round(float(np.median([r[k] for r in stages32[1:]])), 3) for k in stages32[0]}
     stagesx = {k: round(float(np.median([r[k] for r in results[1:]])), 3) for k in results[0]}
     attn = 30 * (unet_flops(uc, 1, 64, 64, 64)[1] + controlnet_flops(cc, 1, 64, 64, 64)[1])
-    floorx = (flop - attn) / F16X2_PEAK + attn / FP32_PEAK
+    floorx = (flop - attn) / F16X2_PEAK + attn / ATTN_F16X2_PEAK
     return {"s": round(sec, 3), "stages_s": stages, "tflop": round(flop / 1e12, 2), "decode_windows": windows,
             "roofline_s": round(flop / FP32_PEAK, 3), "frac_roofline": round(flop / FP32_PEAK / sec, 4),
             "f16x2_s": round(secx, 3), "f16x2_stages_s": stagesx, "f16x2_roofline_s": round(floorx, 3),
@@ -608,7 +627,7 @@ def production_grids(pkg, dev, uw, vw, timed):
         progress(f"{name} generation {sec:.3f} s, f16x2 {secx:.3f} s")
         flop = 30 * sum(unet_flops(uc, 2, *latent)) + vae_decoder_flops(vc, *latent)
         attn = 30 * unet_flops(uc, 2, *latent)[1]
-        floorx = (flop - attn) / F16X2_PEAK + attn / FP32_PEAK
+        floorx = (flop - attn) / F16X2_PEAK + attn / ATTN_F16X2_PEAK
         out[name] = {"s": round(sec, 3), "tflop": round(flop / 1e12, 2), "roofline_s": round(flop / FP32_PEAK, 3),
                      "frac_roofline": round(flop / FP32_PEAK / sec, 4), "f16x2_s": round(secx, 3),
                      "f16x2_roofline_s": round(floorx, 3), "f16x2_frac_roofline": round(floorx / secx, 4),
@@ -635,7 +654,7 @@ def production_grids(pkg, dev, uw, vw, timed):
     step_f = sum(unet_flops(uc, 1, 64, 64, 32)) + sum(controlnet_flops(cc, 1, 64, 64, 32))
     flop = controlnet_cond_flops(cc, 1, 256, 256, 128) + 30 * step_f + vae_decoder_flops(vc, 64, 64, 32)
     attn = 30 * (unet_flops(uc, 1, 64, 64, 32)[1] + controlnet_flops(cc, 1, 64, 64, 32)[1])
-    floorx = (flop - attn) / F16X2_PEAK + attn / FP32_PEAK
+    floorx = (flop - attn) / F16X2_PEAK + attn / ATTN_F16X2_PEAK
     out["ct_from_mask_256x256x128_30steps"] = {
         "s": round(sec, 3), "tflop": round(flop / 1e12, 2), "roofline_s": round(flop / FP32_PEAK, 3),
         "frac_roofline": round(flop / FP32_PEAK / sec, 4), "f16x2_s": round(secx, 3),
@@ -795,7 +814,7 @@ def profile_only(pkg, dev, what, steps, warmup):
             fn = lambda: f.conv3d(x, w, b, padding=1, stride=2)
         else:
             fn = lambda: f.norm_conv3d(x, w, b, norm=None, num_groups=1, eps=1e-6, apply_silu=False, upsample=True)
-    elif what == "attention":
+    elif what in ("attention", "attention_f16x2"):
         # production UNet level-2 attention: 16x16x8 latent = 2048 tokens, 256 channels = 8 heads, batch 2
         g = torch.Generator(device=dev).manual_seed(0)
         qkv = torch.randn(2, 2048, 3 * 256, device=dev, generator=g)
@@ -826,7 +845,7 @@ def main() -> int:
     ap.add_argument("--no-generation", action="store_true", help="skip the full 256^3 generation")
     ap.add_argument("--only", choices=["unet", "unet_bf16", "unet_f16x2", "controlnet", "controlnet_f16x2", "decode",
                                        "decode_bf16", "decode_f16x2", "resblock", "resblock_f16x2",
-                                       "attention", "pointwise", "gemms", "gemms_stream", "config2a", "config2b",
+                                       "attention", "attention_f16x2", "pointwise", "gemms", "gemms_stream", "config2a", "config2b",
                                        "output_convs"],
                     help="profiling mode: run only this workload --steps times and print its timing")
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -31,6 +31,8 @@
  *   ctmr_flash_attention      <- _flash_attention.flash_attention (_flash_attention.py:320-360),
  *                                selected by flash_eligible (_flash_attention.py:276-289) from
  *                                fast_fp32.self_attention_tokens (fast_fp32.py:352-392)
+ *   ctmr_flash_attention_f16x2 <- the split-fp16 branch of _flash_attention.flash_attention
+ *                                (_flash_attention.py:336-350: _split, _nax_kernel / _NAX_SOURCE)
  */
 #ifndef CTMR_H
 #define CTMR_H
@@ -42,7 +44,7 @@
 extern "C" {
 #endif
 
-#define CTMR_ABI_VERSION 4
+#define CTMR_ABI_VERSION 5
 
 enum ctmr_status {
   CTMR_OK = 0,
@@ -383,6 +385,23 @@ typedef struct ctmr_attn_desc {
 
 int ctmr_flash_attention(const ctmr_attn_desc* desc, const float* q, const float* k, const float* v,
                          float* out, void* stream);
+
+/* The same attention in the reference's split-fp16 arithmetic, its matrix-unit
+ * kernel (_flash_attention.py:140-290, chosen at :336-350 when the device has
+ * one): q * scale * log2(e), k and v are split into fp16 halves hi = fp16(x),
+ * lo = fp16((x - hi) * 2^11) (_flash_attention.py:314-317) in the caller's
+ * workspace, and each product runs as hi*hi + (hi*lo + lo*hi) * 2^-11 on fp16
+ * MFMA with fp32 accumulation; P = 2^(S - m) is split the same way and the
+ * cross terms of P V are summed apart and added at the end.  About 2^-22
+ * relative per product; |q * scale * log2(e)|, |k| and |v| must stay below
+ * 65504.  Same descriptor, checks, tilings and bit-identity across
+ * query_tiles as ctmr_flash_attention.  workspace: at least
+ * ctmr_flash_attention_f16x2_workspace_bytes(desc) bytes, 256-byte aligned
+ * (-1 from that call for an invalid shape); calls sharing a workspace must not
+ * overlap. */
+int64_t ctmr_flash_attention_f16x2_workspace_bytes(const ctmr_attn_desc* desc);
+int ctmr_flash_attention_f16x2(const ctmr_attn_desc* desc, const float* q, const float* k, const float* v,
+                               float* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

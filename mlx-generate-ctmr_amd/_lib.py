@@ -25,7 +25,7 @@ DT_F32, DT_BF16, DT_F16X2 = 0, 1, 2
 KERNEL_NAMES = ("stream", "stream_direct", "lds", "lds_bf16", "pointwise", "split_waves", "tap_expand", "lds_small",
                 "small_cout", "lds_f16x2")
 AVGPOOL2, NEAREST2X, TRILINEAR2X = 0, 1, 2
-ABI_VERSION = 4
+ABI_VERSION = 5
 NOALLOC_SCRATCH_BYTES = 256 << 20  # CTMR_NOALLOC_SCRATCH_BYTES
 
 
@@ -82,6 +82,8 @@ _PROTOTYPES = {
     "ctmr_resample": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _vp, _vp]),
     "ctmr_gn_avgpool": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _vp, _c_i32, _vp, _vp, _vp]),
     "ctmr_flash_attention": (_c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp, _vp]),
+    "ctmr_flash_attention_f16x2_workspace_bytes": (_c_i64, [ctypes.POINTER(AttnDesc)]),
+    "ctmr_flash_attention_f16x2": (_c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp, _vp, _c_i64, _vp]),
 }
 
 _lock = threading.Lock()

@@ -61,7 +61,8 @@ def precision(mode: str) -> Iterator[None]:
     output column by a power of two, and every product is summed as hi*hi + lo*hi + hi*lo on fp16
     MFMA with fp32 accumulation (about 2^-22 relative per product).  It applies to the stride-1
     3x3x3 convs the LDS-staged 16-bit GEMM takes (cout a multiple of 64, at least 16 input
-    channels); every other conv runs on FP32 MFMA.  Values must stay below 65504 in magnitude."""
+    channels) and to flash attention (the reference's split-fp16 kernel, ``_flash_attention.py:
+    140-290``); every other conv runs on FP32 MFMA.  Values must stay below 65504 in magnitude."""
     if mode not in PRECISIONS:
         raise ValueError(f"precision must be one of {PRECISIONS}; got {mode!r}")
     token = _precision.set(mode)
@@ -699,12 +700,22 @@ def _rows(t: Tensor, name: str) -> Tensor:
 def flash_attention(q: Tensor, k: Tensor, v: Tensor, *, heads: int, scale: float, mx=None,
                     query_tiles: int = 0) -> Tensor:
     """``softmax(q k^T * scale) v`` on head-interleaved ``(B, L, heads * 32)`` projections
-    (``_flash_attention.flash_attention``, :320-360); FP32 throughout, output in the same layout."""
+    (``_flash_attention.flash_attention``, :320-360); FP32 MFMA, or under ``precision("f16x2")``
+    the reference's split-fp16 kernel; output in the same layout."""
     q, k, v = _rows(q, "q"), _rows(k, "k"), _rows(v, "v")
     if not flash_eligible(q, k, heads) or v.shape != k.shape or q.shape[0] != k.shape[0]:
         raise ValueError(f"flash attention needs (B, L, heads*32) q/k/v with heads={heads}; got "
                          f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
-    return ops.flash_attention(q, k, v, int(heads), float(scale), int(query_tiles))
+    return _flash(q, k, v, int(heads), float(scale), int(query_tiles))
+
+
+def _flash(q: Tensor, k: Tensor, v: Tensor, heads: int, scale: float, query_tiles: int) -> Tensor:
+    """The HIP flash kernel for the active precision: under ``precision("f16x2")`` the
+    reference's split-fp16 attention (its matrix-unit path, ``_flash_attention.py:336-350``),
+    else FP32 MFMA (``bf16`` keeps attention in FP32, as its norms and projections)."""
+    if _precision.get() == "f16x2":
+        return ops.flash_attention_f16x2(q, k, v, heads, scale, query_tiles)
+    return ops.flash_attention(q, k, v, heads, scale, query_tiles)
 
 
 # Fused (3C, C) Q/K/V projection weights and biases, keyed by all six source
@@ -737,8 +748,8 @@ def attention(query: Tensor, key: Tensor, value: Tensor, *, scale: float, mx=Non
         q = query.contiguous().reshape(b * h, lq, d)
         k = key.contiguous().reshape(b * h, -1, d)
         v = value.contiguous().reshape(b * h, -1, d)
-        return ops.flash_attention(_rows(q, "query"), _rows(k, "key"), _rows(v, "value"), 1, float(scale),
-                                   0).reshape(b, h, lq, d)
+        return _flash(_rows(q, "query"), _rows(k, "key"), _rows(v, "value"), 1, float(scale),
+                      0).reshape(b, h, lq, d)
     return F.scaled_dot_product_attention(query, key, value, scale=scale)
 
 
@@ -761,7 +772,7 @@ def self_attention_tokens(tokens: Tensor, weights: Mapping[str, Tensor], *, head
     qkv = F.linear(tokens, w, b)
     q, k, v = qkv[..., :c], qkv[..., c:2 * c], qkv[..., 2 * c:]
     if c == heads * FLASH_HEAD_DIM:
-        merged = ops.flash_attention(q, k, v, int(heads), float(scale), 0)
+        merged = _flash(q, k, v, int(heads), float(scale), 0)
     else:
         def split(t: Tensor) -> Tensor:
             return t.reshape(n, length, heads, c // heads).transpose(1, 2).contiguous()

@@ -507,3 +507,34 @@ def flash_attention(q: Tensor, k: Tensor, v: Tensor, heads: int, scale: float, q
 @flash_attention.register_fake
 def _(q, k, v, heads, scale, query_tiles=0):
     return q.new_empty(q.shape)
+
+
+@_custom_op("ctmr::flash_attention_f16x2")
+def flash_attention_f16x2(q: Tensor, k: Tensor, v: Tensor, heads: int, scale: float,
+                          query_tiles: int = 0) -> Tensor:
+    """``flash_attention`` in the reference's split-fp16 arithmetic (its matrix-unit kernel,
+    ``_flash_attention.py:140-290``): q (scaled by ``scale * log2(e)``), k and v split into fp16
+    halves in a workspace, products hi*hi + (hi*lo + lo*hi) * 2^-11 on fp16 MFMA with fp32
+    accumulation.  ``|q * scale * log2(e)|``, ``|k|`` and ``|v|`` must stay below 65504."""
+    _require_device(q, k, v)
+    n, lq, c = (int(s) for s in q.shape)
+    lk = int(k.shape[1])
+    out = torch.empty((n, lq, c), device=q.device, dtype=torch.float32)
+    desc = _lib.AttnDesc(n, lq, lk, int(heads), c // int(heads), int(query_tiles),
+                         q.stride(1), k.stride(1), v.stride(1), c, float(scale))
+    lib = _lib.lib()
+    nbytes = int(lib.ctmr_flash_attention_f16x2_workspace_bytes(ctypes.byref(desc)))
+    if nbytes < 0:
+        raise ValueError(f"flash_attention_f16x2: invalid shape {(n, lq, lk, heads)}")
+    ws = torch.empty((nbytes,), device=q.device, dtype=torch.uint8)
+    _lib.check(
+        lib.ctmr_flash_attention_f16x2(ctypes.byref(desc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       out.data_ptr(), ws.data_ptr(), nbytes, _stream(q.device)),
+        "ctmr_flash_attention_f16x2",
+    )
+    return out
+
+
+@flash_attention_f16x2.register_fake
+def _(q, k, v, heads, scale, query_tiles=0):
+    return q.new_empty(q.shape)

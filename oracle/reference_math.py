@@ -1,4 +1,5 @@
-"""Float64 NumPy restatement of the reference's conv / norm math — test infrastructure only.
+"""Float64 NumPy restatement of the reference's conv / norm / split-attention math — test
+infrastructure only.
 
 Layout: activations NDHWC ``(N, D, H, W, C)`` (the reference is NCDHW; the
 math is layout-independent), conv weights Torch ``(O, C, k, k, k)``.
@@ -254,6 +255,43 @@ def apply_affine(x: np.ndarray, affine: np.ndarray, apply_silu: bool) -> np.ndar
     n, c = x.shape[0], x.shape[-1]
     y = x * a[..., 0].reshape(n, 1, 1, 1, c) + a[..., 1].reshape(n, 1, 1, 1, c)
     return silu(y) if apply_silu else y
+
+
+def split_f16(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's split of fp32 values into fp16 halves (_flash_attention.py:314-317, the
+    same split as _nax_conv.py:27-35): ``hi = fp16(x)``, ``lo = fp16((x - hi) * 2^11)``, both
+    rounded to nearest even; returned as float64 (``x ~ hi + lo * 2^-11``)."""
+    x = np.asarray(x, np.float32)
+    hi = x.astype(np.float16)
+    lo = ((x - hi.astype(np.float32)) * np.float32(2048.0)).astype(np.float16)
+    return hi.astype(F64), lo.astype(F64)
+
+
+def flash_attention_split_f16(q: np.ndarray, k: np.ndarray, v: np.ndarray, heads: int,
+                              scale: float) -> np.ndarray:
+    """The reference's split-fp16 multi-head attention (_flash_attention.py:140-290 on the
+    operands prepared at :336-350), with exact (float64) sums of its products.
+
+    ``q * (scale * log2 e)`` (an fp32 product), ``k`` and ``v`` are split by ``split_f16``;
+    scores are ``qh kh + (qh kl + ql kh) * 2^-11`` in log2 units; ``P = 2^(S - max)`` is
+    rounded to fp32 and split the same way, and the output is
+    ``(Ph Vh + (Ph Vl + Pl Vh) * 2^-11) / sum(P)`` per head.  ``(B, L, heads * dh)`` arrays.
+    """
+    q32 = np.asarray(q, np.float32) * np.float32(scale * 1.4426950408889634)
+    n, lq, c = q32.shape
+    dh = c // heads
+
+    def per_head(t: np.ndarray) -> np.ndarray:
+        return t.reshape(n, -1, heads, dh).transpose(0, 2, 1, 3)
+
+    qh, ql = (per_head(t) for t in split_f16(q32))
+    kh, kl = (per_head(t).transpose(0, 1, 3, 2) for t in split_f16(k))
+    vh, vl = (per_head(t) for t in split_f16(v))
+    s = qh @ kh + (qh @ kl + ql @ kh) * 2.0**-11
+    p = np.exp2(s - s.max(axis=-1, keepdims=True)).astype(np.float32)
+    ph, pl = split_f16(p)
+    o = (ph @ vh + (ph @ vl + pl @ vh) * 2.0**-11) / p.astype(F64).sum(axis=-1, keepdims=True)
+    return o.transpose(0, 2, 1, 3).reshape(n, lq, c)
 
 
 def ncdhw_to_ndhwc(x: np.ndarray) -> np.ndarray:

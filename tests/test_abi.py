@@ -225,6 +225,40 @@ def test_attention_host_checks(ctmr, native_loaded, kw, status, message):
     assert "16-byte aligned" in ctmr._lib.last_error()
 
 
+@pytest.mark.parametrize(
+    ("kw", "status", "message"),
+    [
+        ({"head_dim": 16}, -2, "head_dim 16 unsupported"),
+        ({"query_tiles": 3}, -1, "query_tiles"),
+        ({"lq": 0}, -1, ">= 1"),
+        ({"n": 300, "heads": 256}, -1, "65535"),
+        ({"ldo": 60}, -1, "below heads"),
+        ({"ldq": 66}, -1, "multiples of 4"),
+        ({"scale": float("nan")}, -1, "finite"),
+    ],
+)
+def test_split_attention_host_checks(ctmr, native_loaded, kw, status, message):
+    """ctmr_flash_attention_f16x2 applies the same checks, then its workspace's size and alignment,
+    all on the host before any launch (fake pointers are never touched)."""
+    base = dict(n=2, lq=64, lk=50, heads=2, head_dim=32, query_tiles=0, ldq=64, ldk=64, ldv=64, ldo=64, scale=0.17)
+    fake, ws = ctypes.c_void_p(1 << 20), ctypes.c_void_p(1 << 24)
+    d = ctmr._lib.AttnDesc(**{**base, **kw})
+    assert native_loaded.ctmr_flash_attention_f16x2(ctypes.byref(d), fake, fake, fake, fake, ws, 1 << 30, None) == status
+    assert message in ctmr._lib.last_error() and "ctmr_flash_attention_f16x2" in ctmr._lib.last_error()
+    good = ctmr._lib.AttnDesc(**base)
+    # six fp16 planes of n * heads * 32 values per row: Q over lq rows, K and V over lk rounded up to 32
+    need = native_loaded.ctmr_flash_attention_f16x2_workspace_bytes(ctypes.byref(good))
+    assert need == 2 * 2 * 2 * 2 * 32 * (64 + 2 * 64)
+    if kw.get("lq") == 0:
+        assert native_loaded.ctmr_flash_attention_f16x2_workspace_bytes(ctypes.byref(d)) == -1
+    args = (ctypes.byref(good), fake, fake, fake, fake)
+    assert native_loaded.ctmr_flash_attention_f16x2(*args, ws, need - 1, None) == -1
+    assert "workspace of" in ctmr._lib.last_error()
+    assert native_loaded.ctmr_flash_attention_f16x2(*args, None, need, None) == -1
+    assert native_loaded.ctmr_flash_attention_f16x2(*args, ctypes.c_void_p((1 << 24) + 128), need, None) == -1
+    assert "256-byte aligned" in ctmr._lib.last_error()
+
+
 def test_conv_group_norm_partial_tiles(ctmr, native_loaded):
     """``ctmr_conv3d_stats_tiles``: partials per batch item, or 0 where the epilogue cannot write them."""
     L = ctmr._lib

@@ -209,3 +209,43 @@ def test_silu_closed_form():
     v = np.array([0.0, 1.0, -1.0, 20.0, -20.0])
     np.testing.assert_allclose(rm.silu(v), [0.0, 1 / (1 + np.exp(-1)), -1 / (1 + np.e), 20 / (1 + np.exp(-20)), -20 * np.exp(-20) / (1 + np.exp(-20))],
                                rtol=1e-12, atol=1e-12)
+
+
+# --- split-fp16 attention (the reference's matrix-unit kernel) ---------------
+def _attention_f64(q, k, v, heads, scale):
+    n, lq, c = q.shape
+    dh = c // heads
+    split = lambda t: torch.from_numpy(np.asarray(t, np.float64)).reshape(n, -1, heads, dh).transpose(1, 2)
+    s = split(q) @ split(k).transpose(-1, -2).contiguous() * scale
+    return (torch.softmax(s, dim=-1) @ split(v)).transpose(1, 2).reshape(n, lq, c).numpy()
+
+
+def test_split_f16_closed_forms():
+    """fp16-exact values split with a zero low half; 1 + 2^-12 (a tie-free value below half an fp16
+    ulp) splits into 1 and 0.5; random values rebuild to within 2^-22 relative."""
+    hi, lo = rm.split_f16(np.array([1.0, -0.375, 1024.0, 0.0], np.float32))
+    np.testing.assert_array_equal(hi, [1.0, -0.375, 1024.0, 0.0])
+    np.testing.assert_array_equal(lo, 0.0)
+    hi, lo = rm.split_f16(np.array([1.0 + 2.0**-12], np.float32))
+    assert hi[0] == 1.0 and lo[0] == 0.5
+    x = np.random.default_rng(0).standard_normal(10000).astype(np.float32) * 30
+    hi, lo = rm.split_f16(x)
+    assert np.abs(hi + lo * 2.0**-11 - x).max() <= 2.0**-22 * np.abs(x).max()
+
+
+def test_split_attention_is_attention_within_the_split_error():
+    """The restated split attention stays within 1e-6 of float64 attention (the three products carry
+    about 2^-22 relative each), on ragged cross lengths with large scores; the same attention on plain
+    fp16 operands (no low halves: a dropped cross term) misses by more than 1e-4, so the GPU tests'
+    1e-6 bar against this restatement pins the split; a single key returns v."""
+    rng = np.random.default_rng(3)
+    n, lq, lk, heads = 2, 70, 45, 3
+    q, k, v = (rng.standard_normal((n, ln, heads * 32)).astype(np.float32) for ln in (lq, lk, lk))
+    q *= 4
+    scale = 32 ** -0.5
+    ref = _attention_f64(q, k, v, heads, scale)
+    assert rm.max_rel_error(rm.flash_attention_split_f16(q, k, v, heads, scale), ref) <= 1e-6
+    plain = _attention_f64(*(t.astype(np.float16).astype(np.float32) for t in (q, k, v)), heads, scale)
+    assert rm.max_rel_error(plain, ref) > 1e-4
+    one = rm.flash_attention_split_f16(q[:, :5], k[:, :1], v[:, :1], heads, scale)
+    np.testing.assert_allclose(one, np.broadcast_to(v[:, :1], one.shape), rtol=0, atol=2.0**-20)
