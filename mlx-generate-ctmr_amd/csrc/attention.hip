@@ -392,17 +392,19 @@ struct SplitArgs {
   float qscale;        // scale * log2(e), applied to q before the split
 };
 
-// One thread per (tensor, batch item, head, row, 8-dim group); rows run
-// fastest, so the transposed V stores of a wave are contiguous.  Rows at or
-// past the tensor's length (K and V padding) are written as zeros.
+// One thread per (tensor, batch item, head, row, 8-dim group), the four dim
+// groups of a row in adjacent lanes: a row's 128 bytes are read by one
+// quarter-wave, Q's and K's split rows written as 64 contiguous bytes, and V's
+// transposed stores as 32-byte runs.  Rows at or past the tensor's length (K
+// and V padding) are written as zeros.
 __global__ __launch_bounds__(256) void attention_split_kernel(SplitArgs a, int n) {
   const int which = blockIdx.y;
   const int rp = a.rowsp[which];
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)n * a.heads * 4 * rp) return;
-  const int row = (int)(i % rp);
-  const int grp = (int)((i / rp) & 3);
-  const int64_t bh = i / ((int64_t)rp * 4);
+  const int grp = (int)(i & 3);
+  const int row = (int)((i >> 2) % rp);
+  const int64_t bh = (i >> 2) / rp;
   const int b = (int)(bh / a.heads), h = (int)(bh % a.heads);
   f4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
   if (row < a.rows[which]) {
